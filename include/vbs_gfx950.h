@@ -1,0 +1,142 @@
+/* vbs_gfx950.h — C ABI of libvbs_gfx950.so, the MI355X (gfx950) device
+ * library behind Verum's HIP backend slot.
+ *
+ * The reference's HIP backend (src/vbs_backend_hip.c) dlopens the ROCm
+ * runtime and host-stages every op through src/vbs_host_math.h. This library
+ * replaces that: it owns one device, one in-order HIP stream and the
+ * hand-written gfx950 kernels, and exposes them through plain pointers and
+ * sizes (no HIP or torch types). The C11 shim
+ * (host/vbs_backend_gfx950.c) dlopens it, checks vbs_gfx950_abi_version()
+ * and every symbol below, and maps the vbs_backend_ops_t slots onto it.
+ *
+ * Conventions
+ *   - Every function returns 1 on success and 0 on failure; the reason is
+ *     then in vbs_gfx950_last_error(). Nothing aborts or throws.
+ *   - Device pointers come from vbs_gfx950_alloc (or point inside such an
+ *     allocation). All work is enqueued on the library's single stream in
+ *     call order; copies to the host wait for it, so results are visible to
+ *     the caller exactly as with the reference's synchronous backends.
+ *   - `type` values are GGUF type ids (vbs_ggml_type_t): F32 0, F16 1,
+ *     Q4_0 2, Q4_1 3, Q8_0 8, Q4_K 12, Q6_K 14, LNS8 40.
+ */
+#ifndef VBS_GFX950_H
+#define VBS_GFX950_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VBS_GFX950_ABI_VERSION 1
+
+/* ---- library / device ------------------------------------------------ */
+
+/* ABI version of the loaded library; the shim refuses a mismatch, as
+ * vbs_hot_load does for the CPU hot table (src/vbs_hotpath.c:96-101). */
+int vbs_gfx950_abi_version(void);
+
+/* Probe and open the first gfx950 device. Idempotent; a failure is sticky and
+ * explained by vbs_gfx950_last_error(). Replaces hip_init
+ * (src/vbs_backend_hip.c:149-225). */
+int vbs_gfx950_init(void);
+
+/* Last failure reason ("ok" when none). Replaces vbs_hip_last_error
+ * (src/vbs_backend_hip.c:110). */
+const char *vbs_gfx950_last_error(void);
+
+/* Number of usable devices (0 or 1: the backend drives one GPU). Replaces
+ * hip_get_device_count (src/vbs_backend_hip.c:227). */
+int vbs_gfx950_device_count(void);
+
+/* Name, total and free HBM of device `index`. Fills what the reference's HIP
+ * backend left unset (max_working_set_bytes / max_buffer_bytes,
+ * src/vbs_backend_hip.c:214-220). */
+int vbs_gfx950_device_info(int index, char *name, size_t name_cap, uint64_t *total_bytes,
+                           uint64_t *free_bytes);
+
+/* ---- memory (src/vbs_backend_hip.c:230-264) ---------------------------- */
+
+void *vbs_gfx950_alloc(size_t bytes);          /* device memory, 256-B aligned */
+int vbs_gfx950_free(void *dptr);
+void *vbs_gfx950_host_alloc(size_t bytes);     /* pinned host memory */
+int vbs_gfx950_host_free(void *hptr);
+/* Stream-ordered copies that have completed when they return. */
+int vbs_gfx950_copy_h2d(void *dst, const void *src, size_t bytes);
+int vbs_gfx950_copy_d2h(void *dst, const void *src, size_t bytes);
+int vbs_gfx950_copy_d2d(void *dst, const void *src, size_t bytes);
+/* Wait for all enqueued work (src/vbs_backend_hip.c:548-551). */
+int vbs_gfx950_synchronize(void);
+
+/* ---- hot-path kernels --------------------------------------------------- */
+
+/* 1 if `type` has a gfx950 linear kernel: F32, F16, Q4_0, Q4_1, Q8_0, Q4_K,
+ * Q6_K, and LNS8 (the bridge's seventh dispatch type). Mirrors the reference's refusal contract (vbs_host_type_supported,
+ * src/vbs_host_math.h:69-89, and the Q8_K refusal checked by
+ * src/vbs_backend_test.c:952-955). */
+int vbs_gfx950_linear_supported(int type);
+
+/* y[row_off + r] (+)= sum_c deq(W[r, c]) * x[col_off + c] for r < rows,
+ * W row-major in native GGUF blocks, row stride = (cols / block) * bytes.
+ * Replaces hip_dispatch_linear_tile (src/vbs_backend_hip.c:346-394); same
+ * meaning as vbs_host_linear_tile (src/vbs_host_math.h:223-267) with fp32
+ * accumulation. */
+int vbs_gfx950_linear(int type, const void *w, const float *x, float *y, uint32_t cols,
+                      uint32_t rows, uint32_t col_off, uint32_t row_off, int accumulate);
+
+/* out[0..dim) = deq(row `token` of table w), bit-identical to
+ * vbs_host_embed_row (src/vbs_host_math.h:136-142). The EMBEDDING op of
+ * src/vbs_backend_hip.c:405-423. */
+int vbs_gfx950_embed(int type, const void *w, uint32_t token, float *out, uint32_t dim);
+
+/* rms_norm (src/vbs_host_math.h:28-36; NORMALIZE, src/vbs_backend_hip.c:424-439). */
+int vbs_gfx950_rms_norm(const float *in, const float *w, float *out, uint32_t dim, float eps);
+
+/* In-place RoPE on n_heads x head_dim (src/vbs_host_math.h:38-51; ROTARY,
+ * src/vbs_backend_hip.c:440-454). head_dim <= 512. */
+int vbs_gfx950_rope(float *x, uint32_t pos, uint32_t head_dim, uint32_t n_heads, float theta);
+
+/* f16 KV store at ((layer*max_ctx + pos)*kv_dim + i) with the reference
+ * rounding (src/vbs_host_math.h:150-159; CACHE, src/vbs_backend_hip.c:455-481). */
+int vbs_gfx950_cache_store(const float *k, const float *v, uint16_t *kc, uint16_t *vc,
+                           uint32_t pos, uint32_t layer, uint32_t max_ctx, uint32_t kv_dim);
+
+/* Single-query GQA attention over the f16 cache (src/vbs_host_math.h:170-209;
+ * ATTENTION, src/vbs_backend_hip.c:482-512). */
+int vbs_gfx950_attention(const float *q, const uint16_t *kc, const uint16_t *vc, float *out,
+                         uint32_t seq_len, uint32_t layer, uint32_t max_ctx,
+                         uint32_t n_q_heads, uint32_t n_kv_heads, uint32_t head_dim,
+                         float scale);
+
+/* out = gate / (1 + expf(-gate)) * up (src/vbs_host_math.h:53-57; ACTIVATION). */
+int vbs_gfx950_silu_mul(const float *gate, const float *up, float *out, uint32_t n);
+
+/* out = a + b, out may alias a (src/vbs_host_math.h:59-62; ELEMENTWISE). */
+int vbs_gfx950_add(const float *a, const float *b, float *out, uint32_t n);
+
+/* ---- extensions (no slot in vbs_backend_ops_t) -------------------------- */
+
+/* Dequantise rows of a packed tensor: out[i*dim .. +dim) = deq(row ids[i])
+ * (ids == NULL means rows 0..n_rows-1). `ids` is a device array. The batched
+ * form of the one-token-per-dispatch EMBEDDING op, and the bit-exactness
+ * probe of every block decoder. */
+int vbs_gfx950_dequant_rows(int type, const void *w, const uint32_t *ids, uint32_t n_rows,
+                            uint32_t dim, float *out);
+
+/* Batched decode: Y[b*y_stride + r] = sum_c deq(W[r,c]) * X[b*x_stride + c]
+ * for b < batch (<= 16). Equal to `batch` calls of vbs_gfx950_linear; the
+ * weights are read once. The reference has no batched matvec
+ * (src/vbs_specializer.c:353-357 loops tokens one by one). */
+int vbs_gfx950_linear_batch(int type, const void *w, const float *x, uint32_t x_stride,
+                            float *y, uint32_t y_stride, uint32_t cols, uint32_t rows,
+                            uint32_t batch);
+
+/* The library's stream (a hipStream_t), for callers that time kernels with
+ * HIP events or capture the stream into a graph. */
+void *vbs_gfx950_stream(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,252 @@
+"""gfx950 kernels vs the CPU oracle, through the C ABI of libvbs_gfx950.so.
+
+Bars (north star): dequantised values and the gather bit-exact; matvec
+relative L2 error <= 1e-5 against the oracle's double-accumulated
+vbs_host_linear_tile restatement; RoPE, KV store and add bit-exact; RMSNorm
+within 1e-6 relative; SiLU*up 1e-5 and attention 1e-4 (the reference
+self-test's tolerances, src/vbs_backend_test.c:540, 798).
+"""
+import math
+
+import numpy as np
+import pytest
+
+import vbs_gfx950 as V
+
+pytestmark = pytest.mark.gpu
+
+SEED = 20260101
+TYPES = [V.Q4_0, V.Q4_1, V.Q8_0, V.Q4_K, V.Q6_K, V.F16, V.F32]
+LIN_TOL = 1e-5
+
+
+class Mem:
+    """Device allocations freed at the end of a test."""
+
+    def __init__(self, dev):
+        self.dev, self.ptrs = dev, []
+
+    def up(self, a):
+        p = self.dev.upload(a)
+        self.ptrs.append(p)
+        return p
+
+    def zeros(self, n, dtype=np.float32):
+        return self.up(np.zeros(n, dtype))
+
+    def close(self):
+        for p in self.ptrs:
+            self.dev.free(p)
+
+
+@pytest.fixture
+def mem(dev):
+    m = Mem(dev)
+    yield m
+    m.close()
+
+
+def rel_l2(got, want):
+    want = want.astype(np.float64)
+    return float(np.linalg.norm(got.astype(np.float64) - want) / max(np.linalg.norm(want), 1e-30))
+
+
+def synth_x(host, n, stream=7):
+    return V.synth_normal(host, n, SEED, stream)
+
+
+@pytest.mark.parametrize("t", TYPES + [V.LNS8], ids=lambda t: V.TYPE_NAMES[t])
+def test_dequant_rows_bit_exact(dev, host, oracle, mem, t):
+    rows, cols = 48, 4096
+    if t == V.LNS8:
+        # codes U{0..255} (inf above 127 is part of the format) and a finite scale
+        rng = np.random.default_rng(SEED)
+        w = rng.integers(0, 256, size=(rows, cols // 32, 36), dtype=np.uint8)
+        w[:, :, 32:36] = np.frombuffer(np.float32(1.0 / 256).tobytes(), np.uint8)
+        w = w.reshape(rows, -1)
+    else:
+        w = V.synth_matrix(host, t, rows, cols, SEED, 11)
+    pw, out = mem.up(w), mem.zeros(rows * cols)
+    dev.dequant_rows(t, pw, 0, rows, cols, out)
+    got = dev.download(out, (rows, cols), np.float32)
+    want = np.stack([oracle.dequant_row(t, w[r], cols) for r in range(rows)])
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("t", TYPES, ids=lambda t: V.TYPE_NAMES[t])
+@pytest.mark.parametrize("rows,cols", [(16, 4096), (16, 11008), (200, 512), (1, 256)])
+def test_linear_parity(dev, host, oracle, mem, t, rows, cols):
+    w = V.synth_matrix(host, t, rows, cols, SEED, 21)
+    x = synth_x(host, cols)
+    pw, px, py = mem.up(w), mem.up(x), mem.zeros(rows)
+    dev.linear(t, pw, px, py, cols, rows)
+    got = dev.download(py, rows, np.float32)
+    want = oracle.linear(t, w, x, cols, rows)
+    assert rel_l2(got, want) <= LIN_TOL
+
+
+@pytest.mark.parametrize("t,rows,cols", [(V.Q4_K, 4096, 11008), (V.Q4_K, 11008, 4096),
+                                         (V.Q6_K, 4096, 11008), (V.Q8_0, 11008, 4096),
+                                         (V.Q4_0, 4096, 4096)],
+                         ids=["q4k_4096x11008", "q4k_11008x4096", "q6k_4096x11008",
+                              "q80_11008x4096", "q40_4096x4096"])
+def test_linear_full_size(dev, host, oracle, mem, t, rows, cols):
+    w = V.synth_matrix(host, t, rows, cols, SEED, 31)
+    x = synth_x(host, cols)
+    pw, px, py = mem.up(w), mem.up(x), mem.zeros(rows)
+    dev.linear(t, pw, px, py, cols, rows)
+    got = dev.download(py, rows, np.float32)
+    want = oracle.linear(t, w, x, cols, rows, threads=16)
+    assert rel_l2(got, want) <= LIN_TOL
+
+
+def test_linear_offsets_accumulate(dev, host, oracle, mem):
+    """Two column tiles into one output window: offsets index x and y, the
+    second tile accumulates (src/vbs_backend_test.c:888-948)."""
+    t, rows, cols, half = V.Q4_K, 64, 4096, 2048
+    w = V.synth_matrix(host, t, rows, cols, SEED, 41)
+    x = synth_x(host, cols + 512)
+    rb = V.row_bytes(t, half)
+    tiles = [np.ascontiguousarray(w[:, i * rb:(i + 1) * rb]) for i in range(2)]
+    py = mem.up(np.full(rows + 8, 7.0, np.float32))
+    px = mem.up(x)
+    for i, tile in enumerate(tiles):
+        dev.linear(t, mem.up(tile), px, py, half, rows, col_off=256 + i * half, row_off=8,
+                   accumulate=(i == 1))
+    got = dev.download(py, rows + 8, np.float32)
+    want = np.full(rows + 8, 7.0, np.float32)
+    oracle.linear(t, tiles[0], x, half, rows, y=want, col_off=256, row_off=8)
+    oracle.linear(t, tiles[1], x, half, rows, y=want, col_off=256 + half, row_off=8,
+                  accumulate=True)
+    assert np.array_equal(got[:8], want[:8])  # untouched head
+    assert rel_l2(got[8:], want[8:]) <= LIN_TOL
+
+
+@pytest.mark.parametrize("t", [V.Q4_K, V.Q6_K, V.Q8_0], ids=lambda t: V.TYPE_NAMES[t])
+@pytest.mark.parametrize("batch", [1, 3, 8])
+def test_linear_batch_matches_single(dev, host, oracle, mem, t, batch):
+    rows, cols = 96, 4096
+    w = V.synth_matrix(host, t, rows, cols, SEED, 51)
+    X = np.stack([synth_x(host, cols, 60 + b) for b in range(batch)])
+    pw, px, py = mem.up(w), mem.up(X), mem.zeros(batch * rows)
+    dev.linear_batch(t, pw, px, cols, py, rows, cols, rows, batch)
+    got = dev.download(py, (batch, rows), np.float32)
+    for b in range(batch):
+        assert rel_l2(got[b], oracle.linear(t, w, X[b], cols, rows)) <= LIN_TOL
+
+
+@pytest.mark.parametrize("t", TYPES, ids=lambda t: V.TYPE_NAMES[t])
+def test_embed_gather_bit_exact(dev, host, oracle, mem, t):
+    vocab, dim = 1000, 4096
+    table = V.synth_matrix(host, t, vocab, dim, SEED, 61)
+    pt, out = mem.up(table), mem.zeros(dim)
+    ids = [0, 1, 999, 517, 64]
+    for tok in ids:
+        dev.embed(t, pt, tok, out, dim)
+        got = dev.download(out, dim, np.float32)
+        want = oracle.embed(t, table, tok, dim)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_q6k_gather_64_tokens(dev, host, oracle, mem):
+    """Config 3: 64 random ids from a 32000-row Q6_K table, batched gather."""
+    vocab, dim = 32000, 4096
+    table = V.synth_matrix(host, V.Q6_K, vocab, dim, SEED, 62)
+    ids = np.random.default_rng(SEED).integers(0, vocab, 64).astype(np.uint32)
+    pt, pid, out = mem.up(table), mem.up(ids), mem.zeros(64 * dim)
+    dev.dequant_rows(V.Q6_K, pt, pid, 64, dim, out)
+    got = dev.download(out, (64, dim), np.float32)
+    for i, tok in enumerate(ids):
+        want = oracle.embed(V.Q6_K, table, int(tok), dim)
+        assert np.array_equal(got[i].view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("n", [384, 4096, 8192, 1000])
+def test_rms_norm(dev, host, oracle, mem, n):
+    x = synth_x(host, n, 71) * 2.0
+    w = synth_x(host, n, 72)
+    px, pw, po = mem.up(x), mem.up(w), mem.zeros(n)
+    dev.rms_norm(px, pw, po, n, 1e-5)
+    got = dev.download(po, n, np.float32)
+    want = oracle.rms_norm(x, w, 1e-5)
+    assert np.max(np.abs(got - want) / (np.abs(want) + 1e-30)) <= 1e-6
+
+
+@pytest.mark.parametrize("pos", [0, 7, 2047, 2175, 8191])
+@pytest.mark.parametrize("theta", [10000.0, 500000.0])
+def test_rope_bit_exact(dev, host, oracle, mem, pos, theta):
+    nh, hd = 32, 128
+    x = synth_x(host, nh * hd, 81)
+    px = mem.up(x)
+    dev.rope(px, pos, hd, nh, theta)
+    got = dev.download(px, nh * hd, np.float32)
+    want = oracle.rope(x, pos, hd, nh, theta)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_cache_store_bit_exact(dev, host, oracle, mem):
+    layers, max_ctx, kvd = 3, 40, 1024
+    # include subnormal, tie, overflow and NaN inputs
+    k = synth_x(host, kvd, 91) * 1e-5
+    v = synth_x(host, kvd, 92) * 3e4
+    k[:8] = [6.1e-5, -3.05e-5, 2 ** -25, 2 ** -26, 65520.0, -1e9, np.nan, 0.0]
+    kc = np.zeros(layers * max_ctx * kvd, np.uint16)
+    vc = np.zeros_like(kc)
+    pk, pv, pkc, pvc = mem.up(k), mem.up(v), mem.up(kc), mem.up(vc)
+    dev.cache_store(pk, pv, pkc, pvc, 17, 2, max_ctx, kvd)
+    gk = dev.download(pkc, kc.size, np.uint16)
+    gv = dev.download(pvc, vc.size, np.uint16)
+    oracle.cache_store(k, v, kc, vc, 17, 2, max_ctx, kvd)
+    assert np.array_equal(gk, kc) and np.array_equal(gv, vc)
+
+
+@pytest.mark.parametrize("n", [777, 11008, 28672])
+def test_silu_mul(dev, host, oracle, mem, n):
+    g = synth_x(host, n, 101) * 3.0
+    u = synth_x(host, n, 102)
+    pg, pu, po = mem.up(g), mem.up(u), mem.zeros(n)
+    dev.silu_mul(pg, pu, po, n)
+    got = dev.download(po, n, np.float32)
+    want = oracle.silu_mul(g, u)
+    assert np.all(np.abs(got - want) <= 1e-5 + 1e-5 * np.abs(want))
+
+
+def test_add_in_place(dev, host, oracle, mem):
+    n = 4096
+    a, b = synth_x(host, n, 111), synth_x(host, n, 112)
+    pa, pb = mem.up(a), mem.up(b)
+    dev.add(pa, pb, pa, n)
+    got = dev.download(pa, n, np.float32)
+    assert np.array_equal(got, oracle.add(a, b))
+
+
+@pytest.mark.parametrize("nqh,nkh,hd,seq,max_ctx,layer", [
+    (4, 2, 32, 6, 16, 1),          # the reference self-test case
+    (32, 8, 128, 64, 2176, 0),
+    (32, 8, 128, 2049, 2176, 3),
+    (64, 8, 128, 1000, 1024, 1),
+    (8, 8, 64, 130, 200, 0),
+])
+def test_attention(dev, host, oracle, mem, nqh, nkh, hd, seq, max_ctx, layer):
+    layers = layer + 1
+    kvd = nkh * hd
+    kc = V.synth_normal_f16(host, layers * max_ctx * kvd, SEED, 121)
+    vc = V.synth_normal_f16(host, layers * max_ctx * kvd, SEED, 122)
+    q = synth_x(host, nqh * hd, 123)
+    scale = 1.0 / math.sqrt(hd)
+    pq, pkc, pvc, po = mem.up(q), mem.up(kc), mem.up(vc), mem.zeros(nqh * hd)
+    dev.attention(pq, pkc, pvc, po, seq, layer, max_ctx, nqh, nkh, hd, np.float32(scale))
+    got = dev.download(po, nqh * hd, np.float32)
+    want = oracle.attention(q, kc, vc, seq, layer, max_ctx, nqh, nkh, hd, np.float32(scale))
+    assert np.all(np.abs(got - want) <= 1e-4 + 1e-4 * np.abs(want))
+
+
+def test_rejections(dev, mem):
+    """Unsupported types and malformed shapes fail with a reason, not a fault."""
+    import ctypes
+    p = mem.zeros(1024)
+    assert dev._linear(V.Q8_K, p, p, p, 256, 1, 0, 0, 0) == 0
+    assert "no gfx950 kernel" in dev.error()
+    assert dev._linear(V.Q4_K, p, p, p, 100, 1, 0, 0, 0) == 0
+    assert dev._attention(p, p, p, p, 4, 0, 2, 4, 2, 32, ctypes.c_float(1.0)) == 0
+    assert dev._linear_supported(V.Q5_K) == 0

@@ -1,0 +1,325 @@
+// vbs_gfx950_rt.hip — runtime and C-ABI entry points of libvbs_gfx950.so
+// (declared in include/vbs_gfx950.h).
+//
+// One device, one in-order stream. Entry points validate their arguments on
+// the host (types, shapes, null pointers, head/group limits) before anything
+// is launched, record the reason of any failure in a last-error string and
+// return 0; nothing aborts across the C ABI.
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "vbs_dev_common.h"
+#include "vbs_gfx950.h"
+#include "vbs_internal.h"
+
+namespace {
+
+struct Runtime {
+    bool probed = false;
+    bool ready = false;
+    int device = -1;
+    hipStream_t stream = nullptr;
+    char name[128] = {0};
+    void *scratch = nullptr;
+    size_t scratch_bytes = 0;
+};
+
+Runtime g_rt;
+char g_err[512] = "not initialised";
+
+int fail(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return 0;
+}
+
+int hip_ok(hipError_t e, const char *what) {
+    if (e == hipSuccess) return 1;
+    return fail("%s: %s", what, hipGetErrorString(e));
+}
+
+bool ready_or_fail() {
+    if (g_rt.ready) return true;
+    if (!g_rt.probed) vbs_gfx950_init();
+    if (!g_rt.ready) {
+        if (!g_rt.probed) fail("vbs_gfx950_init has not succeeded");
+        return false;
+    }
+    return true;
+}
+
+}  // namespace
+
+namespace vbs {
+
+uint32_t block_elems(int type) {
+    switch (type) {
+        case kF32: case kF16: return 1;
+        case kQ4_0: case kQ4_1: case kQ8_0: case kLNS8: return 32;
+        case kQ4_K: case kQ6_K: return 256;
+        default: return 0;
+    }
+}
+
+uint64_t row_bytes(int type, uint32_t cols) {
+    switch (type) {
+        case kF32: return 4ull * cols;
+        case kF16: return 2ull * cols;
+        case kQ4_0: return 18ull * (cols / 32u);
+        case kQ4_1: return 20ull * (cols / 32u);
+        case kQ8_0: return 34ull * (cols / 32u);
+        case kQ4_K: return 144ull * (cols / 256u);
+        case kQ6_K: return 210ull * (cols / 256u);
+        case kLNS8: return 36ull * (cols / 32u);
+        default: return 0;
+    }
+}
+
+void *scratch(size_t bytes, hipStream_t s) {
+    if (bytes <= g_rt.scratch_bytes) return g_rt.scratch;
+    size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
+    want = (want + 4095u) & ~(size_t)4095u;
+    if (g_rt.scratch) {
+        (void)hipStreamSynchronize(s);
+        (void)hipFree(g_rt.scratch);
+        g_rt.scratch = nullptr;
+        g_rt.scratch_bytes = 0;
+    }
+    if (hipMalloc(&g_rt.scratch, want) != hipSuccess) {
+        g_rt.scratch = nullptr;
+        return nullptr;
+    }
+    g_rt.scratch_bytes = want;
+    return g_rt.scratch;
+}
+
+}  // namespace vbs
+
+using namespace vbs;
+
+extern "C" {
+
+int vbs_gfx950_abi_version(void) { return VBS_GFX950_ABI_VERSION; }
+
+const char *vbs_gfx950_last_error(void) { return g_err; }
+
+int vbs_gfx950_init(void) {
+    if (g_rt.probed) return g_rt.ready ? 1 : 0;
+    g_rt.probed = true;
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || count <= 0)
+        return fail("no AMD GPU visible to the HIP runtime (%s)",
+                    e == hipSuccess ? "0 devices" : hipGetErrorString(e));
+    int chosen = -1;
+    for (int i = 0; i < count && chosen < 0; i++) {
+        hipDeviceProp_t p;
+        if (hipGetDeviceProperties(&p, i) != hipSuccess) continue;
+        if (strncmp(p.gcnArchName, "gfx950", 6) == 0) {
+            chosen = i;
+            snprintf(g_rt.name, sizeof(g_rt.name), "AMD %s (%s, %d CUs)", p.name, p.gcnArchName,
+                     p.multiProcessorCount);
+        }
+    }
+    if (chosen < 0) return fail("no gfx950 (MI355X) device among %d visible GPUs", count);
+    if (!hip_ok(hipSetDevice(chosen), "hipSetDevice")) return 0;
+    if (!hip_ok(hipStreamCreateWithFlags(&g_rt.stream, hipStreamNonBlocking), "hipStreamCreate"))
+        return 0;
+    g_rt.device = chosen;
+    g_rt.ready = true;
+    snprintf(g_err, sizeof(g_err), "ok");
+    return 1;
+}
+
+int vbs_gfx950_device_count(void) { return g_rt.ready ? 1 : 0; }
+
+int vbs_gfx950_device_info(int index, char *name, size_t cap, uint64_t *total, uint64_t *free_b) {
+    if (!ready_or_fail()) return 0;
+    if (index != 0) return fail("device index %d out of range (1 device)", index);
+    if (name && cap) snprintf(name, cap, "%s", g_rt.name);
+    size_t fr = 0, tot = 0;
+    if (!hip_ok(hipMemGetInfo(&fr, &tot), "hipMemGetInfo")) return 0;
+    if (total) *total = tot;
+    if (free_b) *free_b = fr;
+    return 1;
+}
+
+void *vbs_gfx950_alloc(size_t bytes) {
+    if (!ready_or_fail()) return nullptr;
+    void *p = nullptr;
+    if (hipMalloc(&p, bytes ? bytes : 1) != hipSuccess) {
+        fail("hipMalloc(%zu) failed", bytes);
+        return nullptr;
+    }
+    return p;
+}
+
+int vbs_gfx950_free(void *p) {
+    if (!p) return 1;
+    if (!ready_or_fail()) return 0;
+    (void)hipStreamSynchronize(g_rt.stream);
+    return hip_ok(hipFree(p), "hipFree");
+}
+
+void *vbs_gfx950_host_alloc(size_t bytes) {
+    if (!ready_or_fail()) return nullptr;
+    void *p = nullptr;
+    if (hipHostMalloc(&p, bytes ? bytes : 1, hipHostMallocDefault) != hipSuccess) {
+        fail("hipHostMalloc(%zu) failed", bytes);
+        return nullptr;
+    }
+    return p;
+}
+
+int vbs_gfx950_host_free(void *p) {
+    if (!p) return 1;
+    if (!ready_or_fail()) return 0;
+    (void)hipStreamSynchronize(g_rt.stream);
+    return hip_ok(hipHostFree(p), "hipHostFree");
+}
+
+static int copy_sync(void *dst, const void *src, size_t bytes, hipMemcpyKind kind,
+                     const char *what) {
+    if (!ready_or_fail()) return 0;
+    if (bytes == 0) return 1;
+    if (!dst || !src) return fail("%s: null pointer", what);
+    if (!hip_ok(hipMemcpyAsync(dst, src, bytes, kind, g_rt.stream), what)) return 0;
+    return hip_ok(hipStreamSynchronize(g_rt.stream), what);
+}
+
+int vbs_gfx950_copy_h2d(void *dst, const void *src, size_t bytes) {
+    return copy_sync(dst, src, bytes, hipMemcpyHostToDevice, "copy_h2d");
+}
+int vbs_gfx950_copy_d2h(void *dst, const void *src, size_t bytes) {
+    return copy_sync(dst, src, bytes, hipMemcpyDeviceToHost, "copy_d2h");
+}
+int vbs_gfx950_copy_d2d(void *dst, const void *src, size_t bytes) {
+    if (!ready_or_fail()) return 0;
+    if (bytes == 0) return 1;
+    if (!dst || !src) return fail("copy_d2d: null pointer");
+    return hip_ok(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, g_rt.stream),
+                  "copy_d2d");
+}
+
+int vbs_gfx950_synchronize(void) {
+    if (!ready_or_fail()) return 0;
+    return hip_ok(hipStreamSynchronize(g_rt.stream), "synchronize");
+}
+
+void *vbs_gfx950_stream(void) { return g_rt.ready ? (void *)g_rt.stream : nullptr; }
+
+int vbs_gfx950_linear_supported(int type) { return block_elems(type) != 0; }
+
+int vbs_gfx950_linear(int type, const void *w, const float *x, float *y, uint32_t cols,
+                      uint32_t rows, uint32_t col_off, uint32_t row_off, int accumulate) {
+    if (!ready_or_fail()) return 0;
+    uint32_t e = block_elems(type);
+    if (!e) return fail("linear: no gfx950 kernel for weight type %d", type);
+    if (cols % e) return fail("linear: cols %u is not a multiple of the block size %u", cols, e);
+    if (!w || !x || !y) return fail("linear: null pointer");
+    return hip_ok(launch_linear(type, (const uint8_t *)w, x + col_off, y + row_off, cols, rows,
+                                accumulate, g_rt.stream),
+                  "linear");
+}
+
+int vbs_gfx950_linear_batch(int type, const void *w, const float *x, uint32_t x_stride, float *y,
+                            uint32_t y_stride, uint32_t cols, uint32_t rows, uint32_t batch) {
+    if (!ready_or_fail()) return 0;
+    uint32_t e = block_elems(type);
+    if (!e) return fail("linear_batch: no gfx950 kernel for weight type %d", type);
+    if (cols % e) return fail("linear_batch: cols %u not a multiple of %u", cols, e);
+    if (batch > 16) return fail("linear_batch: batch %u exceeds 16", batch);
+    if (x_stride < cols || y_stride < rows) return fail("linear_batch: stride smaller than row");
+    if (!w || !x || !y) return fail("linear_batch: null pointer");
+    return hip_ok(launch_linear_batch(type, (const uint8_t *)w, x, x_stride, y, y_stride, cols,
+                                      rows, batch, g_rt.stream),
+                  "linear_batch");
+}
+
+int vbs_gfx950_embed(int type, const void *w, uint32_t token, float *out, uint32_t dim) {
+    if (!ready_or_fail()) return 0;
+    uint32_t e = block_elems(type);
+    if (!e) return fail("embed: no gfx950 kernel for weight type %d", type);
+    if (dim % e) return fail("embed: dim %u not a multiple of the block size %u", dim, e);
+    if (!w || !out) return fail("embed: null pointer");
+    if (token == 0xFFFFFFFFu) return fail("embed: token id out of range");
+    return hip_ok(launch_dequant_rows(type, (const uint8_t *)w, nullptr, token, 1, dim, out,
+                                      g_rt.stream),
+                  "embed");
+}
+
+int vbs_gfx950_dequant_rows(int type, const void *w, const uint32_t *ids, uint32_t n_rows,
+                            uint32_t dim, float *out) {
+    if (!ready_or_fail()) return 0;
+    uint32_t e = block_elems(type);
+    if (!e) return fail("dequant_rows: no decoder for weight type %d", type);
+    if (dim % e) return fail("dequant_rows: dim %u not a multiple of %u", dim, e);
+    if (n_rows > 65535u) return fail("dequant_rows: at most 65535 rows per call");
+    if (!w || !out) return fail("dequant_rows: null pointer");
+    return hip_ok(launch_dequant_rows(type, (const uint8_t *)w, ids, 0xFFFFFFFFu, n_rows, dim,
+                                      out, g_rt.stream),
+                  "dequant_rows");
+}
+
+int vbs_gfx950_rms_norm(const float *in, const float *w, float *out, uint32_t dim, float eps) {
+    if (!ready_or_fail()) return 0;
+    if (!in || !w || !out) return fail("rms_norm: null pointer");
+    return hip_ok(launch_rms_norm(in, w, out, dim, eps, g_rt.stream), "rms_norm");
+}
+
+int vbs_gfx950_rope(float *x, uint32_t pos, uint32_t head_dim, uint32_t n_heads, float theta) {
+    if (!ready_or_fail()) return 0;
+    if (!x || head_dim == 0 || n_heads == 0) return fail("rope: null pointer or empty shape");
+    if (head_dim > 512) return fail("rope: head_dim %u exceeds 512", head_dim);
+    // Pair angles with the host libm, exactly as src/vbs_host_math.h:43-44.
+    float cs[512];
+    for (uint32_t i = 0; i + 1 < head_dim; i += 2) {
+        float angle = (float)pos * powf(theta, -(float)i / (float)head_dim);
+        cs[i] = cosf(angle);
+        cs[i + 1] = sinf(angle);
+    }
+    return hip_ok(launch_rope(x, head_dim, n_heads, cs, g_rt.stream), "rope");
+}
+
+int vbs_gfx950_cache_store(const float *k, const float *v, uint16_t *kc, uint16_t *vc,
+                           uint32_t pos, uint32_t layer, uint32_t max_ctx, uint32_t kv_dim) {
+    if (!ready_or_fail()) return 0;
+    if (!k || !v || !kc || !vc) return fail("cache_store: null pointer");
+    if (pos >= max_ctx) return fail("cache_store: pos %u >= max_ctx %u", pos, max_ctx);
+    uint64_t base = ((uint64_t)layer * max_ctx + pos) * kv_dim;
+    return hip_ok(launch_cache_store(k, v, kc, vc, base, kv_dim, g_rt.stream), "cache_store");
+}
+
+int vbs_gfx950_attention(const float *q, const uint16_t *kc, const uint16_t *vc, float *out,
+                         uint32_t seq_len, uint32_t layer, uint32_t max_ctx, uint32_t nqh,
+                         uint32_t nkh, uint32_t hd, float scale) {
+    if (!ready_or_fail()) return 0;
+    if (!q || !kc || !vc || !out) return fail("attention: null pointer");
+    if (seq_len == 0 || nqh == 0 || nkh == 0 || hd == 0) return fail("attention: empty shape");
+    if (seq_len > max_ctx) return fail("attention: seq_len %u > max_ctx %u", seq_len, max_ctx);
+    if (nqh % nkh) return fail("attention: %u q heads not a multiple of %u kv heads", nqh, nkh);
+    if (nqh / nkh > 16) return fail("attention: group size %u exceeds 16", nqh / nkh);
+    if (hd > 256 || (hd & 1u)) return fail("attention: head_dim %u must be even and <= 256", hd);
+    uint64_t layer_off = (uint64_t)layer * max_ctx * nkh * hd;
+    return hip_ok(launch_attention(q, kc, vc, out, seq_len, layer_off, nqh, nkh, hd, scale,
+                                   g_rt.stream),
+                  "attention");
+}
+
+int vbs_gfx950_silu_mul(const float *g, const float *u, float *out, uint32_t n) {
+    if (!ready_or_fail()) return 0;
+    if (!g || !u || !out) return fail("silu_mul: null pointer");
+    return hip_ok(launch_silu_mul(g, u, out, n, g_rt.stream), "silu_mul");
+}
+
+int vbs_gfx950_add(const float *a, const float *b, float *out, uint32_t n) {
+    if (!ready_or_fail()) return 0;
+    if (!a || !b || !out) return fail("add: null pointer");
+    return hip_ok(launch_add(a, b, out, n, g_rt.stream), "add");
+}
+
+}  // extern "C"

@@ -1,0 +1,41 @@
+// vbs_internal.h — launchers shared between the runtime (vbs_gfx950_rt.hip)
+// and the kernel translation units. Every launcher enqueues on `s` and
+// returns hipSuccess or the launch error; argument validation is done by the
+// C-ABI entry points before any launcher runs.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace vbs {
+
+// Row stride in bytes of a packed row of `cols` elements (src/vbs_gguf.c:12-40).
+uint64_t row_bytes(int type, uint32_t cols);
+// Elements per block of `type`, 0 if not a hot-path type.
+uint32_t block_elems(int type);
+
+// Device scratch owned by the runtime (grown on demand, never shrunk).
+void *scratch(size_t bytes, hipStream_t s);
+
+hipError_t launch_linear(int type, const uint8_t *w, const float *x, float *y, uint32_t cols,
+                         uint32_t rows, int accumulate, hipStream_t s);
+hipError_t launch_linear_batch(int type, const uint8_t *w, const float *x, uint32_t x_stride,
+                               float *y, uint32_t y_stride, uint32_t cols, uint32_t rows,
+                               uint32_t batch, hipStream_t s);
+hipError_t launch_dequant_rows(int type, const uint8_t *w, const uint32_t *ids, uint32_t token,
+                               uint32_t n_rows, uint32_t dim, float *out, hipStream_t s);
+hipError_t launch_rms_norm(const float *in, const float *w, float *out, uint32_t n, float eps,
+                           hipStream_t s);
+hipError_t launch_rope(float *x, uint32_t head_dim, uint32_t n_heads, const float *cs,
+                       hipStream_t s);
+hipError_t launch_cache_store(const float *k, const float *v, uint16_t *kc, uint16_t *vc,
+                              uint64_t base, uint32_t kv_dim, hipStream_t s);
+hipError_t launch_attention(const float *q, const uint16_t *kc, const uint16_t *vc, float *out,
+                            uint32_t seq_len, uint64_t layer_off, uint32_t nqh, uint32_t nkh,
+                            uint32_t hd, float scale, hipStream_t s);
+hipError_t launch_silu_mul(const float *g, const float *u, float *out, uint32_t n,
+                           hipStream_t s);
+hipError_t launch_add(const float *a, const float *b, float *out, uint32_t n, hipStream_t s);
+
+}  // namespace vbs

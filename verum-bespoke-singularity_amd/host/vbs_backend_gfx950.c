@@ -1,0 +1,457 @@
+/* vbs_backend_gfx950.c — Verum's HIP backend slot (g_vbs_hip_backend) on the
+ * MI355X device library libvbs_gfx950.so.
+ *
+ * Drop-in for src/vbs_backend_hip.c: same exported symbols
+ * (g_vbs_hip_backend, vbs_hip_last_error), same vbs_backend_ops_t contract,
+ * same "init fails -> false + reason -> selection falls through to the CPU"
+ * behaviour (src/vbs_backend_select.c:42-58). What changes is underneath: the
+ * reference dlopens libamdhip64 and host-stages every op through
+ * src/vbs_host_math.h; this shim dlopens the gfx950 library, checks its ABI
+ * version and every entry point (as vbs_hot_load does,
+ * src/vbs_hotpath.c:78-109), and forwards each op to a device kernel.
+ *
+ * Library search order: $VBS_GFX950_LIB, then libvbs_gfx950.so next to this
+ * shim, then the loader's default search path.
+ *
+ * C11, no HIP headers: the shim only sees the C ABI of include/vbs_gfx950.h.
+ */
+#ifndef _GNU_SOURCE
+#define _GNU_SOURCE
+#endif
+#include "vbs_abi.h"
+#include "vbs_gfx950.h"
+
+#include <dlfcn.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ---- the device library's entry points -------------------------------- */
+
+typedef struct {
+    void *handle;
+    char path[1200];
+    int (*abi_version)(void);
+    int (*init)(void);
+    const char *(*last_error)(void);
+    int (*device_count)(void);
+    int (*device_info)(int, char *, size_t, uint64_t *, uint64_t *);
+    void *(*alloc)(size_t);
+    int (*free)(void *);
+    void *(*host_alloc)(size_t);
+    int (*host_free)(void *);
+    int (*copy_h2d)(void *, const void *, size_t);
+    int (*copy_d2h)(void *, const void *, size_t);
+    int (*synchronize)(void);
+    int (*linear_supported)(int);
+    int (*linear)(int, const void *, const float *, float *, uint32_t, uint32_t, uint32_t,
+                  uint32_t, int);
+    int (*embed)(int, const void *, uint32_t, float *, uint32_t);
+    int (*rms_norm)(const float *, const float *, float *, uint32_t, float);
+    int (*rope)(float *, uint32_t, uint32_t, uint32_t, float);
+    int (*cache_store)(const float *, const float *, uint16_t *, uint16_t *, uint32_t, uint32_t,
+                       uint32_t, uint32_t);
+    int (*attention)(const float *, const uint16_t *, const uint16_t *, float *, uint32_t,
+                     uint32_t, uint32_t, uint32_t, uint32_t, uint32_t, float);
+    int (*silu_mul)(const float *, const float *, float *, uint32_t);
+    int (*add)(const float *, const float *, float *, uint32_t);
+} gfx950_lib_t;
+
+static gfx950_lib_t g_lib;
+static int g_probed, g_ready;
+static char g_err[512] = "not probed yet";
+static vbs_device_t g_device;
+
+static void set_err(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+}
+
+/* A device-library failure: keep its reason. */
+static bool lib_fail(const char *what) {
+    set_err("%s: %s", what, g_lib.last_error ? g_lib.last_error() : "unknown");
+    return false;
+}
+
+const char *vbs_hip_last_error(void) { return g_err; }
+
+/* Path of the device library in use ("" before a successful init). Lets a
+ * caller confirm which native library is serving the backend. */
+const char *vbs_gfx950_shim_library_path(void) { return g_ready ? g_lib.path : ""; }
+
+static void *open_lib(void) {
+    const char *env = getenv("VBS_GFX950_LIB");
+    if (env && *env) {
+        void *h = dlopen(env, RTLD_NOW | RTLD_LOCAL);
+        if (h) snprintf(g_lib.path, sizeof(g_lib.path), "%s", env);
+        else set_err("cannot load %s: %s", env, dlerror());
+        return h;
+    }
+    Dl_info info;
+    if (dladdr((void *)&open_lib, &info) && info.dli_fname) {
+        char dir[1024];
+        snprintf(dir, sizeof(dir), "%s", info.dli_fname);
+        char *slash = strrchr(dir, '/');
+        if (slash) {
+            *slash = '\0';
+            char cand[1100];
+            snprintf(cand, sizeof(cand), "%s/libvbs_gfx950.so", dir);
+            void *h = dlopen(cand, RTLD_NOW | RTLD_LOCAL);
+            if (h) {
+                snprintf(g_lib.path, sizeof(g_lib.path), "%s", cand);
+                return h;
+            }
+        }
+    }
+    void *h = dlopen("libvbs_gfx950.so", RTLD_NOW | RTLD_LOCAL);
+    if (h) snprintf(g_lib.path, sizeof(g_lib.path), "libvbs_gfx950.so");
+    else set_err("gfx950 device library not found (libvbs_gfx950.so): %s", dlerror());
+    return h;
+}
+
+static bool gfx950_init(void) {
+    if (g_probed) return g_ready != 0;
+    g_probed = 1;
+    memset(&g_lib, 0, sizeof(g_lib));
+    g_lib.handle = open_lib();
+    if (!g_lib.handle) return false;
+
+#define BIND(field, sym)                                                       \
+    do {                                                                       \
+        *(void **)(&g_lib.field) = dlsym(g_lib.handle, sym);                   \
+        if (!g_lib.field) {                                                    \
+            set_err("%s lacks %s", g_lib.path, sym);                           \
+            dlclose(g_lib.handle);                                             \
+            g_lib.handle = NULL;                                               \
+            return false;                                                      \
+        }                                                                      \
+    } while (0)
+    BIND(abi_version, "vbs_gfx950_abi_version");
+    BIND(init, "vbs_gfx950_init");
+    BIND(last_error, "vbs_gfx950_last_error");
+    BIND(device_count, "vbs_gfx950_device_count");
+    BIND(device_info, "vbs_gfx950_device_info");
+    BIND(alloc, "vbs_gfx950_alloc");
+    BIND(free, "vbs_gfx950_free");
+    BIND(host_alloc, "vbs_gfx950_host_alloc");
+    BIND(host_free, "vbs_gfx950_host_free");
+    BIND(copy_h2d, "vbs_gfx950_copy_h2d");
+    BIND(copy_d2h, "vbs_gfx950_copy_d2h");
+    BIND(synchronize, "vbs_gfx950_synchronize");
+    BIND(linear_supported, "vbs_gfx950_linear_supported");
+    BIND(linear, "vbs_gfx950_linear");
+    BIND(embed, "vbs_gfx950_embed");
+    BIND(rms_norm, "vbs_gfx950_rms_norm");
+    BIND(rope, "vbs_gfx950_rope");
+    BIND(cache_store, "vbs_gfx950_cache_store");
+    BIND(attention, "vbs_gfx950_attention");
+    BIND(silu_mul, "vbs_gfx950_silu_mul");
+    BIND(add, "vbs_gfx950_add");
+#undef BIND
+
+    int ver = g_lib.abi_version();
+    if (ver != VBS_GFX950_ABI_VERSION) {
+        set_err("%s has ABI version %d, this backend needs %d", g_lib.path, ver,
+                VBS_GFX950_ABI_VERSION);
+        dlclose(g_lib.handle);
+        g_lib.handle = NULL;
+        return false;
+    }
+    if (!g_lib.init()) return lib_fail("gfx950 init");
+    if (g_lib.device_count() < 1) {
+        set_err("gfx950 library reports no device");
+        return false;
+    }
+    memset(&g_device, 0, sizeof(g_device));
+    uint64_t total = 0, free_b = 0;
+    char name[128] = {0};
+    if (!g_lib.device_info(0, name, sizeof(name), &total, &free_b)) return lib_fail("device info");
+    snprintf(g_device.name, sizeof(g_device.name), "%s", name);
+    g_device.type = VBS_BACKEND_HIP;
+    g_device.max_working_set_bytes = total;
+    g_device.max_buffer_bytes = total;
+    g_device.internal_handle = NULL;
+    g_ready = 1;
+    set_err("ok");
+    return true;
+}
+
+static size_t gfx950_get_device_count(void) { return g_ready ? 1 : 0; }
+
+static vbs_device_t *gfx950_get_device(size_t i) { return (g_ready && i == 0) ? &g_device : NULL; }
+
+/* Device memory plus a host shadow: pinned for staging windows (shared),
+ * lazily committed calloc otherwise, as the reference provides host_ptr for
+ * every buffer (src/vbs_backend_hip.c:241) and the slice executor and the
+ * backend self-test write tiles through it. */
+typedef struct {
+    vbs_buffer_t pub;
+    int pinned;
+} gfx950_buffer_t;
+
+static vbs_buffer_t *gfx950_alloc_buffer(vbs_device_t *dev, size_t bytes, bool shared) {
+    if (!g_ready) { set_err("alloc_buffer before a successful init"); return NULL; }
+    if (bytes == 0) bytes = 1;
+    gfx950_buffer_t *b = (gfx950_buffer_t *)calloc(1, sizeof(*b));
+    if (!b) return NULL;
+    b->pub.internal_handle = g_lib.alloc(bytes);
+    if (!b->pub.internal_handle) { lib_fail("alloc_buffer"); free(b); return NULL; }
+    if (shared) {
+        b->pub.host_ptr = g_lib.host_alloc(bytes);
+        b->pinned = b->pub.host_ptr != NULL;
+    }
+    if (!b->pub.host_ptr) b->pub.host_ptr = calloc(1, bytes);
+    b->pub.size = bytes;
+    b->pub.device = dev;
+    return &b->pub;
+}
+
+static void gfx950_free_buffer(vbs_buffer_t *buf) {
+    if (!buf) return;
+    gfx950_buffer_t *b = (gfx950_buffer_t *)buf;
+    if (g_ready) g_lib.free(buf->internal_handle);
+    if (b->pinned) g_lib.host_free(buf->host_ptr);
+    else free(buf->host_ptr);
+    free(b);
+}
+
+static bool gfx950_copy_to_device(vbs_buffer_t *dst, const void *src, size_t bytes) {
+    if (!g_ready || !dst || !src) return false;
+    return g_lib.copy_h2d(dst->internal_handle, src, bytes) ? true : lib_fail("copy_to_device");
+}
+
+/* Waits for all earlier work: the bridge reads logits without a prior
+ * synchronize (src/vbs_specializer_bridge.c:201-206). */
+static bool gfx950_copy_to_host(void *dst, const vbs_buffer_t *src, size_t bytes) {
+    if (!g_ready || !dst || !src) return false;
+    return g_lib.copy_d2h(dst, src->internal_handle, bytes) ? true : lib_fail("copy_to_host");
+}
+
+/* ---- pipelines ---------------------------------------------------------- */
+
+typedef struct {
+    vbs_ggml_type_t type;
+} gfx950_linear_pipe_t;
+
+typedef struct {
+    vbs_prim_pipeline_t base; /* .native = this struct, .kind = op kind */
+    vbs_ggml_type_t type;     /* EMBEDDING table type */
+} gfx950_prim_pipe_t;
+
+static const char *type_name(vbs_ggml_type_t t) {
+    switch (t) {
+        case VBS_GGML_TYPE_F32: return "F32";
+        case VBS_GGML_TYPE_F16: return "F16";
+        case VBS_GGML_TYPE_Q4_0: return "Q4_0";
+        case VBS_GGML_TYPE_Q4_1: return "Q4_1";
+        case VBS_GGML_TYPE_Q8_0: return "Q8_0";
+        case VBS_GGML_TYPE_Q4_K: return "Q4_K";
+        case VBS_GGML_TYPE_Q6_K: return "Q6_K";
+        case VBS_GGML_TYPE_LNS8: return "LNS8";
+        default: return "unsupported";
+    }
+}
+
+static void *gfx950_compile_linear_pipeline(vbs_device_t *dev, vbs_ggml_type_t type, char *err,
+                                            size_t cap) {
+    (void)dev;
+    if (!g_ready || !g_lib.linear_supported((int)type)) {
+        if (err && cap)
+            snprintf(err, cap, "gfx950 backend: no linear kernel for weight type %d", (int)type);
+        return NULL;
+    }
+    gfx950_linear_pipe_t *p = (gfx950_linear_pipe_t *)malloc(sizeof(*p));
+    if (p) p->type = type;
+    return p;
+}
+
+static gfx950_prim_pipe_t *prim_pipe(vbs_op_kind_t kind, vbs_ggml_type_t type) {
+    gfx950_prim_pipe_t *p = (gfx950_prim_pipe_t *)malloc(sizeof(*p));
+    if (!p) return NULL;
+    p->base.native = p;
+    p->base.kind = kind;
+    p->type = type;
+    return p;
+}
+
+static void *gfx950_compile_embed_pipeline(vbs_device_t *dev, vbs_ggml_type_t type, char *err,
+                                           size_t cap) {
+    (void)dev;
+    if (!g_ready || !g_lib.linear_supported((int)type)) {
+        if (err && cap)
+            snprintf(err, cap, "gfx950 backend: no embedding kernel for weight type %d", (int)type);
+        return NULL;
+    }
+    return prim_pipe(VBS_OP_EMBEDDING, type);
+}
+
+static void *gfx950_compile_primitive_pipeline(vbs_device_t *dev, vbs_op_kind_t kind, char *err,
+                                               size_t cap) {
+    (void)dev;
+    switch (kind) {
+        case VBS_OP_EMBEDDING: /* F32 table, as in the reference */
+        case VBS_OP_NORMALIZE:
+        case VBS_OP_ROTARY:
+        case VBS_OP_CACHE:
+        case VBS_OP_ATTENTION:
+        case VBS_OP_ACTIVATION:
+        case VBS_OP_ELEMENTWISE:
+            if (g_ready) return prim_pipe(kind, VBS_GGML_TYPE_F32);
+            /* fall through */
+        default:
+            if (err && cap)
+                snprintf(err, cap, "gfx950 backend: no primitive kernel for op kind %d", (int)kind);
+            return NULL;
+    }
+}
+
+/* ---- dispatch ----------------------------------------------------------- */
+
+static uint64_t packed_row_bytes(vbs_ggml_type_t t, uint32_t cols) {
+    switch (t) {
+        case VBS_GGML_TYPE_F32: return 4ull * cols;
+        case VBS_GGML_TYPE_F16: return 2ull * cols;
+        case VBS_GGML_TYPE_Q4_0: return 18ull * (cols / 32u);
+        case VBS_GGML_TYPE_Q4_1: return 20ull * (cols / 32u);
+        case VBS_GGML_TYPE_Q8_0: return 34ull * (cols / 32u);
+        case VBS_GGML_TYPE_Q4_K: return 144ull * (cols / 256u);
+        case VBS_GGML_TYPE_Q6_K: return 210ull * (cols / 256u);
+        case VBS_GGML_TYPE_LNS8: return 36ull * (cols / 32u);
+        default: return 0;
+    }
+}
+
+/* Two calling conventions (src/vbs_backend_hip.c:346-394):
+ *  A (bridge, resident): ws == NULL, wp->internal_handle is the packed tensor.
+ *  B (slice executor, staged): ws->host_ptr holds a packed tile; it is
+ *    uploaded into the private device buffer wp and computed there.
+ * Offsets index x and y; accumulate adds into y. */
+static bool gfx950_dispatch_linear_tile(vbs_device_t *dev, void *pipeline, vbs_buffer_t *wp,
+                                        vbs_buffer_t *ws, size_t copied_bytes, vbs_buffer_t *in,
+                                        vbs_buffer_t *out, uint32_t cols, uint32_t rows,
+                                        uint32_t col_off, uint32_t row_off, bool accumulate) {
+    (void)dev;
+    gfx950_linear_pipe_t *p = (gfx950_linear_pipe_t *)pipeline;
+    if (!g_ready || !p || !wp || !in || !out) return false;
+    uint64_t need = packed_row_bytes(p->type, cols) * rows;
+    if (ws && ws->host_ptr) {
+        size_t n = copied_bytes ? copied_bytes : (size_t)need;
+        if (n < need) {
+            set_err("linear tile: staged %zu bytes, %s %ux%u needs %llu", n, type_name(p->type),
+                    rows, cols, (unsigned long long)need);
+            return false;
+        }
+        if ((ws->size && ws->size < need) || (wp->size && wp->size < need)) {
+            set_err("linear tile: window smaller than the %llu-byte tile", (unsigned long long)need);
+            return false;
+        }
+        if (!g_lib.copy_h2d(wp->internal_handle, ws->host_ptr, (size_t)need))
+            return lib_fail("linear tile upload");
+    }
+    if (!g_lib.linear((int)p->type, wp->internal_handle, (const float *)in->internal_handle,
+                      (float *)out->internal_handle, cols, rows, col_off, row_off,
+                      accumulate ? 1 : 0))
+        return lib_fail("linear tile");
+    return true;
+}
+
+static bool arg_ok(const vbs_arg_t *a, vbs_arg_tag_t tag) {
+    if (a->tag != tag) return false;
+    if (tag == VBS_ARG_SCALAR) return a->value && a->size == 4;
+    return a->value != NULL;
+}
+
+#define BUF(i) ((void *)args[i].value)
+#define U32(i) (*(const uint32_t *)args[i].value)
+#define F32(i) (*(const float *)args[i].value)
+
+/* Canonical bridge argument order (include/vbs_specializer_bridge.h:44-53).
+ * grid_x/block_x are launch hints for other backends; gfx950 kernels size
+ * their own grids. */
+static bool gfx950_dispatch_primitive(vbs_device_t *dev, void *pipeline, const vbs_arg_t *args,
+                                      size_t n_args, size_t grid_x, size_t block_x) {
+    (void)dev; (void)grid_x; (void)block_x;
+    gfx950_prim_pipe_t *pp = (gfx950_prim_pipe_t *)pipeline;
+    if (!g_ready || !pp || !args) return false;
+    static const char *const sig[] = {
+        [VBS_OP_EMBEDDING] = "BSBS", [VBS_OP_NORMALIZE] = "BBBSS", [VBS_OP_ROTARY] = "BSSSS",
+        [VBS_OP_CACHE] = "BBBBSSSS", [VBS_OP_ATTENTION] = "BBBBSSSSSSS",
+        [VBS_OP_ACTIVATION] = "BBBS", [VBS_OP_ELEMENTWISE] = "BBBS",
+    };
+    if ((unsigned)pp->base.kind >= sizeof(sig) / sizeof(sig[0]) || !sig[pp->base.kind]) {
+        set_err("dispatch_primitive: op kind %d has no kernel", (int)pp->base.kind);
+        return false;
+    }
+    const char *s = sig[pp->base.kind];
+    if (n_args != strlen(s)) {
+        set_err("dispatch_primitive: op kind %d takes %zu arguments, got %zu", (int)pp->base.kind,
+                strlen(s), n_args);
+        return false;
+    }
+    for (size_t i = 0; i < n_args; i++) {
+        if (!arg_ok(&args[i], s[i] == 'B' ? VBS_ARG_BUFFER : VBS_ARG_SCALAR)) {
+            set_err("dispatch_primitive: op kind %d argument %zu is malformed", (int)pp->base.kind, i);
+            return false;
+        }
+    }
+    int ok = 0;
+    switch (pp->base.kind) {
+        case VBS_OP_EMBEDDING:
+            ok = g_lib.embed((int)pp->type, BUF(0), U32(1), (float *)BUF(2), U32(3));
+            break;
+        case VBS_OP_NORMALIZE:
+            ok = g_lib.rms_norm((const float *)BUF(0), (const float *)BUF(1), (float *)BUF(2), U32(3),
+                                F32(4));
+            break;
+        case VBS_OP_ROTARY:
+            ok = g_lib.rope((float *)BUF(0), U32(1), U32(2), U32(3), F32(4));
+            break;
+        case VBS_OP_CACHE:
+            ok = g_lib.cache_store((const float *)BUF(0), (const float *)BUF(1), (uint16_t *)BUF(2),
+                                   (uint16_t *)BUF(3), U32(4), U32(5), U32(6), U32(7));
+            break;
+        case VBS_OP_ATTENTION:
+            ok = g_lib.attention((const float *)BUF(0), (const uint16_t *)BUF(1),
+                                 (const uint16_t *)BUF(2), (float *)BUF(3), U32(4), U32(5), U32(6),
+                                 U32(7), U32(8), U32(9), F32(10));
+            break;
+        case VBS_OP_ACTIVATION:
+            ok = g_lib.silu_mul((const float *)BUF(0), (const float *)BUF(1), (float *)BUF(2), U32(3));
+            break;
+        case VBS_OP_ELEMENTWISE:
+            ok = g_lib.add((const float *)BUF(0), (const float *)BUF(1), (float *)BUF(2), U32(3));
+            break;
+        default:
+            break;
+    }
+    return ok ? true : lib_fail("dispatch_primitive");
+}
+
+#undef BUF
+#undef U32
+#undef F32
+
+static void gfx950_synchronize(vbs_device_t *dev) {
+    (void)dev;
+    if (g_ready && !g_lib.synchronize()) lib_fail("synchronize");
+}
+
+const vbs_backend_ops_t g_vbs_hip_backend = {
+    .init = gfx950_init,
+    .get_device_count = gfx950_get_device_count,
+    .get_device = gfx950_get_device,
+    .alloc_buffer = gfx950_alloc_buffer,
+    .free_buffer = gfx950_free_buffer,
+    .copy_to_device = gfx950_copy_to_device,
+    .copy_to_host = gfx950_copy_to_host,
+    .compile_linear_pipeline = gfx950_compile_linear_pipeline,
+    .compile_embed_pipeline = gfx950_compile_embed_pipeline,
+    .compile_primitive_pipeline = gfx950_compile_primitive_pipeline,
+    .dispatch_linear_tile = gfx950_dispatch_linear_tile,
+    .dispatch_primitive = gfx950_dispatch_primitive,
+    .synchronize_device = gfx950_synchronize,
+    .launch_persistent_kernel = NULL,
+};
