@@ -100,6 +100,43 @@ def test_linear_full_size(dev, host, oracle, mem, t, rows, cols):
     assert rel_l2(got, want) <= LIN_TOL
 
 
+@pytest.mark.parametrize("t", [V.Q4_K, V.Q6_K, V.Q8_0, V.Q4_0], ids=lambda t: V.TYPE_NAMES[t])
+def test_linear_activation_edge_cases(dev, host, oracle, mem, t):
+    """x with all-zero sub-blocks, 1e4 outliers, subnormal-scale blocks and
+    huge blocks: the result must stay within the same relative L2 bar."""
+    rows, cols = 64, 4096
+    w = V.synth_matrix(host, t, rows, cols, SEED, 23)
+    x = synth_x(host, cols, 24)
+    x[0:32] = 0.0                      # an all-zero sub-block
+    x[40] = 1.0e4                      # an outlier in an otherwise N(0,1) sub-block
+    x[64:96] *= 1e-40                  # subnormal-scale sub-block
+    x[96:128] *= 1e30                  # huge sub-block
+    x[200] = -0.0
+    pw, px, py = mem.up(w), mem.up(x), mem.zeros(rows)
+    dev.linear(t, pw, px, py, cols, rows)
+    got = dev.download(py, rows, np.float32)
+    want = oracle.linear(t, w, x, cols, rows)
+    assert rel_l2(got, want) <= LIN_TOL
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 256), (3, 768), (37, 4352), (700, 8192), (64, 16640),
+                                       (5, 28672)])
+def test_q4k_odd_shapes(dev, host, oracle, mem, rows, cols):
+    """Row counts that leave streams and waves partly idle, several waves per
+    row (cols > 4096), misaligned x (col_off 3) and y (row_off 5) windows."""
+    t = V.Q4_K
+    w = V.synth_matrix(host, t, rows, cols, SEED, 25)
+    x = synth_x(host, cols + 3, 26)
+    pw, px = mem.up(w), mem.up(x)
+    py = mem.up(np.full(rows + 5, -2.0, np.float32))
+    dev.linear(t, pw, px, py, cols, rows, col_off=3, row_off=5, accumulate=True)
+    got = dev.download(py, rows + 5, np.float32)
+    want = np.full(rows + 5, -2.0, np.float32)
+    oracle.linear(t, w, x, cols, rows, y=want, col_off=3, row_off=5, accumulate=True)
+    assert np.array_equal(got[:5], want[:5])
+    assert rel_l2(got[5:], want[5:]) <= LIN_TOL
+
+
 def test_linear_offsets_accumulate(dev, host, oracle, mem):
     """Two column tiles into one output window: offsets index x and y, the
     second tile accumulates (src/vbs_backend_test.c:888-948)."""

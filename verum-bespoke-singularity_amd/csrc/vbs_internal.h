@@ -18,6 +18,11 @@ uint32_t block_elems(int type);
 // Device scratch owned by the runtime (grown on demand, never shrunk).
 void *scratch(size_t bytes, hipStream_t s);
 
+// Specialised Q4_K matvec; hipErrorNotSupported when the shape/alignment is
+// outside its range (the generic kernel then runs).
+hipError_t launch_q4k_fast(const uint8_t *w, const float *x, float *y, uint32_t cols,
+                           uint32_t rows, int accumulate, hipStream_t s);
+
 hipError_t launch_linear(int type, const uint8_t *w, const float *x, float *y, uint32_t cols,
                          uint32_t rows, int accumulate, hipStream_t s);
 hipError_t launch_linear_batch(int type, const uint8_t *w, const float *x, uint32_t x_stride,
