@@ -1,0 +1,189 @@
+"""The drop-in boundary: g_vbs_hip_backend (host/vbs_backend_gfx950.c) and the
+C ABI of libvbs_gfx950.so (include/vbs_gfx950.h).
+
+CPU tests load private copies of the shim so that each one runs its own
+init() (the shim probes once per process, as src/vbs_backend_hip.c:150-151
+does) and point it with VBS_GFX950_LIB at a test-only mock device library
+(tests/mock/mock_gfx950.c, built here over the CPU oracle) or at variants of it
+with a wrong ABI version or a missing entry point. The GPU test runs the same
+suite against the real library.
+"""
+import ctypes as C
+import os
+import re
+import shutil
+import subprocess
+
+import numpy as np
+import pytest
+
+import vbs_gfx950 as V
+from backend_suite import run_suite
+from oracle_lib import Oracle
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+MOCK_SRC = os.path.join(ROOT, "tests", "mock", "mock_gfx950.c")
+ORACLE_SRC = os.path.join(ROOT, "oracle", "vbs_oracle.c")
+
+
+def build_mock(outdir, name, defines=()):
+    so = os.path.join(outdir, name)
+    cmd = ["gcc", "-std=c11", "-O2", "-fPIC", "-shared", "-ffp-contract=off",
+           "-I" + os.path.join(ROOT, "include"), "-I" + os.path.join(ROOT, "oracle"),
+           *[f"-D{d}" for d in defines], MOCK_SRC, ORACLE_SRC, "-o", so, "-lm", "-lpthread"]
+    subprocess.run(cmd, check=True)
+    return so
+
+
+def fresh_shim(outdir, device_lib):
+    """A private copy of the shim whose init() will load `device_lib`."""
+    copy = os.path.join(outdir, f"shim_{len(os.listdir(outdir))}.so")
+    shutil.copy(V.HOST_LIB, copy)
+    old = os.environ.get("VBS_GFX950_LIB")
+    if device_lib is None:
+        os.environ.pop("VBS_GFX950_LIB", None)
+    else:
+        os.environ["VBS_GFX950_LIB"] = device_lib
+    be = V.Backend(C.CDLL(copy), "g_vbs_hip_backend", "vbs_hip_last_error")
+    ok = be.init()
+    if old is None:
+        os.environ.pop("VBS_GFX950_LIB", None)
+    else:
+        os.environ["VBS_GFX950_LIB"] = old
+    return be, ok
+
+
+@pytest.fixture(scope="module")
+def tmpdir_mod(tmp_path_factory):
+    return str(tmp_path_factory.mktemp("shim"))
+
+
+def test_device_library_exports_every_declared_symbol():
+    """Every function declared in include/vbs_gfx950.h is exported by the
+    built library (loaded without touching a GPU)."""
+    hdr = open(os.path.join(ROOT, "include", "vbs_gfx950.h")).read()
+    declared = sorted(set(re.findall(r"\b(vbs_gfx950_\w+)\s*\(", hdr)))
+    assert len(declared) >= 25
+    lib = C.CDLL(V.DEVICE_LIB)
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert set(declared) == set(V.DEVICE_SYMBOLS)
+
+
+def test_shim_exports_the_reference_symbols():
+    lib = C.CDLL(V.HOST_LIB)
+    ops = V.VbsOps.in_dll(lib, "g_vbs_hip_backend")
+    assert C.sizeof(V.VbsOps) == 14 * C.sizeof(C.c_void_p)
+    for name, _ in V.VbsOps._fields_[:-1]:
+        assert getattr(ops, name), name
+    assert not ops.launch_persistent_kernel  # must be NULL (include/vbs_backend.h:94-98)
+    assert hasattr(lib, "vbs_hip_last_error")
+
+
+@pytest.mark.skipif(not os.path.isdir("/root/reference/include"),
+                    reason="reference headers not mounted")
+def test_abi_layout_matches_reference_headers(tmp_path):
+    """sizeof/offsetof of every boundary struct and the enum values agree
+    between include/vbs_abi.h and the reference's own headers."""
+    probe = r'''
+#include <stdio.h>
+#include <stddef.h>
+#include HDR
+int main(void) {
+  printf("%zu %zu %zu %zu %zu\n", sizeof(vbs_device_t), sizeof(vbs_buffer_t), sizeof(vbs_arg_t),
+         sizeof(vbs_prim_pipeline_t), sizeof(vbs_backend_ops_t));
+  printf("%zu %zu %zu %zu\n", offsetof(vbs_device_t, max_working_set_bytes),
+         offsetof(vbs_device_t, internal_handle), offsetof(vbs_buffer_t, device),
+         offsetof(vbs_arg_t, size));
+  printf("%zu %zu %zu\n", offsetof(vbs_backend_ops_t, dispatch_linear_tile),
+         offsetof(vbs_backend_ops_t, synchronize_device), offsetof(vbs_backend_ops_t, launch_persistent_kernel));
+  printf("%d %d %d %d %d %d\n", VBS_GGML_TYPE_Q4_K, VBS_GGML_TYPE_Q6_K, VBS_GGML_TYPE_LNS8,
+         VBS_OP_CACHE, VBS_OP_PROJECTION, VBS_BACKEND_HIP);
+  return 0;
+}
+'''
+    src = tmp_path / "probe.c"
+    src.write_text(probe)
+    outs = []
+    for hdr, inc in (('"vbs_abi.h"', os.path.join(ROOT, "include")),
+                     ('"vbs_backend.h"', "/root/reference/include")):
+        exe = tmp_path / f"probe{len(outs)}"
+        subprocess.run(["gcc", "-std=c11", "-D_GNU_SOURCE", f"-DHDR={hdr}", "-I" + inc,
+                        str(src), "-o", str(exe)], check=True)
+        outs.append(subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout)
+    assert outs[0] == outs[1]
+
+
+def test_shim_without_gpu_reports_reason(tmpdir_mod):
+    """Init fails with a reason when no gfx950 is visible (this container),
+    so backend selection falls through to the CPU (vbs_backend_select.c:42-58)."""
+    probe = V.DeviceLib()
+    if probe.init():
+        pytest.skip("a GPU is visible here")
+    be, ok = fresh_shim(tmpdir_mod, V.DEVICE_LIB)
+    assert not ok
+    assert "gfx950 init" in be.last_error() and ("GPU" in be.last_error() or "gfx950" in be.last_error())
+    assert be.ops.get_device_count() == 0
+
+
+def test_shim_rejects_wrong_abi_version(tmpdir_mod):
+    so = build_mock(tmpdir_mod, "mock_badabi.so", ["MOCK_ABI=999"])
+    be, ok = fresh_shim(tmpdir_mod, so)
+    assert not ok and "ABI version 999" in be.last_error()
+
+
+def test_shim_rejects_library_missing_an_entry_point(tmpdir_mod):
+    so = build_mock(tmpdir_mod, "mock_noadd.so", ["MOCK_DROP_ADD"])
+    be, ok = fresh_shim(tmpdir_mod, so)
+    assert not ok and "lacks vbs_gfx950_add" in be.last_error()
+
+
+def test_shim_rejects_missing_library(tmpdir_mod):
+    be, ok = fresh_shim(tmpdir_mod, os.path.join(tmpdir_mod, "does_not_exist.so"))
+    assert not ok and "cannot load" in be.last_error()
+
+
+def test_backend_suite_through_shim_on_host_mock(tmpdir_mod, host):
+    """The restated reference self-test, through the shim's ops table, with
+    the device library replaced by the host mock: checks the argument
+    marshalling, both linear conventions, offsets/accumulate and refusals."""
+    so = build_mock(tmpdir_mod, "mock_ok.so")
+    be, ok = fresh_shim(tmpdir_mod, so)
+    assert ok, be.last_error()
+    dev = be.ops.get_device(0).contents
+    assert dev.type == 2 and dev.max_working_set_bytes == 1 << 30 and b"mock" in dev.name
+    res = run_suite(be, Oracle(), host)
+    bad = [r[0] for r in res if not r[1]]
+    assert not bad, bad
+    assert len(res) >= 33
+
+
+def test_shim_marshalling_rejects_malformed_arguments(tmpdir_mod):
+    so = build_mock(tmpdir_mod, "mock_ok2.so")
+    be, ok = fresh_shim(tmpdir_mod, so)
+    assert ok
+    keep = []
+    x = be.upload(np.zeros(16, np.float32))
+    pipe = be.ops.compile_primitive_pipeline(be.device(), V.OP_ELEMENTWISE, None, 0)
+    A = V.Backend.buf_arg
+    assert not be.dispatch(pipe, [A(x), A(x), A(x)])                      # too few
+    assert "takes 4 arguments" in be.last_error()
+    assert not be.dispatch(pipe, [A(x), be.u32_arg(keep, 1), A(x), be.u32_arg(keep, 4)])
+    assert "malformed" in be.last_error()
+    err = C.create_string_buffer(128)
+    assert not be.ops.compile_primitive_pipeline(be.device(), V.OP_STATE_SPACE, err, 128)
+    assert b"no primitive kernel" in err.value
+
+
+@pytest.mark.gpu
+def test_backend_suite_on_gfx950(backend, host):
+    """The same suite through g_vbs_hip_backend on the MI355X."""
+    lib = backend.lib
+    lib.vbs_gfx950_shim_library_path.restype = C.c_char_p
+    path = lib.vbs_gfx950_shim_library_path().decode()
+    assert path.endswith("lib/libvbs_gfx950.so"), path
+    dev = backend.ops.get_device(0).contents
+    assert b"gfx950" in dev.name and dev.max_working_set_bytes > (200 << 30)
+    res = run_suite(backend, Oracle(), host)
+    bad = [r[0] for r in res if not r[1]]
+    assert not bad, bad
