@@ -12,9 +12,15 @@ of the layer set rotate so the 256 MB Infinity Cache cannot serve re-reads.
 `value` is algorithmic bytes (packed W + 4*cols + 4*rows per matvec) per
 second over the timed steps.
 
+Each step is one HIP graph of its seven launches (captured from the library's
+stream), so the timed region measures the kernels rather than the host's
+per-call launch cost.
+
 roofline: the dominant kernel is the Q4_K matvec at 11008x4096 / 4096x11008;
-its per-launch duration comes from HIP events recorded around every such
-launch on the library's stream inside the timed region.
+its average duration is the elapsed time between two HIP events on the
+library's stream around `roof_reps` replays of a graph holding those launches
+for every weight copy, divided by the number of launches (inter-kernel gaps
+included, so it is an upper bound on the kernel time rocprof reports).
 
 cpu_baseline: the reference's own CPU backend (oracle/_ref, compiled from the
 reference sources) -- or, where that file is absent, the oracle restatement --
@@ -22,8 +28,9 @@ runs dispatch_linear_tile over the same layer set, single-threaded as the
 reference is, for a bounded number of passes.
 
 Also reported: decode tokens/sec of the synthetic 7B Q4_K_M model (config 4:
-32 layers, KV prefilled to 2048, greedy from position 2048) through the
-g_vbs_hip_backend ops table, one dispatch per bridge call.
+32 layers, KV prefilled to 2048, greedy from position 2048) through the graph
+decoder (vbs_gfx950_decoder_*), and through the g_vbs_hip_backend ops table
+with one dispatch per bridge call.
 """
 import argparse
 import ctypes as C
@@ -50,40 +57,61 @@ def algo_bytes(t, rows, cols):
     return V.row_bytes(t, cols) * rows + 4 * cols + 4 * rows
 
 
-class HipEvents:
-    """hipEvent timing on a given stream (the device library's stream)."""
+class Hip:
+    """hipEvent timing and stream capture on the device library's stream."""
 
     def __init__(self):
-        self.hip = C.CDLL("libamdhip64.so")
-        self.hip.hipEventCreate.argtypes = [C.POINTER(C.c_void_p)]
-        self.hip.hipEventRecord.argtypes = [C.c_void_p, C.c_void_p]
-        self.hip.hipEventSynchronize.argtypes = [C.c_void_p]
-        self.hip.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
-        self.hip.hipEventDestroy.argtypes = [C.c_void_p]
+        h = self.h = C.CDLL("libamdhip64.so")
+        vp, pvp = C.c_void_p, C.POINTER(C.c_void_p)
+        h.hipEventCreate.argtypes = [pvp]
+        h.hipEventRecord.argtypes = [vp, vp]
+        h.hipEventSynchronize.argtypes = [vp]
+        h.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), vp, vp]
+        h.hipEventDestroy.argtypes = [vp]
+        h.hipStreamBeginCapture.argtypes = [vp, C.c_int]
+        h.hipStreamEndCapture.argtypes = [vp, pvp]
+        h.hipGraphInstantiate.argtypes = [pvp, vp, vp, vp, C.c_size_t]
+        h.hipGraphLaunch.argtypes = [vp, vp]
+        h.hipGraphExecDestroy.argtypes = [vp]
+        h.hipGraphDestroy.argtypes = [vp]
 
-    def create(self, n):
-        evs = []
-        for _ in range(n):
-            e = C.c_void_p()
-            if self.hip.hipEventCreate(C.byref(e)) != 0:
-                raise RuntimeError("hipEventCreate failed")
-            evs.append(e)
-        return evs
+    def _ok(self, rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what} failed ({rc})")
+
+    def event(self):
+        e = C.c_void_p()
+        self._ok(self.h.hipEventCreate(C.byref(e)), "hipEventCreate")
+        return e
 
     def record(self, ev, stream):
-        if self.hip.hipEventRecord(ev, C.c_void_p(stream)) != 0:
-            raise RuntimeError("hipEventRecord failed")
+        self._ok(self.h.hipEventRecord(ev, C.c_void_p(stream)), "hipEventRecord")
 
     def elapsed_ms(self, a, b):
-        self.hip.hipEventSynchronize(b)
+        self._ok(self.h.hipEventSynchronize(b), "hipEventSynchronize")
         ms = C.c_float()
-        if self.hip.hipEventElapsedTime(C.byref(ms), a, b) != 0:
-            raise RuntimeError("hipEventElapsedTime failed")
+        self._ok(self.h.hipEventElapsedTime(C.byref(ms), a, b), "hipEventElapsedTime")
         return ms.value
 
-    def destroy(self, evs):
-        for e in evs:
-            self.hip.hipEventDestroy(e)
+    def capture(self, stream, enqueue):
+        """Graph of the work `enqueue()` puts on `stream` (thread-local capture)."""
+        self._ok(self.h.hipStreamBeginCapture(C.c_void_p(stream), 1), "hipStreamBeginCapture")
+        try:
+            enqueue()
+        finally:
+            g = C.c_void_p()
+            rc = self.h.hipStreamEndCapture(C.c_void_p(stream), C.byref(g))
+        self._ok(rc, "hipStreamEndCapture")
+        ex = C.c_void_p()
+        self._ok(self.h.hipGraphInstantiate(C.byref(ex), g, None, None, 0), "hipGraphInstantiate")
+        return g, ex
+
+    def launch(self, graph, stream):
+        self._ok(self.h.hipGraphLaunch(graph[1], C.c_void_p(stream)), "hipGraphLaunch")
+
+    def destroy(self, graph):
+        self.h.hipGraphExecDestroy(graph[1])
+        self.h.hipGraphDestroy(graph[0])
 
 
 def cpu_baseline(host, weights, xs, max_seconds=20.0):
@@ -136,7 +164,7 @@ def cpu_baseline(host, weights, xs, max_seconds=20.0):
                       f"host: {cpu}, nproc {os.cpu_count()}"}
 
 
-def bench_matvec(dev, host, steps, warmup, ncopy):
+def bench_matvec(dev, host, steps, warmup, ncopy, roof_reps):
     t = V.Q4_K
     weights_host = [V.synth_matrix(host, t, r, c, SEED, 10 + i) for i, (_, r, c) in enumerate(LAYER_SET)]
     xs_host = [V.synth_normal(host, c, SEED, 30 + i) for i, (_, _, c) in enumerate(LAYER_SET)]
@@ -151,56 +179,54 @@ def bench_matvec(dev, host, steps, warmup, ncopy):
     px = [dev.upload(x) for x in xs_host]
     py = [dev.upload(np.zeros(r, np.float32)) for _, r, _ in LAYER_SET]
     stream = dev.stream()
-    ev = HipEvents()
+    hip = Hip()
     big = [i for i, (_, r, c) in enumerate(LAYER_SET) if r * c == H * FF]
-    n_big = steps * len(big)
-    evs = ev.create(2 * n_big + 2)
 
-    def step(s, timed_evs=None):
-        cp = copies[s % ncopy]
-        j = 0
-        for i, (_, r, c) in enumerate(LAYER_SET):
-            if timed_evs is not None and i in big:
-                ev.record(timed_evs[2 * j], stream)
-            dev.linear(t, cp[i], px[i], py[i], c, r)
-            if timed_evs is not None and i in big:
-                ev.record(timed_evs[2 * j + 1], stream)
-                j += 1
-        return j
+    def enqueue(k, which):
+        for i in which:
+            _, r, c = LAYER_SET[i]
+            dev.linear(t, copies[k][i], px[i], py[i], c, r)
 
+    # one graph per copy: the seven launches of a step, replayed per step
+    step_graphs = [hip.capture(stream, lambda k=k: enqueue(k, range(len(LAYER_SET))))
+                   for k in range(ncopy)]
     for s in range(warmup):
-        step(s)
+        hip.launch(step_graphs[s % ncopy], stream)
     dev.sync()
-    # timed region: K steps, sync on both sides; events around the big matvecs
+    # timed region: exactly K steps, synchronised on both sides
+    e0, e1 = hip.event(), hip.event()
     t0 = time.perf_counter()
-    ev.record(evs[-2], stream)
-    k = 0
+    hip.record(e0, stream)
     for s in range(steps):
-        k += step(s, evs[2 * k:])
-    ev.record(evs[-1], stream)
+        hip.launch(step_graphs[s % ncopy], stream)
+    hip.record(e1, stream)
     dev.sync()
     wall = time.perf_counter() - t0
-    gpu_ms = ev.elapsed_ms(evs[-2], evs[-1])
-    per_launch = [ev.elapsed_ms(evs[2 * i], evs[2 * i + 1]) for i in range(n_big)]
-    ev.destroy(evs)
-    # untimed: events-free timing of the same steps, to show event overhead is small
+    gpu_ms = hip.elapsed_ms(e0, e1)
+    # dominant kernel: the three 11008-wide matvecs of every copy back to back,
+    # replayed roof_reps times between two events on the same stream
+    big_graph = hip.capture(stream, lambda: [enqueue(k, big) for k in range(ncopy)])
+    hip.launch(big_graph, stream)
     dev.sync()
-    t1 = time.perf_counter()
-    for s in range(steps):
-        step(s)
-    dev.sync()
-    wall_plain = time.perf_counter() - t1
-
+    hip.record(e0, stream)
+    for _ in range(roof_reps):
+        hip.launch(big_graph, stream)
+    hip.record(e1, stream)
+    big_ms = hip.elapsed_ms(e0, e1) / (roof_reps * ncopy * len(big))
+    # a replay of copy 0's step graph against the same launches issued eagerly
+    hip.launch(step_graphs[0], stream)
+    y_graph = [dev.download(py[i], (r,), np.float32) for i, (_, r, _) in enumerate(LAYER_SET)]
+    for g in step_graphs + [big_graph]:
+        hip.destroy(g)
+    enqueue(0, range(len(LAYER_SET)))
+    y_eager = [dev.download(py[i], (r,), np.float32) for i, (_, r, _) in enumerate(LAYER_SET)]
+    replay_equal = all(np.array_equal(a.view(np.uint32), b.view(np.uint32))
+                       for a, b in zip(y_graph, y_eager))
     step_bytes = sum(algo_bytes(t, r, c) for _, r, c in LAYER_SET)
-    big_bytes = algo_bytes(t, FF, H)
-    avg_ms = float(np.mean(per_launch))
-    res = {
-        "step_bytes": step_bytes, "wall_s": wall, "gpu_ms": gpu_ms, "wall_plain_s": wall_plain,
-        "per_launch_ms": per_launch, "big_bytes": big_bytes, "avg_big_ms": avg_ms,
-        "med_big_ms": float(np.median(per_launch)), "min_big_ms": float(np.min(per_launch)),
-        "weights_host": weights_host, "xs_host": xs_host,
-    }
-    # parity spot check of copy 0 against the oracle (one matvec)
+    res = {"step_bytes": step_bytes, "wall_s": wall, "gpu_ms": gpu_ms,
+           "big_bytes": algo_bytes(t, FF, H), "avg_big_ms": big_ms,
+           "replay_equals_eager": replay_equal,
+           "weights_host": weights_host, "xs_host": xs_host}
     for k_ in copies:
         for p in k_:
             dev.free(p)
@@ -209,7 +235,10 @@ def bench_matvec(dev, host, steps, warmup, ncopy):
     return res
 
 
-def bench_decode(dev, host, n_tokens, n_layers=32, ctx=2048):
+def bench_decode(dev, host, n_tokens, path="both", n_layers=32, ctx=2048, n_dispatch_tokens=16):
+    """Greedy decode of the 7B Q4_K_M synthetic model (config 4) from position
+    `ctx` with the KV cache prefilled N(0,1): the graph decoder (one graph
+    launch per token) and, for comparison, the per-dispatch ops-table path."""
     model = V.SynthModel(host, n_layers=n_layers, hidden=4096, ffn=11008, n_heads=32,
                          n_kv_heads=8, head_dim=128, vocab=32000, max_ctx=ctx + n_tokens + 1,
                          seed=SEED)
@@ -219,20 +248,38 @@ def bench_decode(dev, host, n_tokens, n_layers=32, ctx=2048):
         raise RuntimeError(be.last_error())
     d = V.Decoder(host, be, model)
     d.load_kv(kc, vc, ctx)
-    d.greedy(1, ctx, 2)  # warm-up (pipelines, scratch)
-    d.load_kv(kc, vc, ctx)
+    # per-dispatch path (src/vbs_specializer.c order through the ops table)
+    d.greedy(1, ctx, 2)
     t0 = time.perf_counter()
-    toks, margins = d.greedy(1, ctx, n_tokens)
-    dt = time.perf_counter() - t0
-    wbytes = model.weight_bytes() - model.tok_embd.nbytes
-    kv_bytes = sum(n_layers * (ctx + i + 1) * 1024 * 2 * 2 for i in range(n_tokens)) / n_tokens
+    dtoks, dmargins = d.greedy(1, ctx, n_dispatch_tokens)
+    dt_dispatch = time.perf_counter() - t0
     dispatches = d.dispatch_count()
+    dispatch = {"tokens_per_s": round(n_dispatch_tokens / dt_dispatch, 2),
+                "dispatches_per_token": dispatches,
+                "path": "g_vbs_hip_backend ops table, one dispatch per bridge call"}
+    if path == "dispatch":
+        d.close()
+        return {"dispatch_path": dispatch, "first_tokens": [int(x) for x in dtoks[:8]],
+                "min_margin": float(np.min(dmargins))}
+    # graph decoder over the same device weights and cache
+    g = V.GraphDecoder(dev, d, max_steps=n_tokens)
+    g.greedy(1, ctx, 2)
+    dev.sync()
+    t0 = time.perf_counter()
+    toks, margins = g.greedy(1, ctx, n_tokens)
+    dt = time.perf_counter() - t0
+    g.close()
     d.close()
+    wbytes = model.weight_bytes() - model.tok_embd.nbytes
+    kvd = model.cfg["n_kv_heads"] * model.cfg["head_dim"]
+    kv_bytes = sum(n_layers * (ctx + i + 1) * kvd * 2 * 2 for i in range(n_tokens)) / n_tokens
     return {"tokens_per_s": round(n_tokens / dt, 2), "ms_per_token": round(1e3 * dt / n_tokens, 3),
-            "n_tokens": n_tokens, "context": ctx, "dispatches_per_token": dispatches,
+            "n_tokens": n_tokens, "context": ctx,
             "bytes_per_token": int(wbytes + kv_bytes),
             "roofline_frac": round((wbytes + kv_bytes) / (dt / n_tokens) / (PEAK_HBM_GBS * 1e9), 4),
-            "path": "g_vbs_hip_backend ops table, one dispatch per bridge call",
+            "path": "vbs_gfx950_decoder: one HIP graph launch per token",
+            "dispatch_path": dispatch,
+            "paths_agree": bool(np.array_equal(toks[:n_dispatch_tokens], dtoks)),
             "first_tokens": [int(x) for x in toks[:8]],
             "min_margin": float(np.min(margins))}
 
@@ -240,21 +287,35 @@ def bench_decode(dev, host, n_tokens, n_layers=32, ctx=2048):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--ncopy", type=int, default=4)
+    ap.add_argument("--roof-reps", type=int, default=50)
     ap.add_argument("--decode-tokens", type=int, default=128)
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="first copy this many MiB device-to-device once (a known-size "
+                         "transfer that scales HBM byte counters)")
+    ap.add_argument("--decode-path", choices=("both", "dispatch"), default="both",
+                    help="'dispatch' times only the per-dispatch ops-table decode")
     ap.add_argument("--no-cpu", action="store_true")
     a = ap.parse_args()
     if a.gpus != 1:
-        print(json.dumps({"error": "this backend drives exactly one GPU; run with --gpus 1"}))
+        print(json.dumps({"error": "this build drives exactly one GPU (one process, one device); "
+                                   "run with --gpus 1"}))
         sys.exit(2)
     dev = V.DeviceLib()
     if not dev.init():
         raise SystemExit(f"gfx950 device unavailable: {dev.error()}")
     host = V.load_host()
-    r = bench_matvec(dev, host, a.steps, a.warmup, a.ncopy)
+    if a.copy_probe_mib:
+        n = a.copy_probe_mib << 20
+        src, dst = dev.alloc(n), dev.alloc(n)
+        dev.check(dev._copy_d2d(dst, src, n), "copy probe")
+        dev.sync()
+        dev.free(src)
+        dev.free(dst)
+    r = bench_matvec(dev, host, a.steps, a.warmup, a.ncopy, a.roof_reps)
     value = r["step_bytes"] * a.steps / r["wall_s"] / 1e9
     achieved = r["big_bytes"] / (r["avg_big_ms"] * 1e-3) / 1e9
     out = {
@@ -262,23 +323,23 @@ def main():
         "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": a.steps,
         "warmup": a.warmup, "ms_per_step": round(1e3 * r["wall_s"] / a.steps, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "q4_k weights, f32 activations, f32 accumulate", "data": "synthetic",
+        "dtype": "q4_k", "data": "synthetic",
         "config": {"workload": "Llama-7B layer matvec set, Q4_K, batch 1 (config 2)",
                    "shapes": [[n, r, c] for n, r, c in LAYER_SET], "weight_copies": a.ncopy,
                    "rotating_bytes": a.ncopy * sum(V.row_bytes(V.Q4_K, c) * r
-                                                   for _, r, c in LAYER_SET)},
+                                                   for _, r, c in LAYER_SET),
+                   "issue": "one HIP graph of the 7 launches per step"},
         "pct_of_peak": round(100 * value / PEAK_HBM_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
-                     "kernel": "k_linear (Q4_K) 11008x4096 and 4096x11008",
+                     "kernel": "k_q4k_mv, 11008x4096 and 4096x11008",
                      "algorithmic_bytes_per_launch": r["big_bytes"],
-                     "avg_launch_us": round(1e3 * r["avg_big_ms"], 3),
-                     "median_launch_us": round(1e3 * r["med_big_ms"], 3),
-                     "min_launch_us": round(1e3 * r["min_big_ms"], 3)},
+                     "avg_launch_us": round(1e3 * r["avg_big_ms"], 3)},
         "gpu_event_ms_per_step": round(r["gpu_ms"] / a.steps, 4),
+        "graph_replay_equals_eager": r["replay_equals_eager"],
     }
     if not a.no_decode:
-        out["decode"] = bench_decode(dev, host, a.decode_tokens)
+        out["decode"] = bench_decode(dev, host, a.decode_tokens, a.decode_path)
     if not a.no_cpu:
         out["cpu_baseline"] = cpu_baseline(host, r["weights_host"], r["xs_host"])
     print(json.dumps(out))

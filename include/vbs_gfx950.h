@@ -136,6 +136,41 @@ int vbs_gfx950_linear_batch(int type, const void *w, const float *x, uint32_t x_
  * HIP events or capture the stream into a graph. */
 void *vbs_gfx950_stream(void);
 
+/* ---- graph-replayed decode step (extension) -------------------------------
+ * The caller side of one token (src/vbs_specializer.c:231-359) issues ~16
+ * dispatches per layer through the ops table, each a separate host launch.
+ * The decoder below runs the same sequence, with the same kernels and the
+ * same arithmetic, from one HIP graph per model: the token and position live
+ * in device memory (RoPE angles come from a table computed once with the host
+ * libm, exactly as src/vbs_host_math.h:43-44), and a greedy argmax kernel
+ * (first maximum, as main.c:929-932) writes the next token and advances the
+ * position, so consecutive tokens replay the graph back to back. */
+typedef struct {
+    uint32_t n_layers, hidden, ffn, n_heads, n_kv_heads, head_dim, vocab, max_ctx;
+    float rope_theta, rms_eps;
+    int embd_type;
+    const void *tok_embd;            /* device: vocab x hidden packed */
+    const float *out_norm;           /* device: hidden */
+    int head_type;
+    const void *lm_head;             /* device: vocab x hidden packed */
+    const float *const *attn_norm;   /* host array of n_layers device pointers */
+    const float *const *ffn_norm;    /* host array of n_layers device pointers */
+    const int *wtype;                /* host array n_layers x 7 (q,k,v,o,gate,up,down) */
+    const void *const *wdata;        /* host array n_layers x 7 device pointers */
+    uint16_t *kc, *vc;               /* device f16 caches [n_layers][max_ctx][n_kv_heads*head_dim] */
+} vbs_gfx950_model_t;
+
+/* Build the per-token graph (the model's device memory is borrowed, not
+ * copied). max_steps bounds one vbs_gfx950_decoder_greedy call. */
+int vbs_gfx950_decoder_create(const vbs_gfx950_model_t *m, uint32_t max_steps, void **handle);
+/* One token at `pos`; logits (vocab floats, host) may be NULL. */
+int vbs_gfx950_decoder_step(void *handle, uint32_t token, uint32_t pos, float *logits);
+/* Greedy: feed `token` at `pos`, then n-1 further argmax tokens; tokens[i]
+ * is the i-th argmax, margins (may be NULL) top-1 minus top-2 logit. */
+int vbs_gfx950_decoder_greedy(void *handle, uint32_t token, uint32_t pos, uint32_t n,
+                              uint32_t *tokens, float *margins);
+int vbs_gfx950_decoder_destroy(void *handle);
+
 #ifdef __cplusplus
 }
 #endif

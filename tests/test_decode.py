@@ -8,6 +8,9 @@ vbs_oracle_forward_token, following src/vbs_specializer.c:231-349).
   reference code.
 * GPU: the driver over g_vbs_hip_backend must produce the oracle's greedy
   token sequence, with logits within 1e-4 relative L2 per step.
+* GPU: the graph-replayed decoder (vbs_gfx950_decoder_*) runs the same kernels
+  with device-resident token/position, so its logits and KV stores must equal
+  the per-dispatch driver's bit for bit, and its greedy tokens the oracle's.
 """
 import numpy as np
 import pytest
@@ -96,7 +99,7 @@ def test_gpu_tiny_model_greedy(host, backend, tiny):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("n_layers,n_tok", [(4, 12), (32, 3)], ids=["7b_4layers", "7b_full"])
-def test_gpu_7b_shape_greedy(host, backend, n_layers, n_tok):
+def test_gpu_7b_shape_greedy(host, backend, dev, n_layers, n_tok):
     """7B geometry (config 4), KV prefilled N(0,1) to 2048, greedy from 2048."""
     ctx = 2048
     model = V.SynthModel(host, n_layers=n_layers, hidden=4096, ffn=11008, n_heads=32,
@@ -106,7 +109,74 @@ def test_gpu_7b_shape_greedy(host, backend, n_layers, n_tok):
     d = V.Decoder(host, backend, model)
     d.load_kv(kc_p, vc_p, ctx)
     toks, margins = d.greedy(1, ctx, n_tok)
+    # the graph decoder over the same device model rewrites the same cache rows
+    g = V.GraphDecoder(dev, d, max_steps=n_tok)
+    gtoks, gmargins = g.greedy(1, ctx, n_tok)
+    g.close()
     d.close()
+    assert np.array_equal(gtoks, toks), (gtoks, toks)
+    assert np.array_equal(gmargins.view(np.uint32), margins.view(np.uint32))
     kc, vc = full_cache(model, kc_p, vc_p, ctx)
     want, _ = oracle_greedy(Oracle(), model, kc, vc, 1, ctx, n_tok)
     assert np.array_equal(toks, want), (toks, want, margins)
+
+
+@pytest.mark.gpu
+def test_gpu_graph_decoder_equals_dispatch_path(host, backend, dev, tiny):
+    """Logits and KV stores of graph replays equal the per-dispatch driver's."""
+    c = tiny.cfg
+    kvd = c["n_kv_heads"] * c["head_dim"]
+    kc_p, vc_p = tiny.kv_prefill(host, 7)
+    d = V.Decoder(host, backend, tiny)
+    d.load_kv(kc_p, vc_p, 7)
+    want, tok = [], 5
+    for pos in range(7, 19):
+        want.append(d.step(tok, pos))
+        tok = int(np.argmax(want[-1]))
+    want_kc, want_vc = d.read_kv(19)
+    # reset the rows the dispatch path wrote, then replay them with the graph
+    d.load_kv(kc_p, vc_p, 7)
+    g = V.GraphDecoder(dev, d, max_steps=12)
+    tok = 5
+    for i, pos in enumerate(range(7, 19)):
+        got = g.step(tok, pos)
+        assert np.array_equal(got.view(np.uint32), want[i].view(np.uint32)), f"pos {pos}"
+        tok = int(np.argmax(got))
+    gk, gv = d.read_kv(19)
+    assert np.array_equal(gk, want_kc) and np.array_equal(gv, want_vc)
+    # greedy replays (token fed back on the device) give the same tokens
+    toks, margins = g.greedy(5, 7, 12)
+    assert list(toks) == [int(np.argmax(w)) for w in want]
+    for i, w in enumerate(want):
+        top2 = np.sort(w)[-2:]
+        assert margins[i] == np.float32(top2[1] - top2[0])
+    g.close()
+    d.close()
+
+
+@pytest.mark.gpu
+def test_gpu_graph_decoder_tiny_greedy_matches_oracle(host, backend, dev, tiny):
+    d = V.Decoder(host, backend, tiny)
+    g = V.GraphDecoder(dev, d, max_steps=40)
+    kc, vc = full_cache(tiny, None, None, 0)
+    want_toks, _ = oracle_greedy(Oracle(), tiny, kc, vc, 1, 0, 40)
+    toks, _ = g.greedy(1, 0, 40)
+    g.close()
+    d.close()
+    assert np.array_equal(toks, want_toks)
+
+
+@pytest.mark.gpu
+def test_gpu_graph_decoder_rejects_bad_state(host, backend, dev, tiny):
+    d = V.Decoder(host, backend, tiny)
+    g = V.GraphDecoder(dev, d, max_steps=4)
+    with pytest.raises(V.GpuError, match="vocab"):
+        g.step(tiny.cfg["vocab"], 0)
+    with pytest.raises(V.GpuError, match="max_ctx"):
+        g.step(0, tiny.cfg["max_ctx"])
+    with pytest.raises(V.GpuError, match="max_steps"):
+        g.greedy(0, 0, 5)
+    with pytest.raises(V.GpuError, match="context"):
+        g.greedy(0, tiny.cfg["max_ctx"] - 2, 4)
+    g.close()
+    d.close()

@@ -1,0 +1,354 @@
+// vbs_decoder.hip — one decode token as a replayable HIP graph.
+//
+// The step is the specializer's forward_token (src/vbs_specializer.c:270-349)
+// with the bridge's scalars (src/vbs_specializer_bridge.c:148-183): embed ->
+// per layer [attn_norm, Q, rope(Q), K, rope(K), V, cache, attention, O, add,
+// ffn_norm, gate, up, silu, down, add] -> output_norm -> lm_head, followed by
+// a greedy argmax. It uses the same kernels as the per-dispatch C ABI; only
+// the position-dependent ones read the position from device memory so one
+// captured graph serves every token:
+//   * RoPE reads cos/sin of each pair from a [max_ctx][head_dim/2] table that
+//     the host fills with the reference's own expressions and libm;
+//   * the KV store and attention compute their offsets / sequence length from
+//     the device position;
+//   * the argmax kernel writes the next token, records it, and advances the
+//     position.
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <vector>
+
+#include "vbs_dev_common.h"
+#include "vbs_gfx950.h"
+#include "vbs_internal.h"
+
+namespace vbs {
+
+// ---- position-dependent kernels ---------------------------------------------
+
+__global__ __launch_bounds__(256) void k_rope_table(float *__restrict__ x,
+                                                    const uint32_t *__restrict__ pos_dev,
+                                                    const float2 *__restrict__ tab, uint32_t hd,
+                                                    uint32_t nh) {
+    const uint32_t pairs = hd / 2u;
+    const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
+    if (idx >= pairs * nh) return;
+    const uint32_t h = idx / pairs, p = idx % pairs;
+    const float2 cs = tab[(uint64_t)pos_dev[0] * pairs + p];
+    float *v = x + (uint64_t)h * hd + 2u * p;
+    const float x0 = v[0], x1 = v[1];
+    v[0] = __fsub_rn(__fmul_rn(x0, cs.x), __fmul_rn(x1, cs.y));
+    v[1] = __fadd_rn(__fmul_rn(x0, cs.y), __fmul_rn(x1, cs.x));
+}
+
+__global__ __launch_bounds__(256) void k_cache_store_pos(const float *__restrict__ k,
+                                                         const float *__restrict__ v,
+                                                         uint16_t *__restrict__ kc,
+                                                         uint16_t *__restrict__ vc,
+                                                         const uint32_t *__restrict__ pos_dev,
+                                                         uint32_t layer, uint32_t max_ctx,
+                                                         uint32_t kv_dim) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i >= kv_dim) return;
+    const uint64_t base = ((uint64_t)layer * max_ctx + pos_dev[0]) * kv_dim;
+    kc[base + i] = vbs_f2h(k[i]);
+    vc[base + i] = vbs_f2h(v[i]);
+}
+
+// Greedy pick: the first index of the maximum (strict '>' scan order, as
+// main.c:929-932), and the runner-up value for the margin report. Writes the
+// token for the next replay, records it at tokens[step], advances pos and step.
+struct Top2 {
+    float v1;
+    uint32_t i1;
+    float v2;
+};
+
+__device__ __forceinline__ Top2 top2_merge(Top2 a, Top2 b) {
+    // a's indices precede b's only when a came from a lower index range; the
+    // comparison keeps the lower index on ties so the first maximum wins
+    const bool b_wins = b.v1 > a.v1 || (b.v1 == a.v1 && b.i1 < a.i1);
+    Top2 r;
+    r.v1 = b_wins ? b.v1 : a.v1;
+    r.i1 = b_wins ? b.i1 : a.i1;
+    const float loser = b_wins ? a.v1 : b.v1;
+    r.v2 = fmaxf(loser, fmaxf(a.v2, b.v2));
+    return r;
+}
+
+__global__ __launch_bounds__(1024) void k_argmax_advance(const float *__restrict__ logits,
+                                                         uint32_t n, uint32_t *token_dev,
+                                                         uint32_t *pos_dev, uint32_t *step_dev,
+                                                         uint32_t *tokens, float *margins,
+                                                         uint32_t max_steps) {
+    __shared__ Top2 red[1024];
+    Top2 t{-INFINITY, 0xFFFFFFFFu, -INFINITY};
+    for (uint32_t i = threadIdx.x; i < n; i += 1024u) {
+        const float v = logits[i];
+        if (v != v && i != 0u) continue;  // a NaN never beats anything after index 0
+        if (t.i1 == 0xFFFFFFFFu || v > t.v1) {
+            if (t.i1 != 0xFFFFFFFFu) t.v2 = fmaxf(t.v2, t.v1);
+            t.v1 = v;
+            t.i1 = i;
+        } else {
+            t.v2 = fmaxf(t.v2, v);
+        }
+    }
+    red[threadIdx.x] = t;
+    __syncthreads();
+    for (uint32_t s = 512u; s > 0; s >>= 1) {
+        if (threadIdx.x < s) {
+            Top2 a = red[threadIdx.x], b = red[threadIdx.x + s];
+            if (a.i1 == 0xFFFFFFFFu) a = b;
+            else if (b.i1 != 0xFFFFFFFFu) a = top2_merge(a, b);
+            red[threadIdx.x] = a;
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        const uint32_t step = step_dev[0];
+        if (step < max_steps) {
+            tokens[step] = red[0].i1;
+            margins[step] = red[0].v1 - red[0].v2;
+        }
+        token_dev[0] = red[0].i1;
+        pos_dev[0] = pos_dev[0] + 1u;
+        step_dev[0] = step + 1u;
+    }
+}
+
+// ---- decoder -------------------------------------------------------------------
+
+struct Decoder {
+    vbs_gfx950_model_t m;
+    std::vector<const float *> attn_norm, ffn_norm;
+    std::vector<int> wtype;
+    std::vector<const void *> wdata;
+    float *stream = nullptr, *tmp, *normed, *q, *k, *v, *attn, *gate, *up, *hid, *logits;
+    uint32_t *state = nullptr;  // [token, pos, step]
+    uint32_t *tokens = nullptr;
+    float *margins = nullptr;
+    float *part = nullptr;
+    float2 *rope = nullptr;
+    uint32_t max_steps = 0;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    void *arena = nullptr;
+};
+
+static hipError_t enqueue_step(const Decoder &d, hipStream_t s) {
+    const vbs_gfx950_model_t &m = d.m;
+    const uint32_t H = m.hidden, F = m.ffn, hd = m.head_dim, nq = m.n_heads, nkv = m.n_kv_heads;
+    const uint32_t qd = nq * hd, kvd = nkv * hd;
+    const float scale = 1.0f / sqrtf((float)hd);
+    uint32_t *token_dev = d.state, *pos_dev = d.state + 1, *step_dev = d.state + 2;
+    const uint32_t pairs = hd / 2u;
+#define VBS_TRY(expr)                     \
+    do {                                  \
+        hipError_t e_ = (expr);           \
+        if (e_ != hipSuccess) return e_;  \
+    } while (0)
+    VBS_TRY(launch_dequant_rows(m.embd_type, (const uint8_t *)m.tok_embd, token_dev, 0, 1, H,
+                                d.stream, s));
+    for (uint32_t L = 0; L < m.n_layers; L++) {
+        const int *t = d.wtype.data() + 7 * L;
+        const uint8_t *const *w = (const uint8_t *const *)d.wdata.data() + 7 * L;
+        VBS_TRY(launch_rms_norm(d.stream, d.attn_norm[L], d.normed, H, m.rms_eps, s));
+        VBS_TRY(launch_linear(t[0], w[0], d.normed, d.q, H, qd, 0, s));
+        k_rope_table<<<(pairs * nq + 255u) / 256u, 256, 0, s>>>(d.q, pos_dev, d.rope, hd, nq);
+        VBS_TRY(hipGetLastError());
+        VBS_TRY(launch_linear(t[1], w[1], d.normed, d.k, H, kvd, 0, s));
+        k_rope_table<<<(pairs * nkv + 255u) / 256u, 256, 0, s>>>(d.k, pos_dev, d.rope, hd, nkv);
+        VBS_TRY(hipGetLastError());
+        VBS_TRY(launch_linear(t[2], w[2], d.normed, d.v, H, kvd, 0, s));
+        k_cache_store_pos<<<(kvd + 255u) / 256u, 256, 0, s>>>(d.k, d.v, m.kc, m.vc, pos_dev, L,
+                                                                m.max_ctx, kvd);
+        VBS_TRY(hipGetLastError());
+        const uint64_t layer_off = (uint64_t)L * m.max_ctx * kvd;
+        VBS_TRY(launch_attention(d.q, m.kc, m.vc, d.attn, m.max_ctx, pos_dev, d.part, layer_off,
+                                 nq, nkv, hd, scale, s));
+        VBS_TRY(launch_linear(t[3], w[3], d.attn, d.tmp, qd, H, 0, s));
+        VBS_TRY(launch_add(d.stream, d.tmp, d.stream, H, s));
+        VBS_TRY(launch_rms_norm(d.stream, d.ffn_norm[L], d.normed, H, m.rms_eps, s));
+        VBS_TRY(launch_linear(t[4], w[4], d.normed, d.gate, H, F, 0, s));
+        VBS_TRY(launch_linear(t[5], w[5], d.normed, d.up, H, F, 0, s));
+        VBS_TRY(launch_silu_mul(d.gate, d.up, d.hid, F, s));
+        VBS_TRY(launch_linear(t[6], w[6], d.hid, d.tmp, F, H, 0, s));
+        VBS_TRY(launch_add(d.stream, d.tmp, d.stream, H, s));
+    }
+    VBS_TRY(launch_rms_norm(d.stream, m.out_norm, d.normed, H, m.rms_eps, s));
+    VBS_TRY(launch_linear(m.head_type, (const uint8_t *)m.lm_head, d.normed, d.logits, H, m.vocab,
+                          0, s));
+    k_argmax_advance<<<1, 1024, 0, s>>>(d.logits, m.vocab, token_dev, pos_dev, step_dev,
+                                        d.tokens, d.margins, d.max_steps);
+    VBS_TRY(hipGetLastError());
+#undef VBS_TRY
+    return hipSuccess;
+}
+
+static void decoder_free(Decoder *d) {
+    if (!d) return;
+    if (d->exec) (void)hipGraphExecDestroy(d->exec);
+    if (d->graph) (void)hipGraphDestroy(d->graph);
+    if (d->arena) {
+        (void)hipStreamSynchronize(rt_stream());
+        (void)hipFree(d->arena);
+    }
+    delete d;
+}
+
+}  // namespace vbs
+
+using namespace vbs;
+
+extern "C" {
+
+int vbs_gfx950_decoder_create(const vbs_gfx950_model_t *m, uint32_t max_steps, void **handle) {
+    if (!rt_ready()) return 0;
+    if (!m || !handle) return rt_fail("decoder_create: null argument");
+    *handle = nullptr;
+    if (!m->n_layers || !m->hidden || !m->ffn || !m->n_heads || !m->n_kv_heads || !m->head_dim ||
+        !m->vocab || !m->max_ctx)
+        return rt_fail("decoder_create: empty model dimension");
+    if (m->n_heads % m->n_kv_heads || m->n_heads / m->n_kv_heads > 16 || m->head_dim > 256 ||
+        (m->head_dim & 1u))
+        return rt_fail("decoder_create: unsupported head geometry");
+    if (!m->tok_embd || !m->out_norm || !m->lm_head || !m->attn_norm || !m->ffn_norm ||
+        !m->wtype || !m->wdata || !m->kc || !m->vc)
+        return rt_fail("decoder_create: null model pointer");
+    if (!block_elems(m->embd_type) || !block_elems(m->head_type))
+        return rt_fail("decoder_create: unsupported embedding/head type");
+    for (uint32_t i = 0; i < 7 * m->n_layers; i++) {
+        if (!block_elems(m->wtype[i]) || !m->wdata[i])
+            return rt_fail("decoder_create: layer %u matrix %u unsupported or null", i / 7, i % 7);
+    }
+    Decoder *d = new Decoder();
+    d->m = *m;
+    d->attn_norm.assign(m->attn_norm, m->attn_norm + m->n_layers);
+    d->ffn_norm.assign(m->ffn_norm, m->ffn_norm + m->n_layers);
+    d->wtype.assign(m->wtype, m->wtype + 7 * m->n_layers);
+    d->wdata.assign(m->wdata, m->wdata + 7 * m->n_layers);
+    d->max_steps = max_steps ? max_steps : 1;
+    const uint32_t H = m->hidden, F = m->ffn, qd = m->n_heads * m->head_dim;
+    const uint32_t kvd = m->n_kv_heads * m->head_dim, pairs = m->head_dim / 2u;
+    // one arena: activations, state, outputs, attention partials, RoPE table
+    const size_t n_f32 = 3ull * H + 2ull * qd + 2ull * kvd + 3ull * F + m->vocab;
+    const size_t part = attention_partial_bytes(m->max_ctx, m->n_heads, m->head_dim);
+    const size_t rope = (size_t)m->max_ctx * pairs * sizeof(float2);
+    auto up256 = [](size_t b) { return (b + 255u) & ~(size_t)255u; };
+    const size_t sz_f = up256(n_f32 * 4), sz_st = 256, sz_tok = up256(d->max_steps * 4ull);
+    const size_t total = sz_f + sz_st + 2 * sz_tok + up256(part) + up256(rope);
+    if (hipMalloc(&d->arena, total) != hipSuccess) {
+        delete d;
+        return rt_fail("decoder_create: hipMalloc(%zu) failed", total);
+    }
+    uint8_t *p = (uint8_t *)d->arena;
+    float *f = (float *)p;
+    d->stream = f; f += H;
+    d->tmp = f; f += H;
+    d->normed = f; f += H;
+    d->q = f; f += qd;
+    d->attn = f; f += qd;
+    d->k = f; f += kvd;
+    d->v = f; f += kvd;
+    d->gate = f; f += F;
+    d->up = f; f += F;
+    d->hid = f; f += F;
+    d->logits = f;
+    p += sz_f;
+    d->state = (uint32_t *)p; p += sz_st;
+    d->tokens = (uint32_t *)p; p += sz_tok;
+    d->margins = (float *)p; p += sz_tok;
+    d->part = (float *)p; p += up256(part);
+    d->rope = (float2 *)p;
+    // RoPE table with the reference's expressions (src/vbs_host_math.h:43-44)
+    std::vector<float2> tab((size_t)m->max_ctx * pairs);
+    for (uint32_t pos = 0; pos < m->max_ctx; pos++)
+        for (uint32_t pr = 0; pr < pairs; pr++) {
+            const uint32_t i = 2u * pr;
+            const float angle = (float)pos * powf(m->rope_theta, -(float)i / (float)m->head_dim);
+            tab[(size_t)pos * pairs + pr] = make_float2(cosf(angle), sinf(angle));
+        }
+    hipStream_t s = rt_stream();
+    if (!rt_hip_ok(hipMemcpyAsync(d->rope, tab.data(), rope, hipMemcpyHostToDevice, s),
+                   "decoder_create: rope table") ||
+        !rt_hip_ok(hipMemsetAsync(d->state, 0, sz_st, s), "decoder_create: state") ||
+        !rt_hip_ok(hipStreamSynchronize(s), "decoder_create")) {
+        decoder_free(d);
+        return 0;
+    }
+    // capture one token step
+    if (!rt_hip_ok(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "begin capture")) {
+        decoder_free(d);
+        return 0;
+    }
+    hipError_t e = enqueue_step(*d, s);
+    hipGraph_t g = nullptr;
+    hipError_t e2 = hipStreamEndCapture(s, &g);
+    if (e != hipSuccess || e2 != hipSuccess) {
+        if (g) (void)hipGraphDestroy(g);
+        decoder_free(d);
+        return rt_fail("decoder_create: capture failed (%s)",
+                       hipGetErrorString(e != hipSuccess ? e : e2));
+    }
+    d->graph = g;
+    if (!rt_hip_ok(hipGraphInstantiate(&d->exec, g, nullptr, nullptr, 0), "graph instantiate")) {
+        decoder_free(d);
+        return 0;
+    }
+    *handle = d;
+    return 1;
+}
+
+static int set_state(Decoder *d, uint32_t token, uint32_t pos) {
+    if (token >= d->m.vocab) return rt_fail("decoder: token %u >= vocab %u", token, d->m.vocab);
+    if (pos >= d->m.max_ctx) return rt_fail("decoder: pos %u >= max_ctx %u", pos, d->m.max_ctx);
+    const uint32_t st[3] = {token, pos, 0};
+    hipStream_t s = rt_stream();
+    return rt_hip_ok(hipMemcpyAsync(d->state, st, sizeof(st), hipMemcpyHostToDevice, s),
+                     "decoder: state") &&
+           rt_hip_ok(hipStreamSynchronize(s), "decoder: state");
+}
+
+int vbs_gfx950_decoder_step(void *handle, uint32_t token, uint32_t pos, float *logits) {
+    if (!rt_ready()) return 0;
+    Decoder *d = (Decoder *)handle;
+    if (!d) return rt_fail("decoder_step: null handle");
+    if (!set_state(d, token, pos)) return 0;
+    hipStream_t s = rt_stream();
+    if (!rt_hip_ok(hipGraphLaunch(d->exec, s), "decoder_step: graph launch")) return 0;
+    if (logits &&
+        !rt_hip_ok(hipMemcpyAsync(logits, d->logits, (size_t)d->m.vocab * 4, hipMemcpyDeviceToHost, s),
+                   "decoder_step: logits"))
+        return 0;
+    return rt_hip_ok(hipStreamSynchronize(s), "decoder_step");
+}
+
+int vbs_gfx950_decoder_greedy(void *handle, uint32_t token, uint32_t pos, uint32_t n,
+                              uint32_t *tokens, float *margins) {
+    if (!rt_ready()) return 0;
+    Decoder *d = (Decoder *)handle;
+    if (!d || !tokens) return rt_fail("decoder_greedy: null argument");
+    if (n > d->max_steps) return rt_fail("decoder_greedy: %u steps > max_steps %u", n, d->max_steps);
+    if ((uint64_t)pos + n > d->m.max_ctx) return rt_fail("decoder_greedy: context exhausted");
+    if (!set_state(d, token, pos)) return 0;
+    hipStream_t s = rt_stream();
+    for (uint32_t i = 0; i < n; i++)
+        if (!rt_hip_ok(hipGraphLaunch(d->exec, s), "decoder_greedy: graph launch")) return 0;
+    if (!rt_hip_ok(hipMemcpyAsync(tokens, d->tokens, (size_t)n * 4, hipMemcpyDeviceToHost, s),
+                   "decoder_greedy: tokens"))
+        return 0;
+    if (margins &&
+        !rt_hip_ok(hipMemcpyAsync(margins, d->margins, (size_t)n * 4, hipMemcpyDeviceToHost, s),
+                   "decoder_greedy: margins"))
+        return 0;
+    return rt_hip_ok(hipStreamSynchronize(s), "decoder_greedy");
+}
+
+int vbs_gfx950_decoder_destroy(void *handle) {
+    decoder_free((Decoder *)handle);
+    return 1;
+}
+
+}  // extern "C"

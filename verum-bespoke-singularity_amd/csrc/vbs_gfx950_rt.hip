@@ -97,6 +97,20 @@ void *scratch(size_t bytes, hipStream_t s) {
     return g_rt.scratch;
 }
 
+hipStream_t rt_stream() { return g_rt.stream; }
+
+int rt_fail(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return 0;
+}
+
+int rt_hip_ok(hipError_t e, const char *what) { return hip_ok(e, what); }
+
+bool rt_ready() { return ready_or_fail(); }
+
 }  // namespace vbs
 
 using namespace vbs;
@@ -305,8 +319,8 @@ int vbs_gfx950_attention(const float *q, const uint16_t *kc, const uint16_t *vc,
     if (nqh / nkh > 16) return fail("attention: group size %u exceeds 16", nqh / nkh);
     if (hd > 256 || (hd & 1u)) return fail("attention: head_dim %u must be even and <= 256", hd);
     uint64_t layer_off = (uint64_t)layer * max_ctx * nkh * hd;
-    return hip_ok(launch_attention(q, kc, vc, out, seq_len, layer_off, nqh, nkh, hd, scale,
-                                   g_rt.stream),
+    return hip_ok(launch_attention(q, kc, vc, out, seq_len, nullptr, nullptr, layer_off, nqh, nkh,
+                                   hd, scale, g_rt.stream),
                   "attention");
 }
 

@@ -18,6 +18,12 @@ uint32_t block_elems(int type);
 // Device scratch owned by the runtime (grown on demand, never shrunk).
 void *scratch(size_t bytes, hipStream_t s);
 
+// The library's stream, and the last-error writer of the C ABI.
+hipStream_t rt_stream();
+int rt_fail(const char *fmt, ...);
+int rt_hip_ok(hipError_t e, const char *what);
+bool rt_ready();
+
 // Specialised Q4_K matvec; hipErrorNotSupported when the shape/alignment is
 // outside its range (the generic kernel then runs).
 hipError_t launch_q4k_fast(const uint8_t *w, const float *x, float *y, uint32_t cols,
@@ -36,9 +42,14 @@ hipError_t launch_rope(float *x, uint32_t head_dim, uint32_t n_heads, const floa
                        hipStream_t s);
 hipError_t launch_cache_store(const float *k, const float *v, uint16_t *kc, uint16_t *vc,
                               uint64_t base, uint32_t kv_dim, hipStream_t s);
+// Split-sequence attention. With pos_dev the sequence length is read on the
+// device (pos + 1) and seq_len only sizes the grid; `part` may be NULL (then
+// the runtime scratch holds the per-chunk partials).
+size_t attention_partial_bytes(uint32_t max_seq, uint32_t nqh, uint32_t hd);
 hipError_t launch_attention(const float *q, const uint16_t *kc, const uint16_t *vc, float *out,
-                            uint32_t seq_len, uint64_t layer_off, uint32_t nqh, uint32_t nkh,
-                            uint32_t hd, float scale, hipStream_t s);
+                            uint32_t seq_len, const uint32_t *pos_dev, float *part,
+                            uint64_t layer_off, uint32_t nqh, uint32_t nkh, uint32_t hd,
+                            float scale, hipStream_t s);
 hipError_t launch_silu_mul(const float *g, const float *u, float *out, uint32_t n,
                            hipStream_t s);
 hipError_t launch_add(const float *a, const float *b, float *out, uint32_t n, hipStream_t s);

@@ -23,16 +23,20 @@ __global__ __launch_bounds__(256) void k_attn_partial(const float *__restrict__ 
                                                       const uint16_t *__restrict__ kc,
                                                       const uint16_t *__restrict__ vc,
                                                       float *__restrict__ part,
-                                                      uint32_t seq_len, uint64_t layer_off,
-                                                      uint32_t nkh, uint32_t hd, uint32_t group,
-                                                      float scale, uint32_t n_chunks) {
+                                                      uint32_t seq_len, const uint32_t *pos_dev,
+                                                      uint64_t layer_off, uint32_t nkh, uint32_t hd,
+                                                      uint32_t group, float scale,
+                                                      uint32_t n_chunks) {
     extern __shared__ float lds[];
     float *qs = lds;                       // [group][hd]
     float *ps = qs + group * hd;           // [group][kChunk]
     float *red = ps + group * kChunk;      // [256 / hd][group][hd] partial acc
 
     const uint32_t chunk = blockIdx.x, kvh = blockIdx.y, t = threadIdx.x;
+    // graph replays take the position from device memory: seq_len = pos + 1
+    if (pos_dev) seq_len = pos_dev[0] + 1u;
     const uint32_t s0 = chunk * kChunk;
+    if (s0 >= seq_len) return;  // chunk past the current sequence (grid sized for the maximum)
     const uint32_t valid = min(kChunk, seq_len - s0);
 
     for (uint32_t i = t; i < group * hd; i += 256u) qs[i] = q[(uint64_t)kvh * group * hd + i];
@@ -110,9 +114,11 @@ __global__ __launch_bounds__(256) void k_attn_partial(const float *__restrict__ 
 
 __global__ __launch_bounds__(256) void k_attn_combine(const float *__restrict__ part,
                                                       float *__restrict__ out, uint32_t hd,
-                                                      uint32_t n_chunks) {
+                                                      uint32_t n_chunks, const uint32_t *pos_dev) {
     const uint32_t h = blockIdx.x;
-    const float *ph = part + (uint64_t)h * n_chunks * (hd + 2u);
+    const uint32_t stride = n_chunks;  // partial rows are laid out for the full grid
+    if (pos_dev) n_chunks = (pos_dev[0] + kChunk) / kChunk;  // chunks of seq_len = pos + 1
+    const float *ph = part + (uint64_t)h * stride * (hd + 2u);
     float M = -INFINITY;
     for (uint32_t c = 0; c < n_chunks; c++) M = fmaxf(M, ph[(uint64_t)c * (hd + 2u)]);
     float l = 0.f;
@@ -131,24 +137,30 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float *__restrict__ 
     }
 }
 
+size_t attention_partial_bytes(uint32_t max_seq, uint32_t nqh, uint32_t hd) {
+    return (size_t)nqh * ((max_seq + kChunk - 1u) / kChunk) * (hd + 2u) * sizeof(float);
+}
+
 hipError_t launch_attention(const float *q, const uint16_t *kc, const uint16_t *vc, float *out,
-                            uint32_t seq_len, uint64_t layer_off, uint32_t nqh, uint32_t nkh,
-                            uint32_t hd, float scale, hipStream_t s) {
+                            uint32_t seq_len, const uint32_t *pos_dev, float *part,
+                            uint64_t layer_off, uint32_t nqh, uint32_t nkh, uint32_t hd,
+                            float scale, hipStream_t s) {
     if (seq_len == 0 || nkh == 0 || nqh % nkh != 0 || hd == 0 || hd > 256 || (hd & 1u))
         return hipErrorInvalidValue;
     uint32_t group = nqh / nkh;
     if (group > kMaxGroup) return hipErrorInvalidValue;
+    // with pos_dev, seq_len is the largest sequence the grid must cover
     uint32_t n_chunks = (seq_len + kChunk - 1u) / kChunk;
-    float *part = (float *)scratch((size_t)nqh * n_chunks * (hd + 2u) * sizeof(float), s);
+    if (!part) part = (float *)scratch(attention_partial_bytes(seq_len, nqh, hd), s);
     if (!part) return hipErrorOutOfMemory;
     size_t lds = ((size_t)group * hd + (size_t)group * kChunk + (size_t)(256u / hd) * group * hd) *
                  sizeof(float);
     dim3 grid(n_chunks, nkh);
-    k_attn_partial<<<grid, 256, lds, s>>>(q, kc, vc, part, seq_len, layer_off, nkh, hd, group,
-                                          scale, n_chunks);
+    k_attn_partial<<<grid, 256, lds, s>>>(q, kc, vc, part, seq_len, pos_dev, layer_off, nkh, hd,
+                                          group, scale, n_chunks);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    k_attn_combine<<<nqh, hd < 256u ? hd : 256u, 0, s>>>(part, out, hd, n_chunks);
+    k_attn_combine<<<nqh, hd < 256u ? hd : 256u, 0, s>>>(part, out, hd, n_chunks, pos_dev);
     return hipGetLastError();
 }
 

@@ -4,6 +4,7 @@
  * convention A (weight_stage == NULL, zero offsets, no accumulate), and
  * primitives pass the canonical argument order with the same scalars. */
 #include "vbs_decode.h"
+#include "vbs_gfx950.h"
 
 #include <math.h>
 #include <stdio.h>
@@ -27,6 +28,10 @@ struct vbs_decode {
     uint64_t weight_bytes;
     float *host_logits;
     int ok;
+    /* device-pointer view for the graph decoder */
+    const float **view_attn_norm, **view_ffn_norm;
+    const void **view_w;
+    int *view_wtype;
 };
 
 static uint64_t row_bytes(int type, uint32_t cols) {
@@ -91,6 +96,10 @@ void vbs_decode_destroy(vbs_decode_t *d) {
     free(d->attn_norm);
     free(d->ffn_norm);
     free(d->w);
+    free(d->view_attn_norm);
+    free(d->view_ffn_norm);
+    free(d->view_w);
+    free(d->view_wtype);
     free(d->host_logits);
     free(d);
 }
@@ -339,5 +348,50 @@ int vbs_decode_greedy(vbs_decode_t *d, uint32_t token, uint32_t pos, uint32_t n,
         if (margins_out) margins_out[i] = bv - second;
         token = best;
     }
+    return 1;
+}
+
+int vbs_decode_device_model(vbs_decode_t *d, void *out) {
+    if (!d || !out) return 0;
+    vbs_gfx950_model_t *v = (vbs_gfx950_model_t *)out;
+    const vbs_decode_model_t *m = &d->m;
+    uint32_t L = m->n_layers;
+    if (!d->view_w) {
+        d->view_attn_norm = (const float **)calloc(L, sizeof(void *));
+        d->view_ffn_norm = (const float **)calloc(L, sizeof(void *));
+        d->view_w = (const void **)calloc((size_t)7 * L, sizeof(void *));
+        d->view_wtype = (int *)calloc((size_t)7 * L, sizeof(int));
+        if (!d->view_attn_norm || !d->view_ffn_norm || !d->view_w || !d->view_wtype) return 0;
+        for (uint32_t i = 0; i < L; i++) {
+            d->view_attn_norm[i] = (const float *)d->attn_norm[i]->internal_handle;
+            d->view_ffn_norm[i] = (const float *)d->ffn_norm[i]->internal_handle;
+        }
+        for (uint32_t i = 0; i < 7 * L; i++) {
+            d->view_w[i] = d->w[i]->internal_handle;
+            d->view_wtype[i] = m->wtype[i];
+        }
+    }
+    memset(v, 0, sizeof(*v));
+    v->n_layers = L;
+    v->hidden = m->hidden;
+    v->ffn = m->ffn;
+    v->n_heads = m->n_heads;
+    v->n_kv_heads = m->n_kv_heads;
+    v->head_dim = m->head_dim;
+    v->vocab = m->vocab;
+    v->max_ctx = m->max_ctx;
+    v->rope_theta = m->rope_theta;
+    v->rms_eps = m->rms_eps;
+    v->embd_type = m->embd_type;
+    v->tok_embd = d->tok_embd->internal_handle;
+    v->out_norm = (const float *)d->out_norm->internal_handle;
+    v->head_type = m->head_type;
+    v->lm_head = d->lm_head->internal_handle;
+    v->attn_norm = d->view_attn_norm;
+    v->ffn_norm = d->view_ffn_norm;
+    v->wtype = d->view_wtype;
+    v->wdata = d->view_w;
+    v->kc = (uint16_t *)d->kc->internal_handle;
+    v->vc = (uint16_t *)d->vc->internal_handle;
     return 1;
 }

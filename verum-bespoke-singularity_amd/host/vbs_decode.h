@@ -67,6 +67,11 @@ uint32_t vbs_decode_dispatch_count(const vbs_decode_t *d);
 /* Total bytes of weights resident on the device. */
 uint64_t vbs_decode_weight_bytes(const vbs_decode_t *d);
 
+/* Device-side view of the uploaded model (weights, norms and KV caches as
+ * device pointers) for the gfx950 graph decoder, vbs_gfx950_decoder_create
+ * (include/vbs_gfx950.h). Valid while `d` lives. */
+int vbs_decode_device_model(vbs_decode_t *d, void *out_vbs_gfx950_model_t);
+
 #ifdef __cplusplus
 }
 #endif

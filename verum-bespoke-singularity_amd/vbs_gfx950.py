@@ -83,6 +83,10 @@ _DEVICE_SIGS = {
     "dequant_rows": (_I, [_I, _P, _P, _U32, _U32, _P]),
     "linear_batch": (_I, [_I, _P, _P, _U32, _P, _U32, _U32, _U32, _U32]),
     "stream": (_P, []),
+    "decoder_create": (_I, [_P, _U32, C.POINTER(C.c_void_p)]),
+    "decoder_step": (_I, [_P, _U32, _U32, _P]),
+    "decoder_greedy": (_I, [_P, _U32, _U32, _U32, _P, _P]),
+    "decoder_destroy": (_I, [_P]),
 }
 
 DEVICE_SYMBOLS = ["vbs_gfx950_" + k for k in _DEVICE_SIGS]
@@ -311,6 +315,7 @@ def load_host() -> C.CDLL:
     lib.vbs_decode_dispatch_count.argtypes = [C.c_void_p]
     lib.vbs_decode_weight_bytes.restype = C.c_uint64
     lib.vbs_decode_weight_bytes.argtypes = [C.c_void_p]
+    lib.vbs_decode_device_model.argtypes = [C.c_void_p, C.c_void_p]
     return lib
 
 
@@ -469,4 +474,54 @@ class Decoder:
     def close(self):
         if self.h:
             self.host.vbs_decode_destroy(self.h)
+            self.h = None
+
+
+class Gfx950ModelStruct(C.Structure):
+    """vbs_gfx950_model_t (include/vbs_gfx950.h)."""
+    _fields_ = [("n_layers", C.c_uint32), ("hidden", C.c_uint32), ("ffn", C.c_uint32),
+                ("n_heads", C.c_uint32), ("n_kv_heads", C.c_uint32), ("head_dim", C.c_uint32),
+                ("vocab", C.c_uint32), ("max_ctx", C.c_uint32),
+                ("rope_theta", C.c_float), ("rms_eps", C.c_float),
+                ("embd_type", C.c_int), ("tok_embd", C.c_void_p), ("out_norm", C.c_void_p),
+                ("head_type", C.c_int), ("lm_head", C.c_void_p),
+                ("attn_norm", C.c_void_p), ("ffn_norm", C.c_void_p),
+                ("wtype", C.c_void_p), ("wdata", C.c_void_p),
+                ("kc", C.c_void_p), ("vc", C.c_void_p)]
+
+
+class GraphDecoder:
+    """vbs_gfx950_decoder over the device memory a Decoder uploaded.
+
+    Shares the Decoder's weights and KV caches: both paths write the same
+    cache rows, so a test may drive one and check the other's state."""
+
+    def __init__(self, dev: DeviceLib, decoder: Decoder, max_steps: int = 256):
+        self.dev, self.decoder = dev, decoder
+        self.vocab = decoder.model.cfg["vocab"]
+        self._view = Gfx950ModelStruct()
+        if not decoder.host.vbs_decode_device_model(decoder.h, C.addressof(self._view)):
+            raise GpuError("vbs_decode_device_model failed")
+        h = C.c_void_p()
+        dev.check(dev._decoder_create(C.addressof(self._view), max_steps, C.byref(h)),
+                  "decoder_create")
+        self.h = h.value
+
+    def step(self, token: int, pos: int, want_logits=True):
+        out = np.empty(self.vocab, np.float32) if want_logits else None
+        self.dev.check(self.dev._decoder_step(self.h, token, pos,
+                                              out.ctypes.data if want_logits else None),
+                       "decoder_step")
+        return out
+
+    def greedy(self, token: int, pos: int, n: int):
+        toks = np.empty(n, np.uint32)
+        margins = np.empty(n, np.float32)
+        self.dev.check(self.dev._decoder_greedy(self.h, token, pos, n, toks.ctypes.data,
+                                                margins.ctypes.data), "decoder_greedy")
+        return toks, margins
+
+    def close(self):
+        if self.h:
+            self.dev._decoder_destroy(self.h)
             self.h = None
