@@ -332,7 +332,7 @@ def main():
         "pct_of_peak": round(100 * value / PEAK_HBM_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
-                     "kernel": "k_q4k_mv, 11008x4096 and 4096x11008",
+                     "kernel": "k_mv<Q4K> (matrix-core Q4_K matvec), 11008x4096 and 4096x11008",
                      "algorithmic_bytes_per_launch": r["big_bytes"],
                      "avg_launch_us": round(1e3 * r["avg_big_ms"], 3)},
         "gpu_event_ms_per_step": round(r["gpu_ms"] / a.steps, 4),

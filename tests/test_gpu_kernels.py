@@ -263,6 +263,11 @@ def test_add_in_place(dev, host, oracle, mem):
     (32, 8, 128, 2049, 2176, 3),
     (64, 8, 128, 1000, 1024, 1),
     (8, 8, 64, 130, 200, 0),
+    (64, 8, 128, 8192, 8200, 0),   # 70B shape at the config-5 context
+    (16, 1, 256, 300, 512, 0),     # group 16, head_dim 256 (LDS above 64 KiB)
+    (4, 4, 128, 1, 8, 2),          # one position
+    (3, 1, 64, 65, 70, 0),         # group 3; last chunk holds one position
+    (6, 2, 96, 100, 128, 0),       # head_dim 96: generic two-kernel path
 ])
 def test_attention(dev, host, oracle, mem, nqh, nkh, hd, seq, max_ctx, layer):
     layers = layer + 1

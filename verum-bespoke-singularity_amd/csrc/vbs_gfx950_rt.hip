@@ -24,6 +24,8 @@ struct Runtime {
     char name[128] = {0};
     void *scratch = nullptr;
     size_t scratch_bytes = 0;
+    uint32_t *counters = nullptr;  // zeroed once; kernels that use one leave it at 0
+    uint8_t *xq = nullptr;         // x in digit form for the matrix-core matvecs
 };
 
 Runtime g_rt;
@@ -99,6 +101,10 @@ void *scratch(size_t bytes, hipStream_t s) {
 
 hipStream_t rt_stream() { return g_rt.stream; }
 
+uint32_t *rt_counters() { return g_rt.counters; }
+
+uint8_t *rt_xq() { return g_rt.xq; }
+
 int rt_fail(const char *fmt, ...) {
     va_list ap;
     va_start(ap, fmt);
@@ -142,6 +148,11 @@ int vbs_gfx950_init(void) {
     if (chosen < 0) return fail("no gfx950 (MI355X) device among %d visible GPUs", count);
     if (!hip_ok(hipSetDevice(chosen), "hipSetDevice")) return 0;
     if (!hip_ok(hipStreamCreateWithFlags(&g_rt.stream, hipStreamNonBlocking), "hipStreamCreate"))
+        return 0;
+    if (!hip_ok(hipMalloc(&g_rt.counters, kCounterSlots * sizeof(uint32_t)), "hipMalloc(counters)") ||
+        !hip_ok(hipMemset(g_rt.counters, 0, kCounterSlots * sizeof(uint32_t)), "hipMemset(counters)") ||
+        !hip_ok(hipMalloc(&g_rt.xq, xq_bytes(kXqMaxCols)), "hipMalloc(xq)") ||
+        !hip_ok(hipDeviceSynchronize(), "init"))
         return 0;
     g_rt.device = chosen;
     g_rt.ready = true;

@@ -20,9 +20,27 @@ void *scratch(size_t bytes, hipStream_t s);
 
 // The library's stream, and the last-error writer of the C ABI.
 hipStream_t rt_stream();
+// kCounterSlots arrival counters, zeroed at init. A kernel that counts
+// finished workgroups in one resets it to zero before it exits, so the
+// slots are zero between launches (the library has one in-order stream).
+constexpr uint32_t kCounterSlots = 1024;
+uint32_t *rt_counters();
 int rt_fail(const char *fmt, ...);
 int rt_hip_ok(hipError_t e, const char *what);
 bool rt_ready();
+
+// x in digit form for the matrix-core matvecs: bytes needed for `cols`, and
+// the runtime's buffer (sized for kXqMaxCols, allocated at init).
+constexpr uint32_t kXqMaxCols = 65536;
+size_t xq_bytes(uint32_t cols);
+uint8_t *rt_xq();
+hipError_t launch_xprep(const float *x, uint32_t cols, uint8_t *xq, hipStream_t s);
+// Q4_K / Q6_K matvec on the matrix cores (x is prepared inside the kernel);
+// hipErrorNotSupported outside their range.
+hipError_t launch_q4k_mfma(const uint8_t *w, const float *x, float *y, uint32_t cols,
+                           uint32_t rows, int accumulate, hipStream_t s);
+hipError_t launch_q6k_mfma(const uint8_t *w, const float *x, float *y, uint32_t cols,
+                           uint32_t rows, int accumulate, hipStream_t s);
 
 // Specialised Q4_K matvec; hipErrorNotSupported when the shape/alignment is
 // outside its range (the generic kernel then runs).

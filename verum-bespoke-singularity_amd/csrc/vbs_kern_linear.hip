@@ -168,7 +168,13 @@ hipError_t launch_linear(int type, const uint8_t *w, const float *x, float *y, u
                          uint32_t rows, int accumulate, hipStream_t s) {
     if (rows == 0) return hipSuccess;
     if (type == kQ4_K) {
-        hipError_t e = launch_q4k_fast(w, x, y, cols, rows, accumulate, s);
+        hipError_t e = launch_q4k_mfma(w, x, y, cols, rows, accumulate, s);
+        if (e != hipErrorNotSupported) return e;
+        e = launch_q4k_fast(w, x, y, cols, rows, accumulate, s);
+        if (e != hipErrorNotSupported) return e;
+    }
+    if (type == kQ6_K) {
+        hipError_t e = launch_q6k_mfma(w, x, y, cols, rows, accumulate, s);
         if (e != hipErrorNotSupported) return e;
     }
     uint64_t rb = row_bytes(type, cols);

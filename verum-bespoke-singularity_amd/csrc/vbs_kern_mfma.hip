@@ -1,0 +1,502 @@
+// vbs_kern_mfma.hip — batch-1 K-quant matvec on the gfx950 matrix cores.
+//
+// y[r] (+)= sum_c deq(W[r,c]) * x[c] with W in native GGUF super-blocks
+// (src/vbs_dequant.c:225-277 for Q4_K, 316-333 for Q6_K); the reference's
+// linear is vbs_host_linear_tile (src/vbs_host_math.h:223-267).
+//
+// x in digit form: every 32-element sub-block j of x gets an exponent e_j with
+// 2^e_j > max|x| over the sub-block, and each element becomes the integer
+// X = rint(x * 2^(22 - e_j)) (|X| <= 2^22), split into three balanced signed
+// bytes X = D0 + 2^8 D1 + 2^16 D2. A dot of quantised weights with x is then
+// an exact integer dot per digit plane, scaled back by 2^(e_j - 22): x is
+// represented to 2^-22 of its sub-block maximum, which keeps each row within
+// ~1e-7 of the reference's double-accumulated result.
+//
+// The three digit planes make the batch-1 matvec a skinny integer GEMM, which
+// is what v_mfma_i32_16x16x64_i8 computes: A (16 x 64) holds digit planes of
+// x, B (64 x 16) the unpacked quants of 16 weight rows, and D (16 x 16) gets,
+// per row, one integer dot per (scale group, plane). Operand layout: lane l
+// holds A[l%16][ks(l/16, b)] and B[ks(l/16, b)][l%16] for its 16 bytes b, and
+// D[4(l/16)+r][l%16] for r < 4 (checked on the device with a one-hot probe).
+// A row 4t+p carries plane p of scale group t at exactly the lanes whose B
+// bytes belong to group t, so lane (n, g) = (l%16, l/16) of D receives the
+// three plane dots of group g of row n. A rows of other groups are zero (read
+// from a 16-byte zero pad).
+//
+// Work split. A workgroup owns TPW tiles of 16 rows; its waves split each row
+// into slices of KS super-blocks and add their partial sums in LDS. Every
+// thread first loads its part of x (so that preparing x does not wait behind
+// the weight stream: loads return in order), then every weight load of all
+// TPW tiles is issued, then x is turned into digits in LDS, once per
+// workgroup, while the weights arrive.
+//
+// Q4_K (144-byte blocks). Lane (n, g) reads the 16-byte header of row n and 16
+// bytes of nibbles at qs offsets 16g and 64 + 16g. qs bytes 32s..32s+31 hold
+// sub-block 2s in their low and 2s+1 in their high nibbles; per 64-byte span
+// one MFMA takes the low and one the high nibbles, accumulating into one D in
+// which group g is sub-block 4*span + g. Value per sub-block, as the
+// reference's d*sc*nib - dmin*m summed: d*sc*2^(e-22)*S - dmin*m*sum(x).
+//
+// Q6_K (210-byte blocks, 6-bit quants, 16-element int8 scales). Lane group
+// g = (h, u) covers elements 16u..16u+15 of every 32-element quarter of half h
+// of the block: it reads the ql bytes of quarters 0/2 and 1/3 and the qh bytes
+// of those elements, plus the 16 scales and d. MFMA q in 0..3 takes quarter q
+// of both halves, so every shift in the 6-bit unpack is the same for all
+// lanes, and lane group g holds scale group 8h + 2q + u. Value per group, as
+// d*sc*(q - 32) summed: d*sc*(2^(e-22)*S - 32*sum16(x)).
+#include "vbs_dev_common.h"
+#include "vbs_internal.h"
+
+namespace vbs {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// ---- digit buffer ---------------------------------------------------------------
+// [3][cols] int8 planes | 16 zero bytes | float2 xs[cols/32] = {2^(e-22), sum x}
+// | float xs16[cols/16] = sum of x per 16 elements.
+struct XqLayout {
+    uint32_t zero, xs, xs16, bytes;
+};
+__host__ __device__ inline XqLayout xq_layout(uint32_t cols) {
+    XqLayout L;
+    L.zero = 3u * cols;
+    L.xs = (L.zero + 16u + 15u) & ~15u;
+    L.xs16 = L.xs + 8u * (cols / 32u);
+    L.bytes = L.xs16 + 4u * (cols / 16u);
+    return L;
+}
+
+size_t xq_bytes(uint32_t cols) { return (size_t)xq_layout(cols).bytes; }
+
+__device__ __forceinline__ uint32_t pack4b(int a, int b, int c, int d) {
+    return (uint32_t)(a & 255) | ((uint32_t)(b & 255) << 8) | ((uint32_t)(c & 255) << 16) |
+           ((uint32_t)d << 24);
+}
+
+// Digits of one 16-element half sub-block `item` (values in v); the two halves
+// of a sub-block are adjacent lanes and exchange their maximum and sum. Writes
+// the three planes, xs (by the even half) and xs16 into `xq` (LDS or global).
+__device__ __forceinline__ void prep_item(const float *v, uint32_t cols, uint32_t item,
+                                          uint8_t *xq, const XqLayout &L) {
+    const bool valid = item < cols / 16u;
+    float amax = 0.f, sum = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+        amax = fmaxf(amax, fabsf(v[k]));
+        sum += v[k];
+    }
+    const uint32_t h = item & 1u;
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    const float other = __shfl_xor(sum, 1, 64);
+    const float sum32 = h ? other + sum : sum + other;  // same order in both lanes
+    if (!valid) return;
+    int e;
+    (void)frexpf(amax, &e);  // amax < 2^e
+    const bool finite = amax <= 3.4028235e38f;
+    uint32_t d0[4], d1[4], d2[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        int D0[4], D1[4], D2[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int X = finite ? __float2int_rn(ldexpf(v[4 * q + k], 22 - e)) : 0;
+            const int a = (int)(int8_t)X;
+            const int X1 = (X - a) >> 8;
+            const int c = (int)(int8_t)X1;
+            D0[k] = a;
+            D1[k] = c;
+            D2[k] = (X1 - c) >> 8;
+        }
+        d0[q] = pack4b(D0[0], D0[1], D0[2], D0[3]);
+        d1[q] = pack4b(D1[0], D1[1], D1[2], D1[3]);
+        d2[q] = pack4b(D2[0], D2[1], D2[2], D2[3]);
+    }
+    const uint32_t off = item * 16u;
+    *reinterpret_cast<uint4 *>(xq + off) = make_uint4(d0[0], d0[1], d0[2], d0[3]);
+    *reinterpret_cast<uint4 *>(xq + cols + off) = make_uint4(d1[0], d1[1], d1[2], d1[3]);
+    *reinterpret_cast<uint4 *>(xq + 2u * cols + off) = make_uint4(d2[0], d2[1], d2[2], d2[3]);
+    reinterpret_cast<float *>(xq + L.xs16)[item] = sum;
+    if (h == 0)
+        reinterpret_cast<float2 *>(xq + L.xs)[item >> 1] =
+            make_float2(finite ? ldexpf(1.0f, e - 22) : __builtin_nanf(""), sum32);
+}
+
+// 16 elements of x for `item` (items past the end read item 0 and are not used).
+__device__ __forceinline__ void load16(const float *x, uint32_t cols, uint32_t item, float *v) {
+    const float *xp = x + (item < cols / 16u ? item * 16u : 0u);
+#pragma unroll
+    for (int k = 0; k < 16; k++) v[k] = xp[k];
+}
+
+// x -> digits in global memory (for callers that keep x in digit form).
+__global__ __launch_bounds__(256) void k_xprep(const float *__restrict__ x, uint32_t cols,
+                                               uint8_t *__restrict__ xq) {
+    const uint32_t item = blockIdx.x * 256u + threadIdx.x;
+    const XqLayout L = xq_layout(cols);
+    float v[16];
+    load16(x, cols, item, v);
+    if (item == 0) *reinterpret_cast<uint4 *>(xq + L.zero) = make_uint4(0, 0, 0, 0);
+    prep_item(v, cols, item, xq, L);
+}
+
+hipError_t launch_xprep(const float *x, uint32_t cols, uint8_t *xq, hipStream_t s) {
+    const uint32_t items = cols / 16u;
+    k_xprep<<<(items + 255u) / 256u, 256, 0, s>>>(x, cols, xq);
+    return hipGetLastError();
+}
+
+// ---- helpers ------------------------------------------------------------------------
+// 16 bytes from a 16-byte aligned address.
+__device__ __forceinline__ u32x4 lda4(const uint8_t *p) {
+    return *reinterpret_cast<const u32x4 *>(p);
+}
+// 16 bytes from a 2-byte aligned address (used on LDS).
+__device__ __forceinline__ u32x4 ldu(const uint8_t *p) {
+    typedef u32x4 __attribute__((aligned(2))) u32x4u;
+    return *reinterpret_cast<const u32x4u *>(p);
+}
+__device__ __forceinline__ i32x4 lda(const uint8_t *p) {
+    return *reinterpret_cast<const i32x4 *>(p);
+}
+__device__ __forceinline__ float cvt_h(uint32_t bits16) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}
+__device__ __forceinline__ uint32_t bfe(uint32_t v, uint32_t off, uint32_t w) {
+    return __builtin_amdgcn_ubfe(v, off, w);
+}
+__device__ __forceinline__ i32x4 mfma(i32x4 a, i32x4 b, i32x4 c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+// The three plane dots combined, exact up to one rounding (|D0 + 256 D1| < 2^24).
+__device__ __forceinline__ float plane_sum(i32x4 D) {
+    return fmaf((float)D[2], 65536.f, (float)(D[0] + D[1] * 256));
+}
+
+// ---- weight types ---------------------------------------------------------------------
+// Where a wave's tile lives: row r of the matrix starts at w + r * rb; rows of
+// the tile past the end re-read the last row; w_end bounds every load.
+struct Src {
+    const uint8_t *w, *w_end;
+    uint64_t rb;
+    uint32_t row0, rows;
+    __device__ const uint8_t *row(uint32_t n) const {
+        return w + (uint64_t)min(row0 + n, rows - 1u) * rb;
+    }
+};
+
+// load(): this lane's share of block b of the tile (NLD 16-byte words).
+// dot(): the block's contribution to the lane's row partial sum; (n, g) is the
+// lane as MFMA operand (A row n, lane group g); `scratch` is the wave's LDS.
+struct Q4K {
+    static constexpr uint32_t BYTES = 144, NLD = 3, SCRATCH = 0;
+    __device__ static void load(const Src &src, uint32_t b, uint32_t n, uint32_t g, u32x4 *r) {
+        const uint8_t *blk = src.row(n) + (uint64_t)b * BYTES;
+        r[0] = lda4(blk);
+        r[1] = lda4(blk + 16u + 16u * g);
+        r[2] = lda4(blk + 80u + 16u * g);
+    }
+    __device__ static float dot(const u32x4 *r, uint8_t *, const Src &, const uint8_t *xq,
+                                const XqLayout &L, uint32_t cols, uint32_t b, uint32_t n,
+                                uint32_t g) {
+        // A row n = 4t+p: lane group g carries sub-blocks 2(g>>1) (low nibbles,
+        // t even) and 2(g>>1)+1 (high nibbles, t odd) at element offset 16(g&1)
+        const uint32_t t = n >> 2, p = n & 3u;
+        const bool on = p < 3u && (g >> 1) == (t >> 1);
+        const uint32_t ao = p * cols + 256u * b + 32u * t + 16u * (g & 1u);
+        const i32x4 A0l = lda(xq + (on && !(t & 1u) ? ao : L.zero));
+        const i32x4 A0h = lda(xq + (on && (t & 1u) ? ao : L.zero));
+        const i32x4 A1l = lda(xq + (on && !(t & 1u) ? ao + 128u : L.zero));
+        const i32x4 A1h = lda(xq + (on && (t & 1u) ? ao + 128u : L.zero));
+        const uint32_t M4 = 0x0F0F0F0Fu;
+        const u32x4 qa = r[1], qb = r[2];
+        const i32x4 B0l = {(int)(qa.x & M4), (int)(qa.y & M4), (int)(qa.z & M4), (int)(qa.w & M4)};
+        const i32x4 B0h = {(int)((qa.x >> 4) & M4), (int)((qa.y >> 4) & M4),
+                           (int)((qa.z >> 4) & M4), (int)((qa.w >> 4) & M4)};
+        const i32x4 B1l = {(int)(qb.x & M4), (int)(qb.y & M4), (int)(qb.z & M4), (int)(qb.w & M4)};
+        const i32x4 B1h = {(int)((qb.x >> 4) & M4), (int)((qb.y >> 4) & M4),
+                           (int)((qb.z >> 4) & M4), (int)((qb.w >> 4) & M4)};
+        const i32x4 z = {0, 0, 0, 0};
+        const float S0 = plane_sum(mfma(A0h, B0h, mfma(A0l, B0l, z)));
+        const float S1 = plane_sum(mfma(A1h, B1h, mfma(A1l, B1l, z)));
+        // D group g: sub-blocks g (span 0) and 4 + g (span 1); scales and mins
+        // as src/vbs_dequant.c:225-233
+        const float2 *xs = reinterpret_cast<const float2 *>(xq + L.xs);
+        const float2 xs0 = xs[8u * b + g], xs1 = xs[8u * b + 4u + g];
+        const u32x4 hd = r[0];
+        const uint32_t sh = 8u * g;
+        const uint32_t sc0 = bfe(hd.y, sh, 6), m0 = bfe(hd.z, sh, 6);
+        const uint32_t sc1 = bfe(hd.w, sh, 4) | (bfe(hd.y, sh + 6u, 2) << 4);
+        const uint32_t m1 = bfe(hd.w, sh + 4u, 4) | (bfe(hd.z, sh + 6u, 2) << 4);
+        const float d = cvt_h(hd.x & 0xFFFFu), dmin = cvt_h(hd.x >> 16);
+        const float sd = fmaf((float)sc0 * xs0.x, S0, (float)sc1 * xs1.x * S1);
+        const float sm = fmaf((float)m0, xs0.y, (float)m1 * xs1.y);
+        return fmaf(d, sd, -dmin * sm);
+    }
+};
+
+// 16 aligned bytes at a, of which only those below `end` (2-byte aligned) are
+// read; the rest are zero.
+__device__ __noinline__ u32x4 ld_tail(const uint8_t *a, const uint8_t *end) {
+    uint32_t v[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const uint8_t *p = a + 4 * k;
+        v[k] = p + 4 <= end   ? *reinterpret_cast<const uint32_t *>(p)
+               : p + 2 <= end ? (uint32_t)*reinterpret_cast<const uint16_t *>(p)
+                              : 0u;
+    }
+    const u32x4 r = {v[0], v[1], v[2], v[3]};
+    return r;
+}
+
+struct Q6K {
+    // A 210-byte block is 2-byte aligned, and 16-byte loads at such addresses
+    // run at about half the rate of aligned ones. So the wave reads each block
+    // of its 16 rows as 14 aligned 16-byte chunks per row (covering the block
+    // at any 2-byte offset), chunk c = 14n + k going to lane c mod 64, stores
+    // them to its LDS scratch in row order and reads its fields from there.
+    static constexpr uint32_t BYTES = 210, NLD = 4, SCRATCH = 16u * 224u;
+    __device__ static void load(const Src &src, uint32_t b, uint32_t n, uint32_t g, u32x4 *r) {
+        const uint32_t lane = 16u * g + n;
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++) {
+            const uint32_t c = lane + 64u * i;
+            if (i < 3u || c < 224u) {
+                const uint8_t *s = src.row(c / 14u) + (uint64_t)b * BYTES;
+                const uint8_t *a = reinterpret_cast<const uint8_t *>(
+                    ((uintptr_t)s & ~(uintptr_t)15) + 16u * (c % 14u));
+                r[i] = a + 16 <= src.w_end ? lda4(a) : ld_tail(a, src.w_end);
+            } else {
+                r[i] = u32x4{0u, 0u, 0u, 0u};
+            }
+        }
+    }
+    __device__ static float dot(const u32x4 *r, uint8_t *scratch, const Src &src,
+                                const uint8_t *xq, const XqLayout &L, uint32_t cols, uint32_t b,
+                                uint32_t n, uint32_t g) {
+        const uint32_t lane = 16u * g + n;
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++) {
+            const uint32_t c = lane + 64u * i;
+            if (i < 3u || c < 224u) *reinterpret_cast<u32x4 *>(scratch + 16u * c) = r[i];
+        }
+        // row n's block starts (its address mod 16) into its 224 scratch bytes
+        const uint8_t *blk = scratch + 224u * n +
+                             (uint32_t)((uintptr_t)(src.row(n) + (uint64_t)b * BYTES) & 15u);
+        // lane group g = (h, u) = (g >> 1, g & 1): half h of the block, elements
+        // 16u..16u+15 of each of its 32-element quarters
+        const uint32_t h = g >> 1, u = g & 1u;
+        const u32x4 qe = ldu(blk + 64u * h + 16u * u);         // ql, quarters 0 / 2
+        const u32x4 qo = ldu(blk + 64u * h + 32u + 16u * u);   // ql, quarters 1 / 3
+        const u32x4 qh = ldu(blk + 128u + 32u * h + 16u * u);  // qh, 2 bits per quarter
+        const u32x4 scw = ldu(blk + 192u);                     // int8 scales
+        const uint32_t dbits = *reinterpret_cast<const uint16_t *>(blk + 208u);
+        // MFMA q (quarter q of both halves): lane group g holds scale group
+        // 8h + 2q + u; A row n = 4t+p carries plane p of the group of lane group t
+        const uint32_t t = n >> 2, p = n & 3u;
+        const bool on = p < 3u && t == g;
+        const float2 *xs = reinterpret_cast<const float2 *>(xq + L.xs);
+        const float *xs16 = reinterpret_cast<const float *>(xq + L.xs16);
+        const uint32_t qew[4] = {qe.x, qe.y, qe.z, qe.w}, qow[4] = {qo.x, qo.y, qo.z, qo.w};
+        const uint32_t qhw[4] = {qh.x, qh.y, qh.z, qh.w};
+        const uint32_t sc_lo = h ? scw.z : scw.x, sc_hi = h ? scw.w : scw.y;
+        const uint32_t a0 = p * cols + 256u * b + 128u * (t >> 1) + 16u * (t & 1u);
+        float acc = 0.f;
+#pragma unroll
+        for (uint32_t q = 0; q < 4; q++) {
+            // 6-bit quants, src/vbs_dequant.c:316-333: low 4 bits from ql
+            // (nibble q >> 1 of region q & 1), high 2 bits from qh bits 2q
+            const uint32_t *ql = (q & 1u) ? qow : qew;
+            int bw[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint32_t hi = (q <= 2u ? (qhw[k] << (4u - 2u * q)) : (qhw[k] >> 2u)) &
+                                    0x30303030u;
+                bw[k] = (int)(((ql[k] >> (4u * (q >> 1))) & 0x0F0F0F0Fu) | hi);
+            }
+            const i32x4 B = {bw[0], bw[1], bw[2], bw[3]};
+            const i32x4 A = lda(xq + (on ? a0 + 32u * q : L.zero));
+            const i32x4 z = {0, 0, 0, 0};
+            const float S = plane_sum(mfma(A, B, z));
+            // scale 8h + 2q + u: dword 2h + (q >> 1), byte 2(q & 1) + u; the group
+            // is half u of sub-block 4h + q
+            const uint32_t scd = (q >> 1) ? sc_hi : sc_lo;
+            const float sc = (float)(int)(int8_t)bfe(scd, 16u * (q & 1u) + 8u * u, 8);
+            const uint32_t j = 8u * b + 4u * h + q;
+            acc = fmaf(sc, fmaf(xs[j].x, S, -32.f * xs16[2u * j + u]), acc);
+        }
+        return cvt_h(dbits) * acc;
+    }
+};
+
+// ---- the kernel -------------------------------------------------------------------------
+template <class T, uint32_t KS, uint32_t TPW, uint32_t MAXT, bool ACC>
+__global__ __launch_bounds__(MAXT) void k_mv(const uint8_t *__restrict__ w,
+                                             const float *__restrict__ x,
+                                             float *__restrict__ y, uint32_t cols,
+                                             uint32_t rows) {
+    extern __shared__ __align__(16) uint8_t xq[];
+    __shared__ float red[2][16][16];
+    const uint32_t nblk = cols >> 8;
+    const uint64_t rb = (uint64_t)nblk * T::BYTES;
+    const XqLayout L = xq_layout(cols);
+    const uint32_t nth = blockDim.x;
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const uint32_t nw = nth >> 6;
+    const uint32_t n = lane & 15u, g = lane >> 4;
+    const uint32_t ntiles = (rows + 15u) / 16u;
+    const uint32_t b0 = wave * KS;
+
+    // 1. x first (one or two 16-element items per thread)
+    const uint32_t items = cols / 16u;
+    const uint32_t i0 = threadIdx.x, i1 = threadIdx.x + nth;
+    const bool two = nth < items;
+    float v0[16], v1[16];
+    load16(x, cols, i0, v0);
+    load16(x, cols, two ? i1 : items, v1);
+
+    // 2. every weight load of this wave (tail tiles, rows and blocks re-read
+    // valid data and are masked below)
+    u32x4 r[TPW][KS][T::NLD];
+    const uint32_t tile0 = blockIdx.x * TPW;
+    const uint8_t *w_end = w + (uint64_t)rows * rb;
+#pragma unroll
+    for (uint32_t j = 0; j < TPW; j++) {
+        const Src src{w, w_end, rb, min(tile0 + j, ntiles - 1u) * 16u, rows};
+#pragma unroll
+        for (uint32_t k = 0; k < KS; k++) T::load(src, min(b0 + k, nblk - 1u), n, g, r[j][k]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 3. x -> digits in LDS while the weights arrive
+    prep_item(v0, cols, i0, xq, L);
+    if (two) prep_item(v1, cols, i1, xq, L);
+    if (threadIdx.x == 0) *reinterpret_cast<uint4 *>(xq + L.zero) = make_uint4(0, 0, 0, 0);
+    __syncthreads();
+
+    // 4. tiles
+    uint8_t *scratch = xq + L.bytes + wave * T::SCRATCH;
+#pragma unroll
+    for (uint32_t j = 0; j < TPW; j++) {
+        float acc = 0.f;
+#pragma unroll
+        for (uint32_t k = 0; k < KS; k++) {
+            const bool live = b0 + k < nblk;  // slots past the row contribute zero
+            const Src src{w, w_end, rb, min(tile0 + j, ntiles - 1u) * 16u, rows};
+            const float part = T::dot(r[j][k], scratch, src, xq, L, cols,
+                                      min(b0 + k, nblk - 1u), n, g);
+            acc += live ? part : 0.f;
+        }
+        // the four lane groups of a row hold different groups of its blocks
+        acc += __shfl_xor(acc, 16, 64);
+        acc += __shfl_xor(acc, 32, 64);
+        const uint32_t row = (tile0 + j) * 16u + n;
+        if (nw == 1) {
+            if (lane < 16u && row < rows) y[row] = ACC ? y[row] + acc : acc;
+            continue;
+        }
+        if (lane < 16u) red[j & 1u][wave][n] = acc;
+        __syncthreads();
+        if (wave == 0 && lane < 16u && row < rows) {
+            float t = 0.f;
+            for (uint32_t k = 0; k < nw; k++) t += red[j & 1u][k][n];
+            y[row] = ACC ? y[row] + t : t;
+        }
+    }
+}
+
+// ---- launch ---------------------------------------------------------------------------
+struct MvPlan {
+    uint32_t ks, tpw, nw;
+};
+
+// Super-blocks per wave and tiles per workgroup (measured on the 7B shapes).
+// Every combination used keeps its loads in registers without spilling:
+// Q4_K two super-blocks x three tiles, three x one; Q6_K two x two only with
+// at most 8 waves (a 256-VGPR budget), else one tile.
+template <class T>
+static MvPlan mv_plan(uint32_t cols, uint32_t rows) {
+    const uint32_t nblk = cols / 256u, tiles = (rows + 15u) / 16u;
+    MvPlan p;
+    p.ks = nblk <= 32u ? 2u : 3u;
+    p.nw = (nblk + p.ks - 1u) / p.ks;
+    p.tpw = 1u;
+    if (tiles > 512u && p.ks == 2u) {
+        if (T::NLD == 3u)
+            p.tpw = tiles <= 1600u ? 3u : 2u;
+        else if (p.nw <= 8u)
+            p.tpw = 2u;
+    }
+    return p;
+}
+
+template <class T, uint32_t KS, uint32_t TPW, uint32_t MAXT>
+static hipError_t launch_mv_t(const uint8_t *w, const float *x, float *y, uint32_t cols,
+                              uint32_t rows, int acc, uint32_t nw, hipStream_t s) {
+    const size_t lds = xq_layout(cols).bytes + (size_t)nw * T::SCRATCH;
+    if (lds > 65536u) {  // beyond the default per-workgroup LDS window: opt in once
+        static size_t granted = 0;
+        if (lds > granted) {
+            const void *f0 = (const void *)k_mv<T, KS, TPW, MAXT, false>;
+            const void *f1 = (const void *)k_mv<T, KS, TPW, MAXT, true>;
+            if (hipFuncSetAttribute(f0, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
+                    hipSuccess ||
+                hipFuncSetAttribute(f1, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
+                    hipSuccess) {
+                (void)hipGetLastError();
+                return hipErrorNotSupported;
+            }
+            granted = lds;
+        }
+    }
+    const uint32_t tiles = (rows + 15u) / 16u;
+    const dim3 grid((tiles + TPW - 1u) / TPW), block(64u * nw);
+    if (acc)
+        k_mv<T, KS, TPW, MAXT, true><<<grid, block, lds, s>>>(w, x, y, cols, rows);
+    else
+        k_mv<T, KS, TPW, MAXT, false><<<grid, block, lds, s>>>(w, x, y, cols, rows);
+    return hipGetLastError();
+}
+
+template <class T>
+static hipError_t launch_mv(const uint8_t *w, const float *x, float *y, uint32_t cols,
+                            uint32_t rows, int acc, hipStream_t s) {
+    const uint32_t nblk = cols / 256u;
+    // at most 16 waves of at most 3 super-blocks; x items fit two per thread
+    if (cols % 256u || rows == 0 || nblk > 48u) return hipErrorNotSupported;
+    // Q4_K rows are 16-byte multiples, so its 16-byte loads need an aligned w;
+    // Q6_K aligns every load itself
+    if (((uintptr_t)x & 3u) || ((uintptr_t)w & (T::SCRATCH ? 1u : 15u))) return hipErrorNotSupported;
+    const MvPlan p = mv_plan<T>(cols, rows);
+    if (p.nw > 16u || cols / 16u > 2u * 64u * p.nw) return hipErrorNotSupported;
+#define VBS_MV(KS, TPW, MAXT) return launch_mv_t<T, KS, TPW, MAXT>(w, x, y, cols, rows, acc, p.nw, s)
+    if (p.ks == 3u) VBS_MV(3, 1, 1024);
+    if (p.tpw == 1u) {
+        if (p.nw <= 8u) VBS_MV(2, 1, 512);
+        VBS_MV(2, 1, 1024);
+    }
+    if constexpr (T::NLD == 3u) {
+        if (p.tpw == 3u) {
+            if (p.nw <= 8u) VBS_MV(2, 3, 512);
+            VBS_MV(2, 3, 1024);
+        }
+        if (p.nw <= 8u) VBS_MV(2, 2, 512);
+        VBS_MV(2, 2, 1024);
+    } else {
+        VBS_MV(2, 2, 512);
+    }
+#undef VBS_MV
+}
+
+hipError_t launch_q4k_mfma(const uint8_t *w, const float *x, float *y, uint32_t cols,
+                           uint32_t rows, int accumulate, hipStream_t s) {
+    return launch_mv<Q4K>(w, x, y, cols, rows, accumulate, s);
+}
+
+hipError_t launch_q6k_mfma(const uint8_t *w, const float *x, float *y, uint32_t cols,
+                           uint32_t rows, int accumulate, hipStream_t s) {
+    return launch_mv<Q6K>(w, x, y, cols, rows, accumulate, s);
+}
+
+}  // namespace vbs
