@@ -4,8 +4,12 @@
 // with the bridge's scalars (src/vbs_specializer_bridge.c:148-183): embed ->
 // per layer [attn_norm, Q, rope(Q), K, rope(K), V, cache, attention, O, add,
 // ffn_norm, gate, up, silu, down, add] -> output_norm -> lm_head, followed by
-// a greedy argmax. It uses the same kernels as the per-dispatch C ABI; only
-// the position-dependent ones read the position from device memory so one
+// a greedy argmax. Neighbouring ops run as one launch where the matrix-core
+// matvec can carry them (same arithmetic, one kernel): attn_norm + Q/K/V +
+// RoPE + cache store; O + residual add; ffn_norm + gate/up + SiLU*up; down +
+// residual add; output_norm + lm_head: six launches per layer with attention's
+// two. Other weight types run the per-op kernels of the C ABI. The
+// position-dependent kernels read the position from device memory, so one
 // captured graph serves every token:
 //   * RoPE reads cos/sin of each pair from a [max_ctx][head_dim/2] table that
 //     the host fills with the reference's own expressions and libm;
@@ -154,32 +158,71 @@ static hipError_t enqueue_step(const Decoder &d, hipStream_t s) {
     for (uint32_t L = 0; L < m.n_layers; L++) {
         const int *t = d.wtype.data() + 7 * L;
         const uint8_t *const *w = (const uint8_t *const *)d.wdata.data() + 7 * L;
-        VBS_TRY(launch_rms_norm(d.stream, d.attn_norm[L], d.normed, H, m.rms_eps, s));
-        VBS_TRY(launch_linear(t[0], w[0], d.normed, d.q, H, qd, 0, s));
-        k_rope_table<<<(pairs * nq + 255u) / 256u, 256, 0, s>>>(d.q, pos_dev, d.rope, hd, nq);
-        VBS_TRY(hipGetLastError());
-        VBS_TRY(launch_linear(t[1], w[1], d.normed, d.k, H, kvd, 0, s));
-        k_rope_table<<<(pairs * nkv + 255u) / 256u, 256, 0, s>>>(d.k, pos_dev, d.rope, hd, nkv);
-        VBS_TRY(hipGetLastError());
-        VBS_TRY(launch_linear(t[2], w[2], d.normed, d.v, H, kvd, 0, s));
-        k_cache_store_pos<<<(kvd + 255u) / 256u, 256, 0, s>>>(d.k, d.v, m.kc, m.vc, pos_dev, L,
-                                                                m.max_ctx, kvd);
-        VBS_TRY(hipGetLastError());
         const uint64_t layer_off = (uint64_t)L * m.max_ctx * kvd;
+        // attn_norm, Q, K, V, RoPE and the cache store: one matrix-core launch
+        // when q, k and v share a K-quant type
+        hipError_t e = hipErrorNotSupported;
+        if (t[0] == t[1] && t[1] == t[2]) {
+            const uint32_t rows[3] = {qd, kvd, kvd};
+            e = launch_kq_qkv(t[0], w, 3, 0, d.stream, d.attn_norm[L], m.rms_eps, H, rows, d.q,
+                              m.kc, m.vc, layer_off, kvd, d.rope, pos_dev, hd, s);
+        }
+        if (e == hipErrorNotSupported) {
+            VBS_TRY(launch_rms_norm(d.stream, d.attn_norm[L], d.normed, H, m.rms_eps, s));
+            VBS_TRY(launch_linear(t[0], w[0], d.normed, d.q, H, qd, 0, s));
+            k_rope_table<<<(pairs * nq + 255u) / 256u, 256, 0, s>>>(d.q, pos_dev, d.rope, hd, nq);
+            VBS_TRY(hipGetLastError());
+            VBS_TRY(launch_linear(t[1], w[1], d.normed, d.k, H, kvd, 0, s));
+            k_rope_table<<<(pairs * nkv + 255u) / 256u, 256, 0, s>>>(d.k, pos_dev, d.rope, hd, nkv);
+            VBS_TRY(hipGetLastError());
+            VBS_TRY(launch_linear(t[2], w[2], d.normed, d.v, H, kvd, 0, s));
+            k_cache_store_pos<<<(kvd + 255u) / 256u, 256, 0, s>>>(d.k, d.v, m.kc, m.vc, pos_dev,
+                                                                    L, m.max_ctx, kvd);
+            VBS_TRY(hipGetLastError());
+        } else {
+            VBS_TRY(e);
+        }
         VBS_TRY(launch_attention(d.q, m.kc, m.vc, d.attn, m.max_ctx, pos_dev, d.part, layer_off,
                                  nq, nkv, hd, scale, s));
-        VBS_TRY(launch_linear(t[3], w[3], d.attn, d.tmp, qd, H, 0, s));
-        VBS_TRY(launch_add(d.stream, d.tmp, d.stream, H, s));
-        VBS_TRY(launch_rms_norm(d.stream, d.ffn_norm[L], d.normed, H, m.rms_eps, s));
-        VBS_TRY(launch_linear(t[4], w[4], d.normed, d.gate, H, F, 0, s));
-        VBS_TRY(launch_linear(t[5], w[5], d.normed, d.up, H, F, 0, s));
-        VBS_TRY(launch_silu_mul(d.gate, d.up, d.hid, F, s));
-        VBS_TRY(launch_linear(t[6], w[6], d.hid, d.tmp, F, H, 0, s));
-        VBS_TRY(launch_add(d.stream, d.tmp, d.stream, H, s));
+        // O with the residual add folded in (stream + O*attn, as the add computes it)
+        e = launch_kq_linear(t[3], w[3], d.attn, d.stream, qd, H, 1, s);
+        if (e == hipErrorNotSupported) {
+            VBS_TRY(launch_linear(t[3], w[3], d.attn, d.tmp, qd, H, 0, s));
+            VBS_TRY(launch_add(d.stream, d.tmp, d.stream, H, s));
+        } else {
+            VBS_TRY(e);
+        }
+        // ffn_norm, gate, up and SiLU*up: one launch when gate and up share a type
+        e = t[4] == t[5] ? launch_kq_silu(t[4], w[4], w[5], d.stream, d.ffn_norm[L], m.rms_eps, H,
+                                          F, d.hid, s)
+                         : hipErrorNotSupported;
+        if (e == hipErrorNotSupported) {
+            VBS_TRY(launch_rms_norm(d.stream, d.ffn_norm[L], d.normed, H, m.rms_eps, s));
+            VBS_TRY(launch_linear(t[4], w[4], d.normed, d.gate, H, F, 0, s));
+            VBS_TRY(launch_linear(t[5], w[5], d.normed, d.up, H, F, 0, s));
+            VBS_TRY(launch_silu_mul(d.gate, d.up, d.hid, F, s));
+        } else {
+            VBS_TRY(e);
+        }
+        // down with the residual add folded in
+        e = launch_kq_linear(t[6], w[6], d.hid, d.stream, F, H, 1, s);
+        if (e == hipErrorNotSupported) {
+            VBS_TRY(launch_linear(t[6], w[6], d.hid, d.tmp, F, H, 0, s));
+            VBS_TRY(launch_add(d.stream, d.tmp, d.stream, H, s));
+        } else {
+            VBS_TRY(e);
+        }
     }
-    VBS_TRY(launch_rms_norm(d.stream, m.out_norm, d.normed, H, m.rms_eps, s));
-    VBS_TRY(launch_linear(m.head_type, (const uint8_t *)m.lm_head, d.normed, d.logits, H, m.vocab,
-                          0, s));
+    // output_norm and lm_head
+    hipError_t e = launch_kq_norm_linear(m.head_type, (const uint8_t *)m.lm_head, d.stream,
+                                         m.out_norm, m.rms_eps, d.logits, H, m.vocab, s);
+    if (e == hipErrorNotSupported) {
+        VBS_TRY(launch_rms_norm(d.stream, m.out_norm, d.normed, H, m.rms_eps, s));
+        VBS_TRY(launch_linear(m.head_type, (const uint8_t *)m.lm_head, d.normed, d.logits, H,
+                              m.vocab, 0, s));
+    } else {
+        VBS_TRY(e);
+    }
     k_argmax_advance<<<1, 1024, 0, s>>>(d.logits, m.vocab, token_dev, pos_dev, step_dev,
                                         d.tokens, d.margins, d.max_steps);
     VBS_TRY(hipGetLastError());

@@ -35,12 +35,26 @@ constexpr uint32_t kXqMaxCols = 65536;
 size_t xq_bytes(uint32_t cols);
 uint8_t *rt_xq();
 hipError_t launch_xprep(const float *x, uint32_t cols, uint8_t *xq, hipStream_t s);
-// Q4_K / Q6_K matvec on the matrix cores (x is prepared inside the kernel);
-// hipErrorNotSupported outside their range.
-hipError_t launch_q4k_mfma(const uint8_t *w, const float *x, float *y, uint32_t cols,
-                           uint32_t rows, int accumulate, hipStream_t s);
-hipError_t launch_q6k_mfma(const uint8_t *w, const float *x, float *y, uint32_t cols,
-                           uint32_t rows, int accumulate, hipStream_t s);
+// Q4_K / Q6_K matvecs on the matrix cores (x is prepared inside the kernel);
+// hipErrorNotSupported outside their shape/alignment range.
+hipError_t launch_kq_linear(int type, const uint8_t *w, const float *x, float *y, uint32_t cols,
+                            uint32_t rows, int accumulate, hipStream_t s);
+// y = W * rms_norm(x, norm_w) (the norm as k_rms_norm computes it).
+hipError_t launch_kq_norm_linear(int type, const uint8_t *w, const float *x, const float *norm_w,
+                                 float eps, float *y, uint32_t cols, uint32_t rows,
+                                 hipStream_t s);
+// Matrices q, k, v (roles role0 .. role0 + n_mat - 1, same type and cols) of
+// rms_norm(x) in one launch (norm_w may be NULL): q roped into `q`, k roped
+// and v stored as f16 at position *pos of the caches (offset kv_layer).
+hipError_t launch_kq_qkv(int type, const uint8_t *const w[3], uint32_t n_mat, uint32_t role0,
+                         const float *x, const float *norm_w, float eps, uint32_t cols,
+                         const uint32_t rows[3], float *q, uint16_t *kc, uint16_t *vc,
+                         uint64_t kv_layer, uint32_t kvd, const float2 *rope,
+                         const uint32_t *pos, uint32_t hd, hipStream_t s);
+// hid = silu(Wg * rms_norm(x)) * (Wu * rms_norm(x)) in one launch.
+hipError_t launch_kq_silu(int type, const uint8_t *wg, const uint8_t *wu, const float *x,
+                          const float *norm_w, float eps, uint32_t cols, uint32_t rows,
+                          float *hid, hipStream_t s);
 
 // Specialised Q4_K matvec; hipErrorNotSupported when the shape/alignment is
 // outside its range (the generic kernel then runs).

@@ -167,14 +167,12 @@ __global__ __launch_bounds__(256) void k_linear_dense(const uint8_t *__restrict_
 hipError_t launch_linear(int type, const uint8_t *w, const float *x, float *y, uint32_t cols,
                          uint32_t rows, int accumulate, hipStream_t s) {
     if (rows == 0) return hipSuccess;
-    if (type == kQ4_K) {
-        hipError_t e = launch_q4k_mfma(w, x, y, cols, rows, accumulate, s);
-        if (e != hipErrorNotSupported) return e;
-        e = launch_q4k_fast(w, x, y, cols, rows, accumulate, s);
+    if (type == kQ4_K || type == kQ6_K) {
+        hipError_t e = launch_kq_linear(type, w, x, y, cols, rows, accumulate, s);
         if (e != hipErrorNotSupported) return e;
     }
-    if (type == kQ6_K) {
-        hipError_t e = launch_q6k_mfma(w, x, y, cols, rows, accumulate, s);
+    if (type == kQ4_K) {
+        hipError_t e = launch_q4k_fast(w, x, y, cols, rows, accumulate, s);
         if (e != hipErrorNotSupported) return e;
     }
     uint64_t rb = row_bytes(type, cols);

@@ -330,14 +330,62 @@ struct Q6K {
     }
 };
 
-// ---- the kernel -------------------------------------------------------------------------
-template <class T, uint32_t KS, uint32_t TPW, uint32_t MAXT, bool ACC>
-__global__ __launch_bounds__(MAXT) void k_mv(const uint8_t *__restrict__ w,
-                                             const float *__restrict__ x,
-                                             float *__restrict__ y, uint32_t cols,
-                                             uint32_t rows) {
+// ---- jobs -------------------------------------------------------------------------------
+// One launch computes the rows of up to three matrices that share x (and its
+// type and column count), with an optional RMSNorm of x in front and one of
+// these epilogues on each finished row value t (every arithmetic step is the
+// reference's own):
+//   E_STORE  y[row] = t                       (vbs_host_linear_tile)
+//   E_ACC    y[row] = y[row] + t              (linear, then ELEMENTWISE add)
+//   E_QKV    matrix roles q, k, v: RoPE of q and k rows at the device position
+//            (src/vbs_host_math.h:38-51), q to y[0] in f32, k and v to the f16
+//            caches (src/vbs_host_math.h:150-159)
+//   E_SILU   gate and up: y[0][row] = gate / (1 + expf(-gate)) * up
+//            (src/vbs_host_math.h:53-57)
+enum : int { E_STORE = 0, E_ACC = 1, E_QKV = 2, E_SILU = 3 };
+
+struct MvArgs {
+    const uint8_t *w[3];
+    float *y[3];
+    uint32_t rows[3];
+    uint32_t tile_end[3];  // cumulative 16-row tiles per matrix
+    uint32_t nmat, cols;
+    const float *x;
+    const float *norm_w;  // RMSNorm weights (NORM launches)
+    float eps;
+    const float2 *rope;   // E_QKV: [max_ctx][hd/2] (cos, sin)
+    const uint32_t *pos;  // E_QKV: device position
+    uint32_t hd, kvd, role0;
+    uint16_t *kc, *vc;
+    uint64_t kv_layer;  // layer * max_ctx * kvd
+};
+
+// Sum of squares of x in the order k_rms_norm uses for any n: slot s < 1024
+// sums x[s], x[s + 1024], ... in order, 64 consecutive slots are added by a
+// wave butterfly, the 16 slot groups in index order. xf is x in LDS.
+__device__ double rms_sumsq(const float *xf, uint32_t n, double *part) {
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u, nw = blockDim.x >> 6;
+    for (uint32_t vw = wave; vw < 16u; vw += nw) {
+        double ss = 0.0;
+        for (uint32_t i = 64u * vw + lane; i < n; i += 1024u) {
+            const double v = xf[i];
+            ss = fma(v, v, ss);
+        }
+        ss = wave_sum_d(ss);
+        if (lane == 0) part[vw] = ss;
+    }
+    __syncthreads();
+    double t = 0.0;
+    for (int k = 0; k < 16; k++) t += part[k];
+    return t;
+}
+
+template <class T, uint32_t KS, uint32_t TPW, uint32_t MAXT, bool NORM, int EPI>
+__global__ __launch_bounds__(MAXT) void k_mvf(const MvArgs a) {
     extern __shared__ __align__(16) uint8_t xq[];
     __shared__ float red[2][16][16];
+    __shared__ double part[16];
+    const uint32_t cols = a.cols;
     const uint32_t nblk = cols >> 8;
     const uint64_t rb = (uint64_t)nblk * T::BYTES;
     const XqLayout L = xq_layout(cols);
@@ -345,31 +393,68 @@ __global__ __launch_bounds__(MAXT) void k_mv(const uint8_t *__restrict__ w,
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const uint32_t nw = nth >> 6;
     const uint32_t n = lane & 15u, g = lane >> 4;
-    const uint32_t ntiles = (rows + 15u) / 16u;
     const uint32_t b0 = wave * KS;
+    const uint32_t total = a.tile_end[a.nmat - 1u];
+
+    // matrix and local tile of this workgroup's tile j
+    auto tile_of = [&](uint32_t j, uint32_t &m, uint32_t &lt) {
+        if (EPI == E_SILU) {
+            m = j;
+            lt = blockIdx.x;
+        } else {
+            const uint32_t gt = min(blockIdx.x * TPW + j, total - 1u);
+            m = (gt >= a.tile_end[0]) + (a.nmat > 2u && gt >= a.tile_end[1]);
+            lt = gt - (m ? a.tile_end[m - 1u] : 0u);
+        }
+    };
+    auto src_of = [&](uint32_t m, uint32_t lt) {
+        const uint8_t *w = a.w[m];
+        return Src{w, w + (uint64_t)a.rows[m] * rb, rb, lt * 16u, a.rows[m]};
+    };
 
     // 1. x first (one or two 16-element items per thread)
     const uint32_t items = cols / 16u;
     const uint32_t i0 = threadIdx.x, i1 = threadIdx.x + nth;
     const bool two = nth < items;
     float v0[16], v1[16];
-    load16(x, cols, i0, v0);
-    load16(x, cols, two ? i1 : items, v1);
+    load16(a.x, cols, i0, v0);
+    load16(a.x, cols, two ? i1 : items, v1);
 
     // 2. every weight load of this wave (tail tiles, rows and blocks re-read
     // valid data and are masked below)
     u32x4 r[TPW][KS][T::NLD];
-    const uint32_t tile0 = blockIdx.x * TPW;
-    const uint8_t *w_end = w + (uint64_t)rows * rb;
 #pragma unroll
     for (uint32_t j = 0; j < TPW; j++) {
-        const Src src{w, w_end, rb, min(tile0 + j, ntiles - 1u) * 16u, rows};
+        uint32_t m, lt;
+        tile_of(j, m, lt);
+        const Src src = src_of(m, lt);
 #pragma unroll
         for (uint32_t k = 0; k < KS; k++) T::load(src, min(b0 + k, nblk - 1u), n, g, r[j][k]);
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    // 3. x -> digits in LDS while the weights arrive
+    // 3. (RMSNorm and) x -> digits in LDS while the weights arrive
+    if (NORM) {
+        float *xf = reinterpret_cast<float *>(xq + L.bytes + nw * T::SCRATCH);
+        if (i0 < items)
+#pragma unroll
+            for (int k = 0; k < 16; k++) xf[16u * i0 + k] = v0[k];
+        if (two && i1 < items)
+#pragma unroll
+            for (int k = 0; k < 16; k++) xf[16u * i1 + k] = v1[k];
+        __syncthreads();
+        const double ss = rms_sumsq(xf, cols, part);
+        const float mean = (float)(ss / (double)cols);
+        const float sc = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, a.eps)));
+        float w0[16], w1[16];
+        load16(a.norm_w, cols, i0, w0);
+        load16(a.norm_w, cols, two ? i1 : items, w1);
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            v0[k] = __fmul_rn(__fmul_rn(v0[k], sc), w0[k]);
+            v1[k] = __fmul_rn(__fmul_rn(v1[k], sc), w1[k]);
+        }
+    }
     prep_item(v0, cols, i0, xq, L);
     if (two) prep_item(v1, cols, i1, xq, L);
     if (threadIdx.x == 0) *reinterpret_cast<uint4 *>(xq + L.zero) = make_uint4(0, 0, 0, 0);
@@ -377,31 +462,63 @@ __global__ __launch_bounds__(MAXT) void k_mv(const uint8_t *__restrict__ w,
 
     // 4. tiles
     uint8_t *scratch = xq + L.bytes + wave * T::SCRATCH;
+    float prev = 0.f;  // E_SILU: the gate row value
 #pragma unroll
     for (uint32_t j = 0; j < TPW; j++) {
+        uint32_t m, lt;
+        tile_of(j, m, lt);
+        const Src src = src_of(m, lt);
         float acc = 0.f;
 #pragma unroll
         for (uint32_t k = 0; k < KS; k++) {
             const bool live = b0 + k < nblk;  // slots past the row contribute zero
-            const Src src{w, w_end, rb, min(tile0 + j, ntiles - 1u) * 16u, rows};
-            const float part = T::dot(r[j][k], scratch, src, xq, L, cols,
-                                      min(b0 + k, nblk - 1u), n, g);
-            acc += live ? part : 0.f;
+            const float part_k =
+                T::dot(r[j][k], scratch, src, xq, L, cols, min(b0 + k, nblk - 1u), n, g);
+            acc += live ? part_k : 0.f;
         }
         // the four lane groups of a row hold different groups of its blocks
         acc += __shfl_xor(acc, 16, 64);
         acc += __shfl_xor(acc, 32, 64);
-        const uint32_t row = (tile0 + j) * 16u + n;
-        if (nw == 1) {
-            if (lane < 16u && row < rows) y[row] = ACC ? y[row] + acc : acc;
-            continue;
+        if (nw > 1u) {
+            if (lane < 16u) red[j & 1u][wave][n] = acc;
+            __syncthreads();
+            if (wave != 0) continue;
+            acc = 0.f;
+            for (uint32_t k = 0; k < nw; k++) acc += red[j & 1u][k][n];
         }
-        if (lane < 16u) red[j & 1u][wave][n] = acc;
-        __syncthreads();
-        if (wave == 0 && lane < 16u && row < rows) {
-            float t = 0.f;
-            for (uint32_t k = 0; k < nw; k++) t += red[j & 1u][k][n];
-            y[row] = ACC ? y[row] + t : t;
+        // wave 0: every lane holds the value of row n of the tile
+        const bool own = (EPI == E_SILU || blockIdx.x * TPW + j < total);
+        const uint32_t row = lt * 16u + n;
+        const bool st = lane < 16u && own && row < a.rows[m];
+        if (EPI == E_STORE) {
+            if (st) a.y[m][row] = acc;
+        } else if (EPI == E_ACC) {
+            if (st) a.y[m][row] = __fadd_rn(a.y[m][row], acc);
+        } else if (EPI == E_SILU) {
+            if (j == 0) {
+                prev = acc;
+            } else if (st) {
+                const float den = __fadd_rn(1.0f, expf(-prev));
+                a.y[0][row] = __fmul_rn(__fdiv_rn(prev, den), acc);
+            }
+        } else {  // E_QKV
+            const uint32_t role = a.role0 + m;
+            const float other = __shfl_xor(acc, 1, 64);  // the RoPE partner row
+            const uint32_t p = a.pos[0];
+            float v = acc;
+            if (role < 2u) {
+                const float2 cs = a.rope[(uint64_t)p * (a.hd / 2u) + (row % a.hd) / 2u];
+                const bool even = (row & 1u) == 0u;
+                const float x0 = even ? acc : other, x1 = even ? other : acc;
+                v = even ? __fsub_rn(__fmul_rn(x0, cs.x), __fmul_rn(x1, cs.y))
+                         : __fadd_rn(__fmul_rn(x0, cs.y), __fmul_rn(x1, cs.x));
+            }
+            if (st) {
+                if (role == 0u)
+                    a.y[0][row] = v;
+                else
+                    (role == 1u ? a.kc : a.vc)[a.kv_layer + (uint64_t)p * a.kvd + row] = vbs_f2h(v);
+            }
         }
     }
 }
@@ -416,8 +533,8 @@ struct MvPlan {
 // Q4_K two super-blocks x three tiles, three x one; Q6_K two x two only with
 // at most 8 waves (a 256-VGPR budget), else one tile.
 template <class T>
-static MvPlan mv_plan(uint32_t cols, uint32_t rows) {
-    const uint32_t nblk = cols / 256u, tiles = (rows + 15u) / 16u;
+static MvPlan mv_plan(uint32_t cols, uint32_t tiles) {
+    const uint32_t nblk = cols / 256u;
     MvPlan p;
     p.ks = nblk <= 32u ? 2u : 3u;
     p.nw = (nblk + p.ks - 1u) / p.ks;
@@ -431,46 +548,39 @@ static MvPlan mv_plan(uint32_t cols, uint32_t rows) {
     return p;
 }
 
-template <class T, uint32_t KS, uint32_t TPW, uint32_t MAXT>
-static hipError_t launch_mv_t(const uint8_t *w, const float *x, float *y, uint32_t cols,
-                              uint32_t rows, int acc, uint32_t nw, hipStream_t s) {
-    const size_t lds = xq_layout(cols).bytes + (size_t)nw * T::SCRATCH;
+template <class T, uint32_t KS, uint32_t TPW, uint32_t MAXT, bool NORM, int EPI>
+static hipError_t launch_t(const MvArgs &a, uint32_t nw, uint32_t wgs, hipStream_t s) {
+    const size_t lds = xq_layout(a.cols).bytes + (size_t)nw * T::SCRATCH +
+                       (NORM ? 4u * (size_t)a.cols : 0u);
     if (lds > 65536u) {  // beyond the default per-workgroup LDS window: opt in once
         static size_t granted = 0;
         if (lds > granted) {
-            const void *f0 = (const void *)k_mv<T, KS, TPW, MAXT, false>;
-            const void *f1 = (const void *)k_mv<T, KS, TPW, MAXT, true>;
-            if (hipFuncSetAttribute(f0, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
-                    hipSuccess ||
-                hipFuncSetAttribute(f1, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
-                    hipSuccess) {
+            if (hipFuncSetAttribute((const void *)k_mvf<T, KS, TPW, MAXT, NORM, EPI>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
+                hipSuccess) {
                 (void)hipGetLastError();
                 return hipErrorNotSupported;
             }
             granted = lds;
         }
     }
-    const uint32_t tiles = (rows + 15u) / 16u;
-    const dim3 grid((tiles + TPW - 1u) / TPW), block(64u * nw);
-    if (acc)
-        k_mv<T, KS, TPW, MAXT, true><<<grid, block, lds, s>>>(w, x, y, cols, rows);
-    else
-        k_mv<T, KS, TPW, MAXT, false><<<grid, block, lds, s>>>(w, x, y, cols, rows);
+    k_mvf<T, KS, TPW, MAXT, NORM, EPI><<<wgs, 64u * nw, lds, s>>>(a);
     return hipGetLastError();
 }
 
-template <class T>
-static hipError_t launch_mv(const uint8_t *w, const float *x, float *y, uint32_t cols,
-                            uint32_t rows, int acc, hipStream_t s) {
-    const uint32_t nblk = cols / 256u;
-    // at most 16 waves of at most 3 super-blocks; x items fit two per thread
-    if (cols % 256u || rows == 0 || nblk > 48u) return hipErrorNotSupported;
-    // Q4_K rows are 16-byte multiples, so its 16-byte loads need an aligned w;
-    // Q6_K aligns every load itself
-    if (((uintptr_t)x & 3u) || ((uintptr_t)w & (T::SCRATCH ? 1u : 15u))) return hipErrorNotSupported;
-    const MvPlan p = mv_plan<T>(cols, rows);
-    if (p.nw > 16u || cols / 16u > 2u * 64u * p.nw) return hipErrorNotSupported;
-#define VBS_MV(KS, TPW, MAXT) return launch_mv_t<T, KS, TPW, MAXT>(w, x, y, cols, rows, acc, p.nw, s)
+template <class T, bool NORM, int EPI>
+static hipError_t launch_plan(const MvArgs &a, hipStream_t s) {
+    const uint32_t total = a.tile_end[a.nmat - 1u];
+    MvPlan p = mv_plan<T>(a.cols, total);
+    // the RMSNorm prologue keeps more of x live: at most two tiles per
+    // workgroup under the 128-VGPR budget of 16 waves, none for wide Q6_K rows
+    if (NORM && p.nw > 8u && p.tpw > 2u) p.tpw = 2u;
+    if (NORM && T::NLD > 3u && p.ks == 3u) return hipErrorNotSupported;
+    if (EPI == E_SILU) p.tpw = 2u;  // a gate tile and the same up tile
+    if (p.nw > 16u || a.cols / 16u > 2u * 64u * p.nw) return hipErrorNotSupported;
+    if (p.ks == 3u && p.tpw != 1u) return hipErrorNotSupported;
+    const uint32_t wgs = EPI == E_SILU ? a.tile_end[0] : (total + p.tpw - 1u) / p.tpw;
+#define VBS_MV(KS, TPW, MAXT) return launch_t<T, KS, TPW, MAXT, NORM, EPI>(a, p.nw, wgs, s)
     if (p.ks == 3u) VBS_MV(3, 1, 1024);
     if (p.tpw == 1u) {
         if (p.nw <= 8u) VBS_MV(2, 1, 512);
@@ -484,19 +594,113 @@ static hipError_t launch_mv(const uint8_t *w, const float *x, float *y, uint32_t
         if (p.nw <= 8u) VBS_MV(2, 2, 512);
         VBS_MV(2, 2, 1024);
     } else {
-        VBS_MV(2, 2, 512);
+        if (p.nw <= 8u) VBS_MV(2, 2, 512);
+        return hipErrorNotSupported;
     }
 #undef VBS_MV
 }
 
-hipError_t launch_q4k_mfma(const uint8_t *w, const float *x, float *y, uint32_t cols,
-                           uint32_t rows, int accumulate, hipStream_t s) {
-    return launch_mv<Q4K>(w, x, y, cols, rows, accumulate, s);
+// Shape and alignment range of the matrix-core path: at most 16 waves of at
+// most 3 super-blocks, x items fit two per thread; Q4_K rows are 16-byte
+// multiples, so its 16-byte loads need an aligned w; Q6_K aligns every load.
+static bool mv_fits(int type, const uint8_t *w, const float *x, uint32_t cols) {
+    if (type != kQ4_K && type != kQ6_K) return false;
+    if (cols % 256u || cols / 256u > 48u || ((uintptr_t)x & 3u)) return false;
+    return ((uintptr_t)w & (type == kQ4_K ? 15u : 1u)) == 0;
 }
 
-hipError_t launch_q6k_mfma(const uint8_t *w, const float *x, float *y, uint32_t cols,
-                           uint32_t rows, int accumulate, hipStream_t s) {
-    return launch_mv<Q6K>(w, x, y, cols, rows, accumulate, s);
+template <bool NORM, int EPI>
+static hipError_t launch_type(int type, const MvArgs &a, hipStream_t s) {
+    return type == kQ4_K ? launch_plan<Q4K, NORM, EPI>(a, s) : launch_plan<Q6K, NORM, EPI>(a, s);
+}
+
+static void set_tiles(MvArgs &a) {
+    uint32_t t = 0;
+    for (uint32_t m = 0; m < a.nmat; m++) {
+        t += (a.rows[m] + 15u) / 16u;
+        a.tile_end[m] = t;
+    }
+}
+
+hipError_t launch_kq_linear(int type, const uint8_t *w, const float *x, float *y, uint32_t cols,
+                            uint32_t rows, int accumulate, hipStream_t s) {
+    if (rows == 0 || !mv_fits(type, w, x, cols)) return hipErrorNotSupported;
+    MvArgs a{};
+    a.w[0] = w;
+    a.y[0] = y;
+    a.rows[0] = rows;
+    a.nmat = 1;
+    a.cols = cols;
+    a.x = x;
+    set_tiles(a);
+    return accumulate ? launch_type<false, E_ACC>(type, a, s) : launch_type<false, E_STORE>(type, a, s);
+}
+
+hipError_t launch_kq_norm_linear(int type, const uint8_t *w, const float *x, const float *norm_w,
+                                 float eps, float *y, uint32_t cols, uint32_t rows,
+                                 hipStream_t s) {
+    if (rows == 0 || !mv_fits(type, w, x, cols)) return hipErrorNotSupported;
+    MvArgs a{};
+    a.w[0] = w;
+    a.y[0] = y;
+    a.rows[0] = rows;
+    a.nmat = 1;
+    a.cols = cols;
+    a.x = x;
+    a.norm_w = norm_w;
+    a.eps = eps;
+    set_tiles(a);
+    return launch_type<true, E_STORE>(type, a, s);
+}
+
+hipError_t launch_kq_qkv(int type, const uint8_t *const wqkv[3], uint32_t n_mat, uint32_t role0,
+                         const float *x, const float *norm_w, float eps, uint32_t cols,
+                         const uint32_t rows[3], float *q, uint16_t *kc, uint16_t *vc,
+                         uint64_t kv_layer, uint32_t kvd, const float2 *rope,
+                         const uint32_t *pos, uint32_t hd, hipStream_t s) {
+    if (n_mat == 0 || n_mat > 3u || role0 + n_mat > 3u || (hd & 1u)) return hipErrorNotSupported;
+    MvArgs a{};
+    for (uint32_t m = 0; m < n_mat; m++) {
+        if (!mv_fits(type, wqkv[m], x, cols) || rows[m] == 0 || (n_mat > 1u && rows[m] % 16u))
+            return hipErrorNotSupported;
+        a.w[m] = wqkv[m];
+        a.rows[m] = rows[m];
+    }
+    a.y[0] = q;
+    a.nmat = n_mat;
+    a.role0 = role0;
+    a.cols = cols;
+    a.x = x;
+    a.norm_w = norm_w;
+    a.eps = eps;
+    a.rope = rope;
+    a.pos = pos;
+    a.hd = hd;
+    a.kvd = kvd;
+    a.kc = kc;
+    a.vc = vc;
+    a.kv_layer = kv_layer;
+    set_tiles(a);
+    return norm_w ? launch_type<true, E_QKV>(type, a, s) : launch_type<false, E_QKV>(type, a, s);
+}
+
+hipError_t launch_kq_silu(int type, const uint8_t *wg, const uint8_t *wu, const float *x,
+                          const float *norm_w, float eps, uint32_t cols, uint32_t rows,
+                          float *hid, hipStream_t s) {
+    if (rows == 0 || rows % 16u || !mv_fits(type, wg, x, cols) || !mv_fits(type, wu, x, cols))
+        return hipErrorNotSupported;
+    MvArgs a{};
+    a.w[0] = wg;
+    a.w[1] = wu;
+    a.y[0] = hid;
+    a.rows[0] = a.rows[1] = rows;
+    a.nmat = 2;
+    a.cols = cols;
+    a.x = x;
+    a.norm_w = norm_w;
+    a.eps = eps;
+    set_tiles(a);
+    return norm_w ? launch_type<true, E_SILU>(type, a, s) : launch_type<false, E_SILU>(type, a, s);
 }
 
 }  // namespace vbs
