@@ -262,11 +262,12 @@ def bench_decode(dev, host, n_tokens, path="both", n_layers=32, ctx=2048, n_disp
         return {"dispatch_path": dispatch, "first_tokens": [int(x) for x in dtoks[:8]],
                 "min_margin": float(np.min(dmargins))}
     # graph decoder over the same device weights and cache
+    eager = path == "eager"
     g = V.GraphDecoder(dev, d, max_steps=n_tokens)
-    g.greedy(1, ctx, 2)
+    g.greedy(1, ctx, 2, eager)
     dev.sync()
     t0 = time.perf_counter()
-    toks, margins = g.greedy(1, ctx, n_tokens)
+    toks, margins = g.greedy(1, ctx, n_tokens, eager)
     dt = time.perf_counter() - t0
     g.close()
     d.close()
@@ -277,7 +278,8 @@ def bench_decode(dev, host, n_tokens, path="both", n_layers=32, ctx=2048, n_disp
             "n_tokens": n_tokens, "context": ctx,
             "bytes_per_token": int(wbytes + kv_bytes),
             "roofline_frac": round((wbytes + kv_bytes) / (dt / n_tokens) / (PEAK_HBM_GBS * 1e9), 4),
-            "path": "vbs_gfx950_decoder: one HIP graph launch per token",
+            "path": ("vbs_gfx950_decoder kernels launched one by one" if eager else
+                     "vbs_gfx950_decoder: one HIP graph launch per token"),
             "dispatch_path": dispatch,
             "paths_agree": bool(np.array_equal(toks[:n_dispatch_tokens], dtoks)),
             "first_tokens": [int(x) for x in toks[:8]],
@@ -296,8 +298,10 @@ def main():
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="first copy this many MiB device-to-device once (a known-size "
                          "transfer that scales HBM byte counters)")
-    ap.add_argument("--decode-path", choices=("both", "dispatch"), default="both",
-                    help="'dispatch' times only the per-dispatch ops-table decode")
+    ap.add_argument("--decode-path", choices=("both", "dispatch", "eager"), default="both",
+                    help="'dispatch' times only the per-dispatch ops-table decode; 'eager' "
+                         "runs the graph decoder's kernels without the graph (for kernel "
+                         "tracers)")
     ap.add_argument("--no-cpu", action="store_true")
     a = ap.parse_args()
     if a.gpus != 1:

@@ -169,6 +169,11 @@ int vbs_gfx950_decoder_step(void *handle, uint32_t token, uint32_t pos, float *l
  * is the i-th argmax, margins (may be NULL) top-1 minus top-2 logit. */
 int vbs_gfx950_decoder_greedy(void *handle, uint32_t token, uint32_t pos, uint32_t n,
                               uint32_t *tokens, float *margins);
+/* The same steps as vbs_gfx950_decoder_greedy, each kernel launched directly
+ * instead of replaying the graph (identical results; for tools that trace
+ * kernel launches but not graph replays). */
+int vbs_gfx950_decoder_greedy_eager(void *handle, uint32_t token, uint32_t pos, uint32_t n,
+                                    uint32_t *tokens, float *margins);
 int vbs_gfx950_decoder_destroy(void *handle);
 
 #ifdef __cplusplus

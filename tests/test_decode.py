@@ -160,10 +160,14 @@ def test_gpu_graph_decoder_tiny_greedy_matches_oracle(host, backend, dev, tiny):
     g = V.GraphDecoder(dev, d, max_steps=40)
     kc, vc = full_cache(tiny, None, None, 0)
     want_toks, _ = oracle_greedy(Oracle(), tiny, kc, vc, 1, 0, 40)
-    toks, _ = g.greedy(1, 0, 40)
+    toks, margins = g.greedy(1, 0, 40)
+    # the same kernels launched one by one give the same tokens and margins
+    etoks, emargins = g.greedy(1, 0, 40, eager=True)
     g.close()
     d.close()
     assert np.array_equal(toks, want_toks)
+    assert np.array_equal(etoks, toks)
+    assert np.array_equal(emargins.view(np.uint32), margins.view(np.uint32))
 
 
 @pytest.mark.gpu

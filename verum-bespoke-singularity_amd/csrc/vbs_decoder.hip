@@ -88,9 +88,8 @@ __global__ __launch_bounds__(1024) void k_argmax_advance(const float *__restrict
                                                          uint32_t max_steps) {
     __shared__ Top2 red[1024];
     Top2 t{-INFINITY, 0xFFFFFFFFu, -INFINITY};
-    for (uint32_t i = threadIdx.x; i < n; i += 1024u) {
-        const float v = logits[i];
-        if (v != v && i != 0u) continue;  // a NaN never beats anything after index 0
+    auto consider = [&](float v, uint32_t i) {
+        if (v != v && i != 0u) return;  // a NaN never beats anything after index 0
         if (t.i1 == 0xFFFFFFFFu || v > t.v1) {
             if (t.i1 != 0xFFFFFFFFu) t.v2 = fmaxf(t.v2, t.v1);
             t.v1 = v;
@@ -98,6 +97,22 @@ __global__ __launch_bounds__(1024) void k_argmax_advance(const float *__restrict
         } else {
             t.v2 = fmaxf(t.v2, v);
         }
+    };
+    // each thread scans its indices in increasing order: 16-byte chunks
+    // c, c + 1024, ... when the logits allow it, single floats otherwise
+    const bool vec = (n % 4u) == 0 && ((uintptr_t)logits & 15u) == 0;
+    if (vec) {
+        const float4 *l4 = reinterpret_cast<const float4 *>(logits);
+#pragma unroll 8
+        for (uint32_t c = threadIdx.x; c < n / 4u; c += 1024u) {
+            const float4 f = l4[c];
+            consider(f.x, 4u * c);
+            consider(f.y, 4u * c + 1u);
+            consider(f.z, 4u * c + 2u);
+            consider(f.w, 4u * c + 3u);
+        }
+    } else {
+        for (uint32_t i = threadIdx.x; i < n; i += 1024u) consider(logits[i], i);
     }
     red[threadIdx.x] = t;
     __syncthreads();
@@ -387,6 +402,28 @@ int vbs_gfx950_decoder_greedy(void *handle, uint32_t token, uint32_t pos, uint32
                    "decoder_greedy: margins"))
         return 0;
     return rt_hip_ok(hipStreamSynchronize(s), "decoder_greedy");
+}
+
+int vbs_gfx950_decoder_greedy_eager(void *handle, uint32_t token, uint32_t pos, uint32_t n,
+                                    uint32_t *tokens, float *margins) {
+    if (!rt_ready()) return 0;
+    Decoder *d = (Decoder *)handle;
+    if (!d || !tokens) return rt_fail("decoder_greedy_eager: null argument");
+    if (n > d->max_steps)
+        return rt_fail("decoder_greedy_eager: %u steps > max_steps %u", n, d->max_steps);
+    if ((uint64_t)pos + n > d->m.max_ctx) return rt_fail("decoder_greedy_eager: context exhausted");
+    if (!set_state(d, token, pos)) return 0;
+    hipStream_t s = rt_stream();
+    for (uint32_t i = 0; i < n; i++)
+        if (!rt_hip_ok(enqueue_step(*d, s), "decoder_greedy_eager: step")) return 0;
+    if (!rt_hip_ok(hipMemcpyAsync(tokens, d->tokens, (size_t)n * 4, hipMemcpyDeviceToHost, s),
+                   "decoder_greedy_eager: tokens"))
+        return 0;
+    if (margins &&
+        !rt_hip_ok(hipMemcpyAsync(margins, d->margins, (size_t)n * 4, hipMemcpyDeviceToHost, s),
+                   "decoder_greedy_eager: margins"))
+        return 0;
+    return rt_hip_ok(hipStreamSynchronize(s), "decoder_greedy_eager");
 }
 
 int vbs_gfx950_decoder_destroy(void *handle) {

@@ -360,31 +360,11 @@ struct MvArgs {
     uint64_t kv_layer;  // layer * max_ctx * kvd
 };
 
-// Sum of squares of x in the order k_rms_norm uses for any n: slot s < 1024
-// sums x[s], x[s + 1024], ... in order, 64 consecutive slots are added by a
-// wave butterfly, the 16 slot groups in index order. xf is x in LDS.
-__device__ double rms_sumsq(const float *xf, uint32_t n, double *part) {
-    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u, nw = blockDim.x >> 6;
-    for (uint32_t vw = wave; vw < 16u; vw += nw) {
-        double ss = 0.0;
-        for (uint32_t i = 64u * vw + lane; i < n; i += 1024u) {
-            const double v = xf[i];
-            ss = fma(v, v, ss);
-        }
-        ss = wave_sum_d(ss);
-        if (lane == 0) part[vw] = ss;
-    }
-    __syncthreads();
-    double t = 0.0;
-    for (int k = 0; k < 16; k++) t += part[k];
-    return t;
-}
-
-template <class T, uint32_t KS, uint32_t TPW, uint32_t MAXT, bool NORM, int EPI>
+template <class T, uint32_t KS, uint32_t TPW, uint32_t MAXT, bool NORM, int EPI, bool TWO>
 __global__ __launch_bounds__(MAXT) void k_mvf(const MvArgs a) {
     extern __shared__ __align__(16) uint8_t xq[];
     __shared__ float red[2][16][16];
-    __shared__ double part[16];
+    __shared__ double part[32];
     const uint32_t cols = a.cols;
     const uint32_t nblk = cols >> 8;
     const uint64_t rb = (uint64_t)nblk * T::BYTES;
@@ -412,13 +392,17 @@ __global__ __launch_bounds__(MAXT) void k_mvf(const MvArgs a) {
         return Src{w, w + (uint64_t)a.rows[m] * rb, rb, lt * 16u, a.rows[m]};
     };
 
-    // 1. x first (one or two 16-element items per thread)
+    // 1. x first (one or two 16-element items per thread; with the RMSNorm also
+    // its weights)
     const uint32_t items = cols / 16u;
     const uint32_t i0 = threadIdx.x, i1 = threadIdx.x + nth;
-    const bool two = nth < items;
-    float v0[16], v1[16];
+    float v0[16], v1[TWO ? 16 : 1], w0[NORM ? 16 : 1], w1[NORM && TWO ? 16 : 1];
     load16(a.x, cols, i0, v0);
-    load16(a.x, cols, two ? i1 : items, v1);
+    if (TWO) load16(a.x, cols, i1, v1);
+    if (NORM) {
+        load16(a.norm_w, cols, i0, w0);
+        if (TWO) load16(a.norm_w, cols, i1, w1);
+    }
 
     // 2. every weight load of this wave (tail tiles, rows and blocks re-read
     // valid data and are masked below)
@@ -433,30 +417,40 @@ __global__ __launch_bounds__(MAXT) void k_mvf(const MvArgs a) {
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    // 3. (RMSNorm and) x -> digits in LDS while the weights arrive
+    // 3. (RMSNorm and) x -> digits in LDS while the weights arrive. The sum of
+    // squares follows k_rms_norm's order: squares of a 16-element item in
+    // element order, 64 consecutive items (one wave) by butterfly, the
+    // 64-item groups in index order.
     if (NORM) {
-        float *xf = reinterpret_cast<float *>(xq + L.bytes + nw * T::SCRATCH);
-        if (i0 < items)
+        double ss0 = 0.0, ss1 = 0.0;
 #pragma unroll
-            for (int k = 0; k < 16; k++) xf[16u * i0 + k] = v0[k];
-        if (two && i1 < items)
-#pragma unroll
-            for (int k = 0; k < 16; k++) xf[16u * i1 + k] = v1[k];
+        for (int k = 0; k < 16; k++) {
+            const double d0 = v0[k];
+            ss0 = fma(d0, d0, ss0);
+            if (TWO) {
+                const double d1 = v1[k];
+                ss1 = fma(d1, d1, ss1);
+            }
+        }
+        ss0 = wave_sum_d(i0 < items ? ss0 : 0.0);
+        if (lane == 0 && 64u * wave < items) part[wave] = ss0;
+        if (TWO) {
+            ss1 = wave_sum_d(i1 < items ? ss1 : 0.0);
+            if (lane == 0 && 64u * (wave + nw) < items) part[wave + nw] = ss1;
+        }
         __syncthreads();
-        const double ss = rms_sumsq(xf, cols, part);
-        const float mean = (float)(ss / (double)cols);
+        double t = 0.0;
+        for (uint32_t k = 0; k < (items + 63u) / 64u; k++) t += part[k];
+        const float mean = (float)(t / (double)cols);
         const float sc = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, a.eps)));
-        float w0[16], w1[16];
-        load16(a.norm_w, cols, i0, w0);
-        load16(a.norm_w, cols, two ? i1 : items, w1);
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             v0[k] = __fmul_rn(__fmul_rn(v0[k], sc), w0[k]);
-            v1[k] = __fmul_rn(__fmul_rn(v1[k], sc), w1[k]);
+            if (TWO) v1[k] = __fmul_rn(__fmul_rn(v1[k], sc), w1[k]);
         }
     }
     prep_item(v0, cols, i0, xq, L);
-    if (two) prep_item(v1, cols, i1, xq, L);
+    if (TWO) prep_item(v1, cols, i1, xq, L);
     if (threadIdx.x == 0) *reinterpret_cast<uint4 *>(xq + L.zero) = make_uint4(0, 0, 0, 0);
     __syncthreads();
 
@@ -548,14 +542,13 @@ static MvPlan mv_plan(uint32_t cols, uint32_t tiles) {
     return p;
 }
 
-template <class T, uint32_t KS, uint32_t TPW, uint32_t MAXT, bool NORM, int EPI>
-static hipError_t launch_t(const MvArgs &a, uint32_t nw, uint32_t wgs, hipStream_t s) {
-    const size_t lds = xq_layout(a.cols).bytes + (size_t)nw * T::SCRATCH +
-                       (NORM ? 4u * (size_t)a.cols : 0u);
+template <class T, uint32_t KS, uint32_t TPW, uint32_t MAXT, bool NORM, int EPI, bool TWO>
+static hipError_t launch_t2(const MvArgs &a, uint32_t nw, uint32_t wgs, hipStream_t s) {
+    const size_t lds = xq_layout(a.cols).bytes + (size_t)nw * T::SCRATCH;
     if (lds > 65536u) {  // beyond the default per-workgroup LDS window: opt in once
         static size_t granted = 0;
         if (lds > granted) {
-            if (hipFuncSetAttribute((const void *)k_mvf<T, KS, TPW, MAXT, NORM, EPI>,
+            if (hipFuncSetAttribute((const void *)k_mvf<T, KS, TPW, MAXT, NORM, EPI, TWO>,
                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
                 hipSuccess) {
                 (void)hipGetLastError();
@@ -564,8 +557,15 @@ static hipError_t launch_t(const MvArgs &a, uint32_t nw, uint32_t wgs, hipStream
             granted = lds;
         }
     }
-    k_mvf<T, KS, TPW, MAXT, NORM, EPI><<<wgs, 64u * nw, lds, s>>>(a);
+    k_mvf<T, KS, TPW, MAXT, NORM, EPI, TWO><<<wgs, 64u * nw, lds, s>>>(a);
     return hipGetLastError();
+}
+
+// One or two 16-element x items per thread.
+template <class T, uint32_t KS, uint32_t TPW, uint32_t MAXT, bool NORM, int EPI>
+static hipError_t launch_t(const MvArgs &a, uint32_t nw, uint32_t wgs, hipStream_t s) {
+    if (a.cols / 16u > 64u * nw) return launch_t2<T, KS, TPW, MAXT, NORM, EPI, true>(a, nw, wgs, s);
+    return launch_t2<T, KS, TPW, MAXT, NORM, EPI, false>(a, nw, wgs, s);
 }
 
 template <class T, bool NORM, int EPI>

@@ -86,6 +86,7 @@ _DEVICE_SIGS = {
     "decoder_create": (_I, [_P, _U32, C.POINTER(C.c_void_p)]),
     "decoder_step": (_I, [_P, _U32, _U32, _P]),
     "decoder_greedy": (_I, [_P, _U32, _U32, _U32, _P, _P]),
+    "decoder_greedy_eager": (_I, [_P, _U32, _U32, _U32, _P, _P]),
     "decoder_destroy": (_I, [_P]),
 }
 
@@ -514,11 +515,12 @@ class GraphDecoder:
                        "decoder_step")
         return out
 
-    def greedy(self, token: int, pos: int, n: int):
+    def greedy(self, token: int, pos: int, n: int, eager: bool = False):
         toks = np.empty(n, np.uint32)
         margins = np.empty(n, np.float32)
-        self.dev.check(self.dev._decoder_greedy(self.h, token, pos, n, toks.ctypes.data,
-                                                margins.ctypes.data), "decoder_greedy")
+        fn = self.dev._decoder_greedy_eager if eager else self.dev._decoder_greedy
+        self.dev.check(fn(self.h, token, pos, n, toks.ctypes.data, margins.ctypes.data),
+                       "decoder_greedy")
         return toks, margins
 
     def close(self):
