@@ -52,6 +52,13 @@ LAYER_SET = [("q", H, H), ("k", H, H), ("v", H, H), ("o", H, H),
              ("gate", FF, H), ("up", FF, H), ("down", H, FF)]  # (name, rows, cols)
 SEED = 424242
 
+# HBM bytes per launch of the dominant kernel (11008x4096 Q4_K) from two
+# rocprofv3 --pmc passes over this program (FETCH_SIZE, WRITE_SIZE in KiB per
+# dispatch), each scaled by what the counter reads for a 256 MiB device copy
+# in the same run: FETCH_SIZE x 1.9997 + WRITE_SIZE x 1.0000
+# (profiles/q4k_matvec_7b_layer_set.md).
+TRAFFIC_BYTES = round((12514.7 * 1.9997 + 43.0) * 1024)
+
 
 def algo_bytes(t, rows, cols):
     return V.row_bytes(t, cols) * rows + 4 * cols + 4 * rows
@@ -239,6 +246,7 @@ def bench_decode(dev, host, n_tokens, path="both", n_layers=32, ctx=2048, n_disp
     """Greedy decode of the 7B Q4_K_M synthetic model (config 4) from position
     `ctx` with the KV cache prefilled N(0,1): the graph decoder (one graph
     launch per token) and, for comparison, the per-dispatch ops-table path."""
+    n_dispatch_tokens = min(n_dispatch_tokens, n_tokens)
     model = V.SynthModel(host, n_layers=n_layers, hidden=4096, ffn=11008, n_heads=32,
                          n_kv_heads=8, head_dim=128, vocab=32000, max_ctx=ctx + n_tokens + 1,
                          seed=SEED)
@@ -249,7 +257,7 @@ def bench_decode(dev, host, n_tokens, path="both", n_layers=32, ctx=2048, n_disp
     d = V.Decoder(host, be, model)
     d.load_kv(kc, vc, ctx)
     # per-dispatch path (src/vbs_specializer.c order through the ops table)
-    d.greedy(1, ctx, 2)
+    d.greedy(1, ctx, min(2, n_tokens))
     t0 = time.perf_counter()
     dtoks, dmargins = d.greedy(1, ctx, n_dispatch_tokens)
     dt_dispatch = time.perf_counter() - t0
@@ -264,7 +272,7 @@ def bench_decode(dev, host, n_tokens, path="both", n_layers=32, ctx=2048, n_disp
     # graph decoder over the same device weights and cache
     eager = path == "eager"
     g = V.GraphDecoder(dev, d, max_steps=n_tokens)
-    g.greedy(1, ctx, 2, eager)
+    g.greedy(1, ctx, min(2, n_tokens), eager)
     dev.sync()
     t0 = time.perf_counter()
     toks, margins = g.greedy(1, ctx, n_tokens, eager)
@@ -335,7 +343,10 @@ def main():
                    "issue": "one HIP graph of the 7 launches per step"},
         "pct_of_peak": round(100 * value / PEAK_HBM_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+                     "traffic": TRAFFIC_BYTES,
+                     "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, scaled by a "
+                                       "256 MiB copy (profiles/q4k_matvec_7b_layer_set.md)",
                      "kernel": "k_mv<Q4K> (matrix-core Q4_K matvec), 11008x4096 and 4096x11008",
                      "algorithmic_bytes_per_launch": r["big_bytes"],
                      "avg_launch_us": round(1e3 * r["avg_big_ms"], 3)},

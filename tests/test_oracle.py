@@ -337,3 +337,35 @@ def test_oracle_against_reference_library_random_blocks(orc, host):
     for u in rng.integers(0, 2 ** 32, 50000, dtype=np.uint64):
         f = struct.unpack("<f", struct.pack("<I", int(u)))[0]
         assert ref.vbs_f32_to_f16(f) == orc._f32_to_f16(f)
+
+
+@pytest.mark.skipif(not os.path.exists(REF_SO), reason="oracle/_ref not built here")
+def test_lns8_rows_against_reference_embedding(orc):
+    """LNS8 (value = 2^q * f32 scale) lives in the reference's host math, not in
+    vbs_dequant_block, so it is pinned through the reference CPU backend's
+    EMBEDDING op (vbs_host_embed_row -> vbs_host_dequant_row,
+    src/vbs_host_math.h:111-121): random codes (including those whose power
+    overflows to inf) and random scales, bit for bit."""
+    import ctypes as C
+    ref = V.Backend(C.CDLL(REF_SO), "g_vbs_cpu_backend")
+    assert ref.init()
+    rng = np.random.default_rng(40)
+    dim, rows = 256, 24
+    blocks = rng.integers(0, 256, (rows, dim // 32, 36), dtype=np.uint8)
+    scales = (rng.standard_normal((rows, dim // 32)) * 2.0 ** rng.integers(-140, -100, (rows, dim // 32)))
+    blocks[:, :, 32:36] = scales.astype(np.float32).view(np.uint8).reshape(rows, dim // 32, 4)
+    table = np.ascontiguousarray(blocks.reshape(rows, -1))
+    pipe = ref.ops.compile_embed_pipeline(ref.device(), V.LNS8, None, 0)
+    assert pipe
+    tb = ref.upload(table)
+    out_buf = ref.alloc(dim * 4)
+    for tok in range(rows):
+        keep = []
+        args = [V.Backend.buf_arg(tb), V.Backend.u32_arg(keep, tok), V.Backend.buf_arg(out_buf),
+                V.Backend.u32_arg(keep, dim)]
+        assert ref.dispatch(pipe, args)
+        want = ref.download(out_buf, (dim,), np.float32)
+        got = np.zeros(dim, np.float32)
+        assert orc._dequant_row(V.LNS8, np.ascontiguousarray(table[tok]).ctypes.data, dim,
+                                got.ctypes.data)
+        assert np.array_equal(bits(got), bits(want)), tok

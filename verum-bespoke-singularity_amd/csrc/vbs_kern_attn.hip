@@ -151,18 +151,19 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
-template <uint32_t HD, uint32_t GMAX>
-__global__ __launch_bounds__(256) void k_attn_chunk(
+template <uint32_t HD, uint32_t GMAX, uint32_t NWV>
+__global__ __launch_bounds__(64 * NWV) void k_attn_chunk(
     const float *__restrict__ q, const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc,
     float *__restrict__ part, uint32_t seq_len, const uint32_t *__restrict__ pos_dev,
     uint64_t layer_off, uint32_t nkh, uint32_t group, float scale, uint32_t stride_chunks) {
-    constexpr uint32_t LPP = HD / 8;         // lanes per position
-    constexpr uint32_t PPW = 64 / LPP;       // positions per wave per load
-    constexpr uint32_t NB = kChunk / 4 / PPW;  // loads per wave (K and V each)
+    constexpr uint32_t LPP = HD / 8;            // lanes per position
+    constexpr uint32_t PPW = 64 / LPP;          // positions per wave per load
+    constexpr uint32_t NB = kChunk / NWV / PPW;  // loads per wave (K and V each)
+    static_assert(NB >= 1 && NB * PPW * NWV == kChunk, "chunk split");
     extern __shared__ __align__(16) uint8_t chunk_lds[];
-    float *red = reinterpret_cast<float *>(chunk_lds);  // [4 waves][PPW][group][HD] acc
-    __shared__ float wmax[4][GMAX];
-    __shared__ float lsum[4 * PPW][GMAX];
+    float *red = reinterpret_cast<float *>(chunk_lds);  // [NWV][group][HD] acc
+    __shared__ float wmax[NWV][GMAX];
+    __shared__ float lsum[NWV][GMAX];
 
     const uint32_t chunk = blockIdx.x, kvh = blockIdx.y, t = threadIdx.x;
     const uint32_t wave = t >> 6, lane = t & 63u;
@@ -191,7 +192,8 @@ __global__ __launch_bounds__(256) void k_attn_chunk(
 #pragma unroll
     for (uint32_t g = 0; g < GMAX; g++) {
         const uint32_t gg = g < group ? g : 0u;
-        const float4 *qp = reinterpret_cast<const float4 *>(q + ((uint64_t)kvh * group + gg) * HD + 8u * c);
+        const float4 *qp =
+            reinterpret_cast<const float4 *>(q + ((uint64_t)kvh * group + gg) * HD + 8u * c);
         const float4 a = qp[0], b4 = qp[1];
         qv[g][0] = a.x; qv[g][1] = a.y; qv[g][2] = a.z; qv[g][3] = a.w;
         qv[g][4] = b4.x; qv[g][5] = b4.y; qv[g][6] = b4.z; qv[g][7] = b4.w;
@@ -228,58 +230,71 @@ __global__ __launch_bounds__(256) void k_attn_chunk(
     }
     __syncthreads();
 
-    // ---- e = exp(score - m); acc over this lane's positions -------------------
-    float acc[GMAX][8], l[GMAX];
+    // ---- e = exp(score - m); acc and l over this wave's positions ------------
+    float cm[GMAX];
 #pragma unroll
     for (uint32_t g = 0; g < GMAX; g++) {
-        const float m = fmaxf(fmaxf(wmax[0][g], wmax[1][g]), fmaxf(wmax[2][g], wmax[3][g]));
-        l[g] = 0.f;
+        float m = wmax[0][g];
 #pragma unroll
-        for (uint32_t j = 0; j < 8; j++) acc[g][j] = 0.f;
+        for (uint32_t k = 1; k < NWV; k++) m = fmaxf(m, wmax[k][g]);
+        cm[g] = m;
+        float l = 0.f, acc[8];
+#pragma unroll
+        for (uint32_t j = 0; j < 8; j++) acc[j] = 0.f;
 #pragma unroll
         for (uint32_t b = 0; b < NB; b++) {
             const float e = sc[b][g] == -INFINITY ? 0.f : expf(__fsub_rn(sc[b][g], m));
             const uint32_t vw[4] = {vr[b].x, vr[b].y, vr[b].z, vr[b].w};
-            l[g] += e;
+            l += e;
 #pragma unroll
             for (uint32_t j = 0; j < 8; j++)
-                acc[g][j] = e == 0.f ? acc[g][j] : fmaf(e, hcvt(vw[j >> 1] >> (16u * (j & 1u))), acc[g][j]);
+                acc[j] = e == 0.f ? acc[j] : fmaf(e, hcvt(vw[j >> 1] >> (16u * (j & 1u))), acc[j]);
         }
-    }
-    // per-lane partials to LDS: acc by (wave, slot, g, dim), l by (wave, slot, g)
+        // add the wave's position slots (lanes LPP apart hold the same dims)
 #pragma unroll
-    for (uint32_t g = 0; g < GMAX; g++) {
-        if (g < group) {
-            float *dst = red + (((wave * PPW + slot) * group + g) * HD + 8u * c);
-            reinterpret_cast<float4 *>(dst)[0] = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
-            reinterpret_cast<float4 *>(dst)[1] = make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
-            if (c == 0) lsum[wave * PPW + slot][g] = l[g];
+        for (uint32_t off = LPP; off < 64u; off <<= 1) {
+            l += __shfl_xor(l, (int)off, 64);
+#pragma unroll
+            for (uint32_t j = 0; j < 8; j++) acc[j] += __shfl_xor(acc[j], (int)off, 64);
+        }
+        if (g < group && slot == 0) {
+            float *dst = red + ((wave * group + g) * HD + 8u * c);
+            reinterpret_cast<float4 *>(dst)[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+            reinterpret_cast<float4 *>(dst)[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+            if (c == 0) lsum[wave][g] = l;
         }
     }
     __syncthreads();
 
-    // ---- combine the 4 * PPW partials of the chunk and write (m, l, acc) -------
-    for (uint32_t i = t; i < group * HD; i += 256u) {
+    // ---- combine the waves' partials of the chunk and write (m, l, acc) ------
+    for (uint32_t i = t; i < group * HD; i += 64u * NWV) {
         const uint32_t g = i / HD, d = i % HD;
         float a = 0.f;
 #pragma unroll
-        for (uint32_t k = 0; k < 4u * PPW; k++) a += red[(k * group + g) * HD + d];
+        for (uint32_t k = 0; k < NWV; k++) a += red[(k * group + g) * HD + d];
         float *dst = part + ((uint64_t)(kvh * group + g) * stride_chunks + chunk) * (HD + 2u);
         dst[2u + d] = a;
         if (d == 0) {
             float ls = 0.f;
 #pragma unroll
-            for (uint32_t k = 0; k < 4u * PPW; k++) ls += lsum[k][g];
-            dst[0] = fmaxf(fmaxf(wmax[0][g], wmax[1][g]), fmaxf(wmax[2][g], wmax[3][g]));
+            for (uint32_t k = 0; k < NWV; k++) ls += lsum[k][g];
+            float m = wmax[0][g];
+#pragma unroll
+            for (uint32_t k = 1; k < NWV; k++) m = fmaxf(m, wmax[k][g]);
+            dst[0] = m;
             dst[1] = ls;
         }
     }
+    (void)cm;
 }
 
 // ---- merge of the chunks -------------------------------------------------------
-// One workgroup per q head: the chunk weights e^(m_c - M) go to LDS, then
-// thread (d, slice) sums a slice of the chunks for dim d and the slices are
-// added in LDS in a fixed order.
+// One workgroup per q head. Every partial is requested up front: thread
+// (d, slice) loads acc_c[d] of its chunks c = slice, slice + ns, ... while the
+// chunk maxima and sums are combined (block max, weights e^(m_c - M) in LDS,
+// L = sum l_c e^(m_c - M)); the slices are then added in LDS in a fixed order.
+constexpr uint32_t kMergeBatch = 16;  // chunks per thread held in registers at once
+
 __global__ __launch_bounds__(256) void k_attn_merge(const float *__restrict__ part,
                                                     float *__restrict__ out, uint32_t hd,
                                                     uint32_t n_chunks, uint32_t stride_chunks,
@@ -291,6 +306,15 @@ __global__ __launch_bounds__(256) void k_attn_merge(const float *__restrict__ pa
     const uint32_t h = blockIdx.x, t = threadIdx.x, lane = t & 63u, wave = t >> 6;
     if (pos_dev) n_chunks = (pos_dev[0] + kChunk) / kChunk;  // chunks of seq_len = pos + 1
     const float *ph = part + (uint64_t)h * stride_chunks * (hd + 2u);
+    const uint32_t ns = 256u / hd;
+    const uint32_t d = t % hd, s = t / hd;
+    // this thread's first batch of acc values, requested before anything else
+    float av[kMergeBatch];
+#pragma unroll
+    for (uint32_t k = 0; k < kMergeBatch; k++) {
+        const uint32_t c = s + k * ns;
+        av[k] = (s < ns && c < n_chunks) ? ph[(uint64_t)c * (hd + 2u) + 2u + d] : 0.f;
+    }
     // M = max_c m_c
     float M = -INFINITY;
     for (uint32_t c = t; c < n_chunks; c += 256u) M = fmaxf(M, ph[(uint64_t)c * (hd + 2u)]);
@@ -307,17 +331,18 @@ __global__ __launch_bounds__(256) void k_attn_merge(const float *__restrict__ pa
         L = fmaf(pc[1], wc, L);
     }
     L = wave_sum(L);
-    __syncthreads();
     if (lane == 0) red[4 + wave] = L;
     __syncthreads();
     L = (red[4] + red[5]) + (red[6] + red[7]);
-    // acc[d] = sum_c w_c * acc_c[d]: thread (d, slice) over chunks slice, slice + ns, ...
-    const uint32_t ns = 256u / hd;
-    const uint32_t d = t % hd, s = t / hd;
+    // acc[d] = sum_c w_c * acc_c[d] over this thread's chunks
     float a = 0.f;
     if (s < ns) {
-#pragma unroll 8
-        for (uint32_t c = s; c < n_chunks; c += ns)
+#pragma unroll
+        for (uint32_t k = 0; k < kMergeBatch; k++) {
+            const uint32_t c = s + k * ns;
+            if (c < n_chunks) a = fmaf(av[k], w[c], a);
+        }
+        for (uint32_t c = s + kMergeBatch * ns; c < n_chunks; c += ns)
             a = fmaf(ph[(uint64_t)c * (hd + 2u) + 2u + d], w[c], a);
     }
     sl[t] = a;
@@ -338,22 +363,12 @@ static hipError_t launch_chunk_t(dim3 grid, hipStream_t s, const float *q, const
                                  const uint16_t *vc, float *part, uint32_t seq_len,
                                  const uint32_t *pos_dev, uint64_t layer_off, uint32_t nkh,
                                  uint32_t group, float scale) {
+    // eight waves of 64 / 8 positions where a wave still covers whole loads
     constexpr uint32_t PPW = 64 / (HD / 8);
-    const size_t lds = (size_t)4 * PPW * group * HD * sizeof(float);
-    if (lds > 48u * 1024u) {  // with the static arrays, beyond the default window: opt in once
-        static size_t granted = 0;
-        if (lds > granted) {
-            if (hipFuncSetAttribute((const void *)k_attn_chunk<HD, GMAX>,
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
-                hipSuccess) {
-                (void)hipGetLastError();
-                return hipErrorNotSupported;
-            }
-            granted = lds;
-        }
-    }
-    k_attn_chunk<HD, GMAX><<<grid, 256, lds, s>>>(q, kc, vc, part, seq_len, pos_dev, layer_off,
-                                                  nkh, group, scale, grid.x);
+    constexpr uint32_t NWV = kChunk / PPW >= 8u ? 8u : kChunk / PPW;
+    const size_t lds = (size_t)NWV * group * HD * sizeof(float);
+    k_attn_chunk<HD, GMAX, NWV><<<grid, 64u * NWV, lds, s>>>(q, kc, vc, part, seq_len, pos_dev,
+                                                            layer_off, nkh, group, scale, grid.x);
     return hipGetLastError();
 }
 
