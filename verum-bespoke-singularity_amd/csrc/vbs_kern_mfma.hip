@@ -69,11 +69,6 @@ __host__ __device__ inline XqLayout xq_layout(uint32_t cols) {
 
 size_t xq_bytes(uint32_t cols) { return (size_t)xq_layout(cols).bytes; }
 
-__device__ __forceinline__ uint32_t pack4b(int a, int b, int c, int d) {
-    return (uint32_t)(a & 255) | ((uint32_t)(b & 255) << 8) | ((uint32_t)(c & 255) << 16) |
-           ((uint32_t)d << 24);
-}
-
 // Digits of one 16-element half sub-block `item` (values in v); the two halves
 // of a sub-block are adjacent lanes and exchange their maximum and sum. Writes
 // the three planes, xs (by the even half) and xs16 into `xq` (LDS or global).
@@ -94,23 +89,28 @@ __device__ __forceinline__ void prep_item(const float *v, uint32_t cols, uint32_
     int e;
     (void)frexpf(amax, &e);  // amax < 2^e
     const bool finite = amax <= 3.4028235e38f;
+    // X = rint(x 2^(22-e)) with |X| < 2^22: adding 1.5 * 2^23 rounds to the
+    // nearest integer (ties to even, as rint) and leaves 2^22 + X in the low 23
+    // bits. U = X + 0x808080 then holds the balanced digits as biased bytes:
+    // D_i = byte_i(U) - 128, i.e. byte_i(U) ^ 0x80 in int8 form (the same
+    // digits as D0 = int8(X), D1 = int8((X - D0) / 256), ...). Items whose
+    // maximum is not finite get a NaN scale, which makes their digits moot.
+    uint32_t u[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++)
+        u[k] = __float_as_uint(__fadd_rn(ldexpf(v[k], 22 - e), 12582912.0f)) + 0x408080u;
     uint32_t d0[4], d1[4], d2[4];
 #pragma unroll
     for (int q = 0; q < 4; q++) {
-        int D0[4], D1[4], D2[4];
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const int X = finite ? __float2int_rn(ldexpf(v[4 * q + k], 22 - e)) : 0;
-            const int a = (int)(int8_t)X;
-            const int X1 = (X - a) >> 8;
-            const int c = (int)(int8_t)X1;
-            D0[k] = a;
-            D1[k] = c;
-            D2[k] = (X1 - c) >> 8;
-        }
-        d0[q] = pack4b(D0[0], D0[1], D0[2], D0[3]);
-        d1[q] = pack4b(D1[0], D1[1], D1[2], D1[3]);
-        d2[q] = pack4b(D2[0], D2[1], D2[2], D2[3]);
+        // bytes of elements 4q..4q+3: pairs first, then the planes
+        const uint32_t *w = u + 4 * q;
+        const uint32_t lo01 = __builtin_amdgcn_perm(w[1], w[0], 0x05010400u);
+        const uint32_t lo23 = __builtin_amdgcn_perm(w[3], w[2], 0x05010400u);
+        const uint32_t hi01 = __builtin_amdgcn_perm(w[1], w[0], 0x0c0c0602u);
+        const uint32_t hi23 = __builtin_amdgcn_perm(w[3], w[2], 0x0c0c0602u);
+        d0[q] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u) ^ 0x80808080u;
+        d1[q] = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u) ^ 0x80808080u;
+        d2[q] = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u) ^ 0x80808080u;
     }
     const uint32_t off = item * 16u;
     *reinterpret_cast<uint4 *>(xq + off) = make_uint4(d0[0], d0[1], d0[2], d0[3]);
@@ -175,14 +175,13 @@ __device__ __forceinline__ float plane_sum(i32x4 D) {
 
 // ---- weight types ---------------------------------------------------------------------
 // Where a wave's tile lives: row r of the matrix starts at w + r * rb; rows of
-// the tile past the end re-read the last row; w_end bounds every load.
+// the tile past the end re-read the last row; no load reaches past w + bytes.
+// Offsets are 32-bit (the matrix is below 4 GiB) from the wave-uniform base w,
+// so loads take the scalar-base form.
 struct Src {
-    const uint8_t *w, *w_end;
-    uint64_t rb;
-    uint32_t row0, rows;
-    __device__ const uint8_t *row(uint32_t n) const {
-        return w + (uint64_t)min(row0 + n, rows - 1u) * rb;
-    }
+    const uint8_t *w;
+    uint32_t bytes, rb, row0, rows;
+    __device__ uint32_t row(uint32_t n) const { return min(row0 + n, rows - 1u) * rb; }
 };
 
 // load(): this lane's share of block b of the tile (NLD 16-byte words).
@@ -191,10 +190,10 @@ struct Src {
 struct Q4K {
     static constexpr uint32_t BYTES = 144, NLD = 3, SCRATCH = 0;
     __device__ static void load(const Src &src, uint32_t b, uint32_t n, uint32_t g, u32x4 *r) {
-        const uint8_t *blk = src.row(n) + (uint64_t)b * BYTES;
+        const uint8_t *blk = src.w + (src.row(n) + b * BYTES);
         r[0] = lda4(blk);
-        r[1] = lda4(blk + 16u + 16u * g);
-        r[2] = lda4(blk + 80u + 16u * g);
+        r[1] = lda4(blk + 16u * g + 16u);
+        r[2] = lda4(blk + 16u * g + 80u);
     }
     __device__ static float dot(const u32x4 *r, uint8_t *, const Src &, const uint8_t *xq,
                                 const XqLayout &L, uint32_t cols, uint32_t b, uint32_t n,
@@ -237,7 +236,7 @@ struct Q4K {
 
 // 16 aligned bytes at a, of which only those below `end` (2-byte aligned) are
 // read; the rest are zero.
-__device__ __noinline__ u32x4 ld_tail(const uint8_t *a, const uint8_t *end) {
+__device__ __forceinline__ u32x4 ld_tail(const uint8_t *a, const uint8_t *end) {
     uint32_t v[4];
 #pragma unroll
     for (int k = 0; k < 4; k++) {
@@ -255,21 +254,34 @@ struct Q6K {
     // run at about half the rate of aligned ones. So the wave reads each block
     // of its 16 rows as 14 aligned 16-byte chunks per row (covering the block
     // at any 2-byte offset), chunk c = 14n + k going to lane c mod 64, stores
-    // them to its LDS scratch in row order and reads its fields from there.
+    // them to its LDS scratch in row order and reads its fields from there as
+    // 4-byte aligned words, shifted into place in registers (16-byte LDS reads
+    // at 2-byte aligned addresses are several times slower).
     static constexpr uint32_t BYTES = 210, NLD = 4, SCRATCH = 16u * 224u;
     __device__ static void load(const Src &src, uint32_t b, uint32_t n, uint32_t g, u32x4 *r) {
         const uint32_t lane = 16u * g + n;
+        // only the last block of the matrix's last row has chunks that reach
+        // past its end (by at most 14 bytes); those loads are bounded
+        const uint32_t wlo = (uint32_t)(uintptr_t)src.w & 15u;
+        const uint32_t last = src.row(15u) + b * BYTES;
+        const bool edge = __builtin_amdgcn_readfirstlane(
+                              (uint32_t)(last - ((last + wlo) & 15u) + 224u > src.bytes)) != 0u;
+        uint32_t a[4];
 #pragma unroll
         for (uint32_t i = 0; i < 4; i++) {
-            const uint32_t c = lane + 64u * i;
-            if (i < 3u || c < 224u) {
-                const uint8_t *s = src.row(c / 14u) + (uint64_t)b * BYTES;
-                const uint8_t *a = reinterpret_cast<const uint8_t *>(
-                    ((uintptr_t)s & ~(uintptr_t)15) + 16u * (c % 14u));
-                r[i] = a + 16 <= src.w_end ? lda4(a) : ld_tail(a, src.w_end);
-            } else {
-                r[i] = u32x4{0u, 0u, 0u, 0u};
-            }
+            // chunk c of the tile: 16 aligned bytes
+            const uint32_t c = min(lane + 64u * i, 223u);
+            const uint32_t s = src.row(c / 14u) + b * BYTES;
+            a[i] = s - ((s + wlo) & 15u) + 16u * (c % 14u);
+        }
+        if (!edge) {
+#pragma unroll
+            for (uint32_t i = 0; i < 4; i++) r[i] = lda4(src.w + a[i]);
+        } else {
+            const uint8_t *end = src.w + src.bytes;
+#pragma unroll
+            for (uint32_t i = 0; i < 4; i++)
+                r[i] = a[i] + 16u <= src.bytes ? lda4(src.w + a[i]) : ld_tail(src.w + a[i], end);
         }
     }
     __device__ static float dot(const u32x4 *r, uint8_t *scratch, const Src &src,
@@ -281,17 +293,34 @@ struct Q6K {
             const uint32_t c = lane + 64u * i;
             if (i < 3u || c < 224u) *reinterpret_cast<u32x4 *>(scratch + 16u * c) = r[i];
         }
-        // row n's block starts (its address mod 16) into its 224 scratch bytes
-        const uint8_t *blk = scratch + 224u * n +
-                             (uint32_t)((uintptr_t)(src.row(n) + (uint64_t)b * BYTES) & 15u);
+        // row n's block starts o = (its address mod 16) into its 224 scratch
+        // bytes; rw is the 4-byte aligned word at or below the start and sh
+        // (0 or 2) the byte shift from there. Every word read lies in the row.
+        const uint32_t o = ((uint32_t)(uintptr_t)src.w + src.row(n) + b * BYTES) & 15u;
+        const uint32_t *rw = reinterpret_cast<const uint32_t *>(scratch + 224u * n + (o & 12u));
+        const uint32_t sh = o & 2u;
+        // 16 bytes at block byte f (a multiple of 4)
+        auto field = [&](uint32_t f) {
+            const uint32_t *p = rw + f / 4u;
+            const uint32_t w0 = p[0], w1 = p[1], w2 = p[2], w3 = p[3], w4 = p[4];
+            const u32x4 v = {__builtin_amdgcn_alignbyte(w1, w0, sh),
+                             __builtin_amdgcn_alignbyte(w2, w1, sh),
+                             __builtin_amdgcn_alignbyte(w3, w2, sh),
+                             __builtin_amdgcn_alignbyte(w4, w3, sh)};
+            return v;
+        };
         // lane group g = (h, u) = (g >> 1, g & 1): half h of the block, elements
         // 16u..16u+15 of each of its 32-element quarters
         const uint32_t h = g >> 1, u = g & 1u;
-        const u32x4 qe = ldu(blk + 64u * h + 16u * u);         // ql, quarters 0 / 2
-        const u32x4 qo = ldu(blk + 64u * h + 32u + 16u * u);   // ql, quarters 1 / 3
-        const u32x4 qh = ldu(blk + 128u + 32u * h + 16u * u);  // qh, 2 bits per quarter
-        const u32x4 scw = ldu(blk + 192u);                     // int8 scales
-        const uint32_t dbits = *reinterpret_cast<const uint16_t *>(blk + 208u);
+        const u32x4 qe = field(64u * h + 16u * u);         // ql, quarters 0 / 2
+        const u32x4 qo = field(64u * h + 32u + 16u * u);   // ql, quarters 1 / 3
+        const u32x4 qh = field(128u + 32u * h + 16u * u);  // qh, 2 bits per quarter
+        // int8 scales 8h..8h+7 (bytes 192 + 8h) and the f16 d (bytes 208..209)
+        const uint32_t *ps = rw + 48u + 2u * h;
+        const uint32_t s0 = ps[0], s1 = ps[1], s2 = ps[2];
+        const uint32_t sc_lo = __builtin_amdgcn_alignbyte(s1, s0, sh);
+        const uint32_t sc_hi = __builtin_amdgcn_alignbyte(s2, s1, sh);
+        const uint32_t dbits = (rw[52] >> (8u * sh)) & 0xFFFFu;
         // MFMA q (quarter q of both halves): lane group g holds scale group
         // 8h + 2q + u; A row n = 4t+p carries plane p of the group of lane group t
         const uint32_t t = n >> 2, p = n & 3u;
@@ -300,7 +329,6 @@ struct Q6K {
         const float *xs16 = reinterpret_cast<const float *>(xq + L.xs16);
         const uint32_t qew[4] = {qe.x, qe.y, qe.z, qe.w}, qow[4] = {qo.x, qo.y, qo.z, qo.w};
         const uint32_t qhw[4] = {qh.x, qh.y, qh.z, qh.w};
-        const uint32_t sc_lo = h ? scw.z : scw.x, sc_hi = h ? scw.w : scw.y;
         const uint32_t a0 = p * cols + 256u * b + 128u * (t >> 1) + 16u * (t & 1u);
         float acc = 0.f;
 #pragma unroll
@@ -363,34 +391,40 @@ struct MvArgs {
 template <class T, uint32_t KS, uint32_t TPW, uint32_t MAXT, bool NORM, int EPI, bool TWO>
 __global__ __launch_bounds__(MAXT) void k_mvf(const MvArgs a) {
     extern __shared__ __align__(16) uint8_t xq[];
-    __shared__ float red[2][16][16];
+    __shared__ float red[TPW][16][16];
     __shared__ double part[32];
+    constexpr uint32_t NI = KS * TPW;  // work items (tile, block) per wave
+    constexpr uint32_t P = 2;          // items in flight ahead of the one computed
     const uint32_t cols = a.cols;
     const uint32_t nblk = cols >> 8;
-    const uint64_t rb = (uint64_t)nblk * T::BYTES;
+    const uint32_t rb = nblk * T::BYTES;
     const XqLayout L = xq_layout(cols);
     const uint32_t nth = blockDim.x;
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const uint32_t nw = nth >> 6;
     const uint32_t n = lane & 15u, g = lane >> 4;
-    const uint32_t b0 = wave * KS;
     const uint32_t total = a.tile_end[a.nmat - 1u];
 
     // matrix and local tile of this workgroup's tile j
-    auto tile_of = [&](uint32_t j, uint32_t &m, uint32_t &lt) {
+    uint32_t mt[TPW], lt[TPW];
+    Src src[TPW];
+#pragma unroll
+    for (uint32_t j = 0; j < TPW; j++) {
         if (EPI == E_SILU) {
-            m = j;
-            lt = blockIdx.x;
+            mt[j] = j;
+            lt[j] = blockIdx.x;
         } else {
             const uint32_t gt = min(blockIdx.x * TPW + j, total - 1u);
-            m = (gt >= a.tile_end[0]) + (a.nmat > 2u && gt >= a.tile_end[1]);
-            lt = gt - (m ? a.tile_end[m - 1u] : 0u);
+            mt[j] = (gt >= a.tile_end[0]) + (a.nmat > 2u && gt >= a.tile_end[1]);
+            lt[j] = gt - (mt[j] ? a.tile_end[mt[j] - 1u] : 0u);
         }
-    };
-    auto src_of = [&](uint32_t m, uint32_t lt) {
-        const uint8_t *w = a.w[m];
-        return Src{w, w + (uint64_t)a.rows[m] * rb, rb, lt * 16u, a.rows[m]};
-    };
+        const uint8_t *w = a.w[mt[j]];
+        src[j] = Src{w, a.rows[mt[j]] * rb, rb, lt[j] * 16u, a.rows[mt[j]]};
+    }
+    // item i: tile i / KS, block wave + nw * (i % KS); at each step the
+    // workgroup's waves read adjacent blocks of the same rows. Slots past the
+    // row re-read its last block and contribute zero.
+    auto blk = [&](uint32_t i) { return wave + nw * (i % KS); };
 
     // 1. x first (one or two 16-element items per thread; with the RMSNorm also
     // its weights)
@@ -404,17 +438,11 @@ __global__ __launch_bounds__(MAXT) void k_mvf(const MvArgs a) {
         if (TWO) load16(a.norm_w, cols, i1, w1);
     }
 
-    // 2. every weight load of this wave (tail tiles, rows and blocks re-read
-    // valid data and are masked below)
-    u32x4 r[TPW][KS][T::NLD];
+    // 2. the first P items' weights
+    u32x4 r[NI][T::NLD];
 #pragma unroll
-    for (uint32_t j = 0; j < TPW; j++) {
-        uint32_t m, lt;
-        tile_of(j, m, lt);
-        const Src src = src_of(m, lt);
-#pragma unroll
-        for (uint32_t k = 0; k < KS; k++) T::load(src, min(b0 + k, nblk - 1u), n, g, r[j][k]);
-    }
+    for (uint32_t i = 0; i < P && i < NI; i++)
+        T::load(src[i / KS], min(blk(i), nblk - 1u), n, g, r[i]);
     __builtin_amdgcn_sched_barrier(0);
 
     // 3. (RMSNorm and) x -> digits in LDS while the weights arrive. The sum of
@@ -454,56 +482,69 @@ __global__ __launch_bounds__(MAXT) void k_mvf(const MvArgs a) {
     if (threadIdx.x == 0) *reinterpret_cast<uint4 *>(xq + L.zero) = make_uint4(0, 0, 0, 0);
     __syncthreads();
 
-    // 4. tiles
+    // 4. stream: issue item i + P, then compute item i (loads return in issue
+    // order, so the wait is for item i alone)
     uint8_t *scratch = xq + L.bytes + wave * T::SCRATCH;
+    float acc[TPW];
+#pragma unroll
+    for (uint32_t j = 0; j < TPW; j++) acc[j] = 0.f;
+#pragma unroll
+    for (uint32_t i = 0; i < NI; i++) {
+        if (i + P < NI) T::load(src[(i + P) / KS], min(blk(i + P), nblk - 1u), n, g, r[i + P]);
+        __builtin_amdgcn_sched_barrier(0);
+        const float part_i = T::dot(r[i], scratch, src[i / KS], xq, L, cols,
+                                    min(blk(i), nblk - 1u), n, g);
+        acc[i / KS] += blk(i) < nblk ? part_i : 0.f;
+        // finish item i here: otherwise its arithmetic may sink past later
+        // items and hold their registers
+        asm volatile("" ::"v"(acc[i / KS]));
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // 5. the four lane groups of a row hold different groups of its blocks;
+    // then the waves' partial sums, tile j finished by wave j (both tiles by
+    // wave 0 for E_SILU)
+#pragma unroll
+    for (uint32_t j = 0; j < TPW; j++) {
+        acc[j] += __shfl_xor(acc[j], 16, 64);
+        acc[j] += __shfl_xor(acc[j], 32, 64);
+        if (nw > 1u && lane < 16u) red[j][wave][n] = acc[j];
+    }
+    if (nw > 1u) __syncthreads();
     float prev = 0.f;  // E_SILU: the gate row value
 #pragma unroll
     for (uint32_t j = 0; j < TPW; j++) {
-        uint32_t m, lt;
-        tile_of(j, m, lt);
-        const Src src = src_of(m, lt);
-        float acc = 0.f;
-#pragma unroll
-        for (uint32_t k = 0; k < KS; k++) {
-            const bool live = b0 + k < nblk;  // slots past the row contribute zero
-            const float part_k =
-                T::dot(r[j][k], scratch, src, xq, L, cols, min(b0 + k, nblk - 1u), n, g);
-            acc += live ? part_k : 0.f;
-        }
-        // the four lane groups of a row hold different groups of its blocks
-        acc += __shfl_xor(acc, 16, 64);
-        acc += __shfl_xor(acc, 32, 64);
+        if (wave != (EPI == E_SILU ? 0u : j % nw)) continue;
+        float t = acc[j];
         if (nw > 1u) {
-            if (lane < 16u) red[j & 1u][wave][n] = acc;
-            __syncthreads();
-            if (wave != 0) continue;
-            acc = 0.f;
-            for (uint32_t k = 0; k < nw; k++) acc += red[j & 1u][k][n];
+            t = 0.f;
+            for (uint32_t k = 0; k < nw; k++) t += red[j][k][n];
         }
-        // wave 0: every lane holds the value of row n of the tile
+        // every lane holds the value of row n of the tile
+        const uint32_t m = mt[j];
         const bool own = (EPI == E_SILU || blockIdx.x * TPW + j < total);
-        const uint32_t row = lt * 16u + n;
+        const uint32_t row = lt[j] * 16u + n;
         const bool st = lane < 16u && own && row < a.rows[m];
         if (EPI == E_STORE) {
-            if (st) a.y[m][row] = acc;
+            if (st) a.y[m][row] = t;
         } else if (EPI == E_ACC) {
-            if (st) a.y[m][row] = __fadd_rn(a.y[m][row], acc);
+            if (st) a.y[m][row] = __fadd_rn(a.y[m][row], t);
         } else if (EPI == E_SILU) {
             if (j == 0) {
-                prev = acc;
+                prev = t;
             } else if (st) {
                 const float den = __fadd_rn(1.0f, expf(-prev));
-                a.y[0][row] = __fmul_rn(__fdiv_rn(prev, den), acc);
+                a.y[0][row] = __fmul_rn(__fdiv_rn(prev, den), t);
             }
         } else {  // E_QKV
             const uint32_t role = a.role0 + m;
-            const float other = __shfl_xor(acc, 1, 64);  // the RoPE partner row
+            const float other = __shfl_xor(t, 1, 64);  // the RoPE partner row
             const uint32_t p = a.pos[0];
-            float v = acc;
+            float v = t;
             if (role < 2u) {
                 const float2 cs = a.rope[(uint64_t)p * (a.hd / 2u) + (row % a.hd) / 2u];
                 const bool even = (row & 1u) == 0u;
-                const float x0 = even ? acc : other, x1 = even ? other : acc;
+                const float x0 = even ? t : other, x1 = even ? other : t;
                 v = even ? __fsub_rn(__fmul_rn(x0, cs.x), __fmul_rn(x1, cs.y))
                          : __fadd_rn(__fmul_rn(x0, cs.y), __fmul_rn(x1, cs.x));
             }
@@ -522,23 +563,15 @@ struct MvPlan {
     uint32_t ks, tpw, nw;
 };
 
-// Super-blocks per wave and tiles per workgroup (measured on the 7B shapes).
-// Every combination used keeps its loads in registers without spilling:
-// Q4_K two super-blocks x three tiles, three x one; Q6_K two x two only with
-// at most 8 waves (a 256-VGPR budget), else one tile.
+// Blocks per wave (KS) and waves per tile: enough waves to split the row and
+// enough items per wave that the stream runs ahead of the arithmetic.
 template <class T>
-static MvPlan mv_plan(uint32_t cols, uint32_t tiles) {
+static MvPlan mv_plan(uint32_t cols) {
     const uint32_t nblk = cols / 256u;
     MvPlan p;
-    p.ks = nblk <= 32u ? 2u : 3u;
+    p.ks = nblk <= 32u ? 4u : nblk <= 48u ? 6u : 8u;
     p.nw = (nblk + p.ks - 1u) / p.ks;
     p.tpw = 1u;
-    if (tiles > 512u && p.ks == 2u) {
-        if (T::NLD == 3u)
-            p.tpw = tiles <= 1600u ? 3u : 2u;
-        else if (p.nw <= 8u)
-            p.tpw = 2u;
-    }
     return p;
 }
 
@@ -571,41 +604,31 @@ static hipError_t launch_t(const MvArgs &a, uint32_t nw, uint32_t wgs, hipStream
 template <class T, bool NORM, int EPI>
 static hipError_t launch_plan(const MvArgs &a, hipStream_t s) {
     const uint32_t total = a.tile_end[a.nmat - 1u];
-    MvPlan p = mv_plan<T>(a.cols, total);
-    // the RMSNorm prologue keeps more of x live: at most two tiles per
-    // workgroup under the 128-VGPR budget of 16 waves, none for wide Q6_K rows
-    if (NORM && p.nw > 8u && p.tpw > 2u) p.tpw = 2u;
-    if (NORM && T::NLD > 3u && p.ks == 3u) return hipErrorNotSupported;
-    if (EPI == E_SILU) p.tpw = 2u;  // a gate tile and the same up tile
+    const MvPlan p = mv_plan<T>(a.cols);
+    constexpr uint32_t TPW = EPI == E_SILU ? 2u : 1u;  // a gate tile and the same up tile
     if (p.nw > 16u || a.cols / 16u > 2u * 64u * p.nw) return hipErrorNotSupported;
-    if (p.ks == 3u && p.tpw != 1u) return hipErrorNotSupported;
-    const uint32_t wgs = EPI == E_SILU ? a.tile_end[0] : (total + p.tpw - 1u) / p.tpw;
-#define VBS_MV(KS, TPW, MAXT) return launch_t<T, KS, TPW, MAXT, NORM, EPI>(a, p.nw, wgs, s)
-    if (p.ks == 3u) VBS_MV(3, 1, 1024);
-    if (p.tpw == 1u) {
-        if (p.nw <= 8u) VBS_MV(2, 1, 512);
-        VBS_MV(2, 1, 1024);
+    const uint32_t wgs = EPI == E_SILU ? a.tile_end[0] : total;
+#define VBS_MV(KS, MAXT) return launch_t<T, KS, TPW, MAXT, NORM, EPI>(a, p.nw, wgs, s)
+    if (p.ks == 4u) {
+        if (p.nw <= 8u) VBS_MV(4, 512);
+        VBS_MV(4, 1024);
     }
-    if constexpr (T::NLD == 3u) {
-        if (p.tpw == 3u) {
-            if (p.nw <= 8u) VBS_MV(2, 3, 512);
-            VBS_MV(2, 3, 1024);
-        }
-        if (p.nw <= 8u) VBS_MV(2, 2, 512);
-        VBS_MV(2, 2, 1024);
-    } else {
-        if (p.nw <= 8u) VBS_MV(2, 2, 512);
-        return hipErrorNotSupported;
+    if (p.ks == 6u) {
+        if (p.nw <= 8u) VBS_MV(6, 512);
+        VBS_MV(6, 1024);
     }
+    VBS_MV(8, 1024);
 #undef VBS_MV
 }
 
 // Shape and alignment range of the matrix-core path: at most 16 waves of at
-// most 3 super-blocks, x items fit two per thread; Q4_K rows are 16-byte
+// most 8 super-blocks (the digits of x and the Q6_K scratch must also fit the
+// LDS, else the launch reports it unsupported); Q4_K rows are 16-byte
 // multiples, so its 16-byte loads need an aligned w; Q6_K aligns every load.
-static bool mv_fits(int type, const uint8_t *w, const float *x, uint32_t cols) {
+static bool mv_fits(int type, const uint8_t *w, const float *x, uint32_t cols, uint32_t rows) {
     if (type != kQ4_K && type != kQ6_K) return false;
-    if (cols % 256u || cols / 256u > 48u || ((uintptr_t)x & 3u)) return false;
+    if (cols % 256u || cols / 256u > 128u || ((uintptr_t)x & 3u)) return false;
+    if ((uint64_t)rows * (cols / 256u) * (type == kQ4_K ? 144u : 210u) >= (1ull << 32)) return false;
     return ((uintptr_t)w & (type == kQ4_K ? 15u : 1u)) == 0;
 }
 
@@ -624,7 +647,7 @@ static void set_tiles(MvArgs &a) {
 
 hipError_t launch_kq_linear(int type, const uint8_t *w, const float *x, float *y, uint32_t cols,
                             uint32_t rows, int accumulate, hipStream_t s) {
-    if (rows == 0 || !mv_fits(type, w, x, cols)) return hipErrorNotSupported;
+    if (rows == 0 || !mv_fits(type, w, x, cols, rows)) return hipErrorNotSupported;
     MvArgs a{};
     a.w[0] = w;
     a.y[0] = y;
@@ -639,7 +662,7 @@ hipError_t launch_kq_linear(int type, const uint8_t *w, const float *x, float *y
 hipError_t launch_kq_norm_linear(int type, const uint8_t *w, const float *x, const float *norm_w,
                                  float eps, float *y, uint32_t cols, uint32_t rows,
                                  hipStream_t s) {
-    if (rows == 0 || !mv_fits(type, w, x, cols)) return hipErrorNotSupported;
+    if (rows == 0 || !mv_fits(type, w, x, cols, rows)) return hipErrorNotSupported;
     MvArgs a{};
     a.w[0] = w;
     a.y[0] = y;
@@ -661,7 +684,7 @@ hipError_t launch_kq_qkv(int type, const uint8_t *const wqkv[3], uint32_t n_mat,
     if (n_mat == 0 || n_mat > 3u || role0 + n_mat > 3u || (hd & 1u)) return hipErrorNotSupported;
     MvArgs a{};
     for (uint32_t m = 0; m < n_mat; m++) {
-        if (!mv_fits(type, wqkv[m], x, cols) || rows[m] == 0 || (n_mat > 1u && rows[m] % 16u))
+        if (!mv_fits(type, wqkv[m], x, cols, rows[m]) || rows[m] == 0 || (n_mat > 1u && rows[m] % 16u))
             return hipErrorNotSupported;
         a.w[m] = wqkv[m];
         a.rows[m] = rows[m];
@@ -687,7 +710,7 @@ hipError_t launch_kq_qkv(int type, const uint8_t *const wqkv[3], uint32_t n_mat,
 hipError_t launch_kq_silu(int type, const uint8_t *wg, const uint8_t *wu, const float *x,
                           const float *norm_w, float eps, uint32_t cols, uint32_t rows,
                           float *hid, hipStream_t s) {
-    if (rows == 0 || rows % 16u || !mv_fits(type, wg, x, cols) || !mv_fits(type, wu, x, cols))
+    if (rows == 0 || rows % 16u || !mv_fits(type, wg, x, cols, rows) || !mv_fits(type, wu, x, cols, rows))
         return hipErrorNotSupported;
     MvArgs a{};
     a.w[0] = wg;
