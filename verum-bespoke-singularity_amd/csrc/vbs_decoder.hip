@@ -292,7 +292,7 @@ int vbs_gfx950_decoder_create(const vbs_gfx950_model_t *m, uint32_t max_steps, v
     const uint32_t kvd = m->n_kv_heads * m->head_dim, pairs = m->head_dim / 2u;
     // one arena: activations, state, outputs, attention partials, RoPE table
     const size_t n_f32 = 3ull * H + 2ull * qd + 2ull * kvd + 3ull * F + m->vocab;
-    const size_t part = attention_partial_bytes(m->max_ctx, m->n_heads, m->head_dim);
+    const size_t part = attention_partial_bytes(m->max_ctx, m->n_heads, m->n_kv_heads, m->head_dim);
     const size_t rope = (size_t)m->max_ctx * pairs * sizeof(float2);
     auto up256 = [](size_t b) { return (b + 255u) & ~(size_t)255u; };
     const size_t sz_f = up256(n_f32 * 4), sz_st = 256, sz_tok = up256(d->max_steps * 4ull);

@@ -77,7 +77,7 @@ hipError_t launch_cache_store(const float *k, const float *v, uint16_t *kc, uint
 // Split-sequence attention. With pos_dev the sequence length is read on the
 // device (pos + 1) and seq_len only sizes the grid; `part` may be NULL (then
 // the runtime scratch holds the per-chunk partials).
-size_t attention_partial_bytes(uint32_t max_seq, uint32_t nqh, uint32_t hd);
+size_t attention_partial_bytes(uint32_t max_seq, uint32_t nqh, uint32_t nkh, uint32_t hd);
 hipError_t launch_attention(const float *q, const uint16_t *kc, const uint16_t *vc, float *out,
                             uint32_t seq_len, const uint32_t *pos_dev, float *part,
                             uint64_t layer_off, uint32_t nqh, uint32_t nkh, uint32_t hd,

@@ -394,6 +394,7 @@ __global__ __launch_bounds__(MAXT) void k_mvf(const MvArgs a) {
     __shared__ float red[TPW][16][16];
     __shared__ double part[32];
     constexpr uint32_t NI = KS * TPW;  // work items (tile, block) per wave
+    constexpr uint32_t P0 = 2;         // items issued before x is prepared
     constexpr uint32_t P = 2;          // items in flight ahead of the one computed
     const uint32_t cols = a.cols;
     const uint32_t nblk = cols >> 8;
@@ -438,10 +439,10 @@ __global__ __launch_bounds__(MAXT) void k_mvf(const MvArgs a) {
         if (TWO) load16(a.norm_w, cols, i1, w1);
     }
 
-    // 2. the first P items' weights
+    // 2. the first P0 items' weights
     u32x4 r[NI][T::NLD];
 #pragma unroll
-    for (uint32_t i = 0; i < P && i < NI; i++)
+    for (uint32_t i = 0; i < P0 && i < NI; i++)
         T::load(src[i / KS], min(blk(i), nblk - 1u), n, g, r[i]);
     __builtin_amdgcn_sched_barrier(0);
 
@@ -490,7 +491,9 @@ __global__ __launch_bounds__(MAXT) void k_mvf(const MvArgs a) {
     for (uint32_t j = 0; j < TPW; j++) acc[j] = 0.f;
 #pragma unroll
     for (uint32_t i = 0; i < NI; i++) {
-        if (i + P < NI) T::load(src[(i + P) / KS], min(blk(i + P), nblk - 1u), n, g, r[i + P]);
+#pragma unroll
+        for (uint32_t j = i == 0 ? P0 : max(P0, i + P); j <= i + P && j < NI; j++)
+            T::load(src[j / KS], min(blk(j), nblk - 1u), n, g, r[j]);
         __builtin_amdgcn_sched_barrier(0);
         const float part_i = T::dot(r[i], scratch, src[i / KS], xq, L, cols,
                                     min(blk(i), nblk - 1u), n, g);
