@@ -25,7 +25,6 @@ struct Runtime {
     void *scratch = nullptr;
     size_t scratch_bytes = 0;
     uint32_t *counters = nullptr;  // zeroed once; kernels that use one leave it at 0
-    uint8_t *xq = nullptr;         // x in digit form for the matrix-core matvecs
 };
 
 Runtime g_rt;
@@ -103,7 +102,6 @@ hipStream_t rt_stream() { return g_rt.stream; }
 
 uint32_t *rt_counters() { return g_rt.counters; }
 
-uint8_t *rt_xq() { return g_rt.xq; }
 
 int rt_fail(const char *fmt, ...) {
     va_list ap;
@@ -151,7 +149,6 @@ int vbs_gfx950_init(void) {
         return 0;
     if (!hip_ok(hipMalloc(&g_rt.counters, kCounterSlots * sizeof(uint32_t)), "hipMalloc(counters)") ||
         !hip_ok(hipMemset(g_rt.counters, 0, kCounterSlots * sizeof(uint32_t)), "hipMemset(counters)") ||
-        !hip_ok(hipMalloc(&g_rt.xq, xq_bytes(kXqMaxCols)), "hipMalloc(xq)") ||
         !hip_ok(hipDeviceSynchronize(), "init"))
         return 0;
     g_rt.device = chosen;

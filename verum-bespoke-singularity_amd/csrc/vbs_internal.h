@@ -29,12 +29,6 @@ int rt_fail(const char *fmt, ...);
 int rt_hip_ok(hipError_t e, const char *what);
 bool rt_ready();
 
-// x in digit form for the matrix-core matvecs: bytes needed for `cols`, and
-// the runtime's buffer (sized for kXqMaxCols, allocated at init).
-constexpr uint32_t kXqMaxCols = 65536;
-size_t xq_bytes(uint32_t cols);
-uint8_t *rt_xq();
-hipError_t launch_xprep(const float *x, uint32_t cols, uint8_t *xq, hipStream_t s);
 // Q4_K / Q6_K matvecs on the matrix cores (x is prepared inside the kernel);
 // hipErrorNotSupported outside their shape/alignment range.
 hipError_t launch_kq_linear(int type, const uint8_t *w, const float *x, float *y, uint32_t cols,

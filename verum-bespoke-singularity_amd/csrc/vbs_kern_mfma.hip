@@ -23,12 +23,17 @@
 // three plane dots of group g of row n. A rows of other groups are zero (read
 // from a 16-byte zero pad).
 //
-// Work split. A workgroup owns TPW tiles of 16 rows; its waves split each row
-// into slices of KS super-blocks and add their partial sums in LDS. Every
-// thread first loads its part of x (so that preparing x does not wait behind
-// the weight stream: loads return in order), then every weight load of all
-// TPW tiles is issued, then x is turned into digits in LDS, once per
-// workgroup, while the weights arrive.
+// Work split. A workgroup owns TPW tiles of 16 rows; its nw waves split each
+// row by super-blocks (wave w takes blocks w, w + nw, ..., so the waves read
+// adjacent blocks together) and add their partial sums in LDS at the end. A
+// wave streams its (tile, block) items with two in flight ahead of the one it
+// computes, and turns x into digits one 256-element block at a time, right
+// before the first item that needs it; it reads only the digits of its own
+// blocks, so no barrier stands between the first weight bytes and the matrix
+// cores. With an RMSNorm in front, the sum of squares over all x blocks comes
+// first (one barrier; the loads of the first item are already out). Deeper
+// streams or x travelling with the items measured no faster: the memory
+// system is saturated from the first requests on.
 //
 // Q4_K (144-byte blocks). Lane (n, g) reads the 16-byte header of row n and 16
 // bytes of nibbles at qs offsets 16g and 64 + 16g. qs bytes 32s..32s+31 hold
@@ -67,25 +72,38 @@ __host__ __device__ inline XqLayout xq_layout(uint32_t cols) {
     return L;
 }
 
-size_t xq_bytes(uint32_t cols) { return (size_t)xq_layout(cols).bytes; }
 
-// Digits of one 16-element half sub-block `item` (values in v); the two halves
-// of a sub-block are adjacent lanes and exchange their maximum and sum. Writes
-// the three planes, xs (by the even half) and xs16 into `xq` (LDS or global).
-__device__ __forceinline__ void prep_item(const float *v, uint32_t cols, uint32_t item,
-                                          uint8_t *xq, const XqLayout &L) {
-    const bool valid = item < cols / 16u;
-    float amax = 0.f, sum = 0.f;
-#pragma unroll
-    for (int k = 0; k < 16; k++) {
-        amax = fmaxf(amax, fabsf(v[k]));
-        sum += v[k];
-    }
-    const uint32_t h = item & 1u;
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-    const float other = __shfl_xor(sum, 1, 64);
-    const float sum32 = h ? other + sum : sum + other;  // same order in both lanes
-    if (!valid) return;
+// Group reductions over aligned lane groups with DPP (every lane of the group
+// gets the result): L = 4 (quads) or 8 (half rows).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                                 CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float quad_sum(float v) {
+    v = v + dpp_f<0xB1>(v);  // quad_perm [1,0,3,2]
+    return v + dpp_f<0x4E>(v);  // quad_perm [2,3,0,1]
+}
+__device__ __forceinline__ float quad_max(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    return fmaxf(v, dpp_f<0x4E>(v));
+}
+__device__ __forceinline__ float half_row_other(float v) { return dpp_f<0x141>(v); }  // lane i <-> 7-i
+
+// Digits of block b of x (256 elements) by one wave: lane l holds elements
+// 4l..4l+3 (v), so a 16-element item is a lane quad and a 32-element
+// sub-block a half row. Writes the three planes, xs and xs16 of the block.
+// Sums: per lane in element order, then the quad, then the two quads of a
+// sub-block (the same value in every lane of the group).
+__device__ __forceinline__ void prep_block(const float *v, uint32_t cols, uint32_t b,
+                                           uint32_t lane, uint8_t *xq, const XqLayout &L) {
+    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    const float sum4 = ((v[0] + v[1]) + v[2]) + v[3];
+    amax = quad_max(amax);
+    amax = fmaxf(amax, half_row_other(amax));
+    const float sum16 = quad_sum(sum4);
+    const float other = half_row_other(sum16);
+    const float sum32 = (lane & 4u) ? other + sum16 : sum16 + other;  // same order in both quads
     int e;
     (void)frexpf(amax, &e);  // amax < 2^e
     const bool finite = amax <= 3.4028235e38f;
@@ -93,57 +111,36 @@ __device__ __forceinline__ void prep_item(const float *v, uint32_t cols, uint32_
     // nearest integer (ties to even, as rint) and leaves 2^22 + X in the low 23
     // bits. U = X + 0x808080 then holds the balanced digits as biased bytes:
     // D_i = byte_i(U) - 128, i.e. byte_i(U) ^ 0x80 in int8 form (the same
-    // digits as D0 = int8(X), D1 = int8((X - D0) / 256), ...). Items whose
+    // digits as D0 = int8(X), D1 = int8((X - D0) / 256), ...). Sub-blocks whose
     // maximum is not finite get a NaN scale, which makes their digits moot.
-    uint32_t u[16];
+    uint32_t u[4];
 #pragma unroll
-    for (int k = 0; k < 16; k++)
+    for (int k = 0; k < 4; k++)
         u[k] = __float_as_uint(__fadd_rn(ldexpf(v[k], 22 - e), 12582912.0f)) + 0x408080u;
-    uint32_t d0[4], d1[4], d2[4];
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-        // bytes of elements 4q..4q+3: pairs first, then the planes
-        const uint32_t *w = u + 4 * q;
-        const uint32_t lo01 = __builtin_amdgcn_perm(w[1], w[0], 0x05010400u);
-        const uint32_t lo23 = __builtin_amdgcn_perm(w[3], w[2], 0x05010400u);
-        const uint32_t hi01 = __builtin_amdgcn_perm(w[1], w[0], 0x0c0c0602u);
-        const uint32_t hi23 = __builtin_amdgcn_perm(w[3], w[2], 0x0c0c0602u);
-        d0[q] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u) ^ 0x80808080u;
-        d1[q] = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u) ^ 0x80808080u;
-        d2[q] = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u) ^ 0x80808080u;
-    }
-    const uint32_t off = item * 16u;
-    *reinterpret_cast<uint4 *>(xq + off) = make_uint4(d0[0], d0[1], d0[2], d0[3]);
-    *reinterpret_cast<uint4 *>(xq + cols + off) = make_uint4(d1[0], d1[1], d1[2], d1[3]);
-    *reinterpret_cast<uint4 *>(xq + 2u * cols + off) = make_uint4(d2[0], d2[1], d2[2], d2[3]);
-    reinterpret_cast<float *>(xq + L.xs16)[item] = sum;
-    if (h == 0)
-        reinterpret_cast<float2 *>(xq + L.xs)[item >> 1] =
+    const uint32_t lo01 = __builtin_amdgcn_perm(u[1], u[0], 0x05010400u);
+    const uint32_t lo23 = __builtin_amdgcn_perm(u[3], u[2], 0x05010400u);
+    const uint32_t hi01 = __builtin_amdgcn_perm(u[1], u[0], 0x0c0c0602u);
+    const uint32_t hi23 = __builtin_amdgcn_perm(u[3], u[2], 0x0c0c0602u);
+    const uint32_t off = 256u * b + 4u * lane;
+    *reinterpret_cast<uint32_t *>(xq + off) = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u) ^ 0x80808080u;
+    *reinterpret_cast<uint32_t *>(xq + cols + off) =
+        __builtin_amdgcn_perm(lo23, lo01, 0x07060302u) ^ 0x80808080u;
+    *reinterpret_cast<uint32_t *>(xq + 2u * cols + off) =
+        __builtin_amdgcn_perm(hi23, hi01, 0x05040100u) ^ 0x80808080u;
+    if ((lane & 3u) == 0) reinterpret_cast<float *>(xq + L.xs16)[16u * b + lane / 4u] = sum16;
+    if ((lane & 7u) == 0)
+        reinterpret_cast<float2 *>(xq + L.xs)[8u * b + lane / 8u] =
             make_float2(finite ? ldexpf(1.0f, e - 22) : __builtin_nanf(""), sum32);
 }
 
-// 16 elements of x for `item` (items past the end read item 0 and are not used).
-__device__ __forceinline__ void load16(const float *x, uint32_t cols, uint32_t item, float *v) {
-    const float *xp = x + (item < cols / 16u ? item * 16u : 0u);
+// Sum of squares of block b of x (lane l: elements 4l..4l+3 in element
+// order, then a butterfly over the wave), in double. The RMSNorm adds the
+// blocks in index order; k_rms_norm uses the same order.
+__device__ __forceinline__ double block_sumsq(const float *v) {
+    double ss = 0.0;
 #pragma unroll
-    for (int k = 0; k < 16; k++) v[k] = xp[k];
-}
-
-// x -> digits in global memory (for callers that keep x in digit form).
-__global__ __launch_bounds__(256) void k_xprep(const float *__restrict__ x, uint32_t cols,
-                                               uint8_t *__restrict__ xq) {
-    const uint32_t item = blockIdx.x * 256u + threadIdx.x;
-    const XqLayout L = xq_layout(cols);
-    float v[16];
-    load16(x, cols, item, v);
-    if (item == 0) *reinterpret_cast<uint4 *>(xq + L.zero) = make_uint4(0, 0, 0, 0);
-    prep_item(v, cols, item, xq, L);
-}
-
-hipError_t launch_xprep(const float *x, uint32_t cols, uint8_t *xq, hipStream_t s) {
-    const uint32_t items = cols / 16u;
-    k_xprep<<<(items + 255u) / 256u, 256, 0, s>>>(x, cols, xq);
-    return hipGetLastError();
+    for (int k = 0; k < 4; k++) ss = fma((double)v[k], (double)v[k], ss);
+    return wave_sum_d(ss);
 }
 
 // ---- helpers ------------------------------------------------------------------------
@@ -388,14 +385,14 @@ struct MvArgs {
     uint64_t kv_layer;  // layer * max_ctx * kvd
 };
 
-template <class T, uint32_t KS, uint32_t TPW, uint32_t MAXT, bool NORM, int EPI, bool TWO>
+template <class T, uint32_t KS, uint32_t TPW, uint32_t MAXT, bool NORM, int EPI>
 __global__ __launch_bounds__(MAXT) void k_mvf(const MvArgs a) {
     extern __shared__ __align__(16) uint8_t xq[];
     __shared__ float red[TPW][16][16];
-    __shared__ double part[32];
+    __shared__ double bsum[128];
     constexpr uint32_t NI = KS * TPW;  // work items (tile, block) per wave
-    constexpr uint32_t P0 = 2;         // items issued before x is prepared
-    constexpr uint32_t P = 2;          // items in flight ahead of the one computed
+    constexpr uint32_t P0 = 1;         // items issued with x, before anything is computed
+    constexpr uint32_t P = 1;          // items in flight ahead of the one computed
     const uint32_t cols = a.cols;
     const uint32_t nblk = cols >> 8;
     const uint32_t rb = nblk * T::BYTES;
@@ -422,69 +419,51 @@ __global__ __launch_bounds__(MAXT) void k_mvf(const MvArgs a) {
         const uint8_t *w = a.w[mt[j]];
         src[j] = Src{w, a.rows[mt[j]] * rb, rb, lt[j] * 16u, a.rows[mt[j]]};
     }
-    // item i: tile i / KS, block wave + nw * (i % KS); at each step the
-    // workgroup's waves read adjacent blocks of the same rows. Slots past the
-    // row re-read its last block and contribute zero.
+    // Block k of this wave: wave + nw * k (at each step the workgroup's waves
+    // read adjacent blocks of the same rows); item i is block i % KS of tile
+    // i / KS. Slots past the row re-read its last block and contribute zero.
+    // A wave prepares the digits of its own blocks only, so the waves share
+    // no x data and need no barrier before the matrix work.
     auto blk = [&](uint32_t i) { return wave + nw * (i % KS); };
 
-    // 1. x first (one or two 16-element items per thread; with the RMSNorm also
-    // its weights)
-    const uint32_t items = cols / 16u;
-    const uint32_t i0 = threadIdx.x, i1 = threadIdx.x + nth;
-    float v0[16], v1[TWO ? 16 : 1], w0[NORM ? 16 : 1], w1[NORM && TWO ? 16 : 1];
-    load16(a.x, cols, i0, v0);
-    if (TWO) load16(a.x, cols, i1, v1);
-    if (NORM) {
-        load16(a.norm_w, cols, i0, w0);
-        if (TWO) load16(a.norm_w, cols, i1, w1);
-    }
-
-    // 2. the first P0 items' weights
+    // x of this wave's blocks, lane l: elements 4l..4l+3 (x may be only
+    // 4-byte aligned), and with the RMSNorm its weights: all requested first.
+    typedef float4 __attribute__((aligned(4))) f4u;
+    float4 xv[KS], wv[NORM ? KS : 1];
+    auto load_x = [&](uint32_t k) {
+        const uint32_t e0 = 256u * min(blk(k), nblk - 1u) + 4u * lane;
+        xv[k] = *reinterpret_cast<const f4u *>(a.x + e0);
+        if (NORM) wv[k] = *reinterpret_cast<const f4u *>(a.norm_w + e0);
+    };
     u32x4 r[NI][T::NLD];
+    auto issue = [&](uint32_t i) { T::load(src[i / KS], min(blk(i), nblk - 1u), n, g, r[i]); };
+
+    // 1-2. x, then the first items
 #pragma unroll
-    for (uint32_t i = 0; i < P0 && i < NI; i++)
-        T::load(src[i / KS], min(blk(i), nblk - 1u), n, g, r[i]);
+    for (uint32_t k = 0; k < KS; k++) load_x(k);
+#pragma unroll
+    for (uint32_t i = 0; i < P0 && i < NI; i++) issue(i);
     __builtin_amdgcn_sched_barrier(0);
 
-    // 3. (RMSNorm and) x -> digits in LDS while the weights arrive. The sum of
-    // squares follows k_rms_norm's order: squares of a 16-element item in
-    // element order, 64 consecutive items (one wave) by butterfly, the
-    // 64-item groups in index order.
+    // 3. RMSNorm scale: block sums of squares, added in block order
+    float sc = 1.0f;
     if (NORM) {
-        double ss0 = 0.0, ss1 = 0.0;
 #pragma unroll
-        for (int k = 0; k < 16; k++) {
-            const double d0 = v0[k];
-            ss0 = fma(d0, d0, ss0);
-            if (TWO) {
-                const double d1 = v1[k];
-                ss1 = fma(d1, d1, ss1);
-            }
-        }
-        ss0 = wave_sum_d(i0 < items ? ss0 : 0.0);
-        if (lane == 0 && 64u * wave < items) part[wave] = ss0;
-        if (TWO) {
-            ss1 = wave_sum_d(i1 < items ? ss1 : 0.0);
-            if (lane == 0 && 64u * (wave + nw) < items) part[wave + nw] = ss1;
+        for (uint32_t k = 0; k < KS; k++) {
+            const float v[4] = {xv[k].x, xv[k].y, xv[k].z, xv[k].w};
+            const double ss = block_sumsq(v);
+            if (lane == 0 && blk(k) < nblk) bsum[blk(k)] = ss;
         }
         __syncthreads();
         double t = 0.0;
-        for (uint32_t k = 0; k < (items + 63u) / 64u; k++) t += part[k];
+        for (uint32_t b = 0; b < nblk; b++) t += bsum[b];
         const float mean = (float)(t / (double)cols);
-        const float sc = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, a.eps)));
-#pragma unroll
-        for (int k = 0; k < 16; k++) {
-            v0[k] = __fmul_rn(__fmul_rn(v0[k], sc), w0[k]);
-            if (TWO) v1[k] = __fmul_rn(__fmul_rn(v1[k], sc), w1[k]);
-        }
+        sc = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, a.eps)));
     }
-    prep_item(v0, cols, i0, xq, L);
-    if (TWO) prep_item(v1, cols, i1, xq, L);
-    if (threadIdx.x == 0) *reinterpret_cast<uint4 *>(xq + L.zero) = make_uint4(0, 0, 0, 0);
-    __syncthreads();
+    if (lane < 4u) reinterpret_cast<uint32_t *>(xq + L.zero)[lane] = 0u;  // each wave's own pad
 
-    // 4. stream: issue item i + P, then compute item i (loads return in issue
-    // order, so the wait is for item i alone)
+    // 4. stream: issue item i + P, prepare x of a new block, compute item i
+    // (loads return in issue order, so the wait is for item i alone)
     uint8_t *scratch = xq + L.bytes + wave * T::SCRATCH;
     float acc[TPW];
 #pragma unroll
@@ -492,9 +471,17 @@ __global__ __launch_bounds__(MAXT) void k_mvf(const MvArgs a) {
 #pragma unroll
     for (uint32_t i = 0; i < NI; i++) {
 #pragma unroll
-        for (uint32_t j = i == 0 ? P0 : max(P0, i + P); j <= i + P && j < NI; j++)
-            T::load(src[j / KS], min(blk(j), nblk - 1u), n, g, r[j]);
+        for (uint32_t j = i == 0 ? P0 : max(P0, i + P); j <= i + P && j < NI; j++) issue(j);
         __builtin_amdgcn_sched_barrier(0);
+        if (i < KS && blk(i) < nblk) {
+            float v[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+            if (NORM) {
+                const float w4[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
+#pragma unroll
+                for (int k = 0; k < 4; k++) v[k] = __fmul_rn(__fmul_rn(v[k], sc), w4[k]);
+            }
+            prep_block(v, cols, blk(i), lane, xq, L);
+        }
         const float part_i = T::dot(r[i], scratch, src[i / KS], xq, L, cols,
                                     min(blk(i), nblk - 1u), n, g);
         acc[i / KS] += blk(i) < nblk ? part_i : 0.f;
@@ -578,13 +565,13 @@ static MvPlan mv_plan(uint32_t cols) {
     return p;
 }
 
-template <class T, uint32_t KS, uint32_t TPW, uint32_t MAXT, bool NORM, int EPI, bool TWO>
-static hipError_t launch_t2(const MvArgs &a, uint32_t nw, uint32_t wgs, hipStream_t s) {
+template <class T, uint32_t KS, uint32_t TPW, uint32_t MAXT, bool NORM, int EPI>
+static hipError_t launch_t(const MvArgs &a, uint32_t nw, uint32_t wgs, hipStream_t s) {
     const size_t lds = xq_layout(a.cols).bytes + (size_t)nw * T::SCRATCH;
     if (lds > 65536u) {  // beyond the default per-workgroup LDS window: opt in once
         static size_t granted = 0;
         if (lds > granted) {
-            if (hipFuncSetAttribute((const void *)k_mvf<T, KS, TPW, MAXT, NORM, EPI, TWO>,
+            if (hipFuncSetAttribute((const void *)k_mvf<T, KS, TPW, MAXT, NORM, EPI>,
                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
                 hipSuccess) {
                 (void)hipGetLastError();
@@ -593,15 +580,8 @@ static hipError_t launch_t2(const MvArgs &a, uint32_t nw, uint32_t wgs, hipStrea
             granted = lds;
         }
     }
-    k_mvf<T, KS, TPW, MAXT, NORM, EPI, TWO><<<wgs, 64u * nw, lds, s>>>(a);
+    k_mvf<T, KS, TPW, MAXT, NORM, EPI><<<wgs, 64u * nw, lds, s>>>(a);
     return hipGetLastError();
-}
-
-// One or two 16-element x items per thread.
-template <class T, uint32_t KS, uint32_t TPW, uint32_t MAXT, bool NORM, int EPI>
-static hipError_t launch_t(const MvArgs &a, uint32_t nw, uint32_t wgs, hipStream_t s) {
-    if (a.cols / 16u > 64u * nw) return launch_t2<T, KS, TPW, MAXT, NORM, EPI, true>(a, nw, wgs, s);
-    return launch_t2<T, KS, TPW, MAXT, NORM, EPI, false>(a, nw, wgs, s);
 }
 
 template <class T, bool NORM, int EPI>
@@ -609,7 +589,7 @@ static hipError_t launch_plan(const MvArgs &a, hipStream_t s) {
     const uint32_t total = a.tile_end[a.nmat - 1u];
     const MvPlan p = mv_plan<T>(a.cols);
     constexpr uint32_t TPW = EPI == E_SILU ? 2u : 1u;  // a gate tile and the same up tile
-    if (p.nw > 16u || a.cols / 16u > 2u * 64u * p.nw) return hipErrorNotSupported;
+    if (p.nw > 16u) return hipErrorNotSupported;
     const uint32_t wgs = EPI == E_SILU ? a.tile_end[0] : total;
 #define VBS_MV(KS, MAXT) return launch_t<T, KS, TPW, MAXT, NORM, EPI>(a, p.nw, wgs, s)
     if (p.ks == 4u) {

@@ -48,35 +48,35 @@ hipError_t launch_dequant_rows(int type, const uint8_t *w, const uint32_t *ids, 
 
 // ---- RMSNorm (src/vbs_host_math.h:28-36) -----------------------------------
 // ss = sum of x^2 in double, in a fixed order that any block size reproduces
-// (the matrix-core matvec's fused RMSNorm uses the same): the squares of each
-// 16-element item are added in element order, 64 consecutive items by a wave
-// butterfly, and the 64-item groups in index order. Then, as the reference,
+// (the matrix-core matvec's fused RMSNorm uses the same): x in blocks of 256
+// elements; in a block, lane l of a wave adds the squares of elements
+// 4l..4l+3 in element order, a wave butterfly adds the 64 lanes, and the
+// blocks are added in index order. Then, as the reference,
 // scale = 1 / sqrtf((float)(ss / n) + eps) and out = x * scale * w.
 __global__ __launch_bounds__(1024) void k_rms_norm(const float *__restrict__ in,
                                                    const float *__restrict__ w,
                                                    float *__restrict__ out, uint32_t n,
                                                    float eps) {
-    extern __shared__ double gpart[];  // one entry per 64-item group
+    extern __shared__ double bpart[];  // one entry per 256-element block
     __shared__ float s_scale;
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
-    const uint32_t items = (n + 15u) / 16u, groups = (items + 63u) / 64u;
-    for (uint32_t grp = wave; grp < groups; grp += 16u) {
-        const uint32_t item = 64u * grp + lane;
+    const uint32_t blocks = (n + 255u) / 256u;
+    for (uint32_t b = wave; b < blocks; b += 16u) {
         double ss = 0.0;
-        for (uint32_t k = 0; k < 16u; k++) {
-            const uint32_t i = 16u * item + k;
+        for (uint32_t k = 0; k < 4u; k++) {
+            const uint32_t i = 256u * b + 4u * lane + k;
             if (i < n) {
                 const double v = in[i];
                 ss = fma(v, v, ss);  // v*v is exact in double, so fusing changes nothing
             }
         }
         ss = wave_sum_d(ss);
-        if (lane == 0) gpart[grp] = ss;
+        if (lane == 0) bpart[b] = ss;
     }
     __syncthreads();
     if (threadIdx.x == 0) {
         double t = 0.0;
-        for (uint32_t k = 0; k < groups; k++) t += gpart[k];
+        for (uint32_t k = 0; k < blocks; k++) t += bpart[k];
         float mean = (float)(t / (double)n);
         s_scale = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, eps)));
     }
@@ -88,9 +88,9 @@ __global__ __launch_bounds__(1024) void k_rms_norm(const float *__restrict__ in,
 hipError_t launch_rms_norm(const float *in, const float *w, float *out, uint32_t n, float eps,
                            hipStream_t s) {
     if (n == 0) return hipSuccess;
-    const size_t groups = ((n + 15u) / 16u + 63u) / 64u;
-    if (groups * sizeof(double) > 64u * 1024u) return hipErrorInvalidValue;
-    k_rms_norm<<<1, 1024, groups * sizeof(double), s>>>(in, w, out, n, eps);
+    const size_t blocks = (n + 255u) / 256u;
+    if (blocks * sizeof(double) > 64u * 1024u) return hipErrorInvalidValue;
+    k_rms_norm<<<1, 1024, blocks * sizeof(double), s>>>(in, w, out, n, eps);
     return hipGetLastError();
 }
 
