@@ -555,11 +555,13 @@ struct MvPlan {
 
 // Blocks per wave (KS) and waves per tile: enough waves to split the row and
 // enough items per wave that the stream runs ahead of the arithmetic.
+// (The gate/up launch, two tiles per workgroup, keeps four blocks per wave:
+// eight waves of two would not all be resident at once.)
 template <class T>
-static MvPlan mv_plan(uint32_t cols) {
+static MvPlan mv_plan(uint32_t cols, bool two_tiles) {
     const uint32_t nblk = cols / 256u;
     MvPlan p;
-    p.ks = nblk <= 32u ? 4u : nblk <= 48u ? 6u : 8u;
+    p.ks = nblk <= 16u && !two_tiles ? 2u : nblk <= 32u ? 4u : nblk <= 48u ? 6u : 8u;
     p.nw = (nblk + p.ks - 1u) / p.ks;
     p.tpw = 1u;
     return p;
@@ -587,11 +589,15 @@ static hipError_t launch_t(const MvArgs &a, uint32_t nw, uint32_t wgs, hipStream
 template <class T, bool NORM, int EPI>
 static hipError_t launch_plan(const MvArgs &a, hipStream_t s) {
     const uint32_t total = a.tile_end[a.nmat - 1u];
-    const MvPlan p = mv_plan<T>(a.cols);
+    const MvPlan p = mv_plan<T>(a.cols, EPI == E_SILU);
     constexpr uint32_t TPW = EPI == E_SILU ? 2u : 1u;  // a gate tile and the same up tile
     if (p.nw > 16u) return hipErrorNotSupported;
     const uint32_t wgs = EPI == E_SILU ? a.tile_end[0] : total;
 #define VBS_MV(KS, MAXT) return launch_t<T, KS, TPW, MAXT, NORM, EPI>(a, p.nw, wgs, s)
+    if (p.ks == 2u) {
+        if (p.nw <= 8u) VBS_MV(2, 512);
+        VBS_MV(2, 1024);
+    }
     if (p.ks == 4u) {
         if (p.nw <= 8u) VBS_MV(4, 512);
         VBS_MV(4, 1024);
