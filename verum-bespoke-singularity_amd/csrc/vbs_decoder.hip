@@ -70,9 +70,12 @@ struct Top2 {
 };
 
 __device__ __forceinline__ Top2 top2_merge(Top2 a, Top2 b) {
-    // a's indices precede b's only when a came from a lower index range; the
-    // comparison keeps the lower index on ties so the first maximum wins
-    const bool b_wins = b.v1 > a.v1 || (b.v1 == a.v1 && b.i1 < a.i1);
+    // Symmetric in a and b (any reduction tree gives the same result): the
+    // larger value wins, the lower index on ties, so the first maximum wins;
+    // a NaN can only sit at index 0 (the scan never takes one elsewhere), and
+    // there it wins, as the reference's strict '>' scan from index 0 keeps it.
+    const bool a_nan = a.v1 != a.v1, b_nan = b.v1 != b.v1;
+    const bool b_wins = b_nan || (!a_nan && (b.v1 > a.v1 || (b.v1 == a.v1 && b.i1 < a.i1)));
     Top2 r;
     r.v1 = b_wins ? b.v1 : a.v1;
     r.i1 = b_wins ? b.i1 : a.i1;
@@ -86,7 +89,7 @@ __global__ __launch_bounds__(1024) void k_argmax_advance(const float *__restrict
                                                          uint32_t *pos_dev, uint32_t *step_dev,
                                                          uint32_t *tokens, float *margins,
                                                          uint32_t max_steps) {
-    __shared__ Top2 red[1024];
+    __shared__ Top2 red[16];
     Top2 t{-INFINITY, 0xFFFFFFFFu, -INFINITY};
     auto consider = [&](float v, uint32_t i) {
         if (v != v && i != 0u) return;  // a NaN never beats anything after index 0
@@ -114,17 +117,27 @@ __global__ __launch_bounds__(1024) void k_argmax_advance(const float *__restrict
     } else {
         for (uint32_t i = threadIdx.x; i < n; i += 1024u) consider(logits[i], i);
     }
-    red[threadIdx.x] = t;
-    __syncthreads();
-    for (uint32_t s = 512u; s > 0; s >>= 1) {
-        if (threadIdx.x < s) {
-            Top2 a = red[threadIdx.x], b = red[threadIdx.x + s];
-            if (a.i1 == 0xFFFFFFFFu) a = b;
-            else if (b.i1 != 0xFFFFFFFFu) a = top2_merge(a, b);
-            red[threadIdx.x] = a;
+    // wave butterflies, then the 16 wave results in one wave
+    auto wave_merge = [](Top2 v, uint32_t width) {
+        for (uint32_t off = width / 2u; off > 0; off >>= 1) {
+            Top2 o;
+            o.v1 = __shfl_xor(v.v1, (int)off, 64);
+            o.i1 = (uint32_t)__shfl_xor((int)v.i1, (int)off, 64);
+            o.v2 = __shfl_xor(v.v2, (int)off, 64);
+            v = top2_merge(v, o);
         }
-        __syncthreads();
+        return v;
+    };
+    t = wave_merge(t, 64u);
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    if (lane == 0) red[wave] = t;
+    __syncthreads();
+    if (wave == 0) {
+        Top2 w = lane < 16u ? red[lane] : Top2{-INFINITY, 0xFFFFFFFFu, -INFINITY};
+        w = wave_merge(w, 16u);
+        if (lane == 0) red[0] = w;
     }
+    __syncthreads();
     if (threadIdx.x == 0) {
         const uint32_t step = step_dev[0];
         if (step < max_steps) {

@@ -25,8 +25,10 @@
 //
 // Work split. A workgroup owns TPW tiles of 16 rows; its nw waves split each
 // row by super-blocks (wave w takes blocks w, w + nw, ..., so the waves read
-// adjacent blocks together) and add their partial sums in LDS at the end. A
-// wave streams its (tile, block) items with two in flight ahead of the one it
+// adjacent blocks together) and leave one sum per (row, block) in LDS; a row
+// adds its blocks in index order at the end, so its value does not depend on
+// the split (fused and per-op launches of one matrix agree bit for bit). A
+// wave streams its (tile, block) items with one in flight ahead of the one it
 // computes, and turns x into digits one 256-element block at a time, right
 // before the first item that needs it; it reads only the digits of its own
 // blocks, so no barrier stands between the first weight bytes and the matrix
@@ -388,7 +390,6 @@ struct MvArgs {
 template <class T, uint32_t KS, uint32_t TPW, uint32_t MAXT, bool NORM, int EPI>
 __global__ __launch_bounds__(MAXT) void k_mvf(const MvArgs a) {
     extern __shared__ __align__(16) uint8_t xq[];
-    __shared__ float red[TPW][16][16];
     __shared__ double bsum[128];
     constexpr uint32_t NI = KS * TPW;  // work items (tile, block) per wave
     constexpr uint32_t P0 = 1;         // items issued with x, before anything is computed
@@ -465,9 +466,9 @@ __global__ __launch_bounds__(MAXT) void k_mvf(const MvArgs a) {
     // 4. stream: issue item i + P, prepare x of a new block, compute item i
     // (loads return in issue order, so the wait is for item i alone)
     uint8_t *scratch = xq + L.bytes + wave * T::SCRATCH;
-    float acc[TPW];
-#pragma unroll
-    for (uint32_t j = 0; j < TPW; j++) acc[j] = 0.f;
+    // per-block row sums [TPW][nblk][16]: every row adds its blocks in index
+    // order at the end, so a row's value does not depend on the work split
+    float *pb = reinterpret_cast<float *>(xq + L.bytes + nw * T::SCRATCH);
 #pragma unroll
     for (uint32_t i = 0; i < NI; i++) {
 #pragma unroll
@@ -482,34 +483,25 @@ __global__ __launch_bounds__(MAXT) void k_mvf(const MvArgs a) {
             }
             prep_block(v, cols, blk(i), lane, xq, L);
         }
-        const float part_i = T::dot(r[i], scratch, src[i / KS], xq, L, cols,
-                                    min(blk(i), nblk - 1u), n, g);
-        acc[i / KS] += blk(i) < nblk ? part_i : 0.f;
+        float part = T::dot(r[i], scratch, src[i / KS], xq, L, cols, min(blk(i), nblk - 1u), n, g);
+        // the four lane groups of a row hold different groups of the block
+        part += __shfl_xor(part, 16, 64);
+        part += __shfl_xor(part, 32, 64);
+        if (lane < 16u && blk(i) < nblk) pb[((i / KS) * nblk + blk(i)) * 16u + n] = part;
         // finish item i here: otherwise its arithmetic may sink past later
         // items and hold their registers
-        asm volatile("" ::"v"(acc[i / KS]));
+        asm volatile("" ::"v"(part));
         __builtin_amdgcn_sched_barrier(0);
     }
 
-    // 5. the four lane groups of a row hold different groups of its blocks;
-    // then the waves' partial sums, tile j finished by wave j (both tiles by
-    // wave 0 for E_SILU)
-#pragma unroll
-    for (uint32_t j = 0; j < TPW; j++) {
-        acc[j] += __shfl_xor(acc[j], 16, 64);
-        acc[j] += __shfl_xor(acc[j], 32, 64);
-        if (nw > 1u && lane < 16u) red[j][wave][n] = acc[j];
-    }
-    if (nw > 1u) __syncthreads();
+    // 5. tile j finished by wave j % nw (both tiles by wave 0 for E_SILU)
+    __syncthreads();
     float prev = 0.f;  // E_SILU: the gate row value
 #pragma unroll
     for (uint32_t j = 0; j < TPW; j++) {
         if (wave != (EPI == E_SILU ? 0u : j % nw)) continue;
-        float t = acc[j];
-        if (nw > 1u) {
-            t = 0.f;
-            for (uint32_t k = 0; k < nw; k++) t += red[j][k][n];
-        }
+        float t = 0.f;
+        for (uint32_t b = 0; b < nblk; b++) t += pb[(j * nblk + b) * 16u + n];
         // every lane holds the value of row n of the tile
         const uint32_t m = mt[j];
         const bool own = (EPI == E_SILU || blockIdx.x * TPW + j < total);
@@ -569,7 +561,8 @@ static MvPlan mv_plan(uint32_t cols, bool two_tiles) {
 
 template <class T, uint32_t KS, uint32_t TPW, uint32_t MAXT, bool NORM, int EPI>
 static hipError_t launch_t(const MvArgs &a, uint32_t nw, uint32_t wgs, hipStream_t s) {
-    const size_t lds = xq_layout(a.cols).bytes + (size_t)nw * T::SCRATCH;
+    const size_t lds = xq_layout(a.cols).bytes + (size_t)nw * T::SCRATCH +
+                       (size_t)TPW * (a.cols / 256u) * 16u * sizeof(float);
     if (lds > 65536u) {  // beyond the default per-workgroup LDS window: opt in once
         static size_t granted = 0;
         if (lds > granted) {
@@ -586,13 +579,8 @@ static hipError_t launch_t(const MvArgs &a, uint32_t nw, uint32_t wgs, hipStream
     return hipGetLastError();
 }
 
-template <class T, bool NORM, int EPI>
-static hipError_t launch_plan(const MvArgs &a, hipStream_t s) {
-    const uint32_t total = a.tile_end[a.nmat - 1u];
-    const MvPlan p = mv_plan<T>(a.cols, EPI == E_SILU);
-    constexpr uint32_t TPW = EPI == E_SILU ? 2u : 1u;  // a gate tile and the same up tile
-    if (p.nw > 16u) return hipErrorNotSupported;
-    const uint32_t wgs = EPI == E_SILU ? a.tile_end[0] : total;
+template <class T, bool NORM, int EPI, uint32_t TPW>
+static hipError_t launch_ks(const MvArgs &a, const MvPlan &p, uint32_t wgs, hipStream_t s) {
 #define VBS_MV(KS, MAXT) return launch_t<T, KS, TPW, MAXT, NORM, EPI>(a, p.nw, wgs, s)
     if (p.ks == 2u) {
         if (p.nw <= 8u) VBS_MV(2, 512);
@@ -608,6 +596,22 @@ static hipError_t launch_plan(const MvArgs &a, hipStream_t s) {
     }
     VBS_MV(8, 1024);
 #undef VBS_MV
+}
+
+template <class T, bool NORM, int EPI>
+static hipError_t launch_plan(const MvArgs &a, hipStream_t s) {
+    const uint32_t total = a.tile_end[a.nmat - 1u];
+    const MvPlan p = mv_plan<T>(a.cols, EPI == E_SILU);
+    if (p.nw > 16u) return hipErrorNotSupported;
+    if constexpr (EPI == E_SILU)  // a gate tile and the same up tile
+        return launch_ks<T, NORM, EPI, 2>(a, p, a.tile_end[0], s);
+    // Launches that would need several rounds of resident workgroups give each
+    // workgroup four tiles instead: x (and the RMSNorm) is prepared once per
+    // four tiles and every workgroup is resident from the start.
+    if constexpr (EPI == E_STORE || EPI == E_ACC) {
+        if (total >= 1024u) return launch_ks<T, NORM, EPI, 4>(a, p, (total + 3u) / 4u, s);
+    }
+    return launch_ks<T, NORM, EPI, 1>(a, p, total, s);
 }
 
 // Shape and alignment range of the matrix-core path: at most 16 waves of at
