@@ -242,20 +242,88 @@ def bench_matvec(dev, host, steps, warmup, ncopy, roof_reps):
     return res
 
 
-def bench_decode(dev, host, n_tokens, path="both", n_layers=32, ctx=2048, n_dispatch_tokens=16):
-    """Greedy decode of the 7B Q4_K_M synthetic model (config 4) from position
-    `ctx` with the KV cache prefilled N(0,1): the graph decoder (one graph
-    launch per token) and, for comparison, the per-dispatch ops-table path."""
+# Llama-70B layer matvec set (config 5) in the Q4_K_M mix: Q, K, V, O, gate, up, down
+LAYER_SET_70B = [("q", V.Q4_K, 8192, 8192), ("k", V.Q4_K, 1024, 8192), ("v", V.Q4_K, 1024, 8192),
+                 ("o", V.Q4_K, 8192, 8192), ("gate", V.Q4_K, 28672, 8192),
+                 ("up", V.Q4_K, 28672, 8192), ("down", V.Q6_K, 8192, 28672)]
+
+
+def bench_batch8_70b(dev, host, steps=20, batch=8, ncopy=2):
+    """Config 5 at batch 8: the 70B layer matvec set through
+    vbs_gfx950_linear_batch (x prepared, then the f16 matrix-core kernel), one
+    HIP graph per step, `ncopy` resident copies (1.08 GB) rotated so the
+    Infinity Cache cannot serve the weights; beside it the same vectors as
+    `batch` batch-1 matvec launches each."""
+    hip, stream = Hip(), dev.stream()
+    copies = [[dev.upload(V.synth_matrix(host, t, r, c, SEED + k, 200 + i))
+               for i, (_, t, r, c) in enumerate(LAYER_SET_70B)] for k in range(ncopy)]
+    px = {c: dev.upload(np.stack([V.synth_normal(host, c, SEED, 300 + b) for b in range(batch)]))
+          for c in {c for _, _, _, c in LAYER_SET_70B}}
+    py = [dev.upload(np.zeros(batch * r, np.float32)) for _, _, r, _ in LAYER_SET_70B]
+
+    def step(k, batched):
+        for i, (_, t, r, c) in enumerate(LAYER_SET_70B):
+            if batched:
+                dev.linear_batch(t, copies[k][i], px[c], c, py[i], r, c, r, batch)
+            else:
+                for b in range(batch):
+                    dev.linear(t, copies[k][i], px[c] + 4 * b * c, py[i] + 4 * b * r, c, r)
+
+    out = {}
+    for batched in (True, False):
+        step(0, batched)  # sizes the runtime scratch before capture
+        dev.sync()
+        graphs = [hip.capture(stream, lambda k=k: step(k, batched)) for k in range(ncopy)]
+        for s in range(2 * ncopy):
+            hip.launch(graphs[s % ncopy], stream)
+        e0, e1 = hip.event(), hip.event()
+        hip.record(e0, stream)
+        for s in range(steps):
+            hip.launch(graphs[s % ncopy], stream)
+        hip.record(e1, stream)
+        dev.sync()
+        ms = hip.elapsed_ms(e0, e1) / steps
+        for g in graphs:
+            hip.destroy(g)
+        out["batched" if batched else "batch1_x8"] = ms
+    wbytes = sum(V.row_bytes(t, c) * r for _, t, r, c in LAYER_SET_70B)
+    for k_ in copies:
+        for p in k_:
+            dev.free(p)
+    for p in list(px.values()) + py:
+        dev.free(p)
+    return {"workload": "Llama-70B layer matvec set (Q4_K_M mix), batch 8 (config 5)",
+            "batch": batch, "weight_bytes_per_step": wbytes, "weight_copies": ncopy,
+            "ms_per_step": round(out["batched"], 4),
+            "weight_GB_per_s": round(wbytes / (out["batched"] * 1e-3) / 1e9, 1),
+            "roofline_frac": round(wbytes / (out["batched"] * 1e-3) / (PEAK_HBM_GBS * 1e9), 4),
+            "vector_matvecs_per_s": round(batch * len(LAYER_SET_70B) / (out["batched"] * 1e-3)),
+            "batch1_x8_ms_per_step": round(out["batch1_x8"], 4),
+            "speedup_vs_batch1_x8": round(out["batch1_x8"] / out["batched"], 2),
+            "path": "vbs_gfx950_linear_batch: k_xprep_b + k_mvb (f16 MFMA) per matrix"}
+
+
+GEO_7B = dict(hidden=4096, ffn=11008, n_heads=32, n_kv_heads=8, head_dim=128, vocab=32000)
+GEO_70B = dict(hidden=8192, ffn=28672, n_heads=64, n_kv_heads=8, head_dim=128, vocab=32000)
+
+
+def bench_decode(dev, host, n_tokens, path="both", geo=GEO_7B, n_layers=32, ctx=2048,
+                 n_dispatch_tokens=16):
+    """Greedy decode of a Q4_K_M synthetic Llama model (config 4: 7B, 32 layers,
+    ctx 2048; config 5: 70B, 80 layers, ctx 8192) from position `ctx` with the
+    KV cache prefilled N(0,1): the graph decoder (one graph launch per token)
+    and, for comparison, the per-dispatch ops-table path."""
     n_dispatch_tokens = min(n_dispatch_tokens, n_tokens)
-    model = V.SynthModel(host, n_layers=n_layers, hidden=4096, ffn=11008, n_heads=32,
-                         n_kv_heads=8, head_dim=128, vocab=32000, max_ctx=ctx + n_tokens + 1,
-                         seed=SEED)
+    t_build = time.perf_counter()
+    model = V.SynthModel(host, n_layers=n_layers, **geo, max_ctx=ctx + n_tokens + 1, seed=SEED)
     kc, vc = model.kv_prefill(host, ctx)
     be = V.gfx950_backend()
     if not be.init():
         raise RuntimeError(be.last_error())
     d = V.Decoder(host, be, model)
     d.load_kv(kc, vc, ctx)
+    del kc, vc
+    t_build = time.perf_counter() - t_build
     # per-dispatch path (src/vbs_specializer.c order through the ops table)
     d.greedy(1, ctx, min(2, n_tokens))
     t0 = time.perf_counter()
@@ -283,7 +351,9 @@ def bench_decode(dev, host, n_tokens, path="both", n_layers=32, ctx=2048, n_disp
     kvd = model.cfg["n_kv_heads"] * model.cfg["head_dim"]
     kv_bytes = sum(n_layers * (ctx + i + 1) * kvd * 2 * 2 for i in range(n_tokens)) / n_tokens
     return {"tokens_per_s": round(n_tokens / dt, 2), "ms_per_token": round(1e3 * dt / n_tokens, 3),
-            "n_tokens": n_tokens, "context": ctx,
+            "n_tokens": n_tokens, "context": ctx, "n_layers": n_layers,
+            "hidden": geo["hidden"], "ffn": geo["ffn"], "heads": [geo["n_heads"], geo["n_kv_heads"]],
+            "model_build_upload_s": round(t_build, 1),
             "bytes_per_token": int(wbytes + kv_bytes),
             "roofline_frac": round((wbytes + kv_bytes) / (dt / n_tokens) / (PEAK_HBM_GBS * 1e9), 4),
             "path": ("vbs_gfx950_decoder kernels launched one by one" if eager else
@@ -303,6 +373,10 @@ def main():
     ap.add_argument("--roof-reps", type=int, default=50)
     ap.add_argument("--decode-tokens", type=int, default=128)
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-batch8", action="store_true",
+                    help="skip the config 5 batch-8 layer matvec set")
+    ap.add_argument("--decode-70b-tokens", type=int, default=32,
+                    help="greedy tokens of the 70B-shaped model (config 5, batch 1); 0 skips it")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="first copy this many MiB device-to-device once (a known-size "
                          "transfer that scales HBM byte counters)")
@@ -353,8 +427,13 @@ def main():
         "gpu_event_ms_per_step": round(r["gpu_ms"] / a.steps, 4),
         "graph_replay_equals_eager": r["replay_equals_eager"],
     }
+    if not a.no_batch8:
+        out["batch8_70b"] = bench_batch8_70b(dev, host)
     if not a.no_decode:
         out["decode"] = bench_decode(dev, host, a.decode_tokens, a.decode_path)
+        if a.decode_70b_tokens and a.decode_path == "both":
+            out["decode_70b"] = bench_decode(dev, host, a.decode_70b_tokens, geo=GEO_70B,
+                                             n_layers=80, ctx=8192, n_dispatch_tokens=4)
     if not a.no_cpu:
         out["cpu_baseline"] = cpu_baseline(host, r["weights_host"], r["xs_host"])
     print(json.dumps(out))

@@ -97,14 +97,19 @@ def test_gpu_tiny_model_greedy(host, backend, tiny):
     d.close()
 
 
+GEO_7B = dict(hidden=4096, ffn=11008, n_heads=32, n_kv_heads=8, head_dim=128, vocab=32000)
+GEO_70B = dict(hidden=8192, ffn=28672, n_heads=64, n_kv_heads=8, head_dim=128, vocab=32000)
+
+
 @pytest.mark.gpu
-@pytest.mark.parametrize("n_layers,n_tok", [(4, 12), (32, 3)], ids=["7b_4layers", "7b_full"])
-def test_gpu_7b_shape_greedy(host, backend, dev, n_layers, n_tok):
-    """7B geometry (config 4), KV prefilled N(0,1) to 2048, greedy from 2048."""
-    ctx = 2048
-    model = V.SynthModel(host, n_layers=n_layers, hidden=4096, ffn=11008, n_heads=32,
-                         n_kv_heads=8, head_dim=128, vocab=32000, max_ctx=ctx + n_tok + 1,
-                         seed=7)
+@pytest.mark.parametrize("geo,n_layers,ctx,n_tok", [(GEO_7B, 4, 2048, 12), (GEO_7B, 32, 2048, 3),
+                                                    (GEO_70B, 2, 8192, 3)],
+                         ids=["7b_4layers", "7b_full", "70b_2layers"])
+def test_gpu_llama_shape_greedy(host, backend, dev, geo, n_layers, ctx, n_tok):
+    """7B geometry (config 4), KV prefilled N(0,1) to 2048, greedy from 2048;
+    70B geometry (config 5) truncated to 2 of its 80 layers, KV prefilled to
+    8192, greedy from 8192."""
+    model = V.SynthModel(host, n_layers=n_layers, **geo, max_ctx=ctx + n_tok + 1, seed=7)
     kc_p, vc_p = model.kv_prefill(host, ctx)
     d = V.Decoder(host, backend, model)
     d.load_kv(kc_p, vc_p, ctx)

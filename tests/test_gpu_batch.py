@@ -1,0 +1,114 @@
+"""Batched (skinny) K-quant matvec on the gfx950 f16 matrix cores vs the oracle.
+
+The reference has no batched matvec (its decode loops tokens one by one,
+src/vbs_specializer.c:353-357), so the oracle of vbs_gfx950_linear_batch is
+`batch` independent vbs_host_linear_tile calls (src/vbs_host_math.h:223-267):
+every vector must meet the single matvec's bar, relative L2 <= 1e-5.
+"""
+import numpy as np
+import pytest
+
+import vbs_gfx950 as V
+from test_gpu_kernels import LIN_TOL, SEED, Mem, mem, rel_l2, synth_x  # noqa: F401 (mem: fixture)
+
+pytestmark = pytest.mark.gpu
+
+KQ = [V.Q4_K, V.Q6_K]
+
+
+def run_batch(dev, mem, t, w, X, rows, cols, xs=None, ys=None):
+    """Y = W X^T through the C ABI; X rows padded to stride xs, Y rows at
+    stride ys pre-filled with -3 (so untouched entries are visible)."""
+    batch = X.shape[0]
+    xs, ys = xs or cols, ys or rows
+    Xp = np.zeros((batch, xs), np.float32)
+    Xp[:, :cols] = X
+    pw, px = mem.up(w), mem.up(Xp)
+    py = mem.up(np.full(batch * ys, -3.0, np.float32))
+    dev.linear_batch(t, pw, px, xs, py, ys, cols, rows, batch)
+    return dev.download(py, (batch, ys), np.float32)
+
+
+def vectors(host, batch, cols, stream):
+    return np.stack([synth_x(host, cols, stream + b) for b in range(batch)])
+
+
+@pytest.mark.parametrize("t", KQ, ids=lambda t: V.TYPE_NAMES[t])
+@pytest.mark.parametrize("batch", [1, 2, 5, 8, 11, 16])
+@pytest.mark.parametrize("rows,cols", [(1, 256), (37, 4352), (700, 8192), (19, 11008),
+                                       (96, 28672), (1030, 4096)])
+def test_batch_parity(dev, host, oracle, mem, t, batch, rows, cols):
+    """Row counts that leave tiles, waves and workgroups partly idle, one to
+    eight blocks per wave, one and two launches of eight vectors."""
+    w = V.synth_matrix(host, t, rows, cols, SEED, 71)
+    X = vectors(host, batch, cols, 80)
+    Y = run_batch(dev, mem, t, w, X, rows, cols)
+    for b in range(batch):
+        assert rel_l2(Y[b], oracle.linear(t, w, X[b], cols, rows)) <= LIN_TOL, b
+
+
+@pytest.mark.parametrize("t", KQ, ids=lambda t: V.TYPE_NAMES[t])
+def test_batch_strides(dev, host, oracle, mem, t):
+    """x and y strides wider than the row; entries past `rows` untouched."""
+    rows, cols, batch = 300, 4096, 6
+    w = V.synth_matrix(host, t, rows, cols, SEED, 72)
+    X = vectors(host, batch, cols, 90)
+    Y = run_batch(dev, mem, t, w, X, rows, cols, xs=cols + 40, ys=rows + 13)
+    assert np.all(Y[:, rows:] == -3.0)
+    for b in range(batch):
+        assert rel_l2(Y[b, :rows], oracle.linear(t, w, X[b], cols, rows)) <= LIN_TOL
+
+
+@pytest.mark.parametrize("t", KQ, ids=lambda t: V.TYPE_NAMES[t])
+def test_batch_activation_edge_cases(dev, host, oracle, mem, t):
+    """Per-vector scaling: an all-zero vector, a vector of 1e-30 scale, one of
+    1e30 scale, outliers, zero and subnormal-scale sub-blocks; every vector
+    meets the bar on its own."""
+    rows, cols = 128, 4096
+    w = V.synth_matrix(host, t, rows, cols, SEED, 73)
+    X = vectors(host, 8, cols, 100)
+    X[0] = 0.0
+    X[1] *= 1e-30
+    X[2] *= 1e30
+    X[3, 40] = 1.0e4
+    X[4, 0:32] = 0.0
+    X[4, 64:96] *= 1e-40
+    X[5, 96:128] *= 1e30
+    X[6, 7] = -0.0
+    Y = run_batch(dev, mem, t, w, X, rows, cols)
+    assert np.all(Y[0] == 0.0)
+    for b in range(1, 8):
+        want = oracle.linear(t, w, X[b], cols, rows)
+        assert np.all(np.isfinite(Y[b])), b
+        assert rel_l2(Y[b], want) <= LIN_TOL, b
+
+
+@pytest.mark.parametrize("t", KQ, ids=lambda t: V.TYPE_NAMES[t])
+def test_batch_non_finite_vector(dev, host, oracle, mem, t):
+    """A vector holding inf or NaN gives NaN rows (as the batch-1 matrix-core
+    kernel does for such a sub-block); the other vectors are unaffected."""
+    rows, cols = 64, 4096
+    w = V.synth_matrix(host, t, rows, cols, SEED, 74)
+    X = vectors(host, 4, cols, 110)
+    X[1, 300] = np.inf
+    X[2, 5] = np.nan
+    Y = run_batch(dev, mem, t, w, X, rows, cols)
+    assert np.all(np.isnan(Y[1])) and np.all(np.isnan(Y[2]))
+    for b in (0, 3):
+        assert rel_l2(Y[b], oracle.linear(t, w, X[b], cols, rows)) <= LIN_TOL
+
+
+@pytest.mark.parametrize("t,rows,cols", [(V.Q4_K, 28672, 8192), (V.Q6_K, 8192, 28672),
+                                         (V.Q6_K, 32000, 8192)],
+                         ids=["q4k_70b_gate", "q6k_70b_down", "q6k_70b_head"])
+def test_batch_70b_shapes(dev, host, oracle, mem, t, rows, cols):
+    """BASELINE config 5 shapes at batch 8, the oracle on the first and last
+    192 rows (the packed rows are sliced out of the full matrix)."""
+    w = V.synth_matrix(host, t, rows, cols, SEED, 75)
+    X = vectors(host, 8, cols, 120)
+    Y = run_batch(dev, mem, t, w, X, rows, cols)
+    k = 192
+    for lo in (0, rows - k):
+        ws = np.ascontiguousarray(w[lo:lo + k])
+        for b in range(8):
+            assert rel_l2(Y[b, lo:lo + k], oracle.linear(t, ws, X[b], cols, k)) <= LIN_TOL, (lo, b)

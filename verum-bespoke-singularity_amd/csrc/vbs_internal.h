@@ -50,6 +50,13 @@ hipError_t launch_kq_silu(int type, const uint8_t *wg, const uint8_t *wu, const 
                           const float *norm_w, float eps, uint32_t cols, uint32_t rows,
                           float *hid, hipStream_t s);
 
+// Y[t] = W * X[t] for t < batch <= 8 (Q4_K / Q6_K) on the f16 matrix cores,
+// W read once; x prepared into the runtime scratch first. hipErrorNotSupported
+// (before anything is launched) outside the matrix-core shape range.
+hipError_t launch_kq_linear_batch(int type, const uint8_t *w, const float *x, uint32_t xs, float *y,
+                                  uint32_t ys, uint32_t cols, uint32_t rows, uint32_t batch,
+                                  hipStream_t s);
+
 // Specialised Q4_K matvec; hipErrorNotSupported when the shape/alignment is
 // outside its range (the generic kernel then runs).
 hipError_t launch_q4k_fast(const uint8_t *w, const float *x, float *y, uint32_t cols,

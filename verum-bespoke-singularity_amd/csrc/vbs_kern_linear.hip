@@ -245,6 +245,14 @@ hipError_t launch_linear_batch(int type, const uint8_t *w, const float *x, uint3
                                uint32_t ys, uint32_t cols, uint32_t rows, uint32_t batch,
                                hipStream_t s) {
     if (rows == 0 || batch == 0) return hipSuccess;
+    // K-quants: the matrix-core kernel, eight vectors per launch
+    if (type == kQ4_K || type == kQ6_K) {
+        hipError_t e = hipSuccess;
+        for (uint32_t b0 = 0; b0 < batch && e == hipSuccess; b0 += 8u)
+            e = launch_kq_linear_batch(type, w, x + (uint64_t)b0 * xs, xs, y + (uint64_t)b0 * ys, ys,
+                                       cols, rows, min(8u, batch - b0), s);
+        if (e != hipErrorNotSupported) return e;  // the shape check fails on the first launch
+    }
     uint64_t rb = row_bytes(type, cols);
     dim3 grid((rows + 3u) / 4u), block(256);
 #define VBS_LB(T) k_linear_batch<T, 16><<<grid, block, 0, s>>>(w, x, xs, y, ys, cols, rows, rb, batch)
