@@ -270,6 +270,10 @@ def test_add_in_place(dev, host, oracle, mem):
     (4, 4, 128, 1, 8, 2),          # one position
     (3, 1, 64, 65, 70, 0),         # group 3; last chunk holds one position
     (6, 2, 96, 100, 128, 0),       # head_dim 96: generic two-kernel path
+    (16, 8, 128, 33, 64, 1),       # group 2; the chunk's second tile holds one position
+    (8, 1, 128, 300, 512, 0),      # one kv head of eight q heads: many short chunks
+    (32, 4, 128, 5000, 5000, 0),   # group 8 over four kv heads, chunks of several tiles
+    (24, 8, 128, 257, 300, 2),     # group 3
 ])
 def test_attention(dev, host, oracle, mem, nqh, nkh, hd, seq, max_ctx, layer):
     layers = layer + 1
@@ -282,6 +286,24 @@ def test_attention(dev, host, oracle, mem, nqh, nkh, hd, seq, max_ctx, layer):
     dev.attention(pq, pkc, pvc, po, seq, layer, max_ctx, nqh, nkh, hd, np.float32(scale))
     got = dev.download(po, nqh * hd, np.float32)
     want = oracle.attention(q, kc, vc, seq, layer, max_ctx, nqh, nkh, hd, np.float32(scale))
+    assert np.all(np.abs(got - want) <= 1e-4 + 1e-4 * np.abs(want))
+
+
+@pytest.mark.parametrize("qscale", [1e-6, 1e4])
+def test_attention_q_magnitude(dev, host, oracle, mem, qscale):
+    """q far from unit scale (the matrix-core kernel rescales each head's q
+    before splitting it into f16 halves); scores stay moderate by a matching
+    softmax scale."""
+    nqh, nkh, hd, seq, max_ctx = 32, 8, 128, 700, 768
+    kvd = nkh * hd
+    kc = V.synth_normal_f16(host, max_ctx * kvd, SEED, 131)
+    vc = V.synth_normal_f16(host, max_ctx * kvd, SEED, 132)
+    q = synth_x(host, nqh * hd, 133) * np.float32(qscale)
+    scale = np.float32(1.0 / (math.sqrt(hd) * qscale))
+    pq, pkc, pvc, po = mem.up(q), mem.up(kc), mem.up(vc), mem.zeros(nqh * hd)
+    dev.attention(pq, pkc, pvc, po, seq, 0, max_ctx, nqh, nkh, hd, scale)
+    got = dev.download(po, nqh * hd, np.float32)
+    want = oracle.attention(q, kc, vc, seq, 0, max_ctx, nqh, nkh, hd, scale)
     assert np.all(np.abs(got - want) <= 1e-4 + 1e-4 * np.abs(want))
 
 

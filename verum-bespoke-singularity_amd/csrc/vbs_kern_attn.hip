@@ -16,13 +16,15 @@
 //
 // Fast chunk kernel (head_dim 32/64/128, group <= 8): four waves; lanes of a
 // wave split a position's head_dim into 8-element slices (16-byte K and V
-// loads), so one wave step covers 64/(head_dim/8) positions ("slots") and a
-// wave holds at most four steps, all loaded before any arithmetic. q lives in
-// registers (the lane's slice for every q head of the group); the partial
-// dot of a slice is an fp32 FMA chain and the slices are added with DPP row
-// operations, which leaves every lane of a slot with its scores. Each slot
-// keeps its own softmax state (max, sum, acc) over its positions, and one
-// LDS pass combines the slots. Scores are fp32 dots of exactly converted f16
+// loads), so one wave step covers 64/(head_dim/8) positions ("slots"). A wave
+// loads four steps at a time (up to four such batches; the next batch's K
+// rows are requested once the scores are taken, its V rows once they are
+// used). q lives in registers (the lane's slice for every q head of the
+// group); the partial dot of a slice is an fp32 FMA chain and the slices are
+// added with DPP row operations, which leaves every lane of a slot with its
+// scores. Each slot keeps a running softmax state (max, sum, acc) over its
+// positions; the slots of a wave are combined with lane shuffles and the four
+// waves in one LDS pass. Scores are fp32 dots of exactly converted f16
 // keys instead of the reference's double dot: a relative difference of order
 // 1e-7 in each score, far inside the 1e-4 the reference's own backend test
 // allows (src/vbs_backend_test.c:617-625).
@@ -36,25 +38,26 @@ namespace vbs {
 
 constexpr uint32_t kChunk = 64;  // positions per workgroup of the generic kernel
 constexpr uint32_t kMaxGroup = 16;
-constexpr uint32_t kTargetWgs = 512;  // workgroups the sequence split aims for
+constexpr uint32_t kTargetWgs = 512;      // workgroups the vector-ALU split aims for
+constexpr uint32_t kMfmaTargetWgs = 1024; // one-wave workgroups of the matrix-core split
 
 // Sequence split: chunks of `len` positions (a multiple of gran, at most lmax)
-// sized so that about kTargetWgs workgroups cover seq x nkh; n chunks per kv
+// sized so that about `target` workgroups cover seq x nkh; n chunks per kv
 // head. The chunk kernel, the merge and the host compute it identically.
 struct AttnSplit {
     uint32_t len, n;
 };
 __host__ __device__ inline AttnSplit attn_split(uint32_t seq, uint32_t nkh, uint32_t gran,
-                                                uint32_t lmax) {
-    const uint32_t per = (uint32_t)(((uint64_t)seq * nkh + kTargetWgs - 1u) / kTargetWgs);
+                                                uint32_t lmax, uint32_t target) {
+    const uint32_t per = (uint32_t)(((uint64_t)seq * nkh + target - 1u) / target);
     uint32_t len = (per + gran - 1u) / gran * gran;
     len = len < gran ? gran : len > lmax ? lmax : len;
     return {len, (seq + len - 1u) / len};
 }
 // Chunks per kv head of any split of a sequence of at most max_seq (every
-// len >= 64 or len >= seq * nkh / kTargetWgs).
+// len >= 64 or len >= seq * nkh / target, target <= kMfmaTargetWgs).
 inline uint32_t attn_max_chunks(uint32_t max_seq, uint32_t nkh) {
-    const uint32_t a = (kTargetWgs + nkh - 1u) / nkh, b = (max_seq + 63u) / 64u;
+    const uint32_t a = (kMfmaTargetWgs + nkh - 1u) / nkh, b = (max_seq + 63u) / 64u;
     return a > b ? a : b;
 }
 
@@ -183,12 +186,13 @@ __device__ __forceinline__ float fast_exp(float x) {
 }
 
 // Shape of the fast kernel: four waves; LPP lanes per position (8 head dims
-// each), so a wave step covers PPW positions; a wave holds at most kSteps steps.
-constexpr uint32_t kWaves = 4, kSteps = 4;
+// each), so a wave step covers PPW positions ("slots"); a wave loads kSteps
+// steps at a time and runs up to kBatches such batches.
+constexpr uint32_t kWaves = 4, kSteps = 4, kBatches = 4;
 template <uint32_t HD>
 struct ChunkShape {
     static constexpr uint32_t LPP = HD / 8, PPW = 64 / LPP, GRAN = kWaves * PPW,
-                              LMAX = kSteps * GRAN;
+                              LMAX = kBatches * kSteps * GRAN;
 };
 
 template <uint32_t HD, uint32_t GMAX>
@@ -197,36 +201,48 @@ __global__ __launch_bounds__(64 * kWaves) void k_attn_chunk(
     float *__restrict__ part, uint32_t seq_len, const uint32_t *__restrict__ pos_dev,
     uint64_t layer_off, uint32_t nkh, uint32_t group, float scale, uint32_t stride_chunks) {
     using S = ChunkShape<HD>;
-    constexpr uint32_t LPP = S::LPP, PPW = S::PPW, NK = kWaves * PPW;  // NK position slots
+    constexpr uint32_t LPP = S::LPP, PPW = S::PPW;
     extern __shared__ __align__(16) uint8_t chunk_lds[];
-    float *red = reinterpret_cast<float *>(chunk_lds);  // [NK][group][HD] acc per slot
-    __shared__ float sm[NK][GMAX], sl[NK][GMAX], sf[NK][GMAX];
+    float *red = reinterpret_cast<float *>(chunk_lds);  // [kWaves][group][HD] acc per wave
+    __shared__ float sm[kWaves][GMAX], sl[kWaves][GMAX], sf[kWaves][GMAX];
 
     const uint32_t chunk = blockIdx.x, kvh = blockIdx.y, t = threadIdx.x;
     const uint32_t wave = t >> 6, lane = t & 63u;
-    const uint32_t slot = lane / LPP, c = lane % LPP, k = wave * PPW + slot;
+    const uint32_t slot = lane / LPP, c = lane % LPP;
     if (pos_dev) seq_len = pos_dev[0] + 1u;  // graph replay: the device holds the position
-    const AttnSplit sp = attn_split(seq_len, nkh, S::GRAN, S::LMAX);
+    const AttnSplit sp = attn_split(seq_len, nkh, S::GRAN, S::LMAX, kTargetWgs);
     if (chunk >= sp.n) return;  // past the sequence (the grid covers the longest split)
     const uint32_t s0 = chunk * sp.len;
     const uint32_t valid = min(sp.len, seq_len - s0);
     const uint32_t pw = sp.len / kWaves, ns = pw / PPW;  // positions and steps per wave
+    const uint32_t nb = (ns + kSteps - 1u) / kSteps;     // batches of kSteps steps
     const uint64_t rstride = (uint64_t)nkh * HD;
     const uint64_t base = layer_off + (uint64_t)s0 * rstride + (uint64_t)kvh * HD + 8u * c;
 
-    // ---- this wave's K and V rows first (position wave*pw + b*PPW + slot;
-    // positions past the chunk re-read its last row and are masked) ----------
+    // position of step i of this lane's slot; positions past the chunk re-read
+    // its last row and are masked (score -inf, v zero)
+    auto pos_of = [&](uint32_t i) { return wave * pw + i * PPW + slot; };
     uint4 kr[kSteps], vr[kSteps];
+    auto load_k = [&](uint32_t bi) {
 #pragma unroll
-    for (uint32_t b = 0; b < kSteps; b++) {
-        if (b < ns) {
-            const uint32_t p = min(wave * pw + b * PPW + slot, valid - 1u);
-            kr[b] = *reinterpret_cast<const uint4 *>(kc + base + (uint64_t)p * rstride);
-            vr[b] = *reinterpret_cast<const uint4 *>(vc + base + (uint64_t)p * rstride);
-            // masked positions (re-read rows) add zeros: e = 0 and v = 0
-            if (wave * pw + b * PPW + slot >= valid) vr[b] = make_uint4(0u, 0u, 0u, 0u);
+        for (uint32_t b = 0; b < kSteps; b++)
+            if (bi * kSteps + b < ns)
+                kr[b] = *reinterpret_cast<const uint4 *>(
+                    kc + base + (uint64_t)min(pos_of(bi * kSteps + b), valid - 1u) * rstride);
+    };
+    auto load_v = [&](uint32_t bi) {
+#pragma unroll
+        for (uint32_t b = 0; b < kSteps; b++) {
+            const uint32_t i = bi * kSteps + b;
+            if (i < ns) {
+                vr[b] = *reinterpret_cast<const uint4 *>(
+                    vc + base + (uint64_t)min(pos_of(i), valid - 1u) * rstride);
+                if (pos_of(i) >= valid) vr[b] = make_uint4(0u, 0u, 0u, 0u);
+            }
         }
-    }
+    };
+    load_k(0);
+    load_v(0);
     float qv[GMAX][8];
 #pragma unroll
     for (uint32_t g = 0; g < GMAX; g++) {
@@ -238,70 +254,105 @@ __global__ __launch_bounds__(64 * kWaves) void k_attn_chunk(
         qv[g][4] = b4.x; qv[g][5] = b4.y; qv[g][6] = b4.z; qv[g][7] = b4.w;
     }
 
-    // ---- scores: every lane of a slot holds its position's scores --------------
-    float sc[kSteps][GMAX];
-#pragma unroll
-    for (uint32_t b = 0; b < kSteps; b++) {
-        const bool in = b < ns && wave * pw + b * PPW + slot < valid;
-        float kf[8];
-        if (b < ns) {
-            const uint32_t kw[4] = {kr[b].x, kr[b].y, kr[b].z, kr[b].w};
-#pragma unroll
-            for (uint32_t j = 0; j < 8; j++) kf[j] = hcvt(kw[j >> 1] >> (16u * (j & 1u)));
-        }
-#pragma unroll
-        for (uint32_t g = 0; g < GMAX; g++) {
-            float p = 0.f;
-            if (b < ns) {
-#pragma unroll
-                for (uint32_t j = 0; j < 8; j++) p = fmaf(qv[g][j], kf[j], p);
-                p = group_sum<LPP>(p);
-            }
-            sc[b][g] = in ? __fmul_rn(p, scale) : -INFINITY;
-        }
-    }
-
-    // ---- per slot: m = max score, l = sum e^(s - m), acc = sum e^(s - m) v -----
+    // per slot and q head: running max m, sum l of e^(s - m), acc of e^(s - m) v
+    float m[GMAX], l[GMAX], acc[GMAX][8];
 #pragma unroll
     for (uint32_t g = 0; g < GMAX; g++) {
-        float m = sc[0][g];
+        m[g] = -INFINITY;
+        l[g] = 0.f;
 #pragma unroll
-        for (uint32_t b = 1; b < kSteps; b++) m = fmaxf(m, sc[b][g]);
-        float l = 0.f, acc[8];
-#pragma unroll
-        for (uint32_t j = 0; j < 8; j++) acc[j] = 0.f;
+        for (uint32_t j = 0; j < 8; j++) acc[g][j] = 0.f;
+    }
+    for (uint32_t bi = 0; bi < nb; bi++) {
+        // scores: every lane of a slot holds its position's scores
+        float sc[kSteps][GMAX];
 #pragma unroll
         for (uint32_t b = 0; b < kSteps; b++) {
-            if (b < ns) {
-                const float e = sc[b][g] == -INFINITY ? 0.f : fast_exp(__fsub_rn(sc[b][g], m));
-                const uint32_t vw[4] = {vr[b].x, vr[b].y, vr[b].z, vr[b].w};
-                l += e;
+            const uint32_t i = bi * kSteps + b;
+            const bool in = i < ns && pos_of(i) < valid;
+            float kf[8];
+            if (i < ns) {
+                const uint32_t kw[4] = {kr[b].x, kr[b].y, kr[b].z, kr[b].w};
 #pragma unroll
-                for (uint32_t j = 0; j < 8; j++)
-                    acc[j] = fmaf(e, hcvt(vw[j >> 1] >> (16u * (j & 1u))), acc[j]);
+                for (uint32_t j = 0; j < 8; j++) kf[j] = hcvt(kw[j >> 1] >> (16u * (j & 1u)));
+            }
+#pragma unroll
+            for (uint32_t g = 0; g < GMAX; g++) {
+                float p = 0.f;
+                if (i < ns) {
+#pragma unroll
+                    for (uint32_t j = 0; j < 8; j++) p = fmaf(qv[g][j], kf[j], p);
+                    p = group_sum<LPP>(p);
+                }
+                sc[b][g] = in ? __fmul_rn(p, scale) : -INFINITY;
             }
         }
-        if (g < group) {
-            float *dst = red + ((k * group + g) * HD + 8u * c);
-            reinterpret_cast<float4 *>(dst)[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
-            reinterpret_cast<float4 *>(dst)[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+        if (bi + 1u < nb) load_k(bi + 1u);  // the K registers are free again
+#pragma unroll
+        for (uint32_t g = 0; g < GMAX; g++) {
+            float mb = sc[0][g];
+#pragma unroll
+            for (uint32_t b = 1; b < kSteps; b++) mb = fmaxf(mb, sc[b][g]);
+            const float mn = fmaxf(m[g], mb);
+            const float r = m[g] == -INFINITY ? 0.f : fast_exp(__fsub_rn(m[g], mn));
+            l[g] *= r;
+#pragma unroll
+            for (uint32_t j = 0; j < 8; j++) acc[g][j] *= r;
+#pragma unroll
+            for (uint32_t b = 0; b < kSteps; b++) {
+                if (bi * kSteps + b < ns) {
+                    const float e = sc[b][g] == -INFINITY ? 0.f : fast_exp(__fsub_rn(sc[b][g], mn));
+                    const uint32_t vw[4] = {vr[b].x, vr[b].y, vr[b].z, vr[b].w};
+                    l[g] += e;
+#pragma unroll
+                    for (uint32_t j = 0; j < 8; j++)
+                        acc[g][j] = fmaf(e, hcvt(vw[j >> 1] >> (16u * (j & 1u))), acc[g][j]);
+                }
+            }
+            m[g] = mn;
+        }
+        if (bi + 1u < nb) load_v(bi + 1u);
+    }
+
+    // ---- the wave's slots combined (lanes of equal c across slots): M = max m,
+    // weights e^(m - M) (0 for an empty slot), then sums; every slot ends with
+    // the totals and slot 0 stores them
+#pragma unroll
+    for (uint32_t g = 0; g < GMAX; g++) {
+        float M = m[g];
+#pragma unroll
+        for (uint32_t off = LPP; off < 64u; off <<= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+        const float f = m[g] == -INFINITY ? 0.f : fast_exp(__fsub_rn(m[g], M));
+        float L = l[g] * f, a[8];
+#pragma unroll
+        for (uint32_t j = 0; j < 8; j++) a[j] = acc[g][j] * f;
+#pragma unroll
+        for (uint32_t off = LPP; off < 64u; off <<= 1) {
+            L += __shfl_xor(L, off, 64);
+#pragma unroll
+            for (uint32_t j = 0; j < 8; j++) a[j] += __shfl_xor(a[j], off, 64);
+        }
+        if (g < group && slot == 0) {
+            float *dst = red + ((wave * group + g) * HD + 8u * c);
+            reinterpret_cast<float4 *>(dst)[0] = make_float4(a[0], a[1], a[2], a[3]);
+            reinterpret_cast<float4 *>(dst)[1] = make_float4(a[4], a[5], a[6], a[7]);
             if (c == 0) {
-                sm[k][g] = m;
-                sl[k][g] = l;
+                sm[wave][g] = M;
+                sl[wave][g] = L;
             }
         }
     }
     __syncthreads();
 
-    // ---- combine the slots: M = max m_k, weights e^(m_k - M) (0 for empty slots)
-    if (t < NK * GMAX) {
-        const uint32_t kk = t / GMAX, g = t % GMAX;
+    // ---- combine the waves: M = max m_w, weights e^(m_w - M) (0 for empty waves)
+    if (t < kWaves * GMAX) {
+        const uint32_t w = t / GMAX, g = t % GMAX;
         if (g < group) {
             float M = sm[0][g];
 #pragma unroll
-            for (uint32_t i = 1; i < NK; i++) M = fmaxf(M, sm[i][g]);
-            const float mk = sm[kk][g];
-            sf[kk][g] = mk == -INFINITY ? 0.f : fast_exp(__fsub_rn(mk, M));
+            for (uint32_t i = 1; i < kWaves; i++) M = fmaxf(M, sm[i][g]);
+            const float mw = sm[w][g];
+            sf[w][g] = mw == -INFINITY ? 0.f : fast_exp(__fsub_rn(mw, M));
         }
     }
     __syncthreads();
@@ -310,42 +361,234 @@ __global__ __launch_bounds__(64 * kWaves) void k_attn_chunk(
         const uint32_t g = i / HD, d = i % HD;
         float a = 0.f;
 #pragma unroll
-        for (uint32_t kk = 0; kk < NK; kk++) a = fmaf(red[(kk * group + g) * HD + d], sf[kk][g], a);
+        for (uint32_t w = 0; w < kWaves; w++) a = fmaf(red[(w * group + g) * HD + d], sf[w][g], a);
         float *dst = pk + ((uint64_t)g * stride_chunks + chunk) * (HD + 2u);
         dst[2u + d] = a;
         if (d == 0) {
             float M = sm[0][g], L = 0.f;
 #pragma unroll
-            for (uint32_t kk = 1; kk < NK; kk++) M = fmaxf(M, sm[kk][g]);
+            for (uint32_t w = 1; w < kWaves; w++) M = fmaxf(M, sm[w][g]);
 #pragma unroll
-            for (uint32_t kk = 0; kk < NK; kk++) L = fmaf(sl[kk][g], sf[kk][g], L);
+            for (uint32_t w = 0; w < kWaves; w++) L = fmaf(sl[w][g], sf[w][g], L);
             dst[0] = M;
             dst[1] = L;
         }
     }
 }
 
-// ---- merge of the chunks -------------------------------------------------------
-// One workgroup per q head; every global load is issued up front: thread
-// (d, slice) loads acc_c[d] of its chunks c = slice, slice + ns, ... and
-// thread t also m_t and l_t. Then M = max_c m_c (block maximum), weights
-// w_c = e^(m_c - M) in LDS, L = sum_c l_c w_c, and the slices' weighted sums
-// are added in LDS in a fixed order.
-constexpr uint32_t kMergeBatch = 32;  // chunks per thread held in registers at once
+// ---- matrix-core chunk kernel (head_dim 128, group <= 8) ------------------------
+// One wave per chunk of up to kMfmaTiles tiles of 32 positions, on
+// v_mfma_f32_16x16x32_f16:
+// * scores, S = K q^T: A = 16 positions x 32 head dims of K (the cache's f16,
+//   exact), B = 32 dims x 16 columns: column n holds q' of head n & 7, its
+//   f16 hi part for n < 8 and lo part (q' - hi) for n >= 8, with q' = q 2^s_h
+//   scaled so that the head's largest |q| lies in [2^14, 2^15). Columns n and
+//   n + 8 add up (a DPP row rotation) to the fp32 dot of k with q' to ~2^-22;
+//   the score is that times 2^-s_h * scale. Lane (n, g) then holds the scores
+//   of head n & 7 at positions 16 hf + 4 g + r (hf, r: the two 16-position
+//   halves of the tile, the four D rows).
+// * online softmax per head over the tiles (running max m, sum l).
+// * P V: A = P, rows n: e^(s - m) of head n & 7 (f16 hi for n < 8, lo for
+//   n >= 8), k slots = exactly the lane's own eight positions; B = V with the
+//   same k slots and column n of dim tile t standing for head dim 8 n + t, so
+//   lane (n, g) takes its B operands from eight 16-byte V rows it loaded
+//   itself (dims 8n..8n+7 of its eight positions) and no transpose is needed.
+//   D rows 0-7 (hi) and 8-15 (lo) add up at the end.
+// The chunk's (m, l, acc) go to the same partials as the vector-ALU kernel.
+constexpr uint32_t kMfmaGran = 32, kMfmaTiles = 8, kMfmaLmax = kMfmaGran * kMfmaTiles;
 
-__global__ __launch_bounds__(256) void k_attn_merge(const float *__restrict__ part,
+typedef _Float16 ah8 __attribute__((ext_vector_type(8)));
+typedef float af4 __attribute__((ext_vector_type(4)));
+typedef uint32_t au4 __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(64) void k_attn_mfma(const float *__restrict__ q,
+                                                  const uint16_t *__restrict__ kc,
+                                                  const uint16_t *__restrict__ vc,
+                                                  float *__restrict__ part, uint32_t seq_len,
+                                                  const uint32_t *__restrict__ pos_dev,
+                                                  uint64_t layer_off, uint32_t nkh, uint32_t group,
+                                                  float scale, uint32_t stride_chunks) {
+    constexpr uint32_t HD = 128;
+    const uint32_t chunk = blockIdx.x, kvh = blockIdx.y, lane = threadIdx.x;
+    const uint32_t n = lane & 15u, g = lane >> 4;
+    if (pos_dev) seq_len = pos_dev[0] + 1u;  // graph replay: the device holds the position
+    const AttnSplit sp = attn_split(seq_len, nkh, kMfmaGran, kMfmaLmax, kMfmaTargetWgs);
+    if (chunk >= sp.n) return;  // past the sequence (the grid covers the longest split)
+    const uint32_t s0 = chunk * sp.len, valid = min(sp.len, seq_len - s0);
+    const uint32_t nt = sp.len / kMfmaGran;
+    const uint64_t rstride = (uint64_t)nkh * HD;
+    const uint64_t base = layer_off + (uint64_t)s0 * rstride + (uint64_t)kvh * HD;
+
+    // ---- q' of head n & 7 (heads past the group repeat head 0 and are not stored)
+    const uint32_t h = n & 7u, hq = h < group ? h : 0u;
+    float qv[4][8];
+    {
+        const float4 *qp = reinterpret_cast<const float4 *>(q + ((uint64_t)kvh * group + hq) * HD);
+#pragma unroll
+        for (uint32_t kk = 0; kk < 4; kk++) {
+            const float4 a = qp[(32u * kk + 8u * g) / 4u], b = qp[(32u * kk + 8u * g) / 4u + 1u];
+            qv[kk][0] = a.x; qv[kk][1] = a.y; qv[kk][2] = a.z; qv[kk][3] = a.w;
+            qv[kk][4] = b.x; qv[kk][5] = b.y; qv[kk][6] = b.z; qv[kk][7] = b.w;
+        }
+    }
+    float amax = 0.f;
+#pragma unroll
+    for (uint32_t kk = 0; kk < 4; kk++)
+#pragma unroll
+        for (uint32_t j = 0; j < 8; j++) amax = fmaxf(amax, fabsf(qv[kk][j]));
+    amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+    int e2 = 0;
+    (void)frexpf(amax, &e2);  // amax < 2^e2
+    const int sq = amax > 0.f ? 15 - e2 : 0;
+    const float csc = ldexpf(scale, -sq);
+    ah8 Qb[4];
+#pragma unroll
+    for (uint32_t kk = 0; kk < 4; kk++)
+#pragma unroll
+        for (uint32_t j = 0; j < 8; j++) {
+            const float x = ldexpf(qv[kk][j], sq);
+            const _Float16 hi = (_Float16)x;
+            Qb[kk][j] = n < 8u ? hi : (_Float16)(x - (float)hi);
+        }
+
+    // ---- tile loads: K rows (A operand: position 16 hf + n, dims 32 kk + 8 g ..),
+    // V rows (position p_j of this lane group, dims 8 n ..); positions past the
+    // chunk re-read its last row and are masked
+    auto pos_of = [&](uint32_t t, uint32_t j) { return 32u * t + 16u * (j >> 2) + 4u * g + (j & 3u); };
+    au4 kr[2][4], vr[8];
+    auto load_k = [&](uint32_t t) {
+#pragma unroll
+        for (uint32_t hf = 0; hf < 2; hf++) {
+            const uint32_t p = min(32u * t + 16u * hf + n, valid - 1u);
+#pragma unroll
+            for (uint32_t kk = 0; kk < 4; kk++)
+                kr[hf][kk] = *reinterpret_cast<const au4 *>(kc + base + (uint64_t)p * rstride +
+                                                            32u * kk + 8u * g);
+        }
+    };
+    auto load_v = [&](uint32_t t) {
+#pragma unroll
+        for (uint32_t j = 0; j < 8; j++)
+            vr[j] = *reinterpret_cast<const au4 *>(
+                vc + base + (uint64_t)min(pos_of(t, j), valid - 1u) * rstride + 8u * n);
+    };
+    load_k(0);
+    load_v(0);
+
+    float m = -INFINITY, l = 0.f;
+    af4 acc[8];
+#pragma unroll
+    for (uint32_t t = 0; t < 8; t++) acc[t] = af4{0.f, 0.f, 0.f, 0.f};
+    for (uint32_t t = 0; t < nt; t++) {
+        af4 S[2];
+#pragma unroll
+        for (uint32_t hf = 0; hf < 2; hf++) {
+            S[hf] = af4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (uint32_t kk = 0; kk < 4; kk++)
+                S[hf] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(ah8, kr[hf][kk]),
+                                                              Qb[kk], S[hf], 0, 0, 0);
+        }
+        if (t + 1u < nt) load_k(t + 1u);  // the K registers are free again
+        // scores of positions p_j: hi + lo columns (lane n and n ^ 8), scaled, masked
+        float sc[8], mt = -INFINITY;
+#pragma unroll
+        for (uint32_t j = 0; j < 8; j++) {
+            const float v = S[j >> 2][j & 3u];
+            const float w = v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                                              0, __builtin_bit_cast(int, v), 0x128,
+                                                              0xF, 0xF, false));  // row_ror:8
+            sc[j] = pos_of(t, j) < valid ? __fmul_rn(w, csc) : -INFINITY;
+            mt = fmaxf(mt, sc[j]);
+        }
+        mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+        const float mn = fmaxf(m, mt);
+        const float rs = m == -INFINITY ? 0.f : fast_exp(__fsub_rn(m, mn));
+        m = mn;
+        l *= rs;
+        ah8 P;
+#pragma unroll
+        for (uint32_t j = 0; j < 8; j++) {
+            const float e = sc[j] == -INFINITY ? 0.f : fast_exp(__fsub_rn(sc[j], mn));
+            l += e;
+            const _Float16 hi = (_Float16)e;
+            P[j] = n < 8u ? hi : (_Float16)(e - (float)hi);
+        }
+        // D rows 4 g + r of the P V accumulators belong to head (4 g + r) & 7
+        float rsr[4];
+#pragma unroll
+        for (uint32_t r = 0; r < 4; r++) rsr[r] = __shfl(rs, (4u * g + r) & 7u, 64);
+#pragma unroll
+        for (uint32_t dt = 0; dt < 8; dt++) {
+            // B: element dt (head dim 8 n + dt) of each of the lane's eight V rows
+            const uint32_t sel = (dt & 1u) ? 0x07060302u : 0x05040100u;
+            au4 b;
+#pragma unroll
+            for (uint32_t i = 0; i < 4; i++)
+                b[i] = __builtin_amdgcn_perm(vr[2 * i + 1][dt >> 1], vr[2 * i][dt >> 1], sel);
+            af4 a = acc[dt];
+#pragma unroll
+            for (uint32_t r = 0; r < 4; r++) a[r] *= rsr[r];
+            acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(P, __builtin_bit_cast(ah8, b), a, 0, 0, 0);
+        }
+        if (t + 1u < nt) load_v(t + 1u);
+    }
+
+    // ---- the chunk's partial: l summed over the lane groups of a head, rows
+    // hi + lo of acc (lane groups g and g + 2), stored by lane groups 0 and 1
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    float a[8][4];
+#pragma unroll
+    for (uint32_t dt = 0; dt < 8; dt++)
+#pragma unroll
+        for (uint32_t r = 0; r < 4; r++) a[dt][r] = acc[dt][r] + __shfl_xor(acc[dt][r], 32, 64);
+    float *const pk = part + (uint64_t)kvh * group * stride_chunks * (HD + 2u);
+    if (g < 2u) {
+#pragma unroll
+        for (uint32_t r = 0; r < 4; r++) {
+            const uint32_t hh = 4u * g + r;
+            if (hh < group) {
+                float *dst = pk + ((uint64_t)hh * stride_chunks + chunk) * (HD + 2u) + 2u + 8u * n;
+#pragma unroll
+                for (uint32_t i = 0; i < 4; i++)
+                    reinterpret_cast<float2 *>(dst)[i] = make_float2(a[2 * i][r], a[2 * i + 1][r]);
+            }
+        }
+    }
+    if (g == 0 && n < group) {
+        float *dst = pk + ((uint64_t)n * stride_chunks + chunk) * (HD + 2u);
+        dst[0] = m;
+        dst[1] = l;
+    }
+}
+
+// ---- merge of the chunks -------------------------------------------------------
+// One workgroup of kMergeThreads per q head; every global load is issued up
+// front: thread (d, slice) loads acc_c[d] of its chunks c = slice, slice + ns,
+// ... and thread t also m_t and l_t. Then M = max_c m_c (block maximum),
+// weights w_c = e^(m_c - M) in LDS, L = sum_c l_c w_c, and the slices'
+// weighted sums are added in LDS in a fixed order.
+constexpr uint32_t kMergeBatch = 32;     // chunks per thread held in registers at once
+constexpr uint32_t kMergeThreads = 1024;
+
+__global__ __launch_bounds__(kMergeThreads) void k_attn_merge(const float *__restrict__ part,
                                                     float *__restrict__ out, uint32_t hd,
                                                     uint32_t n_chunks, uint32_t stride_chunks,
                                                     const uint32_t *__restrict__ pos_dev,
-                                                    uint32_t nkh, uint32_t gran, uint32_t lmax) {
+                                                    uint32_t nkh, uint32_t gran, uint32_t lmax,
+                                                    uint32_t target) {
     extern __shared__ __align__(16) uint8_t merge_lds[];
     float *w = reinterpret_cast<float *>(merge_lds);  // [stride_chunks]
-    float *sl = w + stride_chunks;                    // [256]
-    __shared__ float red[8];
+    float *sl = w + stride_chunks;                    // [kMergeThreads]
+    constexpr uint32_t NW = kMergeThreads / 64u;
+    __shared__ float red[2 * NW];
     const uint32_t h = blockIdx.x, t = threadIdx.x, lane = t & 63u, wave = t >> 6;
-    if (pos_dev) n_chunks = attn_split(pos_dev[0] + 1u, nkh, gran, lmax).n;  // seq_len = pos + 1
+    if (pos_dev) n_chunks = attn_split(pos_dev[0] + 1u, nkh, gran, lmax, target).n;  // seq = pos + 1
     const float *ph = part + (uint64_t)h * stride_chunks * (hd + 2u);
-    const uint32_t ns = 256u / hd;
+    const uint32_t ns = kMergeThreads / hd;
     const uint32_t d = t % hd, s = t / hd;
     float av[kMergeBatch];
 #pragma unroll
@@ -355,22 +598,24 @@ __global__ __launch_bounds__(256) void k_attn_merge(const float *__restrict__ pa
     }
     // this thread's chunks' (m, l): c = t, t + 256, ...
     float M = -INFINITY;
-    for (uint32_t c = t; c < n_chunks; c += 256u) M = fmaxf(M, ph[(uint64_t)c * (hd + 2u)]);
+    for (uint32_t c = t; c < n_chunks; c += kMergeThreads) M = fmaxf(M, ph[(uint64_t)c * (hd + 2u)]);
     M = wave_max(M);
     if (lane == 0) red[wave] = M;
     __syncthreads();
-    M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    M = red[0];
+    for (uint32_t i = 1; i < NW; i++) M = fmaxf(M, red[i]);
     float L = 0.f;
-    for (uint32_t c = t; c < n_chunks; c += 256u) {
+    for (uint32_t c = t; c < n_chunks; c += kMergeThreads) {
         const float *pc = ph + (uint64_t)c * (hd + 2u);
         const float mc = pc[0], wc = mc == -INFINITY ? 0.f : fast_exp(__fsub_rn(mc, M));
         w[c] = wc;
         L = fmaf(pc[1], wc, L);
     }
     L = wave_sum(L);
-    if (lane == 0) red[4 + wave] = L;
+    if (lane == 0) red[NW + wave] = L;
     __syncthreads();
-    L = (red[4] + red[5]) + (red[6] + red[7]);
+    L = 0.f;
+    for (uint32_t i = 0; i < NW; i++) L += red[NW + i];
     float a = 0.f;
     if (s < ns) {
 #pragma unroll
@@ -399,7 +644,7 @@ static hipError_t launch_chunk_hd(dim3 grid, hipStream_t s, const float *q, cons
                                   const uint16_t *vc, float *part, uint32_t seq_len,
                                   const uint32_t *pos_dev, uint64_t layer_off, uint32_t nkh,
                                   uint32_t group, float scale) {
-    const size_t lds = (size_t)ChunkShape<HD>::GRAN * group * HD * sizeof(float);
+    const size_t lds = (size_t)kWaves * group * HD * sizeof(float);
 #define VBS_ATTN_G(GG)                                                                          \
     do {                                                                                        \
         k_attn_chunk<HD, GG><<<grid, 64u * kWaves, lds, s>>>(q, kc, vc, part, seq_len, pos_dev,   \
@@ -429,9 +674,14 @@ hipError_t launch_attention(const float *q, const uint16_t *kc, const uint16_t *
                       ((uintptr_t)q & 15u) == 0 && ((uintptr_t)kc & 15u) == 0 &&
                       ((uintptr_t)vc & 15u) == 0;
     hipError_t e;
-    uint32_t gran = kChunk, lmax = kChunk;
+    uint32_t gran = kChunk, lmax = kChunk, target = kTargetWgs;
     const dim3 grid(stride, nkh);
-    if (fast && hd == 32u) {
+    if (fast && hd == 128u) {
+        gran = kMfmaGran, lmax = kMfmaLmax, target = kMfmaTargetWgs;
+        k_attn_mfma<<<grid, 64, 0, s>>>(q, kc, vc, part, seq_len, pos_dev, layer_off, nkh, group,
+                                        scale, stride);
+        e = hipGetLastError();
+    } else if (fast && hd == 32u) {
         gran = ChunkShape<32>::GRAN, lmax = ChunkShape<32>::LMAX;
         e = launch_chunk_hd<32>(grid, s, q, kc, vc, part, seq_len, pos_dev, layer_off, nkh, group,
                                 scale);
@@ -451,9 +701,10 @@ hipError_t launch_attention(const float *q, const uint16_t *kc, const uint16_t *
         e = hipGetLastError();
     }
     if (e != hipSuccess) return e;
-    const uint32_t n_chunks = attn_split(seq_len, nkh, gran, lmax).n;
-    const size_t mlds = ((size_t)stride + 256u) * sizeof(float);
-    k_attn_merge<<<nqh, 256, mlds, s>>>(part, out, hd, n_chunks, stride, pos_dev, nkh, gran, lmax);
+    const uint32_t n_chunks = attn_split(seq_len, nkh, gran, lmax, target).n;
+    const size_t mlds = ((size_t)stride + kMergeThreads) * sizeof(float);
+    k_attn_merge<<<nqh, kMergeThreads, mlds, s>>>(part, out, hd, n_chunks, stride, pos_dev, nkh, gran,
+                                                  lmax, target);
     return hipGetLastError();
 }
 
