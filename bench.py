@@ -308,7 +308,7 @@ GEO_70B = dict(hidden=8192, ffn=28672, n_heads=64, n_kv_heads=8, head_dim=128, v
 
 
 def bench_decode(dev, host, n_tokens, path="both", geo=GEO_7B, n_layers=32, ctx=2048,
-                 n_dispatch_tokens=16):
+                 n_dispatch_tokens=16, batch=0, batch_tokens=16):
     """Greedy decode of a Q4_K_M synthetic Llama model (config 4: 7B, 32 layers,
     ctx 2048; config 5: 70B, 80 layers, ctx 8192) from position `ctx` with the
     KV cache prefilled N(0,1): the graph decoder (one graph launch per token)
@@ -322,7 +322,6 @@ def bench_decode(dev, host, n_tokens, path="both", geo=GEO_7B, n_layers=32, ctx=
         raise RuntimeError(be.last_error())
     d = V.Decoder(host, be, model)
     d.load_kv(kc, vc, ctx)
-    del kc, vc
     t_build = time.perf_counter() - t_build
     # per-dispatch path (src/vbs_specializer.c order through the ops table)
     d.greedy(1, ctx, min(2, n_tokens))
@@ -346,6 +345,10 @@ def bench_decode(dev, host, n_tokens, path="both", geo=GEO_7B, n_layers=32, ctx=
     toks, margins = g.greedy(1, ctx, n_tokens, eager)
     dt = time.perf_counter() - t0
     g.close()
+    batched = None
+    if batch:
+        batched = bench_batch_decode(dev, d, model, kc, vc, ctx, batch, batch_tokens)
+    del kc, vc
     d.close()
     wbytes = model.weight_bytes() - model.tok_embd.nbytes
     kvd = model.cfg["n_kv_heads"] * model.cfg["head_dim"]
@@ -361,6 +364,36 @@ def bench_decode(dev, host, n_tokens, path="both", geo=GEO_7B, n_layers=32, ctx=
             "dispatch_path": dispatch,
             "paths_agree": bool(np.array_equal(toks[:n_dispatch_tokens], dtoks)),
             "first_tokens": [int(x) for x in toks[:8]],
+            "min_margin": float(np.min(margins)),
+            **({"batch_decode": batched} if batched else {})}
+
+
+def bench_batch_decode(dev, d, model, kc, vc, ctx, batch, n_tokens):
+    """Greedy decode of `batch` sequences at once (vbs_gfx950_bdecoder, one
+    HIP graph per step) over the same device weights: every sequence's own
+    cache holds the same N(0,1) prefill to `ctx`, the start tokens differ."""
+    c = model.cfg
+    bd = V.BatchDecoder(dev, d, batch, max_steps=n_tokens)
+    for b in range(batch):
+        bd.load_kv(b, kc, vc, ctx)
+    tok0, pos0 = [1 + 7 * b for b in range(batch)], [ctx] * batch
+    bd.greedy(tok0, pos0, 2)
+    dev.sync()
+    t0 = time.perf_counter()
+    toks, margins = bd.greedy(tok0, pos0, n_tokens)
+    dt = time.perf_counter() - t0
+    bd.close()
+    kvd = c["n_kv_heads"] * c["head_dim"]
+    wbytes = model.weight_bytes() - model.tok_embd.nbytes
+    kv_bytes = batch * sum(c["n_layers"] * (ctx + i + 1) * kvd * 2 * 2
+                           for i in range(n_tokens)) / n_tokens
+    step_s = dt / n_tokens
+    return {"batch": batch, "tokens_per_s": round(batch * n_tokens / dt, 2),
+            "ms_per_step": round(1e3 * step_s, 3), "steps": n_tokens,
+            "bytes_per_step": int(wbytes + kv_bytes),
+            "roofline_frac": round((wbytes + kv_bytes) / step_s / (PEAK_HBM_GBS * 1e9), 4),
+            "path": "vbs_gfx950_bdecoder: one HIP graph launch per step of all sequences",
+            "first_tokens_seq0": [int(x) for x in toks[:8, 0]],
             "min_margin": float(np.min(margins))}
 
 
@@ -433,7 +466,8 @@ def main():
         out["decode"] = bench_decode(dev, host, a.decode_tokens, a.decode_path)
         if a.decode_70b_tokens and a.decode_path == "both":
             out["decode_70b"] = bench_decode(dev, host, a.decode_70b_tokens, geo=GEO_70B,
-                                             n_layers=80, ctx=8192, n_dispatch_tokens=4)
+                                             n_layers=80, ctx=8192, n_dispatch_tokens=4,
+                                             batch=8, batch_tokens=16)
     if not a.no_cpu:
         out["cpu_baseline"] = cpu_baseline(host, r["weights_host"], r["xs_host"])
     print(json.dumps(out))

@@ -176,6 +176,26 @@ int vbs_gfx950_decoder_greedy_eager(void *handle, uint32_t token, uint32_t pos, 
                                     uint32_t *tokens, float *margins);
 int vbs_gfx950_decoder_destroy(void *handle);
 
+/* ---- batched decode (extension) --------------------------------------------
+ * The decode step above for `batch` (1..8) independent sequences over one copy
+ * of the weights (BASELINE config 5 at batch 8): each sequence has its own
+ * caches, m->kc / m->vc + b * kv_seq_stride elements (the model's layout per
+ * sequence), its own token and position. Every matrix must be Q4_K or Q6_K
+ * (the batched matrix-core kernels; q/k/v and gate/up pairwise of one type).
+ * The reference has no batched decode (src/vbs_specializer.c:353-357 loops
+ * tokens one by one); each sequence computes the single-sequence step. */
+int vbs_gfx950_bdecoder_create(const vbs_gfx950_model_t *m, uint32_t batch, uint64_t kv_seq_stride,
+                               uint32_t max_steps, void **handle);
+/* Greedy for every sequence: feed tokens0[b] at pos0[b], then n-1 further
+ * argmax tokens; tokens[i * batch + b] is sequence b's i-th argmax, margins
+ * (may be NULL) its top-1 minus top-2 logit. */
+int vbs_gfx950_bdecoder_greedy(void *handle, const uint32_t *tokens0, const uint32_t *pos0,
+                               uint32_t n, uint32_t *tokens, float *margins);
+/* The same with every kernel launched directly (for kernel tracers). */
+int vbs_gfx950_bdecoder_greedy_eager(void *handle, const uint32_t *tokens0, const uint32_t *pos0,
+                                     uint32_t n, uint32_t *tokens, float *margins);
+int vbs_gfx950_bdecoder_destroy(void *handle);
+
 #ifdef __cplusplus
 }
 #endif

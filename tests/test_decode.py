@@ -189,3 +189,72 @@ def test_gpu_graph_decoder_rejects_bad_state(host, backend, dev, tiny):
         g.greedy(0, tiny.cfg["max_ctx"] - 2, 4)
     g.close()
     d.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("geo,n_layers,ctx,batch,n_tok", [
+    (dict(TINY, n_layers=None, max_ctx=None), 2, 40, 5, 8),
+    (GEO_7B, 2, 2048, 8, 3),
+    (GEO_70B, 1, 8192, 8, 2)],
+    ids=["tiny_b5", "7b_2layers_b8", "70b_1layer_b8"])
+def test_gpu_batch_decoder_matches_oracle(host, backend, dev, geo, n_layers, ctx, batch, n_tok):
+    """Batched decode (config 5 at batch 8): every sequence has its own KV
+    prefill, start token and position; its greedy tokens must be the
+    oracle's for that sequence alone."""
+    geo = {k: v for k, v in geo.items() if k not in ("n_layers", "max_ctx")}
+    max_ctx = ctx + n_tok + 1
+    model = V.SynthModel(host, n_layers=n_layers, **geo, max_ctx=max_ctx, seed=11)
+    c = model.cfg
+    kvd = c["n_kv_heads"] * c["head_dim"]
+    d = V.Decoder(host, backend, model)
+    bd = V.BatchDecoder(dev, d, batch, max_steps=n_tok)
+    pos0 = [ctx - 3 * b for b in range(batch)]
+    tok0 = [(17 + 101 * b) % c["vocab"] for b in range(batch)]
+    prefills = []
+    for b in range(batch):
+        n = n_layers * pos0[b] * kvd
+        kc_p = V.synth_normal_f16(host, n, 500 + b, 10)
+        vc_p = V.synth_normal_f16(host, n, 500 + b, 11)
+        bd.load_kv(b, kc_p, vc_p, pos0[b])
+        prefills.append((kc_p, vc_p))
+    toks, margins = bd.greedy(tok0, pos0, n_tok)
+    bd.close()
+    d.close()
+    oracle = Oracle()
+    for b in range(batch):
+        kc, vc = full_cache(model, prefills[b][0], prefills[b][1], pos0[b])
+        want, _ = oracle_greedy(oracle, model, kc, vc, tok0[b], pos0[b], n_tok)
+        assert np.array_equal(toks[:, b], want), (b, toks[:, b], want, margins[:, b])
+
+
+@pytest.mark.gpu
+def test_gpu_batch_decoder_graph_equals_eager(host, backend, dev, tiny):
+    """The captured step and the same launches issued directly agree bit for
+    bit (tokens and margins)."""
+    c = tiny.cfg
+    kvd = c["n_kv_heads"] * c["head_dim"]
+    d = V.Decoder(host, backend, tiny)
+    out = []
+    for eager in (False, True):
+        bd = V.BatchDecoder(dev, d, 3, max_steps=6)
+        for b in range(3):
+            n = c["n_layers"] * 20 * kvd
+            bd.load_kv(b, V.synth_normal_f16(host, n, 600 + b, 10),
+                       V.synth_normal_f16(host, n, 600 + b, 11), 20)
+        out.append(bd.greedy([1, 2, 3], [20, 20, 20], 6, eager))
+        bd.close()
+    d.close()
+    assert np.array_equal(out[0][0], out[1][0])
+    assert np.array_equal(out[0][1].view(np.uint32), out[1][1].view(np.uint32))
+
+
+@pytest.mark.gpu
+def test_gpu_batch_decoder_rejects(host, backend, dev, tiny):
+    d = V.Decoder(host, backend, tiny)
+    with pytest.raises(V.GpuError, match="batch"):
+        V.BatchDecoder(dev, d, 9)
+    bd = V.BatchDecoder(dev, d, 2, max_steps=4)
+    with pytest.raises(V.GpuError, match="context exhausted"):
+        bd.greedy([1, 1], [0, tiny.cfg["max_ctx"] - 2], 4)
+    bd.close()
+    d.close()

@@ -84,12 +84,19 @@ __device__ __forceinline__ Top2 top2_merge(Top2 a, Top2 b) {
     return r;
 }
 
+// One workgroup per sequence b of a batch (gridDim.x sequences): logits row b,
+// state token_dev[b], pos_dev[b], step_dev[b], outputs tokens[step * nb + b].
 __global__ __launch_bounds__(1024) void k_argmax_advance(const float *__restrict__ logits,
                                                          uint32_t n, uint32_t *token_dev,
                                                          uint32_t *pos_dev, uint32_t *step_dev,
                                                          uint32_t *tokens, float *margins,
                                                          uint32_t max_steps) {
     __shared__ Top2 red[16];
+    const uint32_t sb = blockIdx.x, nb = gridDim.x;
+    logits += (uint64_t)sb * n;
+    token_dev += sb;
+    pos_dev += sb;
+    step_dev += sb;
     Top2 t{-INFINITY, 0xFFFFFFFFu, -INFINITY};
     auto consider = [&](float v, uint32_t i) {
         if (v != v && i != 0u) return;  // a NaN never beats anything after index 0
@@ -141,8 +148,8 @@ __global__ __launch_bounds__(1024) void k_argmax_advance(const float *__restrict
     if (threadIdx.x == 0) {
         const uint32_t step = step_dev[0];
         if (step < max_steps) {
-            tokens[step] = red[0].i1;
-            margins[step] = red[0].v1 - red[0].v2;
+            tokens[step * nb + sb] = red[0].i1;
+            margins[step * nb + sb] = red[0].v1 - red[0].v2;
         }
         token_dev[0] = red[0].i1;
         pos_dev[0] = pos_dev[0] + 1u;
@@ -441,6 +448,318 @@ int vbs_gfx950_decoder_greedy_eager(void *handle, uint32_t token, uint32_t pos, 
 
 int vbs_gfx950_decoder_destroy(void *handle) {
     decoder_free((Decoder *)handle);
+    return 1;
+}
+
+}  // extern "C"
+
+// ---- batched decode step (up to 8 sequences) ---------------------------------
+//
+// The same token step for `batch` independent sequences, each with its own
+// KV cache (sequence b's caches at + b kv_seq elements) and position, over
+// one copy of the weights: every matrix is one batched matrix-core launch
+// (x prepared once per launch: attn_norm / ffn_norm / output_norm and
+// SiLU*up are folded into the preparation), Q, K, V share a launch, as do
+// gate and up; O and down add into the residual stream; RoPE and the cache
+// store of every sequence are one launch and attention one pair of launches
+// over all sequences. 11 launches per layer. The reference has no batched
+// decode (src/vbs_specializer.c:353-357 loops tokens one by one): each
+// sequence computes the single-sequence step, with the batched matvec's
+// arithmetic.
+namespace vbs {
+
+__global__ __launch_bounds__(256) void k_rope_store_b(float *__restrict__ q, const float *__restrict__ k,
+                                                      const float *__restrict__ v, uint32_t qd,
+                                                      uint32_t kvd, uint32_t hd,
+                                                      const float2 *__restrict__ tab,
+                                                      const uint32_t *__restrict__ pos_dev,
+                                                      uint16_t *__restrict__ kc,
+                                                      uint16_t *__restrict__ vc, uint64_t kv_seq,
+                                                      uint64_t layer_off, uint32_t max_ctx) {
+    const uint32_t b = blockIdx.y, u = blockIdx.x * 256u + threadIdx.x;
+    const uint32_t pairs = hd / 2u, nqp = qd / 2u, nkp = kvd / 2u;
+    if (u >= nqp + 2u * nkp) return;
+    const uint32_t pos = pos_dev[b];
+    if (pos >= max_ctx) return;  // (the host bounds every greedy run by max_ctx)
+    const uint64_t row = (uint64_t)b * kv_seq + layer_off + (uint64_t)pos * kvd;
+    auto rope = [&](float &x0, float &x1, uint32_t p) {
+        const float2 cs = tab[(uint64_t)pos * pairs + p];
+        const float a = x0, c = x1;
+        x0 = __fsub_rn(__fmul_rn(a, cs.x), __fmul_rn(c, cs.y));
+        x1 = __fadd_rn(__fmul_rn(a, cs.y), __fmul_rn(c, cs.x));
+    };
+    if (u < nqp) {  // q pair, in place (src/vbs_host_math.h:38-51)
+        float *x = q + (uint64_t)b * qd + 2u * u;
+        float x0 = x[0], x1 = x[1];
+        rope(x0, x1, u % pairs);
+        x[0] = x0;
+        x[1] = x1;
+    } else if (u < nqp + nkp) {  // k pair: RoPE, then the f16 store (src/vbs_host_math.h:150-159)
+        const uint32_t i = 2u * (u - nqp);
+        float x0 = k[(uint64_t)b * kvd + i], x1 = k[(uint64_t)b * kvd + i + 1u];
+        rope(x0, x1, (u - nqp) % pairs);
+        kc[row + i] = vbs_f2h(x0);
+        kc[row + i + 1u] = vbs_f2h(x1);
+    } else {  // v pair: the f16 store
+        const uint32_t i = 2u * (u - nqp - nkp);
+        vc[row + i] = vbs_f2h(v[(uint64_t)b * kvd + i]);
+        vc[row + i + 1u] = vbs_f2h(v[(uint64_t)b * kvd + i + 1u]);
+    }
+}
+
+struct BDecoder {
+    vbs_gfx950_model_t m;
+    uint32_t batch = 0;
+    uint64_t kv_seq = 0;
+    std::vector<const float *> attn_norm, ffn_norm;
+    std::vector<int> wtype;
+    std::vector<const void *> wdata;
+    float *x = nullptr, *q, *k, *v, *attn, *gate, *up, *logits, *part;
+    uint8_t *xp = nullptr;
+    float2 *rope = nullptr;
+    uint32_t *state = nullptr;  // token[batch], pos[batch], step[batch]
+    uint32_t *tokens = nullptr;
+    float *margins = nullptr;
+    uint32_t max_steps = 0;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    void *arena = nullptr;
+};
+
+static hipError_t enqueue_step_batch(const BDecoder &d, hipStream_t s) {
+    const vbs_gfx950_model_t &m = d.m;
+    const uint32_t B = d.batch, H = m.hidden, F = m.ffn, hd = m.head_dim;
+    const uint32_t nq = m.n_heads, nkv = m.n_kv_heads, qd = nq * hd, kvd = nkv * hd, V = m.vocab;
+    const float scale = 1.0f / sqrtf((float)hd);
+    uint32_t *token_dev = d.state, *pos_dev = d.state + B, *step_dev = d.state + 2u * B;
+#define VBS_TRY(expr)                     \
+    do {                                  \
+        hipError_t e_ = (expr);           \
+        if (e_ != hipSuccess) return e_;  \
+    } while (0)
+    VBS_TRY(launch_dequant_rows(m.embd_type, (const uint8_t *)m.tok_embd, token_dev, 0, B, H, d.x, s));
+    const uint32_t units = qd / 2u + kvd;
+    for (uint32_t L = 0; L < m.n_layers; L++) {
+        const int *t = d.wtype.data() + 7 * L;
+        const uint8_t *const *w = (const uint8_t *const *)d.wdata.data() + 7 * L;
+        const uint64_t layer_off = (uint64_t)L * m.max_ctx * kvd;
+        {  // attn_norm, Q, K, V
+            VBS_TRY(launch_xprep(XP_NORM, d.x, nullptr, H, d.attn_norm[L], m.rms_eps, H, B, d.xp, s));
+            const uint32_t rows[3] = {qd, kvd, kvd}, ys[3] = {qd, kvd, kvd};
+            float *const y[3] = {d.q, d.k, d.v};
+            VBS_TRY(launch_mvb(t[0], 3, w, rows, y, ys, 0, d.xp, H, B, s));
+        }
+        k_rope_store_b<<<dim3((units + 255u) / 256u, B), 256, 0, s>>>(
+            d.q, d.k, d.v, qd, kvd, hd, d.rope, pos_dev, m.kc, m.vc, d.kv_seq, layer_off, m.max_ctx);
+        VBS_TRY(hipGetLastError());
+        VBS_TRY(launch_attention_batch(d.q, m.kc, m.vc, d.attn, m.max_ctx, pos_dev, d.part, layer_off,
+                                       nq, nkv, hd, scale, B, qd, d.kv_seq, s));
+        {  // O, added into the residual stream
+            VBS_TRY(launch_xprep(XP_PLAIN, d.attn, nullptr, qd, nullptr, 0.f, qd, B, d.xp, s));
+            const uint32_t rows[1] = {H}, ys[1] = {H};
+            float *const y[1] = {d.x};
+            VBS_TRY(launch_mvb(t[3], 1, w + 3, rows, y, ys, 1, d.xp, qd, B, s));
+        }
+        {  // ffn_norm, gate and up
+            VBS_TRY(launch_xprep(XP_NORM, d.x, nullptr, H, d.ffn_norm[L], m.rms_eps, H, B, d.xp, s));
+            const uint32_t rows[2] = {F, F}, ys[2] = {F, F};
+            float *const y[2] = {d.gate, d.up};
+            VBS_TRY(launch_mvb(t[4], 2, w + 4, rows, y, ys, 0, d.xp, H, B, s));
+        }
+        {  // SiLU*up, down, added into the residual stream
+            VBS_TRY(launch_xprep(XP_SILU, d.gate, d.up, F, nullptr, 0.f, F, B, d.xp, s));
+            const uint32_t rows[1] = {H}, ys[1] = {H};
+            float *const y[1] = {d.x};
+            VBS_TRY(launch_mvb(t[6], 1, w + 6, rows, y, ys, 1, d.xp, F, B, s));
+        }
+    }
+    {  // output_norm and lm_head
+        VBS_TRY(launch_xprep(XP_NORM, d.x, nullptr, H, m.out_norm, m.rms_eps, H, B, d.xp, s));
+        const uint8_t *wh[1] = {(const uint8_t *)m.lm_head};
+        const uint32_t rows[1] = {V}, ys[1] = {V};
+        float *const y[1] = {d.logits};
+        VBS_TRY(launch_mvb(m.head_type, 1, wh, rows, y, ys, 0, d.xp, H, B, s));
+    }
+    k_argmax_advance<<<B, 1024, 0, s>>>(d.logits, V, token_dev, pos_dev, step_dev, d.tokens,
+                                        d.margins, d.max_steps);
+    VBS_TRY(hipGetLastError());
+#undef VBS_TRY
+    return hipSuccess;
+}
+
+static void bdecoder_free(BDecoder *d) {
+    if (!d) return;
+    if (d->exec) (void)hipGraphExecDestroy(d->exec);
+    if (d->graph) (void)hipGraphDestroy(d->graph);
+    if (d->arena) {
+        (void)hipStreamSynchronize(rt_stream());
+        (void)hipFree(d->arena);
+    }
+    delete d;
+}
+
+static bool kq_type(int t) { return t == kQ4_K || t == kQ6_K; }
+static bool kq_cols(uint32_t c) { return c && c % 256u == 0 && c / 256u <= 128u; }
+
+}  // namespace vbs
+
+extern "C" {
+
+int vbs_gfx950_bdecoder_create(const vbs_gfx950_model_t *m, uint32_t batch, uint64_t kv_seq_stride,
+                               uint32_t max_steps, void **handle) {
+    if (!rt_ready()) return 0;
+    if (!m || !handle) return rt_fail("bdecoder_create: null argument");
+    *handle = nullptr;
+    if (batch == 0 || batch > 8u) return rt_fail("bdecoder_create: batch %u outside 1..8", batch);
+    if (!m->n_layers || !m->hidden || !m->ffn || !m->n_heads || !m->n_kv_heads || !m->head_dim ||
+        !m->vocab || !m->max_ctx)
+        return rt_fail("bdecoder_create: empty model dimension");
+    if (m->n_heads % m->n_kv_heads || m->n_heads / m->n_kv_heads > 16 || m->head_dim > 256 ||
+        (m->head_dim & 1u))
+        return rt_fail("bdecoder_create: unsupported head geometry");
+    if (!m->tok_embd || !m->out_norm || !m->lm_head || !m->attn_norm || !m->ffn_norm ||
+        !m->wtype || !m->wdata || !m->kc || !m->vc)
+        return rt_fail("bdecoder_create: null model pointer");
+    const uint32_t H = m->hidden, F = m->ffn, qd = m->n_heads * m->head_dim;
+    const uint32_t kvd = m->n_kv_heads * m->head_dim, pairs = m->head_dim / 2u;
+    if (kv_seq_stride < (uint64_t)m->n_layers * m->max_ctx * kvd)
+        return rt_fail("bdecoder_create: kv_seq_stride below one sequence's cache");
+    if (!block_elems(m->embd_type)) return rt_fail("bdecoder_create: unsupported embedding type");
+    // every matrix on the batched matrix-core path
+    if (!kq_type(m->head_type) || !kq_cols(H) || !kq_cols(F) || !kq_cols(qd))
+        return rt_fail("bdecoder_create: lm_head and the layer shapes must suit the K-quant "
+                       "matrix-core kernels (Q4_K/Q6_K, widths a multiple of 256 up to 32768)");
+    for (uint32_t L = 0; L < m->n_layers; L++) {
+        const int *t = m->wtype + 7 * L;
+        for (uint32_t i = 0; i < 7; i++)
+            if (!kq_type(t[i]) || !m->wdata[7 * L + i])
+                return rt_fail("bdecoder_create: layer %u matrix %u is not Q4_K/Q6_K", L, i);
+        if (t[0] != t[1] || t[1] != t[2] || t[4] != t[5])
+            return rt_fail("bdecoder_create: layer %u: q/k/v and gate/up must share a type", L);
+    }
+    BDecoder *d = new BDecoder();
+    d->m = *m;
+    d->batch = batch;
+    d->kv_seq = kv_seq_stride;
+    d->attn_norm.assign(m->attn_norm, m->attn_norm + m->n_layers);
+    d->ffn_norm.assign(m->ffn_norm, m->ffn_norm + m->n_layers);
+    d->wtype.assign(m->wtype, m->wtype + 7 * m->n_layers);
+    d->wdata.assign(m->wdata, m->wdata + 7 * m->n_layers);
+    d->max_steps = max_steps ? max_steps : 1;
+    const uint64_t B = batch;
+    const size_t n_f32 = B * (H + 2ull * qd + 2ull * kvd + 2ull * F + m->vocab);
+    const size_t part1 = attention_partial_bytes(m->max_ctx, m->n_heads, m->n_kv_heads, m->head_dim);
+    const size_t xpb = xprep_bytes(H > F ? (H > qd ? H : qd) : (F > qd ? F : qd));
+    const size_t rope = (size_t)m->max_ctx * pairs * sizeof(float2);
+    auto up256 = [](size_t b) { return (b + 255u) & ~(size_t)255u; };
+    const size_t sz_f = up256(n_f32 * 4), sz_st = up256(3 * B * 4);
+    const size_t sz_tok = up256((size_t)d->max_steps * B * 4);
+    const size_t total = sz_f + sz_st + 2 * sz_tok + up256(B * part1) + up256(xpb) + up256(rope);
+    if (hipMalloc(&d->arena, total) != hipSuccess) {
+        delete d;
+        return rt_fail("bdecoder_create: hipMalloc(%zu) failed", total);
+    }
+    uint8_t *p = (uint8_t *)d->arena;
+    float *f = (float *)p;
+    d->x = f; f += B * H;
+    d->q = f; f += B * qd;
+    d->attn = f; f += B * qd;
+    d->k = f; f += B * kvd;
+    d->v = f; f += B * kvd;
+    d->gate = f; f += B * F;
+    d->up = f; f += B * F;
+    d->logits = f;
+    p += sz_f;
+    d->state = (uint32_t *)p; p += sz_st;
+    d->tokens = (uint32_t *)p; p += sz_tok;
+    d->margins = (float *)p; p += sz_tok;
+    d->part = (float *)p; p += up256(B * part1);
+    d->xp = p; p += up256(xpb);
+    d->rope = (float2 *)p;
+    std::vector<float2> tab((size_t)m->max_ctx * pairs);
+    for (uint32_t pos = 0; pos < m->max_ctx; pos++)
+        for (uint32_t pr = 0; pr < pairs; pr++) {
+            const uint32_t i = 2u * pr;
+            const float angle = (float)pos * powf(m->rope_theta, -(float)i / (float)m->head_dim);
+            tab[(size_t)pos * pairs + pr] = make_float2(cosf(angle), sinf(angle));
+        }
+    hipStream_t s = rt_stream();
+    if (!rt_hip_ok(hipMemcpyAsync(d->rope, tab.data(), rope, hipMemcpyHostToDevice, s),
+                   "bdecoder_create: rope table") ||
+        !rt_hip_ok(hipMemsetAsync(d->state, 0, sz_st, s), "bdecoder_create: state") ||
+        !rt_hip_ok(hipStreamSynchronize(s), "bdecoder_create")) {
+        bdecoder_free(d);
+        return 0;
+    }
+    if (!rt_hip_ok(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "begin capture")) {
+        bdecoder_free(d);
+        return 0;
+    }
+    hipError_t e = enqueue_step_batch(*d, s);
+    hipGraph_t g = nullptr;
+    hipError_t e2 = hipStreamEndCapture(s, &g);
+    if (e != hipSuccess || e2 != hipSuccess) {
+        if (g) (void)hipGraphDestroy(g);
+        bdecoder_free(d);
+        return rt_fail("bdecoder_create: capture failed (%s)",
+                       hipGetErrorString(e != hipSuccess ? e : e2));
+    }
+    d->graph = g;
+    if (!rt_hip_ok(hipGraphInstantiate(&d->exec, g, nullptr, nullptr, 0), "graph instantiate")) {
+        bdecoder_free(d);
+        return 0;
+    }
+    *handle = d;
+    return 1;
+}
+
+static int bdecoder_run(void *handle, const uint32_t *tokens0, const uint32_t *pos0, uint32_t n,
+                        uint32_t *tokens, float *margins, bool eager) {
+    if (!rt_ready()) return 0;
+    BDecoder *d = (BDecoder *)handle;
+    if (!d || !tokens0 || !pos0 || !tokens) return rt_fail("bdecoder_greedy: null argument");
+    if (n > d->max_steps) return rt_fail("bdecoder_greedy: %u steps > max_steps %u", n, d->max_steps);
+    const uint32_t B = d->batch;
+    std::vector<uint32_t> st(3 * B, 0u);
+    for (uint32_t b = 0; b < B; b++) {
+        if (tokens0[b] >= d->m.vocab)
+            return rt_fail("bdecoder_greedy: token %u >= vocab %u", tokens0[b], d->m.vocab);
+        if ((uint64_t)pos0[b] + n > d->m.max_ctx)
+            return rt_fail("bdecoder_greedy: sequence %u: context exhausted", b);
+        st[b] = tokens0[b];
+        st[B + b] = pos0[b];
+    }
+    hipStream_t s = rt_stream();
+    if (!rt_hip_ok(hipMemcpyAsync(d->state, st.data(), st.size() * 4, hipMemcpyHostToDevice, s),
+                   "bdecoder_greedy: state"))
+        return 0;
+    for (uint32_t i = 0; i < n; i++) {
+        if (!rt_hip_ok(eager ? enqueue_step_batch(*d, s) : hipGraphLaunch(d->exec, s),
+                       "bdecoder_greedy: step"))
+            return 0;
+    }
+    if (!rt_hip_ok(hipMemcpyAsync(tokens, d->tokens, (size_t)n * B * 4, hipMemcpyDeviceToHost, s),
+                   "bdecoder_greedy: tokens"))
+        return 0;
+    if (margins &&
+        !rt_hip_ok(hipMemcpyAsync(margins, d->margins, (size_t)n * B * 4, hipMemcpyDeviceToHost, s),
+                   "bdecoder_greedy: margins"))
+        return 0;
+    return rt_hip_ok(hipStreamSynchronize(s), "bdecoder_greedy");
+}
+
+int vbs_gfx950_bdecoder_greedy(void *handle, const uint32_t *tokens0, const uint32_t *pos0,
+                               uint32_t n, uint32_t *tokens, float *margins) {
+    return bdecoder_run(handle, tokens0, pos0, n, tokens, margins, false);
+}
+
+int vbs_gfx950_bdecoder_greedy_eager(void *handle, const uint32_t *tokens0, const uint32_t *pos0,
+                                     uint32_t n, uint32_t *tokens, float *margins) {
+    return bdecoder_run(handle, tokens0, pos0, n, tokens, margins, true);
+}
+
+int vbs_gfx950_bdecoder_destroy(void *handle) {
+    bdecoder_free((BDecoder *)handle);
     return 1;
 }
 

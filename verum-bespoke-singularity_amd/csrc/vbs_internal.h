@@ -50,6 +50,20 @@ hipError_t launch_kq_silu(int type, const uint8_t *wg, const uint8_t *wu, const 
                           const float *norm_w, float eps, uint32_t cols, uint32_t rows,
                           float *hid, hipStream_t s);
 
+// Batched matrix-core matvecs in two steps: x of up to 8 vectors prepared
+// once (XP_PLAIN: x; XP_NORM: rms_norm(x) * norm_w; XP_SILU: silu(x) * x2,
+// all at row stride xs) into xprep_bytes(cols) of device memory, then
+// launch_mvb for 1-3 matrices of one K-quant type over it (y = W x, or
+// y += W x with `accumulate`); hipErrorNotSupported (nothing launched)
+// outside the matrix-core shape range.
+enum : int { XP_PLAIN = 0, XP_NORM = 1, XP_SILU = 2 };
+size_t xprep_bytes(uint32_t cols);
+hipError_t launch_xprep(int mode, const float *x, const float *x2, uint32_t xs,
+                        const float *norm_w, float eps, uint32_t cols, uint32_t batch, uint8_t *xp,
+                        hipStream_t s);
+hipError_t launch_mvb(int type, uint32_t nmat, const uint8_t *const w[], const uint32_t rows[],
+                      float *const y[], const uint32_t ys[], int accumulate, const uint8_t *xp,
+                      uint32_t cols, uint32_t batch, hipStream_t s);
 // Y[t] = W * X[t] for t < batch <= 8 (Q4_K / Q6_K) on the f16 matrix cores,
 // W read once; x prepared into the runtime scratch first. hipErrorNotSupported
 // (before anything is launched) outside the matrix-core shape range.
@@ -83,6 +97,15 @@ hipError_t launch_attention(const float *q, const uint16_t *kc, const uint16_t *
                             uint32_t seq_len, const uint32_t *pos_dev, float *part,
                             uint64_t layer_off, uint32_t nqh, uint32_t nkh, uint32_t hd,
                             float scale, hipStream_t s);
+// The same for `batch` sequences with their own caches and positions:
+// sequence b reads q + b q_stride, writes out + b q_stride, uses the caches at
+// + b kv_stride elements, the position pos_dev[b] and the partials at
+// part + b * attention_partial_bytes(max_seq, ...) bytes.
+hipError_t launch_attention_batch(const float *q, const uint16_t *kc, const uint16_t *vc,
+                                  float *out, uint32_t max_seq, const uint32_t *pos_dev,
+                                  float *part, uint64_t layer_off, uint32_t nqh, uint32_t nkh,
+                                  uint32_t hd, float scale, uint32_t batch, uint32_t q_stride,
+                                  uint64_t kv_stride, hipStream_t s);
 hipError_t launch_silu_mul(const float *g, const float *u, float *out, uint32_t n,
                            hipStream_t s);
 hipError_t launch_add(const float *a, const float *b, float *out, uint32_t n, hipStream_t s);

@@ -407,11 +407,18 @@ __global__ __launch_bounds__(64) void k_attn_mfma(const float *__restrict__ q,
                                                   float *__restrict__ part, uint32_t seq_len,
                                                   const uint32_t *__restrict__ pos_dev,
                                                   uint64_t layer_off, uint32_t nkh, uint32_t group,
-                                                  float scale, uint32_t stride_chunks) {
+                                                  float scale, uint32_t stride_chunks,
+                                                  uint32_t q_bstride, uint64_t kv_bstride,
+                                                  uint64_t part_bstride) {
     constexpr uint32_t HD = 128;
-    const uint32_t chunk = blockIdx.x, kvh = blockIdx.y, lane = threadIdx.x;
+    const uint32_t chunk = blockIdx.x, kvh = blockIdx.y, lane = threadIdx.x, bz = blockIdx.z;
     const uint32_t n = lane & 15u, g = lane >> 4;
-    if (pos_dev) seq_len = pos_dev[0] + 1u;  // graph replay: the device holds the position
+    // sequence bz of a batch: its q, caches, position and partials
+    q += (uint64_t)bz * q_bstride;
+    kc += bz * kv_bstride;
+    vc += bz * kv_bstride;
+    part += bz * part_bstride;
+    if (pos_dev) seq_len = pos_dev[bz] + 1u;  // graph replay: the device holds the position
     const AttnSplit sp = attn_split(seq_len, nkh, kMfmaGran, kMfmaLmax, kMfmaTargetWgs);
     if (chunk >= sp.n) return;  // past the sequence (the grid covers the longest split)
     const uint32_t s0 = chunk * sp.len, valid = min(sp.len, seq_len - s0);
@@ -579,14 +586,17 @@ __global__ __launch_bounds__(kMergeThreads) void k_attn_merge(const float *__res
                                                     uint32_t n_chunks, uint32_t stride_chunks,
                                                     const uint32_t *__restrict__ pos_dev,
                                                     uint32_t nkh, uint32_t gran, uint32_t lmax,
-                                                    uint32_t target) {
+                                                    uint32_t target, uint32_t q_bstride,
+                                                    uint64_t part_bstride) {
     extern __shared__ __align__(16) uint8_t merge_lds[];
     float *w = reinterpret_cast<float *>(merge_lds);  // [stride_chunks]
     float *sl = w + stride_chunks;                    // [kMergeThreads]
     constexpr uint32_t NW = kMergeThreads / 64u;
     __shared__ float red[2 * NW];
-    const uint32_t h = blockIdx.x, t = threadIdx.x, lane = t & 63u, wave = t >> 6;
-    if (pos_dev) n_chunks = attn_split(pos_dev[0] + 1u, nkh, gran, lmax, target).n;  // seq = pos + 1
+    const uint32_t h = blockIdx.x, t = threadIdx.x, lane = t & 63u, wave = t >> 6, bz = blockIdx.y;
+    part += bz * part_bstride;  // sequence bz of a batch
+    out += (uint64_t)bz * q_bstride;
+    if (pos_dev) n_chunks = attn_split(pos_dev[bz] + 1u, nkh, gran, lmax, target).n;  // seq = pos + 1
     const float *ph = part + (uint64_t)h * stride_chunks * (hd + 2u);
     const uint32_t ns = kMergeThreads / hd;
     const uint32_t d = t % hd, s = t / hd;
@@ -679,7 +689,7 @@ hipError_t launch_attention(const float *q, const uint16_t *kc, const uint16_t *
     if (fast && hd == 128u) {
         gran = kMfmaGran, lmax = kMfmaLmax, target = kMfmaTargetWgs;
         k_attn_mfma<<<grid, 64, 0, s>>>(q, kc, vc, part, seq_len, pos_dev, layer_off, nkh, group,
-                                        scale, stride);
+                                        scale, stride, 0u, 0ull, 0ull);
         e = hipGetLastError();
     } else if (fast && hd == 32u) {
         gran = ChunkShape<32>::GRAN, lmax = ChunkShape<32>::LMAX;
@@ -704,7 +714,43 @@ hipError_t launch_attention(const float *q, const uint16_t *kc, const uint16_t *
     const uint32_t n_chunks = attn_split(seq_len, nkh, gran, lmax, target).n;
     const size_t mlds = ((size_t)stride + kMergeThreads) * sizeof(float);
     k_attn_merge<<<nqh, kMergeThreads, mlds, s>>>(part, out, hd, n_chunks, stride, pos_dev, nkh, gran,
-                                                  lmax, target);
+                                                  lmax, target, 0u, 0ull);
+    return hipGetLastError();
+}
+
+hipError_t launch_attention_batch(const float *q, const uint16_t *kc, const uint16_t *vc,
+                                  float *out, uint32_t max_seq, const uint32_t *pos_dev,
+                                  float *part, uint64_t layer_off, uint32_t nqh, uint32_t nkh,
+                                  uint32_t hd, float scale, uint32_t batch, uint32_t q_stride,
+                                  uint64_t kv_stride, hipStream_t s) {
+    if (batch == 0 || !part || !pos_dev) return hipErrorInvalidValue;
+    if (max_seq == 0 || nkh == 0 || nqh % nkh != 0) return hipErrorInvalidValue;
+    const uint64_t pstride = attention_partial_bytes(max_seq, nqh, nkh, hd) / sizeof(float);
+    const uint32_t group = nqh / nkh;
+    const bool mfma = hd == 128u && group <= 8u && ((uintptr_t)q & 15u) == 0 &&
+                      ((uintptr_t)kc & 15u) == 0 && ((uintptr_t)vc & 15u) == 0 &&
+                      (q_stride % 4u) == 0 && (kv_stride % 8u) == 0;
+    if (!mfma) {  // one sequence at a time through the single-sequence path
+        for (uint32_t b = 0; b < batch; b++) {
+            const hipError_t e = launch_attention(q + (uint64_t)b * q_stride, kc + b * kv_stride,
+                                                  vc + b * kv_stride, out + (uint64_t)b * q_stride,
+                                                  max_seq, pos_dev + b, part + b * pstride, layer_off,
+                                                  nqh, nkh, hd, scale, s);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
+    const uint32_t stride = attn_max_chunks(max_seq, nkh);
+    k_attn_mfma<<<dim3(stride, nkh, batch), 64, 0, s>>>(q, kc, vc, part, max_seq, pos_dev, layer_off,
+                                                        nkh, group, scale, stride, q_stride,
+                                                        kv_stride, pstride);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const uint32_t n_chunks = attn_split(max_seq, nkh, kMfmaGran, kMfmaLmax, kMfmaTargetWgs).n;
+    const size_t mlds = ((size_t)stride + kMergeThreads) * sizeof(float);
+    k_attn_merge<<<dim3(nqh, batch), kMergeThreads, mlds, s>>>(part, out, hd, n_chunks, stride,
+                                                               pos_dev, nkh, kMfmaGran, kMfmaLmax,
+                                                               kMfmaTargetWgs, q_stride, pstride);
     return hipGetLastError();
 }
 

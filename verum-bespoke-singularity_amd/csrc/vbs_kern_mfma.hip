@@ -777,15 +777,51 @@ __host__ __device__ inline XbLayout xb_layout(uint32_t cols) {
     return L;
 }
 
+// What the prep reads (XP_* in vbs_internal.h): x itself, rms_norm(x) * w
+// (k_rms_norm's arithmetic and block order, src/vbs_host_math.h:28-36), or
+// silu(gate) * up (src/vbs_host_math.h:53-57, the E_SILU epilogue's expression).
 // One wave per (256-element block, vector): lane l holds elements 4l..4l+3.
-__global__ __launch_bounds__(256) void k_xprep_b(const float *x, uint32_t xs, uint32_t cols,
+// XP_NORM: the workgroup first sums the squares of the whole vector (blocks
+// split over its waves, added in block order).
+template <int MODE>
+__global__ __launch_bounds__(256) void k_xprep_b(const float *x, const float *x2, uint32_t xs,
+                                                 const float *norm_w, float eps, uint32_t cols,
                                                  uint8_t *xp) {
-    const uint32_t t = blockIdx.y, lane = threadIdx.x & 63u;
-    const uint32_t b = blockIdx.x * 4u + (threadIdx.x >> 6), nblk = cols >> 8;
-    if (b >= nblk) return;
+    __shared__ double bsum[128];
+    const uint32_t t = blockIdx.y, lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t b = blockIdx.x * 4u + wave, nblk = cols >> 8;
     typedef float4 __attribute__((aligned(4))) f4u;
-    const float4 xv = *reinterpret_cast<const f4u *>(x + (uint64_t)t * xs + 256u * b + 4u * lane);
-    const float v[4] = {xv.x, xv.y, xv.z, xv.w};
+    const float *xt = x + (uint64_t)t * xs;
+    float sc = 1.0f;
+    if (MODE == XP_NORM) {
+        for (uint32_t k = wave; k < nblk; k += 4u) {
+            const float4 a = *reinterpret_cast<const f4u *>(xt + 256u * k + 4u * lane);
+            const float v[4] = {a.x, a.y, a.z, a.w};
+            const double ss = block_sumsq(v);
+            if (lane == 0) bsum[k] = ss;
+        }
+        __syncthreads();
+        double tot = 0.0;
+        for (uint32_t k = 0; k < nblk; k++) tot += bsum[k];
+        const float mean = (float)(tot / (double)cols);
+        sc = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, eps)));
+    }
+    if (b >= nblk) return;
+    const uint32_t e0 = 256u * b + 4u * lane;
+    const float4 xv = *reinterpret_cast<const f4u *>(xt + e0);
+    float v[4] = {xv.x, xv.y, xv.z, xv.w};
+    if (MODE == XP_NORM) {
+        const float4 wv = *reinterpret_cast<const f4u *>(norm_w + e0);
+        const float w4[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) v[k] = __fmul_rn(__fmul_rn(v[k], sc), w4[k]);
+    } else if (MODE == XP_SILU) {
+        const float4 uv = *reinterpret_cast<const f4u *>(x2 + (uint64_t)t * xs + e0);
+        const float u4[4] = {uv.x, uv.y, uv.z, uv.w};
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            v[k] = __fmul_rn(__fdiv_rn(v[k], __fadd_rn(1.0f, expf(-v[k]))), u4[k]);
+    }
     const float amax = wave_max(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
     int e = 0;
     (void)frexpf(amax, &e);  // amax < 2^e
@@ -802,7 +838,7 @@ __global__ __launch_bounds__(256) void k_xprep_b(const float *x, uint32_t xs, ui
     }
     const XbLayout L = xb_layout(cols);
     typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-    _Float16 *ph = reinterpret_cast<_Float16 *>(xp) + (uint64_t)(2u * t) * cols + 256u * b + 4u * lane;
+    _Float16 *ph = reinterpret_cast<_Float16 *>(xp) + (uint64_t)(2u * t) * cols + e0;
     *reinterpret_cast<u32x2 *>(ph) = u32x2{__builtin_bit_cast(uint32_t, hi[0]), __builtin_bit_cast(uint32_t, hi[1])};
     *reinterpret_cast<u32x2 *>(ph + cols) = u32x2{__builtin_bit_cast(uint32_t, lo[0]), __builtin_bit_cast(uint32_t, lo[1])};
     // sub-block sums of x'/32: eight lanes per 32 elements
@@ -820,11 +856,16 @@ __global__ __launch_bounds__(256) void k_xprep_b(const float *x, uint32_t xs, ui
     if (lane == 0) reinterpret_cast<int *>(xp + L.expo)[8u * b + t] = s;
 }
 
+// Up to three matrices of the same type and column count over one prepared x
+// (Q, K, V or gate, up), tiles numbered across them.
 struct MbArgs {
-    const uint8_t *w;
+    const uint8_t *w[3];
+    float *y[3];
+    uint32_t ys[3], rows[3];
+    uint32_t tile_end[3];  // cumulative 16-row tiles per matrix
+    uint32_t nmat;
     const uint8_t *xp;
-    float *y;
-    uint32_t ys, rows, cols, batch;
+    uint32_t cols, batch;
 };
 
 // This lane's A row: its plane and its sub-block-sum plane.
@@ -973,7 +1014,7 @@ struct Q6KB {
     }
 };
 
-template <class T, uint32_t TPW>
+template <class T, uint32_t TPW, bool ACC>
 __global__ __launch_bounds__(512) void k_mvb(const MbArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
     const uint32_t cols = a.cols, nblk = cols >> 8, rb = nblk * T::BYTES;
@@ -984,10 +1025,16 @@ __global__ __launch_bounds__(512) void k_mvb(const MbArgs a) {
     const XbView xv{reinterpret_cast<const _Float16 *>(a.xp) + (uint64_t)p * cols,
                     reinterpret_cast<const _Float16 *>(a.xp + L.msum) + (uint64_t)p * (cols / 32u),
                     reinterpret_cast<const int *>(a.xp + L.expo)};
+    const uint32_t total = a.tile_end[a.nmat - 1u];
     Src src[TPW];
+    uint32_t mt[TPW], lt[TPW];
 #pragma unroll
-    for (uint32_t j = 0; j < TPW; j++)
-        src[j] = Src{a.w, a.rows * rb, rb, (blockIdx.x * TPW + j) * 16u, a.rows};
+    for (uint32_t j = 0; j < TPW; j++) {
+        const uint32_t gt = min(blockIdx.x * TPW + j, total - 1u);
+        mt[j] = (gt >= a.tile_end[0]) + (a.nmat > 2u && gt >= a.tile_end[1]);
+        lt[j] = gt - (mt[j] ? a.tile_end[mt[j] - 1u] : 0u);
+        src[j] = Src{a.w[mt[j]], a.rows[mt[j]] * rb, rb, lt[j] * 16u, a.rows[mt[j]]};
+    }
     uint8_t *scratch = lds + wave * T::SCRATCH;
     float acc[TPW][2];
 #pragma unroll
@@ -1035,28 +1082,73 @@ __global__ __launch_bounds__(512) void k_mvb(const MbArgs a) {
         const uint32_t j = q >> 7, l = (q >> 1) & 63u, tk = q & 1u;
         float s = 0.f;
         for (uint32_t w = 0; w < nw; w++) s += red[(j * nw + w) * 128u + 2u * l + tk];
-        const uint32_t row = (blockIdx.x * TPW + j) * 16u + (l & 15u), t = 2u * (l >> 4) + tk;
-        if (row < a.rows && t < a.batch) a.y[(uint64_t)t * a.ys + row] = s;
+        const uint32_t m = mt[j], row = lt[j] * 16u + (l & 15u), t = 2u * (l >> 4) + tk;
+        if (blockIdx.x * TPW + j < total && row < a.rows[m] && t < a.batch) {
+            float *dst = a.y[m] + (uint64_t)t * a.ys[m] + row;
+            *dst = ACC ? __fadd_rn(*dst, s) : s;
+        }
     }
 }
 
-template <class T, uint32_t TPW>
+template <class T, uint32_t TPW, bool ACC>
 static hipError_t launch_mvb_t(const MbArgs &a, uint32_t nw, hipStream_t s) {
-    const uint32_t tiles = (a.rows + 15u) / 16u;
+    const uint32_t tiles = a.tile_end[a.nmat - 1u];
     const size_t lds = (size_t)nw * T::SCRATCH + (size_t)TPW * nw * 128u * sizeof(float);
-    k_mvb<T, TPW><<<(tiles + TPW - 1u) / TPW, 64u * nw, lds, s>>>(a);
+    k_mvb<T, TPW, ACC><<<(tiles + TPW - 1u) / TPW, 64u * nw, lds, s>>>(a);
     return hipGetLastError();
 }
 
-template <class T>
-static hipError_t launch_mvb(const MbArgs &a, hipStream_t s) {
-    const uint32_t nw = min(8u, a.cols / 256u), tiles = (a.rows + 15u) / 16u;
+template <class T, bool ACC>
+static hipError_t launch_mvb_plan(const MbArgs &a, hipStream_t s) {
+    const uint32_t nw = min(8u, a.cols / 256u), tiles = a.tile_end[a.nmat - 1u];
     // tiles per workgroup: the A operands serve every tile of a wave, so share
     // them as widely as the grid still fills the chip
     if constexpr (T::BYTES == 144u)  // (Q6_K at four tiles would spill registers)
-        if (tiles >= 1024u) return launch_mvb_t<T, 4>(a, nw, s);
-    if (tiles >= 384u) return launch_mvb_t<T, 2>(a, nw, s);
-    return launch_mvb_t<T, 1>(a, nw, s);
+        if (tiles >= 1024u) return launch_mvb_t<T, 4, ACC>(a, nw, s);
+    if (tiles >= 384u) return launch_mvb_t<T, 2, ACC>(a, nw, s);
+    return launch_mvb_t<T, 1, ACC>(a, nw, s);
+}
+
+size_t xprep_bytes(uint32_t cols) { return xb_layout(cols).bytes; }
+
+hipError_t launch_xprep(int mode, const float *x, const float *x2, uint32_t xs,
+                        const float *norm_w, float eps, uint32_t cols, uint32_t batch, uint8_t *xp,
+                        hipStream_t s) {
+    if (batch == 0 || batch > kBatchMax || cols % 256u || cols / 256u > 128u) return hipErrorNotSupported;
+    const dim3 grid((cols / 256u + 3u) / 4u, batch);
+    if (mode == XP_NORM)
+        k_xprep_b<XP_NORM><<<grid, 256, 0, s>>>(x, x2, xs, norm_w, eps, cols, xp);
+    else if (mode == XP_SILU)
+        k_xprep_b<XP_SILU><<<grid, 256, 0, s>>>(x, x2, xs, norm_w, eps, cols, xp);
+    else
+        k_xprep_b<XP_PLAIN><<<grid, 256, 0, s>>>(x, x2, xs, norm_w, eps, cols, xp);
+    return hipGetLastError();
+}
+
+hipError_t launch_mvb(int type, uint32_t nmat, const uint8_t *const w[], const uint32_t rows[],
+                      float *const y[], const uint32_t ys[], int accumulate, const uint8_t *xp,
+                      uint32_t cols, uint32_t batch, hipStream_t s) {
+    if (nmat == 0 || nmat > 3u || batch == 0 || batch > kBatchMax) return hipErrorNotSupported;
+    MbArgs a{};
+    uint32_t tiles = 0;
+    for (uint32_t m = 0; m < nmat; m++) {
+        // (x is read from the prepared planes; any 4-byte aligned pointer passes the check)
+        if (rows[m] == 0 || !mv_fits(type, w[m], reinterpret_cast<const float *>(xp), cols, rows[m]))
+            return hipErrorNotSupported;
+        a.w[m] = w[m];
+        a.y[m] = y[m];
+        a.ys[m] = ys[m];
+        a.rows[m] = rows[m];
+        tiles += (rows[m] + 15u) / 16u;
+        a.tile_end[m] = tiles;
+    }
+    a.nmat = nmat;
+    a.xp = xp;
+    a.cols = cols;
+    a.batch = batch;
+    if (type == kQ4_K)
+        return accumulate ? launch_mvb_plan<Q4KB, true>(a, s) : launch_mvb_plan<Q4KB, false>(a, s);
+    return accumulate ? launch_mvb_plan<Q6KB, true>(a, s) : launch_mvb_plan<Q6KB, false>(a, s);
 }
 
 hipError_t launch_kq_linear_batch(int type, const uint8_t *w, const float *x, uint32_t xs, float *y,
@@ -1066,11 +1158,12 @@ hipError_t launch_kq_linear_batch(int type, const uint8_t *w, const float *x, ui
         return hipErrorNotSupported;
     uint8_t *xp = static_cast<uint8_t *>(scratch(xb_layout(cols).bytes, s));
     if (!xp) return hipErrorOutOfMemory;
-    k_xprep_b<<<dim3((cols / 256u + 3u) / 4u, batch), 256, 0, s>>>(x, xs, cols, xp);
-    const hipError_t e = hipGetLastError();
+    hipError_t e = launch_xprep(XP_PLAIN, x, nullptr, xs, nullptr, 0.f, cols, batch, xp, s);
     if (e != hipSuccess) return e;
-    const MbArgs a{w, xp, y, ys, rows, cols, batch};
-    return type == kQ4_K ? launch_mvb<Q4KB>(a, s) : launch_mvb<Q6KB>(a, s);
+    const uint8_t *wm[1] = {w};
+    float *ym[1] = {y};
+    const uint32_t rm[1] = {rows}, ysm[1] = {ys};
+    return launch_mvb(type, 1, wm, rm, ym, ysm, 0, xp, cols, batch, s);
 }
 
 }  // namespace vbs

@@ -88,6 +88,10 @@ _DEVICE_SIGS = {
     "decoder_greedy": (_I, [_P, _U32, _U32, _U32, _P, _P]),
     "decoder_greedy_eager": (_I, [_P, _U32, _U32, _U32, _P, _P]),
     "decoder_destroy": (_I, [_P]),
+    "bdecoder_create": (_I, [_P, _U32, _U64, _U32, C.POINTER(C.c_void_p)]),
+    "bdecoder_greedy": (_I, [_P, _P, _P, _U32, _P, _P]),
+    "bdecoder_greedy_eager": (_I, [_P, _P, _P, _U32, _P, _P]),
+    "bdecoder_destroy": (_I, [_P]),
 }
 
 DEVICE_SYMBOLS = ["vbs_gfx950_" + k for k in _DEVICE_SIGS]
@@ -527,3 +531,61 @@ class GraphDecoder:
         if self.h:
             self.dev._decoder_destroy(self.h)
             self.h = None
+
+
+class BatchDecoder:
+    """vbs_gfx950_bdecoder over the weights a Decoder uploaded, with `batch`
+    sequences of their own: one device block per cache holding every
+    sequence's [layer][max_ctx][kv_dim] f16 rows back to back."""
+
+    def __init__(self, dev: DeviceLib, decoder: Decoder, batch: int, max_steps: int = 256):
+        c = decoder.model.cfg
+        self.dev, self.batch = dev, batch
+        self.vocab, self.max_ctx = c["vocab"], c["max_ctx"]
+        self.kvd = c["n_kv_heads"] * c["head_dim"]
+        self.n_layers = c["n_layers"]
+        self.seq = self.n_layers * self.max_ctx * self.kvd  # cache elements per sequence
+        self.h = None
+        self.kc = dev.alloc(2 * self.seq * batch)
+        self.vc = dev.alloc(2 * self.seq * batch)
+        self._view = Gfx950ModelStruct()
+        if not decoder.host.vbs_decode_device_model(decoder.h, C.addressof(self._view)):
+            raise GpuError("vbs_decode_device_model failed")
+        self._view.kc, self._view.vc = self.kc, self.vc
+        h = C.c_void_p()
+        if not dev._bdecoder_create(C.addressof(self._view), batch, self.seq, max_steps,
+                                    C.byref(h)):
+            err = dev.error()
+            self.close()
+            raise GpuError(f"bdecoder_create: {err}")
+        self.h = h.value
+
+    def load_kv(self, b: int, kc: np.ndarray, vc: np.ndarray, n_pos: int):
+        """Sequence b's caches from [n_layers][n_pos][kv_dim] f16 prefills."""
+        rows = n_pos * self.kvd
+        for L in range(self.n_layers):
+            off = 2 * (b * self.seq + L * self.max_ctx * self.kvd)
+            for dst, src in ((self.kc, kc), (self.vc, vc)):
+                part = np.ascontiguousarray(src[L * rows:(L + 1) * rows])
+                self.dev.check(self.dev._copy_h2d(dst + off, part.ctypes.data, part.nbytes),
+                               "copy_h2d")
+
+    def greedy(self, tokens0, pos0, n: int, eager: bool = False):
+        """tokens (n, batch) and margins (n, batch) of every sequence's greedy run."""
+        t0 = np.ascontiguousarray(tokens0, np.uint32)
+        p0 = np.ascontiguousarray(pos0, np.uint32)
+        toks = np.empty((n, self.batch), np.uint32)
+        margins = np.empty((n, self.batch), np.float32)
+        fn = self.dev._bdecoder_greedy_eager if eager else self.dev._bdecoder_greedy
+        self.dev.check(fn(self.h, t0.ctypes.data, p0.ctypes.data, n, toks.ctypes.data,
+                          margins.ctypes.data), "bdecoder_greedy")
+        return toks, margins
+
+    def close(self):
+        if self.h:
+            self.dev._bdecoder_destroy(self.h)
+            self.h = None
+        for p in (self.kc, self.vc):
+            if p:
+                self.dev.free(p)
+        self.kc = self.vc = None
