@@ -347,7 +347,7 @@ def bench_decode(dev, host, n_tokens, path="both", geo=GEO_7B, n_layers=32, ctx=
     g.close()
     batched = None
     if batch:
-        batched = bench_batch_decode(dev, d, model, kc, vc, ctx, batch, batch_tokens)
+        batched = bench_batch_decode(dev, d, model, kc, vc, ctx, batch, batch_tokens, eager)
     del kc, vc
     d.close()
     wbytes = model.weight_bytes() - model.tok_embd.nbytes
@@ -368,7 +368,7 @@ def bench_decode(dev, host, n_tokens, path="both", geo=GEO_7B, n_layers=32, ctx=
             **({"batch_decode": batched} if batched else {})}
 
 
-def bench_batch_decode(dev, d, model, kc, vc, ctx, batch, n_tokens):
+def bench_batch_decode(dev, d, model, kc, vc, ctx, batch, n_tokens, eager=False):
     """Greedy decode of `batch` sequences at once (vbs_gfx950_bdecoder, one
     HIP graph per step) over the same device weights: every sequence's own
     cache holds the same N(0,1) prefill to `ctx`, the start tokens differ."""
@@ -377,10 +377,10 @@ def bench_batch_decode(dev, d, model, kc, vc, ctx, batch, n_tokens):
     for b in range(batch):
         bd.load_kv(b, kc, vc, ctx)
     tok0, pos0 = [1 + 7 * b for b in range(batch)], [ctx] * batch
-    bd.greedy(tok0, pos0, 2)
+    bd.greedy(tok0, pos0, 2, eager)
     dev.sync()
     t0 = time.perf_counter()
-    toks, margins = bd.greedy(tok0, pos0, n_tokens)
+    toks, margins = bd.greedy(tok0, pos0, n_tokens, eager)
     dt = time.perf_counter() - t0
     bd.close()
     kvd = c["n_kv_heads"] * c["head_dim"]
@@ -392,7 +392,8 @@ def bench_batch_decode(dev, d, model, kc, vc, ctx, batch, n_tokens):
             "ms_per_step": round(1e3 * step_s, 3), "steps": n_tokens,
             "bytes_per_step": int(wbytes + kv_bytes),
             "roofline_frac": round((wbytes + kv_bytes) / step_s / (PEAK_HBM_GBS * 1e9), 4),
-            "path": "vbs_gfx950_bdecoder: one HIP graph launch per step of all sequences",
+            "path": ("vbs_gfx950_bdecoder kernels launched one by one" if eager else
+                     "vbs_gfx950_bdecoder: one HIP graph launch per step of all sequences"),
             "first_tokens_seq0": [int(x) for x in toks[:8, 0]],
             "min_margin": float(np.min(margins))}
 
@@ -417,6 +418,9 @@ def main():
                     help="'dispatch' times only the per-dispatch ops-table decode; 'eager' "
                          "runs the graph decoder's kernels without the graph (for kernel "
                          "tracers)")
+    ap.add_argument("--decode-geometry", choices=("7b", "70b"), default="7b",
+                    help="model of the 'decode' entry: 7B (config 4) or 70B with its batch-8 "
+                         "run (config 5); the default run adds 'decode_70b' anyway")
     ap.add_argument("--no-cpu", action="store_true")
     a = ap.parse_args()
     if a.gpus != 1:
@@ -462,7 +466,11 @@ def main():
     }
     if not a.no_batch8:
         out["batch8_70b"] = bench_batch8_70b(dev, host)
-    if not a.no_decode:
+    if not a.no_decode and a.decode_geometry == "70b":
+        out["decode"] = bench_decode(dev, host, a.decode_tokens, a.decode_path, geo=GEO_70B,
+                                     n_layers=80, ctx=8192, n_dispatch_tokens=4, batch=8,
+                                     batch_tokens=a.decode_tokens)
+    elif not a.no_decode:
         out["decode"] = bench_decode(dev, host, a.decode_tokens, a.decode_path)
         if a.decode_70b_tokens and a.decode_path == "both":
             out["decode_70b"] = bench_decode(dev, host, a.decode_70b_tokens, geo=GEO_70B,
