@@ -1098,15 +1098,20 @@ static hipError_t launch_mvb_t(const MbArgs &a, uint32_t nw, hipStream_t s) {
     return hipGetLastError();
 }
 
+// Tiles per workgroup and waves (measured at batch 8 on the 70B shapes): the
+// A operands of a block serve every tile of a wave, so they are shared as
+// widely as the grid still fills the chip; four tiles pair best with four
+// waves. Q6_K stops at two tiles (four would spill registers).
 template <class T, bool ACC>
 static hipError_t launch_mvb_plan(const MbArgs &a, hipStream_t s) {
-    const uint32_t nw = min(8u, a.cols / 256u), tiles = a.tile_end[a.nmat - 1u];
-    // tiles per workgroup: the A operands serve every tile of a wave, so share
-    // them as widely as the grid still fills the chip
-    if constexpr (T::BYTES == 144u)  // (Q6_K at four tiles would spill registers)
-        if (tiles >= 1024u) return launch_mvb_t<T, 4, ACC>(a, nw, s);
-    if (tiles >= 384u) return launch_mvb_t<T, 2, ACC>(a, nw, s);
-    return launch_mvb_t<T, 1, ACC>(a, nw, s);
+    const uint32_t nblk = a.cols / 256u, tiles = a.tile_end[a.nmat - 1u];
+    if constexpr (T::BYTES == 144u) {
+        if (tiles >= 640u) return launch_mvb_t<T, 4, ACC>(a, min(4u, nblk), s);
+        if (tiles >= 256u) return launch_mvb_t<T, 2, ACC>(a, min(8u, nblk), s);
+    } else {
+        if (tiles >= 512u) return launch_mvb_t<T, 2, ACC>(a, nblk > 64u ? 8u : min(4u, nblk), s);
+    }
+    return launch_mvb_t<T, 1, ACC>(a, min(8u, nblk), s);
 }
 
 size_t xprep_bytes(uint32_t cols) { return xb_layout(cols).bytes; }
