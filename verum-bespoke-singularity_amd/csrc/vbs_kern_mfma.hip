@@ -550,10 +550,12 @@ struct MvPlan {
 // (The gate/up launch, two tiles per workgroup, keeps four blocks per wave:
 // eight waves of two would not all be resident at once.)
 template <class T>
-static MvPlan mv_plan(uint32_t cols, bool two_tiles) {
+static MvPlan mv_plan(uint32_t cols, bool two_tiles, bool fused) {
     const uint32_t nblk = cols / 256u;
     MvPlan p;
-    p.ks = nblk <= 16u && !two_tiles ? 2u : nblk <= 32u ? 4u : nblk <= 48u ? 6u : 8u;
+    p.ks = nblk <= 16u && !two_tiles ? 2u : nblk <= 32u ? 4u : nblk <= 48u ? 6u
+         : nblk <= 64u || nblk > 112u ? 8u : 14u;
+    if (fused && p.ks == 14u) p.ks = 8u;  // (fused and normed launches keep eight)
     p.nw = (nblk + p.ks - 1u) / p.ks;
     p.tpw = 1u;
     return p;
@@ -594,6 +596,9 @@ static hipError_t launch_ks(const MvArgs &a, const MvPlan &p, uint32_t wgs, hipS
         if (p.nw <= 8u) VBS_MV(6, 512);
         VBS_MV(6, 1024);
     }
+    // rows of 65-112 blocks (70B down: 112), one tile per workgroup
+    if constexpr ((EPI == E_STORE || EPI == E_ACC) && TPW == 1 && !NORM)
+        if (p.ks == 14u) VBS_MV(14, 512);
     VBS_MV(8, 1024);
 #undef VBS_MV
 }
@@ -601,7 +606,11 @@ static hipError_t launch_ks(const MvArgs &a, const MvPlan &p, uint32_t wgs, hipS
 template <class T, bool NORM, int EPI>
 static hipError_t launch_plan(const MvArgs &a, hipStream_t s) {
     const uint32_t total = a.tile_end[a.nmat - 1u];
-    const MvPlan p = mv_plan<T>(a.cols, EPI == E_SILU);
+    MvPlan p = mv_plan<T>(a.cols, EPI == E_SILU, NORM || EPI == E_SILU || EPI == E_QKV);
+    if (p.ks == 14u && a.tile_end[a.nmat - 1u] >= 1024u) {  // (several tiles: keep eight)
+        p.ks = 8u;
+        p.nw = (a.cols / 256u + 7u) / 8u;
+    }
     if (p.nw > 16u) return hipErrorNotSupported;
     if constexpr (EPI == E_SILU)  // a gate tile and the same up tile
         return launch_ks<T, NORM, EPI, 2>(a, p, a.tile_end[0], s);
