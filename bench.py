@@ -242,6 +242,130 @@ def bench_matvec(dev, host, steps, warmup, ncopy, roof_reps):
     return res
 
 
+def gpu_matvec_us(dev, host, t, rows, cols, rotate_bytes=400e6, reps=3):
+    """Average µs per batch-1 vbs_gfx950_linear launch of a (t, rows, cols)
+    matrix: distinct resident copies (>= rotate_bytes together) replayed in
+    one HIP graph, HIP events on the library's stream."""
+    hip, stream = Hip(), dev.stream()
+    w0 = V.synth_matrix(host, t, rows, cols, SEED, 400)
+    ncopy = max(2, int(rotate_bytes // w0.nbytes) + 1)
+    ws = [dev.upload(w0 if k == 0 else V.synth_matrix(host, t, rows, cols, SEED + k, 400))
+          for k in range(ncopy)]
+    x = dev.upload(V.synth_normal(host, cols, SEED, 401))
+    y = dev.upload(np.zeros(rows, np.float32))
+    per = 4
+    g = hip.capture(stream, lambda: [dev.linear(t, ws[i % ncopy], x, y, cols, rows)
+                                     for i in range(per * ncopy)])
+    hip.launch(g, stream)
+    dev.sync()
+    e0, e1 = hip.event(), hip.event()
+    hip.record(e0, stream)
+    for _ in range(reps):
+        hip.launch(g, stream)
+    hip.record(e1, stream)
+    dev.sync()
+    us = hip.elapsed_ms(e0, e1) * 1e3 / (reps * per * ncopy)
+    hip.destroy(g)
+    for p in ws + [x, y]:
+        dev.free(p)
+    return us, w0
+
+
+def cpu_linear_s(t, w, rows, cols, max_seconds=2.0):
+    """Seconds per single-threaded reference CPU matvec (oracle/_ref's
+    dispatch_linear_tile; the oracle restatement when it is not built)."""
+    from oracle_lib import REF_SO, Oracle
+    x = np.ones(cols, np.float32)
+    y = np.zeros(rows, np.float32)
+    if os.path.exists(REF_SO):
+        ref = V.Backend(C.CDLL(REF_SO), "g_vbs_cpu_backend")
+        ref.init()
+        pipe = ref.ops.compile_linear_pipeline(ref.device(), t, None, 0)
+        mk = lambda a: V.VbsBuffer(a.ctypes.data, a.ctypes.data, a.nbytes, ref.device())
+        bw, bx, by = mk(w), mk(x), mk(y)
+        one = lambda: ref.ops.dispatch_linear_tile(ref.device(), pipe, C.byref(bw), None, 0,
+                                                   C.byref(bx), C.byref(by), cols, rows, 0, 0,
+                                                   False)
+        kind = "reference"
+    else:
+        orc = Oracle()
+        one = lambda: orc.linear(t, w, x, cols, rows, y=y, threads=1)
+        kind = "port"
+    n, t0 = 0, time.perf_counter()
+    while True:
+        one()
+        n += 1
+        if time.perf_counter() - t0 >= max_seconds * 0.5:
+            break
+    return (time.perf_counter() - t0) / n, kind
+
+
+def bench_configs(dev, host, with_cpu=True):
+    """The other BASELINE configs at batch 1 on the GPU (and the reference CPU
+    path beside configs 1 and 3): config 1 Q4_0 4096x4096; config 2's Q8_0
+    repetition of the 7B layer set; config 3's Q6_K 32000x4096 head and the
+    64-id Q6_K embedding gather."""
+    out = {}
+    us, w = gpu_matvec_us(dev, host, V.Q4_0, 4096, 4096)
+    b = algo_bytes(V.Q4_0, 4096, 4096)
+    c1 = {"workload": "Q4_0 4096x4096 matvec, batch 1 (config 1)", "us_per_matvec": round(us, 3),
+          "GB_per_s": round(b / us / 1e3, 1), "roofline_frac": round(b / us / 1e3 / PEAK_HBM_GBS, 4)}
+    if with_cpu:
+        sec, kind = cpu_linear_s(V.Q4_0, w, 4096, 4096)
+        c1["cpu_ms_per_matvec"] = round(1e3 * sec, 2)
+        c1["cpu_GB_per_s"] = round(b / sec / 1e9, 4)
+        c1["cpu_kind"] = kind
+        c1["cpu_cores"] = 1
+    out["config1_q4_0"] = c1
+    tot_us, tot_b, per = 0.0, 0, {}
+    for name, r, c in LAYER_SET:
+        key = f"{r}x{c}"
+        if key not in per:
+            per[key] = gpu_matvec_us(dev, host, V.Q8_0, r, c)[0]
+        tot_us += per[key]
+        tot_b += algo_bytes(V.Q8_0, r, c)
+    out["config2_q8_0_layer_set"] = {
+        "workload": "Llama-7B layer matvec set in Q8_0, batch 1 (config 2)",
+        "us_per_set": round(tot_us, 2), "GB_per_s": round(tot_b / tot_us / 1e3, 1),
+        "roofline_frac": round(tot_b / tot_us / 1e3 / PEAK_HBM_GBS, 4),
+        "us_per_shape": {k: round(v, 2) for k, v in per.items()}}
+    us, w = gpu_matvec_us(dev, host, V.Q6_K, 32000, 4096)
+    b = algo_bytes(V.Q6_K, 32000, 4096)
+    c3 = {"workload": "Q6_K 32000x4096 output head, batch 1 (config 3)", "us_per_matvec": round(us, 3),
+          "GB_per_s": round(b / us / 1e3, 1), "roofline_frac": round(b / us / 1e3 / PEAK_HBM_GBS, 4)}
+    if with_cpu:
+        sec, kind = cpu_linear_s(V.Q6_K, w, 32000, 4096, max_seconds=1.0)
+        c3["cpu_ms_per_matvec"] = round(1e3 * sec, 1)
+        c3["cpu_GB_per_s"] = round(b / sec / 1e9, 4)
+        c3["cpu_kind"] = kind
+        c3["cpu_cores"] = 1
+    # 64 random ids gathered from the same table in one launch
+    hip, stream = Hip(), dev.stream()
+    table = dev.upload(w)
+    rng = np.random.default_rng(SEED)
+    ids = dev.upload(rng.integers(0, 32000, 64).astype(np.uint32))
+    outp = dev.upload(np.zeros(64 * 4096, np.float32))
+    g = hip.capture(stream, lambda: [dev.dequant_rows(V.Q6_K, table, ids, 64, 4096, outp)
+                                     for _ in range(50)])
+    hip.launch(g, stream)
+    dev.sync()
+    e0, e1 = hip.event(), hip.event()
+    hip.record(e0, stream)
+    for _ in range(4):
+        hip.launch(g, stream)
+    hip.record(e1, stream)
+    dev.sync()
+    gus = hip.elapsed_ms(e0, e1) * 1e3 / 200
+    hip.destroy(g)
+    for p in (table, ids, outp):
+        dev.free(p)
+    gb = 64 * V.row_bytes(V.Q6_K, 4096) + 64 * 4096 * 4
+    c3["gather_64_ids_us"] = round(gus, 3)
+    c3["gather_GB_per_s"] = round(gb / gus / 1e3, 1)
+    out["config3_q6_k_head"] = c3
+    return out
+
+
 # Llama-70B layer matvec set (config 5) in the Q4_K_M mix: Q, K, V, O, gate, up, down
 LAYER_SET_70B = [("q", V.Q4_K, 8192, 8192), ("k", V.Q4_K, 1024, 8192), ("v", V.Q4_K, 1024, 8192),
                  ("o", V.Q4_K, 8192, 8192), ("gate", V.Q4_K, 28672, 8192),
@@ -407,6 +531,8 @@ def main():
     ap.add_argument("--roof-reps", type=int, default=50)
     ap.add_argument("--decode-tokens", type=int, default=128)
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip BASELINE configs 1, 2 (Q8_0) and 3")
     ap.add_argument("--no-batch8", action="store_true",
                     help="skip the config 5 batch-8 layer matvec set")
     ap.add_argument("--decode-70b-tokens", type=int, default=32,
@@ -464,6 +590,8 @@ def main():
         "gpu_event_ms_per_step": round(r["gpu_ms"] / a.steps, 4),
         "graph_replay_equals_eager": r["replay_equals_eager"],
     }
+    if not a.no_configs:
+        out["configs"] = bench_configs(dev, host, with_cpu=not a.no_cpu)
     if not a.no_batch8:
         out["batch8_70b"] = bench_batch8_70b(dev, host)
     if not a.no_decode and a.decode_geometry == "70b":

@@ -119,14 +119,17 @@ def test_linear_activation_edge_cases(dev, host, oracle, mem, t):
     assert rel_l2(got, want) <= LIN_TOL
 
 
-@pytest.mark.parametrize("t", [V.Q4_K, V.Q6_K], ids=lambda t: V.TYPE_NAMES[t])
+@pytest.mark.parametrize("t", [V.Q4_K, V.Q6_K, V.Q4_0, V.Q4_1, V.Q8_0],
+                         ids=lambda t: V.TYPE_NAMES[t])
 @pytest.mark.parametrize("rows,cols", [(1, 256), (3, 768), (37, 4352), (700, 8192), (64, 16640),
-                                       (5, 28672), (19, 11008)])
+                                       (5, 28672), (19, 11008), (1100, 4096)])
 def test_kquant_odd_shapes(dev, host, oracle, mem, t, rows, cols):
     """Row counts that leave streams and waves partly idle, several waves per
-    row (cols > 4096), misaligned x (col_off 3) and y (row_off 5) windows;
-    for Q6_K also odd block counts per row (rows at every 2-byte offset) and
-    a last block ending off a 16-byte boundary."""
+    row (cols > 4096), 65 and 112 blocks of 256 per row, misaligned x
+    (col_off 3) and y (row_off 5) windows; for Q6_K and the 32-element block
+    types (units of 144, 160, 272 bytes) also rows at every 2-byte offset and
+    a last unit ending off a 16-byte boundary; four tiles per workgroup
+    (1100 rows)."""
     w = V.synth_matrix(host, t, rows, cols, SEED, 25)
     x = synth_x(host, cols + 3, 26)
     pw, px = mem.up(w), mem.up(x)

@@ -30,7 +30,8 @@ int rt_hip_ok(hipError_t e, const char *what);
 bool rt_ready();
 
 // Q4_K / Q6_K matvecs on the matrix cores (x is prepared inside the kernel);
-// hipErrorNotSupported outside their shape/alignment range.
+// launch_kq_linear also takes Q4_0 / Q4_1 / Q8_0 (eight blocks per unit of
+// 256 columns); hipErrorNotSupported outside their shape/alignment range.
 hipError_t launch_kq_linear(int type, const uint8_t *w, const float *x, float *y, uint32_t cols,
                             uint32_t rows, int accumulate, hipStream_t s);
 // y = W * rms_norm(x, norm_w) (the norm as k_rms_norm computes it).

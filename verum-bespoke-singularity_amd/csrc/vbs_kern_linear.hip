@@ -167,7 +167,7 @@ __global__ __launch_bounds__(256) void k_linear_dense(const uint8_t *__restrict_
 hipError_t launch_linear(int type, const uint8_t *w, const float *x, float *y, uint32_t cols,
                          uint32_t rows, int accumulate, hipStream_t s) {
     if (rows == 0) return hipSuccess;
-    if (type == kQ4_K || type == kQ6_K) {
+    if (type == kQ4_K || type == kQ6_K || type == kQ4_0 || type == kQ4_1 || type == kQ8_0) {
         hipError_t e = launch_kq_linear(type, w, x, y, cols, rows, accumulate, s);
         if (e != hipErrorNotSupported) return e;
     }

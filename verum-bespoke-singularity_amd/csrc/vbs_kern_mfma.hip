@@ -357,6 +357,114 @@ struct Q6K {
     }
 };
 
+// ---- 32-element block types: Q4_0, Q4_1, Q8_0 -------------------------------------------
+// Eight consecutive GGUF blocks (256 elements) are one "block" of this kernel:
+// 144 (Q4_0), 160 (Q4_1) or 272 (Q8_0) bytes at 2-byte alignment. As for
+// Q6_K, a wave stages its 16 rows' bytes in LDS as aligned 16-byte chunks (CH
+// per row) and reads its fields there, shifted into place by (row start +
+// field offset) mod 4. MFMA layout: chain c (sub-blocks 4c..4c+3 = GGUF
+// blocks), two MFMAs per chain (elements 0-15, 16-31 of each sub-block); lane
+// group g holds sub-block 4c + g as B, A row n = 4t + p carries plane p of
+// sub-block 4c + t at lane group t only, so D row 4g' + r of lane group g' is
+// plane r of sub-block 4c + g'. Per sub-block j (d, m the block's f16 scale
+// and min, S the plane-combined integer dot, 2^(e-22) and sum x from the
+// digit buffer), as the reference's values summed (src/vbs_dequant.c:123-179):
+//   Q8_0: d*q            -> d * 2^(e-22) * S
+//   Q4_0: (nib - 8) * d  -> d * (2^(e-22) * S - 8 * sum x)
+//   Q4_1: d * nib + m    -> d * 2^(e-22) * S + m * sum x
+template <int TYPE>
+struct KBlk {
+    static constexpr uint32_t BB = TYPE == kQ8_0 ? 34u : TYPE == kQ4_1 ? 20u : 18u;  // GGUF block
+    static constexpr uint32_t QOFF = TYPE == kQ4_1 ? 4u : 2u;  // quants within the GGUF block
+    static constexpr bool NIB = TYPE != kQ8_0;
+    static constexpr uint32_t BYTES = 8u * BB;
+    static constexpr uint32_t CH = (BYTES + 14u + 15u) / 16u;  // chunks covering any 2-byte offset
+    static constexpr uint32_t NCHUNK = 16u * CH;
+    static constexpr uint32_t NLD = (NCHUNK + 63u) / 64u, SCRATCH = 16u * NCHUNK;
+    __device__ static void load(const Src &src, uint32_t b, uint32_t n, uint32_t g, u32x4 *r) {
+        const uint32_t lane = 16u * g + n;
+        // only the last block of the matrix's last row has chunks past its end
+        const uint32_t wlo = (uint32_t)(uintptr_t)src.w & 15u;
+        const uint32_t last = src.row(15u) + b * BYTES;
+        const bool edge = __builtin_amdgcn_readfirstlane(
+                              (uint32_t)(last - ((last + wlo) & 15u) + 16u * CH > src.bytes)) != 0u;
+        uint32_t a[NLD];
+#pragma unroll
+        for (uint32_t i = 0; i < NLD; i++) {
+            const uint32_t c = min(lane + 64u * i, NCHUNK - 1u);
+            const uint32_t s0 = src.row(c / CH) + b * BYTES;
+            a[i] = s0 - ((s0 + wlo) & 15u) + 16u * (c % CH);
+        }
+        if (!edge) {
+#pragma unroll
+            for (uint32_t i = 0; i < NLD; i++) r[i] = lda4(src.w + a[i]);
+        } else {
+            const uint8_t *end = src.w + src.bytes;
+#pragma unroll
+            for (uint32_t i = 0; i < NLD; i++)
+                r[i] = a[i] + 16u <= src.bytes ? lda4(src.w + a[i]) : ld_tail(src.w + a[i], end);
+        }
+    }
+    __device__ static float dot(const u32x4 *r, uint8_t *scratch, const Src &src,
+                                const uint8_t *xq, const XqLayout &L, uint32_t cols, uint32_t b,
+                                uint32_t n, uint32_t g) {
+        const uint32_t lane = 16u * g + n;
+#pragma unroll
+        for (uint32_t i = 0; i < NLD; i++) {
+            const uint32_t c = lane + 64u * i;
+            if (i + 1u < NLD || c < NCHUNK) *reinterpret_cast<u32x4 *>(scratch + 16u * c) = r[i];
+        }
+        // row n's block starts o bytes into its CH chunks
+        const uint32_t o = ((uint32_t)(uintptr_t)src.w + src.row(n) + b * BYTES) & 15u;
+        const uint32_t *rw = reinterpret_cast<const uint32_t *>(scratch + 16u * CH * n);
+        auto field = [&](uint32_t f) {  // 16 bytes at block byte f (even)
+            const uint32_t P = o + f, i = P >> 2, sh = P & 3u;
+            const uint32_t w0 = rw[i], w1 = rw[i + 1u], w2 = rw[i + 2u], w3 = rw[i + 3u], w4 = rw[i + 4u];
+            const u32x4 v = {__builtin_amdgcn_alignbyte(w1, w0, sh), __builtin_amdgcn_alignbyte(w2, w1, sh),
+                             __builtin_amdgcn_alignbyte(w3, w2, sh), __builtin_amdgcn_alignbyte(w4, w3, sh)};
+            return v;
+        };
+        auto half16 = [&](uint32_t f) {  // the f16 bits at block byte f (even)
+            const uint32_t P = o + f;
+            return (rw[P >> 2] >> (8u * (P & 3u))) & 0xFFFFu;
+        };
+        const uint32_t t = n >> 2, p = n & 3u;
+        const bool on = p < 3u && t == g;
+        const float2 *xs = reinterpret_cast<const float2 *>(xq + L.xs);
+        const i32x4 z = {0, 0, 0, 0};
+        float acc = 0.f;
+#pragma unroll
+        for (uint32_t c = 0; c < 2u; c++) {
+            const uint32_t j = 4u * c + g;  // this lane group's sub-block (B) and D sub-block
+            u32x4 q0, q1;
+            if (NIB) {  // qs[16]: element e < 16 low nibble of qs[e], e >= 16 high nibble
+                const u32x4 q = field(BB * j + QOFF);
+                const uint32_t M4 = 0x0F0F0F0Fu;
+                q0 = u32x4{q.x & M4, q.y & M4, q.z & M4, q.w & M4};
+                q1 = u32x4{(q.x >> 4) & M4, (q.y >> 4) & M4, (q.z >> 4) & M4, (q.w >> 4) & M4};
+            } else {  // int8 q[32]
+                q0 = field(BB * j + QOFF);
+                q1 = field(BB * j + QOFF + 16u);
+            }
+            const uint32_t ao = p * cols + 256u * b + 32u * (4u * c + t);
+            const i32x4 A0 = lda(xq + (on ? ao : L.zero));
+            const i32x4 A1 = lda(xq + (on ? ao + 16u : L.zero));
+            const i32x4 D = mfma(A1, __builtin_bit_cast(i32x4, q1),
+                                 mfma(A0, __builtin_bit_cast(i32x4, q0), z));
+            const float S = plane_sum(D);
+            const float2 x2 = xs[8u * b + j];
+            const float d = cvt_h(half16(BB * j));
+            if (TYPE == kQ8_0) acc = fmaf(d * x2.x, S, acc);
+            else if (TYPE == kQ4_0) acc = fmaf(d, fmaf(x2.x, S, -8.f * x2.y), acc);
+            else acc = fmaf(d * x2.x, S, fmaf(cvt_h(half16(BB * j + 2u)), x2.y, acc));
+        }
+        return acc;
+    }
+};
+using Q40 = KBlk<kQ4_0>;
+using Q41 = KBlk<kQ4_1>;
+using Q80 = KBlk<kQ8_0>;
+
 // ---- jobs -------------------------------------------------------------------------------
 // One launch computes the rows of up to three matrices that share x (and its
 // type and column count), with an optional RMSNorm of x in front and one of
@@ -627,6 +735,13 @@ static hipError_t launch_plan(const MvArgs &a, hipStream_t s) {
 // most 8 super-blocks (the digits of x and the Q6_K scratch must also fit the
 // LDS, else the launch reports it unsupported); Q4_K rows are 16-byte
 // multiples, so its 16-byte loads need an aligned w; Q6_K aligns every load.
+// The 32-element block types (batch-1 store / accumulate launches only).
+static bool mv_fits_blk(int type, const uint8_t *w, const float *x, uint32_t cols, uint32_t rows) {
+    if (type != kQ4_0 && type != kQ4_1 && type != kQ8_0) return false;
+    if (cols % 256u || cols / 256u > 128u || ((uintptr_t)x & 3u) || ((uintptr_t)w & 1u)) return false;
+    return (uint64_t)rows * row_bytes(type, cols) < (1ull << 32);
+}
+
 static bool mv_fits(int type, const uint8_t *w, const float *x, uint32_t cols, uint32_t rows) {
     if (type != kQ4_K && type != kQ6_K) return false;
     if (cols % 256u || cols / 256u > 128u || ((uintptr_t)x & 3u)) return false;
@@ -636,6 +751,11 @@ static bool mv_fits(int type, const uint8_t *w, const float *x, uint32_t cols, u
 
 template <bool NORM, int EPI>
 static hipError_t launch_type(int type, const MvArgs &a, hipStream_t s) {
+    if constexpr (!NORM && (EPI == E_STORE || EPI == E_ACC)) {
+        if (type == kQ4_0) return launch_plan<Q40, NORM, EPI>(a, s);
+        if (type == kQ4_1) return launch_plan<Q41, NORM, EPI>(a, s);
+        if (type == kQ8_0) return launch_plan<Q80, NORM, EPI>(a, s);
+    }
     return type == kQ4_K ? launch_plan<Q4K, NORM, EPI>(a, s) : launch_plan<Q6K, NORM, EPI>(a, s);
 }
 
@@ -649,7 +769,8 @@ static void set_tiles(MvArgs &a) {
 
 hipError_t launch_kq_linear(int type, const uint8_t *w, const float *x, float *y, uint32_t cols,
                             uint32_t rows, int accumulate, hipStream_t s) {
-    if (rows == 0 || !mv_fits(type, w, x, cols, rows)) return hipErrorNotSupported;
+    if (rows == 0 || !(mv_fits(type, w, x, cols, rows) || mv_fits_blk(type, w, x, cols, rows)))
+        return hipErrorNotSupported;
     MvArgs a{};
     a.w[0] = w;
     a.y[0] = y;
