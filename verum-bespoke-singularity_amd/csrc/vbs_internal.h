@@ -34,6 +34,9 @@ bool rt_ready();
 // 256 columns); hipErrorNotSupported outside their shape/alignment range.
 hipError_t launch_kq_linear(int type, const uint8_t *w, const float *x, float *y, uint32_t cols,
                             uint32_t rows, int accumulate, hipStream_t s);
+// The Q4_0 / Q4_1 / Q8_0 part of launch_kq_linear.
+hipError_t launch_blk_linear(int type, const uint8_t *w, const float *x, float *y, uint32_t cols,
+                             uint32_t rows, int accumulate, hipStream_t s);
 // y = W * rms_norm(x, norm_w) (the norm as k_rms_norm computes it).
 hipError_t launch_kq_norm_linear(int type, const uint8_t *w, const float *x, const float *norm_w,
                                  float eps, float *y, uint32_t cols, uint32_t rows,

@@ -1,0 +1,459 @@
+// vbs_kern_mfma_batch.hip — batched (skinny) K-quant matvec on the gfx950 f16
+// matrix cores: x preparation (k_xprep_b) and the k_mvb kernel, with the weight
+// loads of the batch-1 kernel (vbs_mfma.h).
+#include "vbs_mfma.h"
+
+namespace vbs {
+
+// ==== batched (skinny) K-quant matvec: up to 8 activation vectors ====================
+//
+// Y[t][r] = sum_c deq(W[r,c]) * X[t][c] for t < batch <= 8, the reference's linear
+// (src/vbs_host_math.h:223-267) once per vector, with W read once. This is a
+// skinny GEMM, computed on the f16 matrix cores with fp32 accumulation:
+//
+// * x in f16 pairs. Every 256-element block b of vector t is scaled by
+//   2^s_tb so that its largest |x| lies in [2^14, 2^15), and each element
+//   x' = x 2^s_tb becomes hi + lo with hi = f16(x') and lo = f16(x' - hi): 22
+//   significant bits, each element represented to ~2^-23 of itself (or of
+//   2^-10 below its block's maximum). Plane 2t holds hi, plane 2t + 1 lo, in
+//   element order; A row n of an MFMA is plane n, so D row 2t + h is vector
+//   t's dot with hi or lo, the two add up in fp32, and the block's sum is
+//   scaled back by 2^-s_tb. Rows past 2 batch re-read the last plane and are
+//   never stored. An inf or NaN in a block makes its lo plane NaN (inf - inf),
+//   so the vector's outputs are NaN.
+// * Q4_K (v_mfma_f32_16x16x32_f16). The weight operand is sc * nib, the 6-bit
+//   sub-block scale times the nibble: an integer below 945, exact in f16. The
+//   scale is inside the operand, so one MFMA may mix sub-blocks and the
+//   eight MFMAs of a block chain into one accumulator; lane group g takes the
+//   nibbles of its two 16-byte loads (qs bytes 16g.. and 64 + 16g..) in any
+//   order as long as its A operand holds the same elements. The mins go
+//   through a ninth MFMA: A = the per-sub-block sums of x'/32 (hi and lo
+//   planes), B = the 6-bit mins, in lane group 0 only. Per block and row:
+//   d * D - 32 dmin * Dmin, as the reference's sum of d*sc*nib - dmin*m.
+// * Q6_K (v_mfma_f32_16x16x16_f16, one 16-element scale group per MFMA). The
+//   int8 scale times (q - 32) can exceed f16's exact integers, so the weight
+//   operand is q - 32 and the scale multiplies each group's dot afterwards:
+//   d * sum_g sc_g * D_g. Rows are read as aligned 16-byte chunks staged in
+//   LDS, as in the batch-1 kernel.
+//
+// Work split as in the batch-1 kernel: a workgroup owns TPW tiles of 16 rows,
+// its waves split the row by super-blocks (wave w: blocks w, w + nw, ...), a
+// wave's A operands of a block serve all its TPW tiles, and the loads of the
+// next block are in flight while one block is computed. The waves' partial
+// sums are added in wave order at the end.
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t kBatchMax = 8;
+
+// Prepared x: [16 planes][cols] f16 | [16 planes][cols/32] f16 sub-block sums
+// of x'/32 | int s[cols/256][8] (block, vector).
+struct XbLayout {
+    uint32_t msum, expo, bytes;
+};
+__host__ __device__ inline XbLayout xb_layout(uint32_t cols) {
+    XbLayout L;
+    L.msum = 32u * cols;
+    L.expo = 33u * cols;
+    L.bytes = 33u * cols + cols / 8u;
+    return L;
+}
+
+// What the prep reads (XP_* in vbs_internal.h): x itself, rms_norm(x) * w
+// (k_rms_norm's arithmetic and block order, src/vbs_host_math.h:28-36), or
+// silu(gate) * up (src/vbs_host_math.h:53-57, the E_SILU epilogue's expression).
+// One wave per (256-element block, vector): lane l holds elements 4l..4l+3.
+// XP_NORM: the workgroup first sums the squares of the whole vector (blocks
+// split over its waves, added in block order).
+template <int MODE>
+__global__ __launch_bounds__(256) void k_xprep_b(const float *x, const float *x2, uint32_t xs,
+                                                 const float *norm_w, float eps, uint32_t cols,
+                                                 uint8_t *xp) {
+    __shared__ double bsum[128];
+    const uint32_t t = blockIdx.y, lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t b = blockIdx.x * 4u + wave, nblk = cols >> 8;
+    typedef float4 __attribute__((aligned(4))) f4u;
+    const float *xt = x + (uint64_t)t * xs;
+    float sc = 1.0f;
+    if (MODE == XP_NORM) {
+        for (uint32_t k = wave; k < nblk; k += 4u) {
+            const float4 a = *reinterpret_cast<const f4u *>(xt + 256u * k + 4u * lane);
+            const float v[4] = {a.x, a.y, a.z, a.w};
+            const double ss = block_sumsq(v);
+            if (lane == 0) bsum[k] = ss;
+        }
+        __syncthreads();
+        double tot = 0.0;
+        for (uint32_t k = 0; k < nblk; k++) tot += bsum[k];
+        const float mean = (float)(tot / (double)cols);
+        sc = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, eps)));
+    }
+    if (b >= nblk) return;
+    const uint32_t e0 = 256u * b + 4u * lane;
+    const float4 xv = *reinterpret_cast<const f4u *>(xt + e0);
+    float v[4] = {xv.x, xv.y, xv.z, xv.w};
+    if (MODE == XP_NORM) {
+        const float4 wv = *reinterpret_cast<const f4u *>(norm_w + e0);
+        const float w4[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) v[k] = __fmul_rn(__fmul_rn(v[k], sc), w4[k]);
+    } else if (MODE == XP_SILU) {
+        const float4 uv = *reinterpret_cast<const f4u *>(x2 + (uint64_t)t * xs + e0);
+        const float u4[4] = {uv.x, uv.y, uv.z, uv.w};
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            v[k] = __fmul_rn(__fdiv_rn(v[k], __fadd_rn(1.0f, expf(-v[k]))), u4[k]);
+    }
+    const float amax = wave_max(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+    int e = 0;
+    (void)frexpf(amax, &e);  // amax < 2^e
+    const int s = amax > 0.f ? 15 - e : 0;
+    h2 hi[2], lo[2];
+    float sum = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const float xs2 = ldexpf(v[k], s);
+        const _Float16 h = (_Float16)xs2;
+        hi[k >> 1][k & 1] = h;
+        lo[k >> 1][k & 1] = (_Float16)(xs2 - (float)h);
+        sum += xs2;
+    }
+    const XbLayout L = xb_layout(cols);
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    _Float16 *ph = reinterpret_cast<_Float16 *>(xp) + (uint64_t)(2u * t) * cols + e0;
+    *reinterpret_cast<u32x2 *>(ph) = u32x2{__builtin_bit_cast(uint32_t, hi[0]), __builtin_bit_cast(uint32_t, hi[1])};
+    *reinterpret_cast<u32x2 *>(ph + cols) = u32x2{__builtin_bit_cast(uint32_t, lo[0]), __builtin_bit_cast(uint32_t, lo[1])};
+    // sub-block sums of x'/32: eight lanes per 32 elements
+    sum += __shfl_xor(sum, 1, 64);
+    sum += __shfl_xor(sum, 2, 64);
+    sum += __shfl_xor(sum, 4, 64);
+    if ((lane & 7u) == 0) {
+        const float m = sum * 0.03125f;
+        const _Float16 h = (_Float16)m;
+        _Float16 *pm = reinterpret_cast<_Float16 *>(xp + L.msum) + (uint64_t)(2u * t) * (cols / 32u) +
+                       8u * b + lane / 8u;
+        pm[0] = h;
+        pm[cols / 32u] = (_Float16)(m - (float)h);
+    }
+    if (lane == 0) reinterpret_cast<int *>(xp + L.expo)[8u * b + t] = s;
+}
+
+// Up to three matrices of the same type and column count over one prepared x
+// (Q, K, V or gate, up), tiles numbered across them.
+struct MbArgs {
+    const uint8_t *w[3];
+    float *y[3];
+    uint32_t ys[3], rows[3];
+    uint32_t tile_end[3];  // cumulative 16-row tiles per matrix
+    uint32_t nmat;
+    const uint8_t *xp;
+    uint32_t cols, batch;
+};
+
+// This lane's A row: its plane and its sub-block-sum plane.
+struct XbView {
+    const _Float16 *plane, *msum;
+    const int *expo;
+};
+
+// {1024 + byte, 1024 + byte'} as an f16 pair: bytes (0, 1) of w for sel
+// 0x00050004, (2, 3) for 0x00070006, (k, k) for 0x00040004 + 0x00010001 k.
+__device__ __forceinline__ h2 f16_bytes(uint32_t w, uint32_t sel) {
+    return __builtin_bit_cast(h2, __builtin_amdgcn_perm(w, 0x64646464u, sel));
+}
+__device__ __forceinline__ h8 join8(h2 a, h2 b, h2 c, h2 d) {
+    const u32x4 v = {__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b),
+                     __builtin_bit_cast(uint32_t, c), __builtin_bit_cast(uint32_t, d)};
+    return __builtin_bit_cast(h8, v);
+}
+__device__ __forceinline__ h4 join4(h2 a, h2 b) {
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 v = {__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b)};
+    return __builtin_bit_cast(h4, v);
+}
+
+struct Q4KB {
+    typedef Q4K Load;
+    static constexpr uint32_t BYTES = 144, NLD = Q4K::NLD, SCRATCH = 0;
+    struct A {
+        h8 m[8], mn;
+        int2 s;  // block exponents of the lane's two D vectors
+    };
+    // MFMA m, lane group g, slot k: element 32 j + 16 (g & 1) + 8 (m & 1) + k of
+    // the block, j = 4 (m >> 2) + 2 (g >> 1) + ((m >> 1) & 1) (the nibbles of
+    // qs byte 16 g + 8 (m & 1) + k, or of byte 64 + ..., low or high half).
+    __device__ static void load_a(const XbView &v, uint32_t b, uint32_t g, A &a) {
+        const _Float16 *p = v.plane + 256u * b + 16u * (g & 1u);
+#pragma unroll
+        for (uint32_t m = 0; m < 8u; m++) {
+            const uint32_t j = 4u * (m >> 2) + 2u * (g >> 1) + ((m >> 1) & 1u);
+            a.m[m] = *reinterpret_cast<const h8 *>(p + 32u * j + 8u * (m & 1u));
+        }
+        const h8 t = *reinterpret_cast<const h8 *>(v.msum + 8u * b), z = {};
+        a.mn = g == 0u ? t : z;
+        a.s = *reinterpret_cast<const int2 *>(v.expo + 8u * b + 2u * g);
+    }
+    __device__ static void dot(const u32x4 *r, const A &x, uint8_t *, const Src &, uint32_t,
+                               uint32_t, uint32_t g, float acc[2]) {
+        const u32x4 hd = r[0], qa = r[1], qb = r[2];
+        // scales and mins, one per byte (src/vbs_dequant.c:225-233)
+        const uint32_t sclo = hd.y & 0x3F3F3F3Fu;
+        const uint32_t schi = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);
+        const uint32_t mnlo = hd.z & 0x3F3F3F3Fu;
+        const uint32_t mnhi = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
+        const h2 n1024 = {(_Float16)-1024.f, (_Float16)-1024.f};
+        const h2 n64 = {(_Float16)-64.f, (_Float16)-64.f};
+        const h2 r16 = {(_Float16)0.0625f, (_Float16)0.0625f};
+        const uint32_t k0 = 0x00040004u + 0x00020002u * (g >> 1);  // byte 2 (g >> 1)
+        // sub-blocks of this lane group: 2(g>>1) (qa low), +1 (qa high), 4 + 2(g>>1)
+        // (qb low), +1 (qb high); low nibbles: fma(1024 + n, sc, -1024 sc),
+        // high nibbles: fma(1024 + 16 n, sc / 16, -64 sc), both exactly sc * n
+        const h2 s0 = f16_bytes(sclo, k0) + n1024, s1 = f16_bytes(sclo, k0 + 0x00010001u) + n1024;
+        const h2 s2 = f16_bytes(schi, k0) + n1024, s3 = f16_bytes(schi, k0 + 0x00010001u) + n1024;
+        const h2 mul[4] = {s0, s1 * r16, s2, s3 * r16};
+        const h2 add[4] = {s0 * n1024, s1 * n64, s2 * n1024, s3 * n64};
+        f4 D = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (uint32_t m = 0; m < 8u; m++) {
+            const u32x4 q = (m >> 2) ? qb : qa;
+            const uint32_t hs = (m >> 1) & 1u, si = 2u * (m >> 2) + hs;
+            const uint32_t mask = hs ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
+            const uint32_t w0 = ((m & 1u) ? q.z : q.x) & mask, w1 = ((m & 1u) ? q.w : q.y) & mask;
+            const h8 B = join8(__builtin_elementwise_fma(f16_bytes(w0, 0x00050004u), mul[si], add[si]),
+                               __builtin_elementwise_fma(f16_bytes(w0, 0x00070006u), mul[si], add[si]),
+                               __builtin_elementwise_fma(f16_bytes(w1, 0x00050004u), mul[si], add[si]),
+                               __builtin_elementwise_fma(f16_bytes(w1, 0x00070006u), mul[si], add[si]));
+            D = __builtin_amdgcn_mfma_f32_16x16x32_f16(x.m[m], B, D, 0, 0, 0);
+        }
+        const h8 Bm = join8(f16_bytes(mnlo, 0x00050004u) + n1024, f16_bytes(mnlo, 0x00070006u) + n1024,
+                            f16_bytes(mnhi, 0x00050004u) + n1024, f16_bytes(mnhi, 0x00070006u) + n1024);
+        const f4 z = {0.f, 0.f, 0.f, 0.f};
+        const f4 Dm = __builtin_amdgcn_mfma_f32_16x16x32_f16(x.mn, Bm, z, 0, 0, 0);
+        const float d = cvt_h(hd.x & 0xFFFFu), md = -32.f * cvt_h(hd.x >> 16);
+        acc[0] += ldexpf(fmaf(d, D[0] + D[1], md * (Dm[0] + Dm[1])), -x.s.x);
+        acc[1] += ldexpf(fmaf(d, D[2] + D[3], md * (Dm[2] + Dm[3])), -x.s.y);
+    }
+};
+
+struct Q6KB {
+    typedef Q6K Load;
+    static constexpr uint32_t BYTES = 210, NLD = Q6K::NLD, SCRATCH = Q6K::SCRATCH;
+    struct A {
+        h4 g[16];
+        int2 s;  // block exponents of the lane's two D vectors
+    };
+    // MFMA G = 8h + 2q + u (scale group G), lane group g, slot k: element
+    // 128 h + 32 q + 16 u + 4 g + k (src/vbs_dequant.c:316-333)
+    __device__ static void load_a(const XbView &v, uint32_t b, uint32_t g, A &a) {
+        const _Float16 *p = v.plane + 256u * b + 4u * g;
+#pragma unroll
+        for (uint32_t G = 0; G < 16u; G++)
+            a.g[G] = *reinterpret_cast<const h4 *>(p + 128u * (G >> 3) + 32u * ((G >> 1) & 3u) +
+                                                   16u * (G & 1u));
+        a.s = *reinterpret_cast<const int2 *>(v.expo + 8u * b + 2u * g);
+    }
+    __device__ static void dot(const u32x4 *r, const A &x, uint8_t *scratch, const Src &src,
+                               uint32_t b, uint32_t n, uint32_t g, float acc[2]) {
+        const uint32_t lane = 16u * g + n;
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++) {
+            const uint32_t c = lane + 64u * i;
+            if (i < 3u || c < 224u) *reinterpret_cast<u32x4 *>(scratch + 16u * c) = r[i];
+        }
+        // row n's block starts o = (its address mod 16) into its 224 scratch bytes
+        const uint32_t o = ((uint32_t)(uintptr_t)src.w + src.row(n) + b * BYTES) & 15u;
+        const uint32_t *rw = reinterpret_cast<const uint32_t *>(scratch + 224u * n + (o & 12u));
+        const uint32_t sh = o & 2u;
+        auto dw = [&](uint32_t f) { return __builtin_amdgcn_alignbyte(rw[f / 4u + 1u], rw[f / 4u], sh); };
+        uint32_t ql[8], qh[4], sc[4];
+#pragma unroll
+        for (uint32_t i = 0; i < 8u; i++)  // i = 4h + 2(q & 1) + u
+            ql[i] = dw(64u * (i >> 2) + 32u * ((i >> 1) & 1u) + 16u * (i & 1u) + 4u * g);
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; i++)  // i = 2h + u
+            qh[i] = dw(128u + 32u * (i >> 1) + 16u * (i & 1u) + 4u * g);
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; i++) sc[i] = dw(192u + 4u * i);
+        const uint32_t dbits = (rw[52] >> (8u * sh)) & 0xFFFFu;
+        const h2 n1056 = {(_Float16)-1056.f, (_Float16)-1056.f};
+        const f4 z = {0.f, 0.f, 0.f, 0.f};
+        float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+        for (uint32_t G = 0; G < 16u; G++) {
+            const uint32_t h = G >> 3, q = (G >> 1) & 3u, u = G & 1u;
+            const uint32_t l4 = (ql[4u * h + 2u * (q & 1u) + u] >> (4u * (q >> 1))) & 0x0F0F0F0Fu;
+            const uint32_t h2b = (qh[2u * h + u] >> (2u * q)) & 0x03030303u;
+            const uint32_t q6 = l4 | (h2b << 4);
+            const h4 B = join4(f16_bytes(q6, 0x00050004u) + n1056, f16_bytes(q6, 0x00070006u) + n1056);
+            const f4 D = __builtin_amdgcn_mfma_f32_16x16x16f16(x.g[G], B, z, 0, 0, 0);
+            const float s = (float)(int)(int8_t)(sc[G >> 2] >> (8u * (G & 3u)));
+            a0 = fmaf(s, D[0] + D[1], a0);
+            a1 = fmaf(s, D[2] + D[3], a1);
+        }
+        const float d = cvt_h(dbits);
+        acc[0] += ldexpf(d * a0, -x.s.x);
+        acc[1] += ldexpf(d * a1, -x.s.y);
+    }
+};
+
+template <class T, uint32_t TPW, bool ACC>
+__global__ __launch_bounds__(512) void k_mvb(const MbArgs a) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const uint32_t cols = a.cols, nblk = cols >> 8, rb = nblk * T::BYTES;
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u, nw = blockDim.x >> 6;
+    const uint32_t n = lane & 15u, g = lane >> 4;
+    const XbLayout L = xb_layout(cols);
+    const uint32_t p = min(n, 2u * a.batch - 1u);
+    const XbView xv{reinterpret_cast<const _Float16 *>(a.xp) + (uint64_t)p * cols,
+                    reinterpret_cast<const _Float16 *>(a.xp + L.msum) + (uint64_t)p * (cols / 32u),
+                    reinterpret_cast<const int *>(a.xp + L.expo)};
+    const uint32_t total = a.tile_end[a.nmat - 1u];
+    Src src[TPW];
+    uint32_t mt[TPW], lt[TPW];
+#pragma unroll
+    for (uint32_t j = 0; j < TPW; j++) {
+        const uint32_t gt = min(blockIdx.x * TPW + j, total - 1u);
+        mt[j] = (gt >= a.tile_end[0]) + (a.nmat > 2u && gt >= a.tile_end[1]);
+        lt[j] = gt - (mt[j] ? a.tile_end[mt[j] - 1u] : 0u);
+        src[j] = Src{a.w[mt[j]], a.rows[mt[j]] * rb, rb, lt[j] * 16u, a.rows[mt[j]]};
+    }
+    uint8_t *scratch = lds + wave * T::SCRATCH;
+    float acc[TPW][2];
+#pragma unroll
+    for (uint32_t j = 0; j < TPW; j++) acc[j][0] = acc[j][1] = 0.f;
+
+    typename T::A A0, A1;
+    u32x4 W0[TPW][T::NLD], W1[TPW][T::NLD];
+    auto issue = [&](uint32_t b, typename T::A &A, u32x4 (&W)[TPW][T::NLD]) {
+        T::load_a(xv, b, g, A);
+#pragma unroll
+        for (uint32_t j = 0; j < TPW; j++) T::Load::load(src[j], b, n, g, W[j]);
+    };
+    auto compute = [&](uint32_t b, const typename T::A &A, const u32x4 (&W)[TPW][T::NLD]) {
+#pragma unroll
+        for (uint32_t j = 0; j < TPW; j++) T::dot(W[j], A, scratch, src[j], b, n, g, acc[j]);
+    };
+    // blocks wave, wave + nw, ...: two register sets, the next block's loads
+    // in flight while the current one is computed
+    uint32_t b = wave;
+    if (b < nblk) {
+        issue(b, A0, W0);
+        for (;;) {
+            const uint32_t b1 = b + nw;
+            if (b1 < nblk) issue(b1, A1, W1);
+            compute(b, A0, W0);
+            if (b1 >= nblk) break;
+            const uint32_t b2 = b1 + nw;
+            if (b2 < nblk) issue(b2, A0, W0);
+            compute(b1, A1, W1);
+            if (b2 >= nblk) break;
+            b = b2;
+        }
+    }
+
+    // partial sums [TPW][nw][lane][2], added in wave order; lane (n, g) holds
+    // row n of the tile for vectors 2g and 2g + 1
+    float *red = reinterpret_cast<float *>(lds + nw * T::SCRATCH);
+#pragma unroll
+    for (uint32_t j = 0; j < TPW; j++) {
+        red[(j * nw + wave) * 128u + 2u * lane] = acc[j][0];
+        red[(j * nw + wave) * 128u + 2u * lane + 1u] = acc[j][1];
+    }
+    __syncthreads();
+    for (uint32_t q = threadIdx.x; q < TPW * 128u; q += blockDim.x) {
+        const uint32_t j = q >> 7, l = (q >> 1) & 63u, tk = q & 1u;
+        float s = 0.f;
+        for (uint32_t w = 0; w < nw; w++) s += red[(j * nw + w) * 128u + 2u * l + tk];
+        const uint32_t m = mt[j], row = lt[j] * 16u + (l & 15u), t = 2u * (l >> 4) + tk;
+        if (blockIdx.x * TPW + j < total && row < a.rows[m] && t < a.batch) {
+            float *dst = a.y[m] + (uint64_t)t * a.ys[m] + row;
+            *dst = ACC ? __fadd_rn(*dst, s) : s;
+        }
+    }
+}
+
+template <class T, uint32_t TPW, bool ACC>
+static hipError_t launch_mvb_t(const MbArgs &a, uint32_t nw, hipStream_t s) {
+    const uint32_t tiles = a.tile_end[a.nmat - 1u];
+    const size_t lds = (size_t)nw * T::SCRATCH + (size_t)TPW * nw * 128u * sizeof(float);
+    k_mvb<T, TPW, ACC><<<(tiles + TPW - 1u) / TPW, 64u * nw, lds, s>>>(a);
+    return hipGetLastError();
+}
+
+// Tiles per workgroup and waves (measured at batch 8 on the 70B shapes): the
+// A operands of a block serve every tile of a wave, so they are shared as
+// widely as the grid still fills the chip; four tiles pair best with four
+// waves. Q6_K stops at two tiles (four would spill registers).
+template <class T, bool ACC>
+static hipError_t launch_mvb_plan(const MbArgs &a, hipStream_t s) {
+    const uint32_t nblk = a.cols / 256u, tiles = a.tile_end[a.nmat - 1u];
+    if constexpr (T::BYTES == 144u) {
+        if (tiles >= 640u) return launch_mvb_t<T, 4, ACC>(a, min(4u, nblk), s);
+        if (tiles >= 256u) return launch_mvb_t<T, 2, ACC>(a, min(8u, nblk), s);
+    } else {
+        if (tiles >= 512u) return launch_mvb_t<T, 2, ACC>(a, nblk > 64u ? 8u : min(4u, nblk), s);
+    }
+    return launch_mvb_t<T, 1, ACC>(a, min(8u, nblk), s);
+}
+
+size_t xprep_bytes(uint32_t cols) { return xb_layout(cols).bytes; }
+
+hipError_t launch_xprep(int mode, const float *x, const float *x2, uint32_t xs,
+                        const float *norm_w, float eps, uint32_t cols, uint32_t batch, uint8_t *xp,
+                        hipStream_t s) {
+    if (batch == 0 || batch > kBatchMax || cols % 256u || cols / 256u > 128u) return hipErrorNotSupported;
+    const dim3 grid((cols / 256u + 3u) / 4u, batch);
+    if (mode == XP_NORM)
+        k_xprep_b<XP_NORM><<<grid, 256, 0, s>>>(x, x2, xs, norm_w, eps, cols, xp);
+    else if (mode == XP_SILU)
+        k_xprep_b<XP_SILU><<<grid, 256, 0, s>>>(x, x2, xs, norm_w, eps, cols, xp);
+    else
+        k_xprep_b<XP_PLAIN><<<grid, 256, 0, s>>>(x, x2, xs, norm_w, eps, cols, xp);
+    return hipGetLastError();
+}
+
+hipError_t launch_mvb(int type, uint32_t nmat, const uint8_t *const w[], const uint32_t rows[],
+                      float *const y[], const uint32_t ys[], int accumulate, const uint8_t *xp,
+                      uint32_t cols, uint32_t batch, hipStream_t s) {
+    if (nmat == 0 || nmat > 3u || batch == 0 || batch > kBatchMax) return hipErrorNotSupported;
+    MbArgs a{};
+    uint32_t tiles = 0;
+    for (uint32_t m = 0; m < nmat; m++) {
+        // (x is read from the prepared planes; any 4-byte aligned pointer passes the check)
+        if (rows[m] == 0 || !mv_fits(type, w[m], reinterpret_cast<const float *>(xp), cols, rows[m]))
+            return hipErrorNotSupported;
+        a.w[m] = w[m];
+        a.y[m] = y[m];
+        a.ys[m] = ys[m];
+        a.rows[m] = rows[m];
+        tiles += (rows[m] + 15u) / 16u;
+        a.tile_end[m] = tiles;
+    }
+    a.nmat = nmat;
+    a.xp = xp;
+    a.cols = cols;
+    a.batch = batch;
+    if (type == kQ4_K)
+        return accumulate ? launch_mvb_plan<Q4KB, true>(a, s) : launch_mvb_plan<Q4KB, false>(a, s);
+    return accumulate ? launch_mvb_plan<Q6KB, true>(a, s) : launch_mvb_plan<Q6KB, false>(a, s);
+}
+
+hipError_t launch_kq_linear_batch(int type, const uint8_t *w, const float *x, uint32_t xs, float *y,
+                                  uint32_t ys, uint32_t cols, uint32_t rows, uint32_t batch,
+                                  hipStream_t s) {
+    if (batch == 0 || batch > kBatchMax || rows == 0 || !mv_fits(type, w, x, cols, rows))
+        return hipErrorNotSupported;
+    uint8_t *xp = static_cast<uint8_t *>(scratch(xb_layout(cols).bytes, s));
+    if (!xp) return hipErrorOutOfMemory;
+    hipError_t e = launch_xprep(XP_PLAIN, x, nullptr, xs, nullptr, 0.f, cols, batch, xp, s);
+    if (e != hipSuccess) return e;
+    const uint8_t *wm[1] = {w};
+    float *ym[1] = {y};
+    const uint32_t rm[1] = {rows}, ysm[1] = {ys};
+    return launch_mvb(type, 1, wm, rm, ym, ysm, 0, xp, cols, batch, s);
+}
+
+}  // namespace vbs

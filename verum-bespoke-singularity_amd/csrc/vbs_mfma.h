@@ -1,0 +1,764 @@
+// vbs_mfma.h — the batch-1 matrix-core matvec (shared by vbs_kern_mfma.hip,
+// vbs_kern_mfma_blk.hip and vbs_kern_mfma_batch.hip): x digits, weight-type
+// policies, the k_mvf kernel template and its launch plan.
+//
+// y[r] (+)= sum_c deq(W[r,c]) * x[c] with W in native GGUF super-blocks
+// (src/vbs_dequant.c:225-277 for Q4_K, 316-333 for Q6_K); the reference's
+// linear is vbs_host_linear_tile (src/vbs_host_math.h:223-267).
+//
+// x in digit form: every 32-element sub-block j of x gets an exponent e_j with
+// 2^e_j > max|x| over the sub-block, and each element becomes the integer
+// X = rint(x * 2^(22 - e_j)) (|X| <= 2^22), split into three balanced signed
+// bytes X = D0 + 2^8 D1 + 2^16 D2. A dot of quantised weights with x is then
+// an exact integer dot per digit plane, scaled back by 2^(e_j - 22): x is
+// represented to 2^-22 of its sub-block maximum, which keeps each row within
+// ~1e-7 of the reference's double-accumulated result.
+//
+// The three digit planes make the batch-1 matvec a skinny integer GEMM, which
+// is what v_mfma_i32_16x16x64_i8 computes: A (16 x 64) holds digit planes of
+// x, B (64 x 16) the unpacked quants of 16 weight rows, and D (16 x 16) gets,
+// per row, one integer dot per (scale group, plane). Operand layout: lane l
+// holds A[l%16][ks(l/16, b)] and B[ks(l/16, b)][l%16] for its 16 bytes b, and
+// D[4(l/16)+r][l%16] for r < 4 (checked on the device with a one-hot probe).
+// A row 4t+p carries plane p of scale group t at exactly the lanes whose B
+// bytes belong to group t, so lane (n, g) = (l%16, l/16) of D receives the
+// three plane dots of group g of row n. A rows of other groups are zero (read
+// from a 16-byte zero pad).
+//
+// Work split. A workgroup owns TPW tiles of 16 rows; its nw waves split each
+// row by super-blocks (wave w takes blocks w, w + nw, ..., so the waves read
+// adjacent blocks together) and leave one sum per (row, block) in LDS; a row
+// adds its blocks in index order at the end, so its value does not depend on
+// the split (fused and per-op launches of one matrix agree bit for bit). A
+// wave streams its (tile, block) items with one in flight ahead of the one it
+// computes, and turns x into digits one 256-element block at a time, right
+// before the first item that needs it; it reads only the digits of its own
+// blocks, so no barrier stands between the first weight bytes and the matrix
+// cores. With an RMSNorm in front, the sum of squares over all x blocks comes
+// first (one barrier; the loads of the first item are already out). Deeper
+// streams or x travelling with the items measured no faster: the memory
+// system is saturated from the first requests on.
+//
+// Q4_K (144-byte blocks). Lane (n, g) reads the 16-byte header of row n and 16
+// bytes of nibbles at qs offsets 16g and 64 + 16g. qs bytes 32s..32s+31 hold
+// sub-block 2s in their low and 2s+1 in their high nibbles; per 64-byte span
+// one MFMA takes the low and one the high nibbles, accumulating into one D in
+// which group g is sub-block 4*span + g. Value per sub-block, as the
+// reference's d*sc*nib - dmin*m summed: d*sc*2^(e-22)*S - dmin*m*sum(x).
+//
+// Q6_K (210-byte blocks, 6-bit quants, 16-element int8 scales). Lane group
+// g = (h, u) covers elements 16u..16u+15 of every 32-element quarter of half h
+// of the block: it reads the ql bytes of quarters 0/2 and 1/3 and the qh bytes
+// of those elements, plus the 16 scales and d. MFMA q in 0..3 takes quarter q
+// of both halves, so every shift in the 6-bit unpack is the same for all
+// lanes, and lane group g holds scale group 8h + 2q + u. Value per group, as
+// d*sc*(q - 32) summed: d*sc*(2^(e-22)*S - 32*sum16(x)).
+#pragma once
+
+#include "vbs_dev_common.h"
+#include "vbs_internal.h"
+
+namespace vbs {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// ---- digit buffer ---------------------------------------------------------------
+// [3][cols] int8 planes | 16 zero bytes | float2 xs[cols/32] = {2^(e-22), sum x}
+// | float xs16[cols/16] = sum of x per 16 elements.
+struct XqLayout {
+    uint32_t zero, xs, xs16, bytes;
+};
+__host__ __device__ inline XqLayout xq_layout(uint32_t cols) {
+    XqLayout L;
+    L.zero = 3u * cols;
+    L.xs = (L.zero + 16u + 15u) & ~15u;
+    L.xs16 = L.xs + 8u * (cols / 32u);
+    L.bytes = L.xs16 + 4u * (cols / 16u);
+    return L;
+}
+
+
+// Group reductions over aligned lane groups with DPP (every lane of the group
+// gets the result): L = 4 (quads) or 8 (half rows).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                                 CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float quad_sum(float v) {
+    v = v + dpp_f<0xB1>(v);  // quad_perm [1,0,3,2]
+    return v + dpp_f<0x4E>(v);  // quad_perm [2,3,0,1]
+}
+__device__ __forceinline__ float quad_max(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    return fmaxf(v, dpp_f<0x4E>(v));
+}
+__device__ __forceinline__ float half_row_other(float v) { return dpp_f<0x141>(v); }  // lane i <-> 7-i
+
+// Digits of block b of x (256 elements) by one wave: lane l holds elements
+// 4l..4l+3 (v), so a 16-element item is a lane quad and a 32-element
+// sub-block a half row. Writes the three planes, xs and xs16 of the block.
+// Sums: per lane in element order, then the quad, then the two quads of a
+// sub-block (the same value in every lane of the group).
+__device__ __forceinline__ void prep_block(const float *v, uint32_t cols, uint32_t b,
+                                           uint32_t lane, uint8_t *xq, const XqLayout &L) {
+    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    const float sum4 = ((v[0] + v[1]) + v[2]) + v[3];
+    amax = quad_max(amax);
+    amax = fmaxf(amax, half_row_other(amax));
+    const float sum16 = quad_sum(sum4);
+    const float other = half_row_other(sum16);
+    const float sum32 = (lane & 4u) ? other + sum16 : sum16 + other;  // same order in both quads
+    int e;
+    (void)frexpf(amax, &e);  // amax < 2^e
+    const bool finite = amax <= 3.4028235e38f;
+    // X = rint(x 2^(22-e)) with |X| < 2^22: adding 1.5 * 2^23 rounds to the
+    // nearest integer (ties to even, as rint) and leaves 2^22 + X in the low 23
+    // bits. U = X + 0x808080 then holds the balanced digits as biased bytes:
+    // D_i = byte_i(U) - 128, i.e. byte_i(U) ^ 0x80 in int8 form (the same
+    // digits as D0 = int8(X), D1 = int8((X - D0) / 256), ...). Sub-blocks whose
+    // maximum is not finite get a NaN scale, which makes their digits moot.
+    uint32_t u[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+        u[k] = __float_as_uint(__fadd_rn(ldexpf(v[k], 22 - e), 12582912.0f)) + 0x408080u;
+    const uint32_t lo01 = __builtin_amdgcn_perm(u[1], u[0], 0x05010400u);
+    const uint32_t lo23 = __builtin_amdgcn_perm(u[3], u[2], 0x05010400u);
+    const uint32_t hi01 = __builtin_amdgcn_perm(u[1], u[0], 0x0c0c0602u);
+    const uint32_t hi23 = __builtin_amdgcn_perm(u[3], u[2], 0x0c0c0602u);
+    const uint32_t off = 256u * b + 4u * lane;
+    *reinterpret_cast<uint32_t *>(xq + off) = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u) ^ 0x80808080u;
+    *reinterpret_cast<uint32_t *>(xq + cols + off) =
+        __builtin_amdgcn_perm(lo23, lo01, 0x07060302u) ^ 0x80808080u;
+    *reinterpret_cast<uint32_t *>(xq + 2u * cols + off) =
+        __builtin_amdgcn_perm(hi23, hi01, 0x05040100u) ^ 0x80808080u;
+    if ((lane & 3u) == 0) reinterpret_cast<float *>(xq + L.xs16)[16u * b + lane / 4u] = sum16;
+    if ((lane & 7u) == 0)
+        reinterpret_cast<float2 *>(xq + L.xs)[8u * b + lane / 8u] =
+            make_float2(finite ? ldexpf(1.0f, e - 22) : __builtin_nanf(""), sum32);
+}
+
+// Sum of squares of block b of x (lane l: elements 4l..4l+3 in element
+// order, then a butterfly over the wave), in double. The RMSNorm adds the
+// blocks in index order; k_rms_norm uses the same order.
+__device__ __forceinline__ double block_sumsq(const float *v) {
+    double ss = 0.0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) ss = fma((double)v[k], (double)v[k], ss);
+    return wave_sum_d(ss);
+}
+
+// ---- helpers ------------------------------------------------------------------------
+// 16 bytes from a 16-byte aligned address.
+__device__ __forceinline__ u32x4 lda4(const uint8_t *p) {
+    return *reinterpret_cast<const u32x4 *>(p);
+}
+// 16 bytes from a 2-byte aligned address (used on LDS).
+__device__ __forceinline__ u32x4 ldu(const uint8_t *p) {
+    typedef u32x4 __attribute__((aligned(2))) u32x4u;
+    return *reinterpret_cast<const u32x4u *>(p);
+}
+__device__ __forceinline__ i32x4 lda(const uint8_t *p) {
+    return *reinterpret_cast<const i32x4 *>(p);
+}
+__device__ __forceinline__ float cvt_h(uint32_t bits16) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}
+__device__ __forceinline__ uint32_t bfe(uint32_t v, uint32_t off, uint32_t w) {
+    return __builtin_amdgcn_ubfe(v, off, w);
+}
+__device__ __forceinline__ i32x4 mfma(i32x4 a, i32x4 b, i32x4 c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+// The three plane dots combined, exact up to one rounding (|D0 + 256 D1| < 2^24).
+__device__ __forceinline__ float plane_sum(i32x4 D) {
+    return fmaf((float)D[2], 65536.f, (float)(D[0] + D[1] * 256));
+}
+
+// ---- weight types ---------------------------------------------------------------------
+// Where a wave's tile lives: row r of the matrix starts at w + r * rb; rows of
+// the tile past the end re-read the last row; no load reaches past w + bytes.
+// Offsets are 32-bit (the matrix is below 4 GiB) from the wave-uniform base w,
+// so loads take the scalar-base form.
+struct Src {
+    const uint8_t *w;
+    uint32_t bytes, rb, row0, rows;
+    __device__ uint32_t row(uint32_t n) const { return min(row0 + n, rows - 1u) * rb; }
+};
+
+// load(): this lane's share of block b of the tile (NLD 16-byte words).
+// dot(): the block's contribution to the lane's row partial sum; (n, g) is the
+// lane as MFMA operand (A row n, lane group g); `scratch` is the wave's LDS.
+struct Q4K {
+    static constexpr uint32_t BYTES = 144, NLD = 3, SCRATCH = 0;
+    __device__ static void load(const Src &src, uint32_t b, uint32_t n, uint32_t g, u32x4 *r) {
+        const uint8_t *blk = src.w + (src.row(n) + b * BYTES);
+        r[0] = lda4(blk);
+        r[1] = lda4(blk + 16u * g + 16u);
+        r[2] = lda4(blk + 16u * g + 80u);
+    }
+    __device__ static float dot(const u32x4 *r, uint8_t *, const Src &, const uint8_t *xq,
+                                const XqLayout &L, uint32_t cols, uint32_t b, uint32_t n,
+                                uint32_t g) {
+        // A row n = 4t+p: lane group g carries sub-blocks 2(g>>1) (low nibbles,
+        // t even) and 2(g>>1)+1 (high nibbles, t odd) at element offset 16(g&1)
+        const uint32_t t = n >> 2, p = n & 3u;
+        const bool on = p < 3u && (g >> 1) == (t >> 1);
+        const uint32_t ao = p * cols + 256u * b + 32u * t + 16u * (g & 1u);
+        const i32x4 A0l = lda(xq + (on && !(t & 1u) ? ao : L.zero));
+        const i32x4 A0h = lda(xq + (on && (t & 1u) ? ao : L.zero));
+        const i32x4 A1l = lda(xq + (on && !(t & 1u) ? ao + 128u : L.zero));
+        const i32x4 A1h = lda(xq + (on && (t & 1u) ? ao + 128u : L.zero));
+        const uint32_t M4 = 0x0F0F0F0Fu;
+        const u32x4 qa = r[1], qb = r[2];
+        const i32x4 B0l = {(int)(qa.x & M4), (int)(qa.y & M4), (int)(qa.z & M4), (int)(qa.w & M4)};
+        const i32x4 B0h = {(int)((qa.x >> 4) & M4), (int)((qa.y >> 4) & M4),
+                           (int)((qa.z >> 4) & M4), (int)((qa.w >> 4) & M4)};
+        const i32x4 B1l = {(int)(qb.x & M4), (int)(qb.y & M4), (int)(qb.z & M4), (int)(qb.w & M4)};
+        const i32x4 B1h = {(int)((qb.x >> 4) & M4), (int)((qb.y >> 4) & M4),
+                           (int)((qb.z >> 4) & M4), (int)((qb.w >> 4) & M4)};
+        const i32x4 z = {0, 0, 0, 0};
+        const float S0 = plane_sum(mfma(A0h, B0h, mfma(A0l, B0l, z)));
+        const float S1 = plane_sum(mfma(A1h, B1h, mfma(A1l, B1l, z)));
+        // D group g: sub-blocks g (span 0) and 4 + g (span 1); scales and mins
+        // as src/vbs_dequant.c:225-233
+        const float2 *xs = reinterpret_cast<const float2 *>(xq + L.xs);
+        const float2 xs0 = xs[8u * b + g], xs1 = xs[8u * b + 4u + g];
+        const u32x4 hd = r[0];
+        const uint32_t sh = 8u * g;
+        const uint32_t sc0 = bfe(hd.y, sh, 6), m0 = bfe(hd.z, sh, 6);
+        const uint32_t sc1 = bfe(hd.w, sh, 4) | (bfe(hd.y, sh + 6u, 2) << 4);
+        const uint32_t m1 = bfe(hd.w, sh + 4u, 4) | (bfe(hd.z, sh + 6u, 2) << 4);
+        const float d = cvt_h(hd.x & 0xFFFFu), dmin = cvt_h(hd.x >> 16);
+        const float sd = fmaf((float)sc0 * xs0.x, S0, (float)sc1 * xs1.x * S1);
+        const float sm = fmaf((float)m0, xs0.y, (float)m1 * xs1.y);
+        return fmaf(d, sd, -dmin * sm);
+    }
+};
+
+// 16 aligned bytes at a, of which only those below `end` (2-byte aligned) are
+// read; the rest are zero.
+__device__ __forceinline__ u32x4 ld_tail(const uint8_t *a, const uint8_t *end) {
+    uint32_t v[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const uint8_t *p = a + 4 * k;
+        v[k] = p + 4 <= end   ? *reinterpret_cast<const uint32_t *>(p)
+               : p + 2 <= end ? (uint32_t)*reinterpret_cast<const uint16_t *>(p)
+                              : 0u;
+    }
+    const u32x4 r = {v[0], v[1], v[2], v[3]};
+    return r;
+}
+
+struct Q6K {
+    // A 210-byte block is 2-byte aligned, and 16-byte loads at such addresses
+    // run at about half the rate of aligned ones. So the wave reads each block
+    // of its 16 rows as 14 aligned 16-byte chunks per row (covering the block
+    // at any 2-byte offset), chunk c = 14n + k going to lane c mod 64, stores
+    // them to its LDS scratch in row order and reads its fields from there as
+    // 4-byte aligned words, shifted into place in registers (16-byte LDS reads
+    // at 2-byte aligned addresses are several times slower).
+    static constexpr uint32_t BYTES = 210, NLD = 4, SCRATCH = 16u * 224u;
+    __device__ static void load(const Src &src, uint32_t b, uint32_t n, uint32_t g, u32x4 *r) {
+        const uint32_t lane = 16u * g + n;
+        // only the last block of the matrix's last row has chunks that reach
+        // past its end (by at most 14 bytes); those loads are bounded
+        const uint32_t wlo = (uint32_t)(uintptr_t)src.w & 15u;
+        const uint32_t last = src.row(15u) + b * BYTES;
+        const bool edge = __builtin_amdgcn_readfirstlane(
+                              (uint32_t)(last - ((last + wlo) & 15u) + 224u > src.bytes)) != 0u;
+        uint32_t a[4];
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++) {
+            // chunk c of the tile: 16 aligned bytes
+            const uint32_t c = min(lane + 64u * i, 223u);
+            const uint32_t s = src.row(c / 14u) + b * BYTES;
+            a[i] = s - ((s + wlo) & 15u) + 16u * (c % 14u);
+        }
+        if (!edge) {
+#pragma unroll
+            for (uint32_t i = 0; i < 4; i++) r[i] = lda4(src.w + a[i]);
+        } else {
+            const uint8_t *end = src.w + src.bytes;
+#pragma unroll
+            for (uint32_t i = 0; i < 4; i++)
+                r[i] = a[i] + 16u <= src.bytes ? lda4(src.w + a[i]) : ld_tail(src.w + a[i], end);
+        }
+    }
+    __device__ static float dot(const u32x4 *r, uint8_t *scratch, const Src &src,
+                                const uint8_t *xq, const XqLayout &L, uint32_t cols, uint32_t b,
+                                uint32_t n, uint32_t g) {
+        const uint32_t lane = 16u * g + n;
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++) {
+            const uint32_t c = lane + 64u * i;
+            if (i < 3u || c < 224u) *reinterpret_cast<u32x4 *>(scratch + 16u * c) = r[i];
+        }
+        // row n's block starts o = (its address mod 16) into its 224 scratch
+        // bytes; rw is the 4-byte aligned word at or below the start and sh
+        // (0 or 2) the byte shift from there. Every word read lies in the row.
+        const uint32_t o = ((uint32_t)(uintptr_t)src.w + src.row(n) + b * BYTES) & 15u;
+        const uint32_t *rw = reinterpret_cast<const uint32_t *>(scratch + 224u * n + (o & 12u));
+        const uint32_t sh = o & 2u;
+        // 16 bytes at block byte f (a multiple of 4)
+        auto field = [&](uint32_t f) {
+            const uint32_t *p = rw + f / 4u;
+            const uint32_t w0 = p[0], w1 = p[1], w2 = p[2], w3 = p[3], w4 = p[4];
+            const u32x4 v = {__builtin_amdgcn_alignbyte(w1, w0, sh),
+                             __builtin_amdgcn_alignbyte(w2, w1, sh),
+                             __builtin_amdgcn_alignbyte(w3, w2, sh),
+                             __builtin_amdgcn_alignbyte(w4, w3, sh)};
+            return v;
+        };
+        // lane group g = (h, u) = (g >> 1, g & 1): half h of the block, elements
+        // 16u..16u+15 of each of its 32-element quarters
+        const uint32_t h = g >> 1, u = g & 1u;
+        const u32x4 qe = field(64u * h + 16u * u);         // ql, quarters 0 / 2
+        const u32x4 qo = field(64u * h + 32u + 16u * u);   // ql, quarters 1 / 3
+        const u32x4 qh = field(128u + 32u * h + 16u * u);  // qh, 2 bits per quarter
+        // int8 scales 8h..8h+7 (bytes 192 + 8h) and the f16 d (bytes 208..209)
+        const uint32_t *ps = rw + 48u + 2u * h;
+        const uint32_t s0 = ps[0], s1 = ps[1], s2 = ps[2];
+        const uint32_t sc_lo = __builtin_amdgcn_alignbyte(s1, s0, sh);
+        const uint32_t sc_hi = __builtin_amdgcn_alignbyte(s2, s1, sh);
+        const uint32_t dbits = (rw[52] >> (8u * sh)) & 0xFFFFu;
+        // MFMA q (quarter q of both halves): lane group g holds scale group
+        // 8h + 2q + u; A row n = 4t+p carries plane p of the group of lane group t
+        const uint32_t t = n >> 2, p = n & 3u;
+        const bool on = p < 3u && t == g;
+        const float2 *xs = reinterpret_cast<const float2 *>(xq + L.xs);
+        const float *xs16 = reinterpret_cast<const float *>(xq + L.xs16);
+        const uint32_t qew[4] = {qe.x, qe.y, qe.z, qe.w}, qow[4] = {qo.x, qo.y, qo.z, qo.w};
+        const uint32_t qhw[4] = {qh.x, qh.y, qh.z, qh.w};
+        const uint32_t a0 = p * cols + 256u * b + 128u * (t >> 1) + 16u * (t & 1u);
+        float acc = 0.f;
+#pragma unroll
+        for (uint32_t q = 0; q < 4; q++) {
+            // 6-bit quants, src/vbs_dequant.c:316-333: low 4 bits from ql
+            // (nibble q >> 1 of region q & 1), high 2 bits from qh bits 2q
+            const uint32_t *ql = (q & 1u) ? qow : qew;
+            int bw[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint32_t hi = (q <= 2u ? (qhw[k] << (4u - 2u * q)) : (qhw[k] >> 2u)) &
+                                    0x30303030u;
+                bw[k] = (int)(((ql[k] >> (4u * (q >> 1))) & 0x0F0F0F0Fu) | hi);
+            }
+            const i32x4 B = {bw[0], bw[1], bw[2], bw[3]};
+            const i32x4 A = lda(xq + (on ? a0 + 32u * q : L.zero));
+            const i32x4 z = {0, 0, 0, 0};
+            const float S = plane_sum(mfma(A, B, z));
+            // scale 8h + 2q + u: dword 2h + (q >> 1), byte 2(q & 1) + u; the group
+            // is half u of sub-block 4h + q
+            const uint32_t scd = (q >> 1) ? sc_hi : sc_lo;
+            const float sc = (float)(int)(int8_t)bfe(scd, 16u * (q & 1u) + 8u * u, 8);
+            const uint32_t j = 8u * b + 4u * h + q;
+            acc = fmaf(sc, fmaf(xs[j].x, S, -32.f * xs16[2u * j + u]), acc);
+        }
+        return cvt_h(dbits) * acc;
+    }
+};
+
+// ---- 32-element block types: Q4_0, Q4_1, Q8_0 -------------------------------------------
+// Eight consecutive GGUF blocks (256 elements) are one "block" of this kernel:
+// 144 (Q4_0), 160 (Q4_1) or 272 (Q8_0) bytes at 2-byte alignment. As for
+// Q6_K, a wave stages its 16 rows' bytes in LDS as aligned 16-byte chunks (CH
+// per row) and reads its fields there, shifted into place by (row start +
+// field offset) mod 4. MFMA layout: chain c (sub-blocks 4c..4c+3 = GGUF
+// blocks), two MFMAs per chain (elements 0-15, 16-31 of each sub-block); lane
+// group g holds sub-block 4c + g as B, A row n = 4t + p carries plane p of
+// sub-block 4c + t at lane group t only, so D row 4g' + r of lane group g' is
+// plane r of sub-block 4c + g'. Per sub-block j (d, m the block's f16 scale
+// and min, S the plane-combined integer dot, 2^(e-22) and sum x from the
+// digit buffer), as the reference's values summed (src/vbs_dequant.c:123-179):
+//   Q8_0: d*q            -> d * 2^(e-22) * S
+//   Q4_0: (nib - 8) * d  -> d * (2^(e-22) * S - 8 * sum x)
+//   Q4_1: d * nib + m    -> d * 2^(e-22) * S + m * sum x
+template <int TYPE>
+struct KBlk {
+    static constexpr uint32_t BB = TYPE == kQ8_0 ? 34u : TYPE == kQ4_1 ? 20u : 18u;  // GGUF block
+    static constexpr uint32_t QOFF = TYPE == kQ4_1 ? 4u : 2u;  // quants within the GGUF block
+    static constexpr bool NIB = TYPE != kQ8_0;
+    static constexpr uint32_t BYTES = 8u * BB;
+    static constexpr uint32_t CH = (BYTES + 14u + 15u) / 16u;  // chunks covering any 2-byte offset
+    static constexpr uint32_t NCHUNK = 16u * CH;
+    static constexpr uint32_t NLD = (NCHUNK + 63u) / 64u, SCRATCH = 16u * NCHUNK;
+    __device__ static void load(const Src &src, uint32_t b, uint32_t n, uint32_t g, u32x4 *r) {
+        const uint32_t lane = 16u * g + n;
+        // only the last block of the matrix's last row has chunks past its end
+        const uint32_t wlo = (uint32_t)(uintptr_t)src.w & 15u;
+        const uint32_t last = src.row(15u) + b * BYTES;
+        const bool edge = __builtin_amdgcn_readfirstlane(
+                              (uint32_t)(last - ((last + wlo) & 15u) + 16u * CH > src.bytes)) != 0u;
+        uint32_t a[NLD];
+#pragma unroll
+        for (uint32_t i = 0; i < NLD; i++) {
+            const uint32_t c = min(lane + 64u * i, NCHUNK - 1u);
+            const uint32_t s0 = src.row(c / CH) + b * BYTES;
+            a[i] = s0 - ((s0 + wlo) & 15u) + 16u * (c % CH);
+        }
+        if (!edge) {
+#pragma unroll
+            for (uint32_t i = 0; i < NLD; i++) r[i] = lda4(src.w + a[i]);
+        } else {
+            const uint8_t *end = src.w + src.bytes;
+#pragma unroll
+            for (uint32_t i = 0; i < NLD; i++)
+                r[i] = a[i] + 16u <= src.bytes ? lda4(src.w + a[i]) : ld_tail(src.w + a[i], end);
+        }
+    }
+    __device__ static float dot(const u32x4 *r, uint8_t *scratch, const Src &src,
+                                const uint8_t *xq, const XqLayout &L, uint32_t cols, uint32_t b,
+                                uint32_t n, uint32_t g) {
+        const uint32_t lane = 16u * g + n;
+#pragma unroll
+        for (uint32_t i = 0; i < NLD; i++) {
+            const uint32_t c = lane + 64u * i;
+            if (i + 1u < NLD || c < NCHUNK) *reinterpret_cast<u32x4 *>(scratch + 16u * c) = r[i];
+        }
+        // row n's block starts o bytes into its CH chunks
+        const uint32_t o = ((uint32_t)(uintptr_t)src.w + src.row(n) + b * BYTES) & 15u;
+        const uint32_t *rw = reinterpret_cast<const uint32_t *>(scratch + 16u * CH * n);
+        auto field = [&](uint32_t f) {  // 16 bytes at block byte f (even)
+            const uint32_t P = o + f, i = P >> 2, sh = P & 3u;
+            const uint32_t w0 = rw[i], w1 = rw[i + 1u], w2 = rw[i + 2u], w3 = rw[i + 3u], w4 = rw[i + 4u];
+            const u32x4 v = {__builtin_amdgcn_alignbyte(w1, w0, sh), __builtin_amdgcn_alignbyte(w2, w1, sh),
+                             __builtin_amdgcn_alignbyte(w3, w2, sh), __builtin_amdgcn_alignbyte(w4, w3, sh)};
+            return v;
+        };
+        auto half16 = [&](uint32_t f) {  // the f16 bits at block byte f (even)
+            const uint32_t P = o + f;
+            return (rw[P >> 2] >> (8u * (P & 3u))) & 0xFFFFu;
+        };
+        const uint32_t t = n >> 2, p = n & 3u;
+        const bool on = p < 3u && t == g;
+        const float2 *xs = reinterpret_cast<const float2 *>(xq + L.xs);
+        const i32x4 z = {0, 0, 0, 0};
+        float acc = 0.f;
+#pragma unroll
+        for (uint32_t c = 0; c < 2u; c++) {
+            const uint32_t j = 4u * c + g;  // this lane group's sub-block (B) and D sub-block
+            u32x4 q0, q1;
+            if (NIB) {  // qs[16]: element e < 16 low nibble of qs[e], e >= 16 high nibble
+                const u32x4 q = field(BB * j + QOFF);
+                const uint32_t M4 = 0x0F0F0F0Fu;
+                q0 = u32x4{q.x & M4, q.y & M4, q.z & M4, q.w & M4};
+                q1 = u32x4{(q.x >> 4) & M4, (q.y >> 4) & M4, (q.z >> 4) & M4, (q.w >> 4) & M4};
+            } else {  // int8 q[32]
+                q0 = field(BB * j + QOFF);
+                q1 = field(BB * j + QOFF + 16u);
+            }
+            const uint32_t ao = p * cols + 256u * b + 32u * (4u * c + t);
+            const i32x4 A0 = lda(xq + (on ? ao : L.zero));
+            const i32x4 A1 = lda(xq + (on ? ao + 16u : L.zero));
+            const i32x4 D = mfma(A1, __builtin_bit_cast(i32x4, q1),
+                                 mfma(A0, __builtin_bit_cast(i32x4, q0), z));
+            const float S = plane_sum(D);
+            const float2 x2 = xs[8u * b + j];
+            const float d = cvt_h(half16(BB * j));
+            if (TYPE == kQ8_0) acc = fmaf(d * x2.x, S, acc);
+            else if (TYPE == kQ4_0) acc = fmaf(d, fmaf(x2.x, S, -8.f * x2.y), acc);
+            else acc = fmaf(d * x2.x, S, fmaf(cvt_h(half16(BB * j + 2u)), x2.y, acc));
+        }
+        return acc;
+    }
+};
+using Q40 = KBlk<kQ4_0>;
+using Q41 = KBlk<kQ4_1>;
+using Q80 = KBlk<kQ8_0>;
+
+// ---- jobs -------------------------------------------------------------------------------
+// One launch computes the rows of up to three matrices that share x (and its
+// type and column count), with an optional RMSNorm of x in front and one of
+// these epilogues on each finished row value t (every arithmetic step is the
+// reference's own):
+//   E_STORE  y[row] = t                       (vbs_host_linear_tile)
+//   E_ACC    y[row] = y[row] + t              (linear, then ELEMENTWISE add)
+//   E_QKV    matrix roles q, k, v: RoPE of q and k rows at the device position
+//            (src/vbs_host_math.h:38-51), q to y[0] in f32, k and v to the f16
+//            caches (src/vbs_host_math.h:150-159)
+//   E_SILU   gate and up: y[0][row] = gate / (1 + expf(-gate)) * up
+//            (src/vbs_host_math.h:53-57)
+enum : int { E_STORE = 0, E_ACC = 1, E_QKV = 2, E_SILU = 3 };
+
+struct MvArgs {
+    const uint8_t *w[3];
+    float *y[3];
+    uint32_t rows[3];
+    uint32_t tile_end[3];  // cumulative 16-row tiles per matrix
+    uint32_t nmat, cols;
+    const float *x;
+    const float *norm_w;  // RMSNorm weights (NORM launches)
+    float eps;
+    const float2 *rope;   // E_QKV: [max_ctx][hd/2] (cos, sin)
+    const uint32_t *pos;  // E_QKV: device position
+    uint32_t hd, kvd, role0;
+    uint16_t *kc, *vc;
+    uint64_t kv_layer;  // layer * max_ctx * kvd
+};
+
+template <class T, uint32_t KS, uint32_t TPW, uint32_t MAXT, bool NORM, int EPI>
+__global__ __launch_bounds__(MAXT) void k_mvf(const MvArgs a) {
+    extern __shared__ __align__(16) uint8_t xq[];
+    __shared__ double bsum[128];
+    constexpr uint32_t NI = KS * TPW;  // work items (tile, block) per wave
+    constexpr uint32_t P0 = 1;         // items issued with x, before anything is computed
+    constexpr uint32_t P = 1;          // items in flight ahead of the one computed
+    const uint32_t cols = a.cols;
+    const uint32_t nblk = cols >> 8;
+    const uint32_t rb = nblk * T::BYTES;
+    const XqLayout L = xq_layout(cols);
+    const uint32_t nth = blockDim.x;
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const uint32_t nw = nth >> 6;
+    const uint32_t n = lane & 15u, g = lane >> 4;
+    const uint32_t total = a.tile_end[a.nmat - 1u];
+
+    // matrix and local tile of this workgroup's tile j
+    uint32_t mt[TPW], lt[TPW];
+    Src src[TPW];
+#pragma unroll
+    for (uint32_t j = 0; j < TPW; j++) {
+        if (EPI == E_SILU) {
+            mt[j] = j;
+            lt[j] = blockIdx.x;
+        } else {
+            const uint32_t gt = min(blockIdx.x * TPW + j, total - 1u);
+            mt[j] = (gt >= a.tile_end[0]) + (a.nmat > 2u && gt >= a.tile_end[1]);
+            lt[j] = gt - (mt[j] ? a.tile_end[mt[j] - 1u] : 0u);
+        }
+        const uint8_t *w = a.w[mt[j]];
+        src[j] = Src{w, a.rows[mt[j]] * rb, rb, lt[j] * 16u, a.rows[mt[j]]};
+    }
+    // Block k of this wave: wave + nw * k (at each step the workgroup's waves
+    // read adjacent blocks of the same rows); item i is block i % KS of tile
+    // i / KS. Slots past the row re-read its last block and contribute zero.
+    // A wave prepares the digits of its own blocks only, so the waves share
+    // no x data and need no barrier before the matrix work.
+    auto blk = [&](uint32_t i) { return wave + nw * (i % KS); };
+
+    // x of this wave's blocks, lane l: elements 4l..4l+3 (x may be only
+    // 4-byte aligned), and with the RMSNorm its weights: all requested first.
+    typedef float4 __attribute__((aligned(4))) f4u;
+    float4 xv[KS], wv[NORM ? KS : 1];
+    auto load_x = [&](uint32_t k) {
+        const uint32_t e0 = 256u * min(blk(k), nblk - 1u) + 4u * lane;
+        xv[k] = *reinterpret_cast<const f4u *>(a.x + e0);
+        if (NORM) wv[k] = *reinterpret_cast<const f4u *>(a.norm_w + e0);
+    };
+    u32x4 r[NI][T::NLD];
+    auto issue = [&](uint32_t i) { T::load(src[i / KS], min(blk(i), nblk - 1u), n, g, r[i]); };
+
+    // 1-2. x, then the first items
+#pragma unroll
+    for (uint32_t k = 0; k < KS; k++) load_x(k);
+#pragma unroll
+    for (uint32_t i = 0; i < P0 && i < NI; i++) issue(i);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 3. RMSNorm scale: block sums of squares, added in block order
+    float sc = 1.0f;
+    if (NORM) {
+#pragma unroll
+        for (uint32_t k = 0; k < KS; k++) {
+            const float v[4] = {xv[k].x, xv[k].y, xv[k].z, xv[k].w};
+            const double ss = block_sumsq(v);
+            if (lane == 0 && blk(k) < nblk) bsum[blk(k)] = ss;
+        }
+        __syncthreads();
+        double t = 0.0;
+        for (uint32_t b = 0; b < nblk; b++) t += bsum[b];
+        const float mean = (float)(t / (double)cols);
+        sc = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, a.eps)));
+    }
+    if (lane < 4u) reinterpret_cast<uint32_t *>(xq + L.zero)[lane] = 0u;  // each wave's own pad
+
+    // 4. stream: issue item i + P, prepare x of a new block, compute item i
+    // (loads return in issue order, so the wait is for item i alone)
+    uint8_t *scratch = xq + L.bytes + wave * T::SCRATCH;
+    // per-block row sums [TPW][nblk][16]: every row adds its blocks in index
+    // order at the end, so a row's value does not depend on the work split
+    float *pb = reinterpret_cast<float *>(xq + L.bytes + nw * T::SCRATCH);
+#pragma unroll
+    for (uint32_t i = 0; i < NI; i++) {
+#pragma unroll
+        for (uint32_t j = i == 0 ? P0 : max(P0, i + P); j <= i + P && j < NI; j++) issue(j);
+        __builtin_amdgcn_sched_barrier(0);
+        if (i < KS && blk(i) < nblk) {
+            float v[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+            if (NORM) {
+                const float w4[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
+#pragma unroll
+                for (int k = 0; k < 4; k++) v[k] = __fmul_rn(__fmul_rn(v[k], sc), w4[k]);
+            }
+            prep_block(v, cols, blk(i), lane, xq, L);
+        }
+        float part = T::dot(r[i], scratch, src[i / KS], xq, L, cols, min(blk(i), nblk - 1u), n, g);
+        // the four lane groups of a row hold different groups of the block
+        part += __shfl_xor(part, 16, 64);
+        part += __shfl_xor(part, 32, 64);
+        if (lane < 16u && blk(i) < nblk) pb[((i / KS) * nblk + blk(i)) * 16u + n] = part;
+        // finish item i here: otherwise its arithmetic may sink past later
+        // items and hold their registers
+        asm volatile("" ::"v"(part));
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // 5. tile j finished by wave j % nw (both tiles by wave 0 for E_SILU)
+    __syncthreads();
+    float prev = 0.f;  // E_SILU: the gate row value
+#pragma unroll
+    for (uint32_t j = 0; j < TPW; j++) {
+        if (wave != (EPI == E_SILU ? 0u : j % nw)) continue;
+        float t = 0.f;
+        for (uint32_t b = 0; b < nblk; b++) t += pb[(j * nblk + b) * 16u + n];
+        // every lane holds the value of row n of the tile
+        const uint32_t m = mt[j];
+        const bool own = (EPI == E_SILU || blockIdx.x * TPW + j < total);
+        const uint32_t row = lt[j] * 16u + n;
+        const bool st = lane < 16u && own && row < a.rows[m];
+        if (EPI == E_STORE) {
+            if (st) a.y[m][row] = t;
+        } else if (EPI == E_ACC) {
+            if (st) a.y[m][row] = __fadd_rn(a.y[m][row], t);
+        } else if (EPI == E_SILU) {
+            if (j == 0) {
+                prev = t;
+            } else if (st) {
+                const float den = __fadd_rn(1.0f, expf(-prev));
+                a.y[0][row] = __fmul_rn(__fdiv_rn(prev, den), t);
+            }
+        } else {  // E_QKV
+            const uint32_t role = a.role0 + m;
+            const float other = __shfl_xor(t, 1, 64);  // the RoPE partner row
+            const uint32_t p = a.pos[0];
+            float v = t;
+            if (role < 2u) {
+                const float2 cs = a.rope[(uint64_t)p * (a.hd / 2u) + (row % a.hd) / 2u];
+                const bool even = (row & 1u) == 0u;
+                const float x0 = even ? t : other, x1 = even ? other : t;
+                v = even ? __fsub_rn(__fmul_rn(x0, cs.x), __fmul_rn(x1, cs.y))
+                         : __fadd_rn(__fmul_rn(x0, cs.y), __fmul_rn(x1, cs.x));
+            }
+            if (st) {
+                if (role == 0u)
+                    a.y[0][row] = v;
+                else
+                    (role == 1u ? a.kc : a.vc)[a.kv_layer + (uint64_t)p * a.kvd + row] = vbs_f2h(v);
+            }
+        }
+    }
+}
+
+// ---- launch ---------------------------------------------------------------------------
+struct MvPlan {
+    uint32_t ks, tpw, nw;
+};
+
+// Blocks per wave (KS) and waves per tile: enough waves to split the row and
+// enough items per wave that the stream runs ahead of the arithmetic.
+// (The gate/up launch, two tiles per workgroup, keeps four blocks per wave:
+// eight waves of two would not all be resident at once.)
+template <class T>
+static MvPlan mv_plan(uint32_t cols, bool two_tiles, bool fused) {
+    const uint32_t nblk = cols / 256u;
+    MvPlan p;
+    p.ks = nblk <= 16u && !two_tiles ? 2u : nblk <= 32u ? 4u : nblk <= 48u ? 6u
+         : nblk <= 64u || nblk > 112u ? 8u : 14u;
+    if (fused && p.ks == 14u) p.ks = 8u;  // (fused and normed launches keep eight)
+    p.nw = (nblk + p.ks - 1u) / p.ks;
+    p.tpw = 1u;
+    return p;
+}
+
+template <class T, uint32_t KS, uint32_t TPW, uint32_t MAXT, bool NORM, int EPI>
+static hipError_t launch_t(const MvArgs &a, uint32_t nw, uint32_t wgs, hipStream_t s) {
+    const size_t lds = xq_layout(a.cols).bytes + (size_t)nw * T::SCRATCH +
+                       (size_t)TPW * (a.cols / 256u) * 16u * sizeof(float);
+    if (lds > 65536u) {  // beyond the default per-workgroup LDS window: opt in once
+        static size_t granted = 0;
+        if (lds > granted) {
+            if (hipFuncSetAttribute((const void *)k_mvf<T, KS, TPW, MAXT, NORM, EPI>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
+                hipSuccess) {
+                (void)hipGetLastError();
+                return hipErrorNotSupported;
+            }
+            granted = lds;
+        }
+    }
+    k_mvf<T, KS, TPW, MAXT, NORM, EPI><<<wgs, 64u * nw, lds, s>>>(a);
+    return hipGetLastError();
+}
+
+template <class T, bool NORM, int EPI, uint32_t TPW>
+static hipError_t launch_ks(const MvArgs &a, const MvPlan &p, uint32_t wgs, hipStream_t s) {
+#define VBS_MV(KS, MAXT) return launch_t<T, KS, TPW, MAXT, NORM, EPI>(a, p.nw, wgs, s)
+    if (p.ks == 2u) {
+        if (p.nw <= 8u) VBS_MV(2, 512);
+        VBS_MV(2, 1024);
+    }
+    if (p.ks == 4u) {
+        if (p.nw <= 8u) VBS_MV(4, 512);
+        VBS_MV(4, 1024);
+    }
+    if (p.ks == 6u) {
+        if (p.nw <= 8u) VBS_MV(6, 512);
+        VBS_MV(6, 1024);
+    }
+    // rows of 65-112 blocks (70B down: 112), one tile per workgroup
+    if constexpr ((EPI == E_STORE || EPI == E_ACC) && TPW == 1 && !NORM)
+        if (p.ks == 14u) VBS_MV(14, 512);
+    VBS_MV(8, 1024);
+#undef VBS_MV
+}
+
+template <class T, bool NORM, int EPI>
+static hipError_t launch_plan(const MvArgs &a, hipStream_t s) {
+    const uint32_t total = a.tile_end[a.nmat - 1u];
+    MvPlan p = mv_plan<T>(a.cols, EPI == E_SILU, NORM || EPI == E_SILU || EPI == E_QKV);
+    if (p.ks == 14u && a.tile_end[a.nmat - 1u] >= 1024u) {  // (several tiles: keep eight)
+        p.ks = 8u;
+        p.nw = (a.cols / 256u + 7u) / 8u;
+    }
+    if (p.nw > 16u) return hipErrorNotSupported;
+    if constexpr (EPI == E_SILU)  // a gate tile and the same up tile
+        return launch_ks<T, NORM, EPI, 2>(a, p, a.tile_end[0], s);
+    // Launches that would need several rounds of resident workgroups give each
+    // workgroup four tiles instead: x (and the RMSNorm) is prepared once per
+    // four tiles and every workgroup is resident from the start.
+    if constexpr (EPI == E_STORE || EPI == E_ACC) {
+        if (total >= 1024u) return launch_ks<T, NORM, EPI, 4>(a, p, (total + 3u) / 4u, s);
+    }
+    return launch_ks<T, NORM, EPI, 1>(a, p, total, s);
+}
+
+// Shape and alignment range of the matrix-core path: at most 16 waves of at
+// most 8 super-blocks (the digits of x and the Q6_K scratch must also fit the
+// LDS, else the launch reports it unsupported); Q4_K rows are 16-byte
+// multiples, so its 16-byte loads need an aligned w; Q6_K aligns every load.
+// The 32-element block types (batch-1 store / accumulate launches only).
+static inline bool mv_fits_blk(int type, const uint8_t *w, const float *x, uint32_t cols, uint32_t rows) {
+    if (type != kQ4_0 && type != kQ4_1 && type != kQ8_0) return false;
+    if (cols % 256u || cols / 256u > 128u || ((uintptr_t)x & 3u) || ((uintptr_t)w & 1u)) return false;
+    return (uint64_t)rows * row_bytes(type, cols) < (1ull << 32);
+}
+
+static inline bool mv_fits(int type, const uint8_t *w, const float *x, uint32_t cols, uint32_t rows) {
+    if (type != kQ4_K && type != kQ6_K) return false;
+    if (cols % 256u || cols / 256u > 128u || ((uintptr_t)x & 3u)) return false;
+    if ((uint64_t)rows * (cols / 256u) * (type == kQ4_K ? 144u : 210u) >= (1ull << 32)) return false;
+    return ((uintptr_t)w & (type == kQ4_K ? 15u : 1u)) == 0;
+}
+
+static inline void set_tiles(MvArgs &a) {
+    uint32_t t = 0;
+    for (uint32_t m = 0; m < a.nmat; m++) {
+        t += (a.rows[m] + 15u) / 16u;
+        a.tile_end[m] = t;
+    }
+}
+
+}  // namespace vbs
