@@ -163,7 +163,25 @@ def cpu_baseline(host, weights, xs, max_seconds=20.0):
             cpu = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), "")
     except OSError:
         pass
+    # beside it: the oracle's row-parallel restatement on every host core
+    # (bit-identical outputs to the single-threaded path, tested)
+    orc_all = Oracle()
+    ncores = min(16, os.cpu_count() or 1)
+    ys_all = [np.zeros(r, np.float32) for _, r, _ in LAYER_SET]
+    p_all, t0 = 0, time.perf_counter()
+    while True:
+        for i, (_, r, c) in enumerate(LAYER_SET):
+            orc_all.linear(V.Q4_K, weights[i], xs[i], c, r, y=ys_all[i], threads=ncores)
+        p_all += 1
+        t_all = time.perf_counter() - t0
+        if t_all >= 2.0 or p_all >= 256:
+            break
+    all_cores = {"value": round(p_all * sum(algo_bytes(V.Q4_K, r, c) for _, r, c in LAYER_SET)
+                                / t_all / 1e9, 4), "unit": "GB/s", "cores": ncores,
+                 "kind": "port", "sample": f"{p_all} pass(es) of the same layer set in "
+                                           f"{t_all:.1f} s, oracle row-parallel linear"}
     return {"value": round(nbytes / t_total / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": kind,
+            "all_cores": all_cores,
             "sample": f"{passes} pass(es) of the Q4_K 7B layer matvec set "
                       f"({len(LAYER_SET)} matvecs, {nbytes / passes / 1e6:.1f} MB each pass) in "
                       f"{t_total:.1f} s, single thread, dispatch_linear_tile of the "
