@@ -308,6 +308,8 @@ def load_host() -> C.CDLL:
     lib.vbs_synth_normal_f16.argtypes = [C.c_uint64, C.c_uint64, C.c_uint64, C.c_size_t, C.c_float,
                                          C.c_void_p, C.c_int]
     lib.vbs_synth_tokens.argtypes = [C.c_uint64, C.c_uint64, C.c_uint32, C.c_size_t, C.c_void_p]
+    lib.vbs_synth_write_gguf.restype = C.c_int
+    lib.vbs_synth_write_gguf.argtypes = [C.c_char_p, C.c_void_p, C.c_char_p, C.c_size_t]
     lib.vbs_decode_create.restype = C.c_void_p
     lib.vbs_decode_create.argtypes = [C.c_void_p, C.c_void_p, C.c_char_p, C.c_size_t]
     lib.vbs_decode_destroy.argtypes = [C.c_void_p]
@@ -433,6 +435,42 @@ class SynthModel:
         c = self.cfg
         n = c["n_layers"] * n_pos * c["n_kv_heads"] * c["head_dim"]
         return (synth_normal_f16(host, n, self.seed, 10), synth_normal_f16(host, n, self.seed, 11))
+
+
+class SynthGgufCfg(C.Structure):
+    """vbs_synth_gguf_cfg_t (host/vbs_synth.h)."""
+    _fields_ = [("n_layers", C.c_uint32), ("hidden", C.c_uint32), ("ffn", C.c_uint32),
+                ("n_heads", C.c_uint32), ("n_kv_heads", C.c_uint32), ("head_dim", C.c_uint32),
+                ("vocab", C.c_uint32), ("context_length", C.c_uint32),
+                ("rope_theta", C.c_float), ("rms_eps", C.c_float),
+                ("embd_type", C.c_int), ("head_type", C.c_int), ("wtype", C.c_int * 7),
+                ("seed", C.c_uint64), ("nthreads", C.c_int)]
+
+
+def write_gguf(host, path: str, model: "SynthModel", context_length: int = 0):
+    """The synthetic model `model` (same generator streams, same bytes) as a
+    GGUF v3 file for the reference loader (src/vbs_gguf.c)."""
+    c = model.cfg
+    write_gguf_geometry(host, path, n_layers=c["n_layers"], hidden=c["hidden"], ffn=c["ffn"],
+                        n_heads=c["n_heads"], n_kv_heads=c["n_kv_heads"],
+                        head_dim=c["head_dim"], vocab=c["vocab"],
+                        context_length=context_length or c["max_ctx"], mix=model.mix,
+                        seed=model.seed, theta=c["theta"], eps=c["eps"])
+
+
+def write_gguf_geometry(host, path: str, *, n_layers, hidden, ffn, n_heads, n_kv_heads,
+                        head_dim, vocab, context_length, mix=None, seed=1234, theta=10000.0,
+                        eps=1e-5):
+    """A synthetic model of any size written straight to disk: the bytes
+    SynthModel would hold for the same arguments, generated and written in
+    32 MiB pieces, so 7B- and 70B-shaped files need no host copy."""
+    mix = dict(Q4_K_M_MIX if mix is None else mix)
+    cfg = SynthGgufCfg(n_layers, hidden, ffn, n_heads, n_kv_heads, head_dim, vocab,
+                       context_length, theta, eps, mix["embd"], mix["head"],
+                       (C.c_int * 7)(*[mix[r] for r in MAT_ROLES]), seed, _THREADS)
+    err = C.create_string_buffer(512)
+    if not host.vbs_synth_write_gguf(path.encode(), C.addressof(cfg), err, 512):
+        raise RuntimeError(f"vbs_synth_write_gguf: {err.value.decode()}")
 
 
 class Decoder:
