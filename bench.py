@@ -25,9 +25,13 @@ included, so it is an upper bound on the kernel time rocprof reports).
 cpu_baseline: the reference's own CPU backend (oracle/_ref, compiled from the
 reference sources) -- or, where that file is absent, the oracle restatement --
 runs dispatch_linear_tile over the same layer set, single-threaded as the
-reference is, for a bounded number of passes.
+reference is, for a bounded number of passes. Its `beside` entries time the
+reference CPU path on the host copies of the other GPU entries (configs 1 and
+3, the hot-table call).
 
-Also reported: decode tokens/sec of the synthetic 7B Q4_K_M model (config 4:
+Also reported: configs 1-3 on the GPU; the CPU hot-kernel table
+(vbs_hotpath.h ABI v1) as a device kernel and as the host-pointer module;
+decode tokens/sec of the synthetic 7B Q4_K_M model (config 4:
 32 layers, KV prefilled to 2048, greedy from position 2048) through the graph
 decoder (vbs_gfx950_decoder_*), and through the g_vbs_hip_backend ops table
 with one dispatch per bridge call.
@@ -121,7 +125,40 @@ class Hip:
         self.h.hipGraphDestroy(graph[0])
 
 
-def cpu_baseline(host, weights, xs, max_seconds=20.0):
+def cpu_hot_q8_0_s(w, xq, qd, rows, cols, max_seconds=1.0):
+    """Seconds per call of the reference's built-in hot-table matvec_q8_0
+    (src/vbs_hotpath.c compiled into oracle/_ref), or None if not built."""
+    from oracle_lib import REF_HOT_SO, reference_hot
+    if not os.path.exists(REF_HOT_SO):
+        return None
+    tb = reference_hot().vbs_hot_builtin().contents
+    y = np.empty(rows, np.float32)
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < max_seconds:
+        tb.matvec_q8_0(w.ctypes.data, rows, cols, xq.ctypes.data, qd.ctypes.data, y.ctypes.data)
+        n += 1
+    return (time.perf_counter() - t0) / n
+
+
+def cpu_beside(work):
+    """The reference CPU path on the host copies of the other GPU entries
+    (single-threaded, as the reference is)."""
+    out = {}
+    for name, job in work.items():
+        if job[0] == "linear":
+            _, t, w, rows, cols, b, budget = job
+            sec, kind = cpu_linear_s(t, w, rows, cols, max_seconds=budget)
+        else:
+            _, w, xq, qd, rows, cols, b, budget = job
+            sec, kind = cpu_hot_q8_0_s(w, xq, qd, rows, cols, budget), "reference"
+            if sec is None:
+                continue
+        out[name] = {"ms_per_matvec": round(1e3 * sec, 3), "GB_per_s": round(b / sec / 1e9, 4),
+                     "kind": kind, "cores": 1}
+    return out
+
+
+def cpu_baseline(host, weights, xs, max_seconds=20.0, beside=None):
     """Single-threaded reference CPU linear over the layer set (bounded)."""
     from oracle_lib import REF_SO, Oracle
     kind, passes, t_total, nbytes = "port", 0, 0.0, 0
@@ -181,7 +218,7 @@ def cpu_baseline(host, weights, xs, max_seconds=20.0):
                  "kind": "port", "sample": f"{p_all} pass(es) of the same layer set in "
                                            f"{t_all:.1f} s, oracle row-parallel linear"}
     return {"value": round(nbytes / t_total / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": kind,
-            "all_cores": all_cores,
+            "all_cores": all_cores, "beside": cpu_beside(beside or {}),
             "sample": f"{passes} pass(es) of the Q4_K 7B layer matvec set "
                       f"({len(LAYER_SET)} matvecs, {nbytes / passes / 1e6:.1f} MB each pass) in "
                       f"{t_total:.1f} s, single thread, dispatch_linear_tile of the "
@@ -318,22 +355,18 @@ def cpu_linear_s(t, w, rows, cols, max_seconds=2.0):
     return (time.perf_counter() - t0) / n, kind
 
 
-def bench_configs(dev, host, with_cpu=True):
-    """The other BASELINE configs at batch 1 on the GPU (and the reference CPU
-    path beside configs 1 and 3): config 1 Q4_0 4096x4096; config 2's Q8_0
-    repetition of the 7B layer set; config 3's Q6_K 32000x4096 head and the
-    64-id Q6_K embedding gather."""
+def bench_configs(dev, host, cpu_work=None):
+    """The other BASELINE configs at batch 1 on the GPU: config 1 Q4_0
+    4096x4096; config 2's Q8_0 repetition of the 7B layer set; config 3's
+    Q6_K 32000x4096 head and the 64-id Q6_K embedding gather. The host copies
+    of configs 1 and 3 go into `cpu_work` for the CPU baseline leg."""
     out = {}
     us, w = gpu_matvec_us(dev, host, V.Q4_0, 4096, 4096)
     b = algo_bytes(V.Q4_0, 4096, 4096)
     c1 = {"workload": "Q4_0 4096x4096 matvec, batch 1 (config 1)", "us_per_matvec": round(us, 3),
           "GB_per_s": round(b / us / 1e3, 1), "roofline_frac": round(b / us / 1e3 / PEAK_HBM_GBS, 4)}
-    if with_cpu:
-        sec, kind = cpu_linear_s(V.Q4_0, w, 4096, 4096)
-        c1["cpu_ms_per_matvec"] = round(1e3 * sec, 2)
-        c1["cpu_GB_per_s"] = round(b / sec / 1e9, 4)
-        c1["cpu_kind"] = kind
-        c1["cpu_cores"] = 1
+    if cpu_work is not None:
+        cpu_work["config1_q4_0"] = ("linear", V.Q4_0, w, 4096, 4096, b, 2.0)
     out["config1_q4_0"] = c1
     tot_us, tot_b, per = 0.0, 0, {}
     for name, r, c in LAYER_SET:
@@ -351,12 +384,8 @@ def bench_configs(dev, host, with_cpu=True):
     b = algo_bytes(V.Q6_K, 32000, 4096)
     c3 = {"workload": "Q6_K 32000x4096 output head, batch 1 (config 3)", "us_per_matvec": round(us, 3),
           "GB_per_s": round(b / us / 1e3, 1), "roofline_frac": round(b / us / 1e3 / PEAK_HBM_GBS, 4)}
-    if with_cpu:
-        sec, kind = cpu_linear_s(V.Q6_K, w, 32000, 4096, max_seconds=1.0)
-        c3["cpu_ms_per_matvec"] = round(1e3 * sec, 1)
-        c3["cpu_GB_per_s"] = round(b / sec / 1e9, 4)
-        c3["cpu_kind"] = kind
-        c3["cpu_cores"] = 1
+    if cpu_work is not None:
+        cpu_work["config3_q6_k_head"] = ("linear", V.Q6_K, w, 32000, 4096, b, 1.0)
     # 64 random ids gathered from the same table in one launch
     hip, stream = Hip(), dev.stream()
     table = dev.upload(w)
@@ -381,6 +410,59 @@ def bench_configs(dev, host, with_cpu=True):
     c3["gather_64_ids_us"] = round(gus, 3)
     c3["gather_GB_per_s"] = round(gb / gus / 1e3, 1)
     out["config3_q6_k_head"] = c3
+    return out
+
+
+def bench_hot_table(dev, host, cpu_work=None, rows=4096, cols=4096):
+    """The CPU hot-kernel table (the reference's vbs_hotpath.h ABI v1) on the
+    device: Q8_0 rows x cols (the CPU model's Q8_0 weights, Q8 activations).
+    Reports the device kernel on resident buffers (distinct copies rotated,
+    one graph, HIP events) and the host-pointer module call as the
+    reference's CPU model would make it (weights over PCIe every call); the
+    same call goes into `cpu_work` for the reference's built-in CPU kernel."""
+    hip, stream = Hip(), dev.stream()
+    w0 = V.synth_matrix(host, V.Q8_0, rows, cols, SEED, 500)
+    # the Q8 activations the CPU model hands over, made by vbs_gfx950_quantize_q8
+    px = dev.upload(V.synth_normal(host, cols, SEED, 501))
+    pq, pd, ps = dev.alloc(cols), dev.alloc(cols // 8), dev.alloc(cols // 8)
+    dev.quantize_q8(px, cols, pq, pd, ps)
+    xq, qd = dev.download(pq, cols, np.int8), dev.download(pd, cols // 32, np.float32)
+    for p in (px, ps):
+        dev.free(p)
+    ncopy = max(2, int(400e6 // w0.nbytes) + 1)
+    ws = [dev.upload(w0 if k == 0 else V.synth_matrix(host, V.Q8_0, rows, cols, SEED + k, 500))
+          for k in range(ncopy)]
+    py = dev.alloc(rows * 4)
+    per = 4
+    g = hip.capture(stream, lambda: [dev.hot_matvec(V.Q8_0, ws[i % ncopy], rows, cols, pq, pd, 0,
+                                                    py) for i in range(per * ncopy)])
+    hip.launch(g, stream)
+    dev.sync()
+    e0, e1 = hip.event(), hip.event()
+    hip.record(e0, stream)
+    for _ in range(3):
+        hip.launch(g, stream)
+    hip.record(e1, stream)
+    dev.sync()
+    us = hip.elapsed_ms(e0, e1) * 1e3 / (3 * per * ncopy)
+    hip.destroy(g)
+    for p in ws + [pq, pd, py]:
+        dev.free(p)
+    b = rows * V.row_bytes(V.Q8_0, cols) + cols + 4 * (cols // 32) + 4 * rows
+    out = {"workload": f"hot-table matvec_q8_0 {rows}x{cols} (Q8 activations)",
+           "device_us_per_matvec": round(us, 3), "device_GB_per_s": round(b / us / 1e3, 1),
+           "device_roofline_frac": round(b / us / 1e3 / PEAK_HBM_GBS, 4)}
+    mod = V.HotModule()
+    mod.matvec(V.Q8_0, w0, rows, cols, xq=xq, qd=qd)
+    n, t0 = 0, time.perf_counter()
+    while n < 20:
+        mod.matvec(V.Q8_0, w0, rows, cols, xq=xq, qd=qd)
+        n += 1
+    sec = (time.perf_counter() - t0) / n
+    out["module_ms_per_call_pcie_inclusive"] = round(1e3 * sec, 3)
+    out["module_GB_per_s_pcie_inclusive"] = round(b / sec / 1e9, 2)
+    if cpu_work is not None:
+        cpu_work["hot_table_q8_0"] = ("hot_q8_0", w0, xq, qd, rows, cols, b, 1.0)
     return out
 
 
@@ -608,8 +690,10 @@ def main():
         "gpu_event_ms_per_step": round(r["gpu_ms"] / a.steps, 4),
         "graph_replay_equals_eager": r["replay_equals_eager"],
     }
+    cpu_work = None if a.no_cpu else {}
     if not a.no_configs:
-        out["configs"] = bench_configs(dev, host, with_cpu=not a.no_cpu)
+        out["configs"] = bench_configs(dev, host, cpu_work)
+        out["hot_table"] = bench_hot_table(dev, host, cpu_work)
     if not a.no_batch8:
         out["batch8_70b"] = bench_batch8_70b(dev, host)
     if not a.no_decode and a.decode_geometry == "70b":
@@ -623,7 +707,7 @@ def main():
                                              n_layers=80, ctx=8192, n_dispatch_tokens=4,
                                              batch=8, batch_tokens=16)
     if not a.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(host, r["weights_host"], r["xs_host"])
+        out["cpu_baseline"] = cpu_baseline(host, r["weights_host"], r["xs_host"], beside=cpu_work)
     print(json.dumps(out))
 
 

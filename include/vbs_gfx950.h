@@ -196,6 +196,26 @@ int vbs_gfx950_bdecoder_greedy_eager(void *handle, const uint32_t *tokens0, cons
                                      uint32_t n, uint32_t *tokens, float *margins);
 int vbs_gfx950_bdecoder_destroy(void *handle);
 
+/* ---- CPU hot-kernel table on the device (parity adapter) --------------------
+ * The arithmetic of the reference's CPU hot-kernel ABI v1
+ * (include/vbs_hotpath.h:38-57, src/hotkernels/vbs_hot_ref_impl.h:49-129) on
+ * device buffers, bit-identical to its built-in table; the host-pointer
+ * module over these is lib/libvbs_hot_gfx950.so (host/vbs_hot_gfx950.c). */
+
+/* Q8 activations of x as the CPU model forms them (src/vbs_cpu.c:166-182):
+ * per 32-element block d = amax/127, xq = round(x/d) clamped to +-127,
+ * qd = f16(d), qsum = f16(sum(xq)*d) (round to nearest even). cols must be a
+ * multiple of 32; x is assumed finite (the CPU model screens non-finite
+ * inputs first, src/vbs_cpu.c:185-190). All buffers 4-byte aligned. */
+int vbs_gfx950_quantize_q8(const float *x, uint32_t cols, int8_t *xq, float *qd, float *qsum);
+
+/* y[r] = the hot table's matvec of row r (replaces matvec_q8_0 / q4_0 / q4_1 /
+ * f32 / f16 of vbs_hot_kernels_t). type Q8_0, Q4_0, Q4_1: act = xq (int8),
+ * qd and (Q4_1) qsum as vbs_gfx950_quantize_q8 makes them, cols a multiple
+ * of 32; type F32, F16: act = x (f32). w packed row-major. */
+int vbs_gfx950_hot_matvec(int type, const void *w, uint32_t rows, uint32_t cols, const void *act,
+                          const float *qd, const float *qsum, float *y);
+
 #ifdef __cplusplus
 }
 #endif

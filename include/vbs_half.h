@@ -63,4 +63,27 @@ VBS_HD uint16_t vbs_f2h(float f) {
     return (uint16_t)(sign | ((uint32_t)he << 10) | (r >> 13));
 }
 
+/* f32 -> f16 as the CPU model's Q8 activation scales are rounded
+ * (src/vbs_cpu.c:74-93): round to nearest even everywhere, subnormals
+ * included; |f| < 2^-25 (and a tie at 2^-25) gives signed zero; |f| >= 2^16,
+ * infinities and NaNs give signed infinity. For finite inputs this is the
+ * IEEE conversion. */
+VBS_HD uint16_t vbs_f2h_rne(float f) {
+    uint32_t u = vbs_float_to_bits(f);
+    uint32_t sign = (u >> 16) & 0x8000u, a = u & 0x7FFFFFFFu;
+    if (a >= 0x47800000u) return (uint16_t)(sign | 0x7C00u);
+    if (a >= 0x38800000u) { /* normal half: rebias 127 -> 15, keep 10 bits */
+        uint32_t h = (a >> 13) - (112u << 10), rest = a & 0x1FFFu;
+        h += (rest > 0x1000u || (rest == 0x1000u && (h & 1u))) ? 1u : 0u;
+        return (uint16_t)(sign | h); /* a carry out of the mantissa is exact */
+    }
+    if (a < 0x33000000u) return (uint16_t)sign;
+    /* subnormal half: value / 2^-24 = significand >> (-e - 1), e in [-25, -15] */
+    uint32_t sig = (a & 0x7FFFFFu) | 0x800000u;
+    uint32_t sh = 126u - (a >> 23);
+    uint32_t h = sig >> sh, rest = sig & ((1u << sh) - 1u), half = 1u << (sh - 1u);
+    h += (rest > half || (rest == half && (h & 1u))) ? 1u : 0u;
+    return (uint16_t)(sign | h);
+}
+
 #endif

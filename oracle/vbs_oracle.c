@@ -500,3 +500,109 @@ int vbs_oracle_forward_token(const vbs_oracle_model_t *m, uint32_t token, uint32
     free(buf);
     return ok;
 }
+
+/* ------------------------------------------------------------------ */
+/* CPU hot-kernel table (ABI v1) and its activation quantiser          */
+/* ------------------------------------------------------------------ */
+
+/* src/vbs_cpu.c:74-93: round to nearest even in the normal and the
+ * subnormal range; exponent above 15 (inf, NaN included) -> infinity;
+ * exponent below -25 -> zero. */
+uint16_t vbs_oracle_f32_to_f16_rne(float f) {
+    uint32_t u = f2u(f);
+    uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+    int e = (int)((u >> 23) & 255u) - 127;
+    uint32_t man = u & 0x7FFFFFu;
+    if (e > 15) return (uint16_t)(sign | 0x7C00u);
+    if (e >= -14) {
+        uint32_t h = (uint32_t)(e + 15) << 10 | man >> 13;
+        uint32_t low = man & 0x1FFFu;
+        if (low > 0x1000u || (low == 0x1000u && (h & 1u))) h++;
+        return (uint16_t)(sign | h);
+    }
+    if (e < -25) return sign;
+    man |= 0x800000u;
+    int sh = -e - 1;
+    uint32_t h = man >> sh, low = man & ((1u << sh) - 1u), half = 1u << (sh - 1);
+    if (low > half || (low == half && (h & 1u))) h++;
+    return (uint16_t)(sign | h);
+}
+
+/* src/vbs_cpu.c:166-182. Per 32-element block: d = amax/127, q =
+ * roundf(x * (1/d)) clamped to +-127 (all zero when d == 0), qd = f16(d),
+ * qsum = f16(sum(q) * d), both through the RNE conversion above. */
+void vbs_oracle_quantize_q8(const float *x, uint32_t cols, int8_t *xq, float *qd, float *qsum) {
+    for (uint32_t b = 0; b < cols / 32; b++) {
+        const float *xb = x + (size_t)b * 32;
+        float amax = 0.0f;
+        for (int i = 0; i < 32; i++)
+            if (fabsf(xb[i]) > amax) amax = fabsf(xb[i]);
+        float d = amax / 127.0f;
+        float inv = d != 0.0f ? 1.0f / d : 0.0f;
+        int total = 0;
+        for (int i = 0; i < 32; i++) {
+            int q = (int)roundf(xb[i] * inv);
+            if (q < -127) q = -127;
+            if (q > 127) q = 127;
+            xq[(size_t)b * 32 + i] = (int8_t)q;
+            total += q;
+        }
+        qd[b] = vbs_oracle_f16_to_f32(vbs_oracle_f32_to_f16_rne(d));
+        qsum[b] = vbs_oracle_f16_to_f32(vbs_oracle_f32_to_f16_rne((float)total * d));
+    }
+}
+
+/* src/hotkernels/vbs_hot_ref_impl.h:49-129. Quantised rows: one float sum
+ * per row, per block `sum += f16(d) * qd[b] * (float)dot` with an exact
+ * int dot (Q4_0 nibbles - 8, Q4_1 nibbles plus `sum += f16(m) * qsum[b]`).
+ * F32 / F16 rows: `sum += w[i] * x[i]` element by element. */
+int vbs_oracle_hot_matvec(int type, const void *wv, uint32_t rows, uint32_t cols,
+                          const int8_t *xq, const float *qd, const float *qsum, const float *x,
+                          float *y) {
+    const uint8_t *w = (const uint8_t *)wv;
+    size_t nb = cols / 32;
+    for (uint32_t r = 0; r < rows; r++) {
+        float sum = 0.0f;
+        switch (type) {
+            case T_Q8_0:
+                for (size_t b = 0; b < nb; b++) {
+                    const uint8_t *blk = w + ((size_t)r * nb + b) * 34;
+                    int dot = 0;
+                    for (int i = 0; i < 32; i++) dot += (int)(int8_t)blk[2 + i] * (int)xq[b * 32 + i];
+                    sum += vbs_oracle_f16_to_f32(rd16(blk)) * qd[b] * (float)dot;
+                }
+                break;
+            case T_Q4_0:
+            case T_Q4_1: {
+                size_t bs = type == T_Q4_0 ? 18 : 20, qo = type == T_Q4_0 ? 2 : 4;
+                int off = type == T_Q4_0 ? 8 : 0;
+                for (size_t b = 0; b < nb; b++) {
+                    const uint8_t *blk = w + ((size_t)r * nb + b) * bs;
+                    int dot = 0;
+                    for (int i = 0; i < 16; i++) {
+                        dot += ((int)(blk[qo + i] & 15u) - off) * (int)xq[b * 32 + i];
+                        dot += ((int)(blk[qo + i] >> 4) - off) * (int)xq[b * 32 + 16 + i];
+                    }
+                    sum += vbs_oracle_f16_to_f32(rd16(blk)) * qd[b] * (float)dot;
+                    if (type == T_Q4_1) sum += vbs_oracle_f16_to_f32(rd16(blk + 2)) * qsum[b];
+                }
+                break;
+            }
+            case T_F32:
+                for (size_t i = 0; i < cols; i++) {
+                    float wi;
+                    memcpy(&wi, w + ((size_t)r * cols + i) * 4, 4);
+                    sum += wi * x[i];
+                }
+                break;
+            case T_F16:
+                for (size_t i = 0; i < cols; i++)
+                    sum += vbs_oracle_f16_to_f32(rd16(w + ((size_t)r * cols + i) * 2)) * x[i];
+                break;
+            default:
+                return 0;
+        }
+        y[r] = sum;
+    }
+    return 1;
+}

@@ -89,6 +89,18 @@ typedef struct {
 int vbs_oracle_forward_token(const vbs_oracle_model_t *m, uint32_t token, uint32_t pos,
                              float *logits, int nthreads);
 
+/* ---- CPU hot-kernel table, ABI v1 (include/vbs_hotpath.h:38-57) ----
+ * The Q8-activation matvecs of src/hotkernels/vbs_hot_ref_impl.h:49-129 and
+ * the CPU model's activation quantiser (src/vbs_cpu.c:166-182) with its
+ * round-to-nearest-even f16 conversion (src/vbs_cpu.c:74-93). */
+uint16_t vbs_oracle_f32_to_f16_rne(float f);
+void vbs_oracle_quantize_q8(const float *x, uint32_t cols, int8_t *xq, float *qd, float *qsum);
+/* type 8 (Q8_0), 2 (Q4_0), 3 (Q4_1): xq/qd (+ qsum for Q4_1) are the
+ * activations; type 0 (F32), 1 (F16): x is. Returns 0 for other types. */
+int vbs_oracle_hot_matvec(int type, const void *w, uint32_t rows, uint32_t cols,
+                          const int8_t *xq, const float *qd, const float *qsum, const float *x,
+                          float *y);
+
 #ifdef __cplusplus
 }
 #endif

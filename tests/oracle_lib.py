@@ -14,6 +14,7 @@ import numpy as np
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 ORACLE_SO = os.path.join(ROOT, "oracle", "liboracle.so")
 REF_SO = os.path.join(ROOT, "oracle", "_ref", "libvbs_ref.so")
+REF_HOT_SO = os.path.join(ROOT, "oracle", "_ref", "libvbs_hotpath_ref.so")
 
 _P, _U32, _I, _F = C.c_void_p, C.c_uint32, C.c_int, C.c_float
 F16FN = C.CFUNCTYPE(C.c_uint16, C.c_float)
@@ -57,6 +58,9 @@ class Oracle:
             "cache_store": (None, [_P, _P, _P, _P, _U32, _U32, _U32, _U32]),
             "attention": (None, [_P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, _U32, _F]),
             "forward_token": (_I, [_P, _U32, _U32, _P, _I]),
+            "f32_to_f16_rne": (C.c_uint16, [C.c_float]),
+            "quantize_q8": (None, [_P, _U32, _P, _P, _P]),
+            "hot_matvec": (_I, [_I, _P, _U32, _U32, _P, _P, _P, _P, _P]),
         }
         for k, (r, a) in sig.items():
             f = getattr(L, "vbs_oracle_" + k)
@@ -117,6 +121,20 @@ class Oracle:
     def f32_to_f16(self, a: np.ndarray) -> np.ndarray:
         return np.array([self._f32_to_f16(float(v)) for v in a.ravel()], np.uint16).reshape(a.shape)
 
+    def quantize_q8(self, x: np.ndarray):
+        """(xq int8[cols], qd f32[cols/32], qsum f32[cols/32])."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        nb = x.size // 32
+        xq, qd, qs = np.empty(nb * 32, np.int8), np.empty(nb, np.float32), np.empty(nb, np.float32)
+        self._quantize_q8(_ptr(x), x.size, _ptr(xq), _ptr(qd), _ptr(qs))
+        return xq, qd, qs
+
+    def hot_matvec(self, t, w, rows, cols, xq=None, qd=None, qsum=None, x=None):
+        y = np.empty(rows, np.float32)
+        assert self._hot_matvec(t, _ptr(np.ascontiguousarray(w)), rows, cols, _ptr(xq), _ptr(qd),
+                                _ptr(qsum), _ptr(x), _ptr(y))
+        return y
+
     def model(self, synth_model, kc: np.ndarray, vc: np.ndarray) -> OracleModel:
         s = synth_model.decode_struct()
         m = OracleModel()
@@ -139,4 +157,30 @@ def reference_cpu():
     lib.vbs_f16_to_f32.restype, lib.vbs_f16_to_f32.argtypes = C.c_float, [C.c_uint16]
     lib.vbs_f32_to_f16.restype, lib.vbs_f32_to_f16.argtypes = C.c_uint16, [C.c_float]
     lib.vbs_dequant_block.restype, lib.vbs_dequant_block.argtypes = C.c_int, [C.c_int, _P, _P]
+    return lib
+
+
+def reference_hot():
+    """The reference's CPU hot-kernel table and module loader
+    (src/vbs_hotpath.c), or None if not built here."""
+    if not os.path.exists(REF_HOT_SO):
+        return None
+    import vbs_gfx950 as V
+    lib = C.CDLL(REF_HOT_SO)
+    lib.vbs_hot_builtin.restype = C.POINTER(V.HotKernels)
+    lib.vbs_hot_current.restype = C.POINTER(V.HotKernels)
+    lib.vbs_hot_load.restype, lib.vbs_hot_load.argtypes = C.c_bool, [C.c_char_p, C.c_char_p, C.c_size_t]
+    lib.vbs_hot_rollback.restype, lib.vbs_hot_rollback.argtypes = C.c_bool, [C.c_char_p, C.c_size_t]
+    lib.vbs_hot_current_name.restype = C.c_char_p
+    lib.vbs_hot_current_path.restype = C.c_char_p
+    lib.vbs_hot_has_rollback.restype = C.c_bool
+    sz = C.c_size_t
+    for n in ("q8_0", "q4_0"):
+        f = getattr(lib, "vbs_hot_matvec_" + n)
+        f.restype, f.argtypes = None, [_P, sz, sz, _P, _P, _P]
+    lib.vbs_hot_matvec_q4_1.restype = None
+    lib.vbs_hot_matvec_q4_1.argtypes = [_P, sz, sz, _P, _P, _P, _P]
+    for n in ("f32", "f16"):
+        f = getattr(lib, "vbs_hot_matvec_" + n)
+        f.restype, f.argtypes = None, [_P, sz, sz, _P, _P]
     return lib

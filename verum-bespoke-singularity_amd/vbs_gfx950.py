@@ -24,6 +24,7 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 LIB_DIR = os.path.join(PKG_DIR, "lib")
 DEVICE_LIB = os.path.join(LIB_DIR, "libvbs_gfx950.so")
 HOST_LIB = os.path.join(LIB_DIR, "libvbs_backend_gfx950.so")
+HOT_LIB = os.path.join(LIB_DIR, "libvbs_hot_gfx950.so")
 
 # GGUF type ids (include/vbs_abi.h, reference include/vbs_gguf.h:13-48)
 F32, F16, Q4_0, Q4_1, Q8_0, Q8_K, Q4_K, Q5_K, Q6_K, LNS8 = 0, 1, 2, 3, 8, 15, 12, 13, 14, 40
@@ -92,6 +93,8 @@ _DEVICE_SIGS = {
     "bdecoder_greedy": (_I, [_P, _P, _P, _U32, _P, _P]),
     "bdecoder_greedy_eager": (_I, [_P, _P, _P, _U32, _P, _P]),
     "bdecoder_destroy": (_I, [_P]),
+    "quantize_q8": (_I, [_P, _U32, _P, _P, _P]),
+    "hot_matvec": (_I, [_I, _P, _U32, _U32, _P, _P, _P, _P]),
 }
 
 DEVICE_SYMBOLS = ["vbs_gfx950_" + k for k in _DEVICE_SIGS]
@@ -166,6 +169,13 @@ class DeviceLib:
 
     def embed(self, t, w, token, out, dim):
         self.check(self._embed(t, w, token, out, dim), "embed")
+
+    def quantize_q8(self, x, cols, xq, qd, qsum):
+        self.check(self._quantize_q8(x, cols, xq, qd, qsum), "quantize_q8")
+
+    def hot_matvec(self, t, w, rows, cols, act, qd, qsum, y):
+        self.check(self._hot_matvec(t, w, rows, cols, act, qd or None, qsum or None, y),
+                   "hot_matvec")
 
     def dequant_rows(self, t, w, ids, n_rows, dim, out):
         self.check(self._dequant_rows(t, w, ids or None, n_rows, dim, out), "dequant_rows")
@@ -471,6 +481,55 @@ def write_gguf_geometry(host, path: str, *, n_layers, hidden, ffn, n_heads, n_kv
     err = C.create_string_buffer(512)
     if not host.vbs_synth_write_gguf(path.encode(), C.addressof(cfg), err, 512):
         raise RuntimeError(f"vbs_synth_write_gguf: {err.value.decode()}")
+
+
+class HotKernels(C.Structure):
+    """vbs_hot_kernels_t (include/vbs_hot_abi.h; the reference's vbs_hotpath.h:43-57)."""
+    _fields_ = [("abi_version", C.c_uint32), ("name", C.c_char_p),
+                ("matvec_q8_0", C.CFUNCTYPE(None, _P, _SZ, _SZ, _P, _P, _P)),
+                ("matvec_q4_0", C.CFUNCTYPE(None, _P, _SZ, _SZ, _P, _P, _P)),
+                ("matvec_q4_1", C.CFUNCTYPE(None, _P, _SZ, _SZ, _P, _P, _P, _P)),
+                ("matvec_f32", C.CFUNCTYPE(None, _P, _SZ, _SZ, _P, _P)),
+                ("matvec_f16", C.CFUNCTYPE(None, _P, _SZ, _SZ, _P, _P))]
+
+
+class HotModule:
+    """lib/libvbs_hot_gfx950.so: the CPU hot-kernel module (ABI v1) whose
+    matvecs run on the device. Host numpy arrays in, host y out."""
+
+    def __init__(self, path: str = HOT_LIB):
+        self.path = path
+        self.lib = _cdll(path)
+        self.lib.vbs_hot_abi_version.restype = C.c_uint32
+        self.lib.vbs_hot_kernels.restype = C.POINTER(HotKernels)
+        self.lib.vbs_hot_gfx950_last_error.restype = C.c_char_p
+        self.table = self.lib.vbs_hot_kernels().contents
+
+    def abi_version(self) -> int:
+        return self.lib.vbs_hot_abi_version()
+
+    def last_error(self) -> str:
+        return self.lib.vbs_hot_gfx950_last_error().decode()
+
+    def matvec(self, t: int, w: np.ndarray, rows: int, cols: int, xq=None, qd=None, qsum=None,
+               x=None) -> np.ndarray:
+        y = np.empty(rows, np.float32)
+        w = np.ascontiguousarray(w)
+        tb = self.table
+        if t == Q8_0:
+            tb.matvec_q8_0(w.ctypes.data, rows, cols, xq.ctypes.data, qd.ctypes.data, y.ctypes.data)
+        elif t == Q4_0:
+            tb.matvec_q4_0(w.ctypes.data, rows, cols, xq.ctypes.data, qd.ctypes.data, y.ctypes.data)
+        elif t == Q4_1:
+            tb.matvec_q4_1(w.ctypes.data, rows, cols, xq.ctypes.data, qd.ctypes.data,
+                           qsum.ctypes.data, y.ctypes.data)
+        elif t == F32:
+            tb.matvec_f32(w.ctypes.data, rows, cols, x.ctypes.data, y.ctypes.data)
+        elif t == F16:
+            tb.matvec_f16(w.ctypes.data, rows, cols, x.ctypes.data, y.ctypes.data)
+        else:
+            raise ValueError(f"type {t} is not in the hot-kernel table")
+        return y
 
 
 class Decoder:
