@@ -466,6 +466,79 @@ def bench_hot_table(dev, host, cpu_work=None, rows=4096, cols=4096):
     return out
 
 
+def bench_weight_streaming(dev, host, upload_mib=1024, window_mib=64, passes=3):
+    """Weight residency and streaming: copy_to_device of pageable host memory
+    (how the fabric registers a model) and of pinned memory, and the 7B
+    Q4_K layer set streamed through g_vbs_hip_backend's convention B the way
+    the slice executor does it (src/vbs_slice_executor.c:42-107): two shared
+    stage windows and two private device windows, each tile copied into a
+    stage window's host_ptr, then dispatch_linear_tile(priv, stage, ...)."""
+    out = {}
+    n = upload_mib << 20
+    src = np.ones(n, np.uint8)
+    p = dev.alloc(n)
+    dev.write(p, src)
+    t0 = time.perf_counter()
+    for _ in range(passes):
+        dev.write(p, src)
+    out["upload_pageable_GB_per_s"] = round(passes * n / (time.perf_counter() - t0) / 1e9, 2)
+    h = dev._host_alloc(n)
+    if h:
+        C.memmove(h, src.ctypes.data, n)
+        dev.check(dev._copy_h2d(p, h, n), "copy_h2d")
+        t0 = time.perf_counter()
+        for _ in range(passes):
+            dev.check(dev._copy_h2d(p, h, n), "copy_h2d")
+        out["upload_pinned_GB_per_s"] = round(passes * n / (time.perf_counter() - t0) / 1e9, 2)
+        dev._host_free(h)
+    dev.free(p)
+    del src
+    be = V.gfx950_backend()
+    if not be.init():
+        raise V.GpuError(f"shim init: {be.last_error()}")
+    d = be.device()
+    win = window_mib << 20
+    stage = [be.alloc(win, True) for _ in range(2)]
+    priv = [be.alloc(win, False) for _ in range(2)]
+    pipe = be.ops.compile_linear_pipeline(d, V.Q4_K, None, 0)
+    mats = [(V.synth_matrix(host, V.Q4_K, r, c, SEED, 600 + i), r, c)
+            for i, (_, r, c) in enumerate(LAYER_SET)]
+    xb = be.upload(V.synth_normal(host, FF, SEED, 601))
+    yb = be.upload(np.zeros(FF, np.float32))
+
+    def one_pass():
+        turn = 0
+        for w, r, c in mats:
+            rb = w.shape[1]
+            rows_per = max(1, win // rb)
+            for rs in range(0, r, rows_per):
+                rc = min(rows_per, r - rs)
+                slot = turn & 1
+                turn += 1
+                C.memmove(stage[slot].contents.host_ptr, w[rs:rs + rc].ctypes.data, rc * rb)
+                ok = be.ops.dispatch_linear_tile(d, pipe, priv[slot], stage[slot], rc * rb, xb,
+                                                 yb, c, rc, 0, rs, False)
+                if not ok:
+                    raise V.GpuError(f"staged tile: {be.last_error()}")
+        be.ops.synchronize_device(d)
+
+    one_pass()
+    t0 = time.perf_counter()
+    for _ in range(passes):
+        one_pass()
+    sec = (time.perf_counter() - t0) / passes
+    wbytes = sum(w.nbytes for w, _, _ in mats)
+    out["staged_layer_set_ms"] = round(1e3 * sec, 3)
+    out["staged_layer_set_GB_per_s"] = round(wbytes / sec / 1e9, 2)
+    out["staged_window_MiB"] = window_mib
+    out["workload"] = ("copy_to_device of %d MiB (pageable, pinned); Q4_K 7B layer set (%.1f MB) "
+                       "streamed through convention B in %d MiB windows" %
+                       (upload_mib, wbytes / 1e6, window_mib))
+    for b in stage + priv + [xb, yb]:
+        be.ops.free_buffer(b)
+    return out
+
+
 # Llama-70B layer matvec set (config 5) in the Q4_K_M mix: Q, K, V, O, gate, up, down
 LAYER_SET_70B = [("q", V.Q4_K, 8192, 8192), ("k", V.Q4_K, 1024, 8192), ("v", V.Q4_K, 1024, 8192),
                  ("o", V.Q4_K, 8192, 8192), ("gate", V.Q4_K, 28672, 8192),
@@ -694,6 +767,7 @@ def main():
     if not a.no_configs:
         out["configs"] = bench_configs(dev, host, cpu_work)
         out["hot_table"] = bench_hot_table(dev, host, cpu_work)
+        out["weight_streaming"] = bench_weight_streaming(dev, host)
     if not a.no_batch8:
         out["batch8_70b"] = bench_batch8_70b(dev, host)
     if not a.no_decode and a.decode_geometry == "70b":
