@@ -15,6 +15,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 ORACLE_SO = os.path.join(ROOT, "oracle", "liboracle.so")
 REF_SO = os.path.join(ROOT, "oracle", "_ref", "libvbs_ref.so")
 REF_HOT_SO = os.path.join(ROOT, "oracle", "_ref", "libvbs_hotpath_ref.so")
+REF_CPU_SO = os.path.join(ROOT, "oracle", "_ref", "libvbs_cpu_ref.so")
 
 _P, _U32, _I, _F = C.c_void_p, C.c_uint32, C.c_int, C.c_float
 F16FN = C.CFUNCTYPE(C.c_uint16, C.c_float)
@@ -184,3 +185,43 @@ def reference_hot():
         f = getattr(lib, "vbs_hot_matvec_" + n)
         f.restype, f.argtypes = None, [_P, sz, sz, _P, _P]
     return lib
+
+
+def reference_cpu_model():
+    """The reference's model-level CPU inference (src/vbs_cpu.c and the hot
+    table it calls through), or None if not built here."""
+    if not os.path.exists(REF_CPU_SO):
+        return None
+    lib = C.CDLL(REF_CPU_SO)
+    sz = C.c_size_t
+    lib.vbs_cpu_open.restype, lib.vbs_cpu_open.argtypes = _P, [C.c_char_p, sz, C.c_char_p, sz]
+    lib.vbs_cpu_close.restype, lib.vbs_cpu_close.argtypes = None, [_P]
+    lib.vbs_cpu_reset.restype, lib.vbs_cpu_reset.argtypes = None, [_P]
+    lib.vbs_cpu_step.restype = C.c_bool
+    lib.vbs_cpu_step.argtypes = [_P, C.c_uint32, C.c_char_p, sz]
+    lib.vbs_cpu_logits.restype, lib.vbs_cpu_logits.argtypes = C.POINTER(C.c_float), [_P]
+    lib.vbs_cpu_vocab_size.restype, lib.vbs_cpu_vocab_size.argtypes = sz, [_P]
+    lib.vbs_cpu_context_capacity.restype, lib.vbs_cpu_context_capacity.argtypes = sz, [_P]
+    lib.vbs_hot_load.restype, lib.vbs_hot_load.argtypes = C.c_bool, [C.c_char_p, C.c_char_p, sz]
+    lib.vbs_hot_rollback.restype, lib.vbs_hot_rollback.argtypes = C.c_bool, [C.c_char_p, sz]
+    lib.vbs_hot_current_name.restype = C.c_char_p
+    return lib
+
+
+def cpu_model_logits(lib, path, tokens, capacity=64):
+    """Logits after each token of `tokens` (positions 0, 1, ...) from the
+    reference CPU model opened on the GGUF file `path`."""
+    err = C.create_string_buffer(512)
+    m = lib.vbs_cpu_open(str(path).encode(), capacity, err, 512)
+    if not m:
+        raise RuntimeError(f"vbs_cpu_open: {err.value.decode()}")
+    try:
+        vocab = lib.vbs_cpu_vocab_size(m)
+        out = []
+        for t in tokens:
+            if not lib.vbs_cpu_step(m, t, err, 512):
+                raise RuntimeError(f"vbs_cpu_step: {err.value.decode()}")
+            out.append(np.ctypeslib.as_array(lib.vbs_cpu_logits(m), (vocab,)).copy())
+        return out
+    finally:
+        lib.vbs_cpu_close(m)

@@ -12,7 +12,8 @@ import numpy as np
 import pytest
 
 import vbs_gfx950 as V
-from oracle_lib import REF_HOT_SO, Oracle, reference_hot
+from oracle_lib import (REF_CPU_SO, REF_HOT_SO, Oracle, cpu_model_logits, reference_cpu_model,
+                        reference_hot)
 
 pytestmark = pytest.mark.gpu
 
@@ -191,3 +192,30 @@ def test_through_the_reference_loader_and_wrappers(dev, host, orc):
             assert same_bits(got, want), V.TYPE_NAMES[t]
     finally:
         assert ref.vbs_hot_rollback(err, 256), err.value
+
+
+@pytest.mark.skipif(not os.path.exists(REF_CPU_SO), reason="oracle/_ref CPU model not built")
+@pytest.mark.parametrize("mix", [None, {"q": V.Q8_0, "k": V.Q4_0, "v": V.Q4_1, "o": V.F16,
+                                        "gate": V.Q4_0, "up": V.Q8_0, "down": V.Q4_1,
+                                        "embd": V.Q8_0, "head": V.F32}],
+                         ids=["q4_k_m", "every_table_type"])
+def test_reference_cpu_model_on_the_module(dev, host, tmp_path, mix):
+    """The reference's own CPU model (src/vbs_cpu.c) with its hot table
+    swapped for lib/libvbs_hot_gfx950.so by its own loader: every step's
+    logits equal the built-in table's bit for bit."""
+    model = V.SynthModel(host, n_layers=2, hidden=256, ffn=512, n_heads=4, n_kv_heads=2,
+                         head_dim=64, vocab=512, max_ctx=64, seed=33, mix=mix)
+    path = tmp_path / "tiny.gguf"
+    V.write_gguf(host, str(path), model, context_length=2176)
+    lib = reference_cpu_model()
+    tokens = [1, 17, 300, 5, 42, 7]
+    want = cpu_model_logits(lib, path, tokens)
+    err = C.create_string_buffer(256)
+    assert lib.vbs_hot_load(V.HOT_LIB.encode(), err, 256), err.value
+    try:
+        assert lib.vbs_hot_current_name() == b"gfx950-hip"
+        got = cpu_model_logits(lib, path, tokens)
+    finally:
+        assert lib.vbs_hot_rollback(err, 256), err.value
+    for step, (a, b) in enumerate(zip(got, want)):
+        assert same_bits(a, b), step
