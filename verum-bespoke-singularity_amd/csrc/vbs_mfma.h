@@ -711,9 +711,12 @@ static hipError_t launch_ks(const MvArgs &a, const MvPlan &p, uint32_t wgs, hipS
         if (p.nw <= 8u) VBS_MV(6, 512);
         VBS_MV(6, 1024);
     }
-    // rows of 65-112 blocks (70B down: 112), one tile per workgroup
-    if constexpr ((EPI == E_STORE || EPI == E_ACC) && TPW == 1 && !NORM)
+    // rows of 65-112 blocks (70B down: 112), one tile per workgroup; rows of
+    // at most 16 blocks over few tiles, one block per wave
+    if constexpr ((EPI == E_STORE || EPI == E_ACC) && TPW == 1 && !NORM) {
         if (p.ks == 14u) VBS_MV(14, 512);
+        if (p.ks == 1u) VBS_MV(1, 1024);
+    }
     VBS_MV(8, 1024);
 #undef VBS_MV
 }
@@ -725,6 +728,17 @@ static hipError_t launch_plan(const MvArgs &a, hipStream_t s) {
     if (p.ks == 14u && a.tile_end[a.nmat - 1u] >= 1024u) {  // (several tiles: keep eight)
         p.ks = 8u;
         p.nw = (a.cols / 256u + 7u) / 8u;
+    }
+    // Unfused launches of rows of at most 16 blocks over few tiles: one block
+    // per wave on up to sixteen waves (measured 2-12% faster at up to 384
+    // tiles for every type, and for Q6_K up to 688; slower for the other types
+    // at 688 tiles)
+    if constexpr ((EPI == E_STORE || EPI == E_ACC) && !NORM) {
+        const uint32_t nblk = a.cols / 256u;
+        if (nblk <= 16u && (total <= 384u || (T::BYTES == 210u && total < 1024u))) {
+            p.ks = 1u;
+            p.nw = nblk;
+        }
     }
     if (p.nw > 16u) return hipErrorNotSupported;
     if constexpr (EPI == E_SILU)  // a gate tile and the same up tile
