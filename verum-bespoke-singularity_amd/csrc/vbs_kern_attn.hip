@@ -606,16 +606,28 @@ __global__ __launch_bounds__(kMergeThreads) void k_attn_merge(const float *__res
         const uint32_t c = s + k * ns;
         av[k] = (s < ns && c < n_chunks) ? ph[(uint64_t)c * (hd + 2u) + 2u + d] : 0.f;
     }
-    // this thread's chunks' (m, l): c = t, t + 256, ...
-    float M = -INFINITY;
-    for (uint32_t c = t; c < n_chunks; c += kMergeThreads) M = fmaxf(M, ph[(uint64_t)c * (hd + 2u)]);
+    // this thread's chunks' (m, l): c = t, t + kMergeThreads, ...; the first
+    // pair is loaded with the acc values, before any reduction
+    float m0 = -INFINITY, l0 = 0.f;
+    if (t < n_chunks) {
+        m0 = ph[(uint64_t)t * (hd + 2u)];
+        l0 = ph[(uint64_t)t * (hd + 2u) + 1u];
+    }
+    float M = m0;
+    for (uint32_t c = t + kMergeThreads; c < n_chunks; c += kMergeThreads)
+        M = fmaxf(M, ph[(uint64_t)c * (hd + 2u)]);
     M = wave_max(M);
     if (lane == 0) red[wave] = M;
     __syncthreads();
     M = red[0];
     for (uint32_t i = 1; i < NW; i++) M = fmaxf(M, red[i]);
     float L = 0.f;
-    for (uint32_t c = t; c < n_chunks; c += kMergeThreads) {
+    if (t < n_chunks) {
+        const float wc = m0 == -INFINITY ? 0.f : fast_exp(__fsub_rn(m0, M));
+        w[t] = wc;
+        L = fmaf(l0, wc, L);
+    }
+    for (uint32_t c = t + kMergeThreads; c < n_chunks; c += kMergeThreads) {
         const float *pc = ph + (uint64_t)c * (hd + 2u);
         const float mc = pc[0], wc = mc == -INFINITY ? 0.f : fast_exp(__fsub_rn(mc, M));
         w[c] = wc;
