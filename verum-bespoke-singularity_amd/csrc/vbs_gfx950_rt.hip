@@ -10,6 +10,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
 #include <thread>
 
 #include "vbs_dev_common.h"
@@ -218,10 +219,11 @@ struct Staging {
     void *buf[2] = {nullptr, nullptr};
     hipEvent_t done[2] = {nullptr, nullptr};
     bool tried = false, ok = false;
+    std::mutex lock;  // one staged copy at a time (the buffers are shared)
 };
 static Staging g_stage;
 
-static bool staging_ready() {
+static bool staging_ready() {  // called with g_stage.lock held
     if (g_stage.tried) return g_stage.ok;
     g_stage.tried = true;
     for (int i = 0; i < 2; i++) {
@@ -293,9 +295,10 @@ static int copy_sync(void *dst, const void *src, size_t bytes, hipMemcpyKind kin
 }
 
 int vbs_gfx950_copy_h2d(void *dst, const void *src, size_t bytes) {
-    if (bytes >= kStagedMin && dst && src && ready_or_fail() && !host_pinned(src) &&
-        staging_ready())
-        return copy_h2d_staged(dst, src, bytes);
+    if (bytes >= kStagedMin && dst && src && ready_or_fail() && !host_pinned(src)) {
+        std::lock_guard<std::mutex> hold(g_stage.lock);
+        if (staging_ready()) return copy_h2d_staged(dst, src, bytes);
+    }
     return copy_sync(dst, src, bytes, hipMemcpyHostToDevice, "copy_h2d");
 }
 int vbs_gfx950_copy_d2h(void *dst, const void *src, size_t bytes) {
