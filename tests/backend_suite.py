@@ -173,3 +173,61 @@ def run_suite(be: V.Backend, orc, host, seed=12345):
     p = be.ops.compile_linear_pipeline(dev, V.Q8_K, err, 256)
     res.append(("linear Q8_K refused", not p and len(err.value) > 0, 0))
     return res
+
+
+def bind_linear_batch(be: V.Backend):
+    """vbs_hip_dispatch_linear_batch / vbs_hip_linear_batch_version of the
+    shim (include/vbs_hip_batch.h)."""
+    lib = be.lib
+    lib.vbs_hip_linear_batch_version.restype = C.c_uint32
+    f = lib.vbs_hip_dispatch_linear_batch
+    f.restype = C.c_bool
+    f.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p,
+                  C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32]
+    return f
+
+
+def run_linear_batch(be: V.Backend, orc, host, shapes, batches, seed=777):
+    """The batched extension through the shim against `batch` independent
+    oracle linear tiles (src/vbs_host_math.h:223-267): (name, ok) pairs,
+    including the argument refusals."""
+    fn = bind_linear_batch(be)
+    res = [("linear batch version", be.lib.vbs_hip_linear_batch_version() == 1)]
+    dev = be.device()
+    for t, rows, cols in shapes:
+        pipe = be.ops.compile_linear_pipeline(dev, t, None, 0)
+        w = V.synth_matrix(host, t, rows, cols, seed, 5)
+        bw = be.upload(w)
+        for batch in batches:
+            xs, ys = cols + 32, rows + 7  # strides beyond the shape
+            x = np.zeros(batch * xs, np.float32)
+            for b in range(batch):
+                x[b * xs:b * xs + cols] = V.synth_normal(host, cols, seed + b, 6)
+            bx, by = be.upload(x), be.upload(np.full(batch * ys, -1.0, np.float32))
+            ok = fn(dev, pipe, bw, bx, xs, by, ys, cols, rows, batch)
+            y = be.download(by, batch * ys, np.float32) if ok else None
+            good = bool(ok)
+            for b in range(batch if ok else 0):
+                want = orc.linear(t, w, x[b * xs:b * xs + cols], cols, rows)
+                got = y[b * ys:b * ys + rows]
+                rel = np.linalg.norm(got.astype(np.float64) - want) / max(
+                    np.linalg.norm(want.astype(np.float64)), 1e-30)
+                good &= bool(rel <= 1e-5) and bool(np.all(y[b * ys + rows:(b + 1) * ys] == -1.0))
+            res.append((f"linear batch {V.TYPE_NAMES[t]} {rows}x{cols} b{batch}", good))
+            be.ops.free_buffer(bx)
+            be.ops.free_buffer(by)
+        # refusals: nothing launched, a reason left
+        bx = be.upload(np.zeros(cols * 17, np.float32))
+        by = be.upload(np.zeros(rows * 17, np.float32))
+        for name, args in [("batch 0", (cols, rows, 0)), ("batch 17", (cols, rows, 17)),
+                           ("x stride", (cols - 1, rows, 2)), ("y stride", (cols, rows - 1, 2))]:
+            xs_, ys_, b_ = args
+            res.append((f"linear batch refuses {name}",
+                        not fn(dev, pipe, bw, bx, xs_, by, ys_, cols, rows, b_)
+                        and "linear batch" in be.last_error()))
+        small = be.upload(np.zeros(cols, np.float32))
+        res.append(("linear batch refuses a short x",
+                    not fn(dev, pipe, bw, small, cols, by, rows, cols, rows, 2)))
+        for b_ in (bw, bx, by, small):
+            be.ops.free_buffer(b_)
+    return res

@@ -18,7 +18,7 @@ import numpy as np
 import pytest
 
 import vbs_gfx950 as V
-from backend_suite import run_suite
+from backend_suite import run_linear_batch, run_suite
 from oracle_lib import Oracle
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -78,6 +78,12 @@ def test_shim_exports_the_reference_symbols():
         assert getattr(ops, name), name
     assert not ops.launch_persistent_kernel  # must be NULL (include/vbs_backend.h:94-98)
     assert hasattr(lib, "vbs_hip_last_error")
+    # the batched extension's entry points (include/vbs_hip_batch.h)
+    hdr = open(os.path.join(ROOT, "include", "vbs_hip_batch.h")).read()
+    declared = sorted(set(re.findall(r"\b(vbs_hip_\w+)\s*\(", hdr)) - {"vbs_hip_last_error"})
+    assert declared == ["vbs_hip_dispatch_linear_batch", "vbs_hip_linear_batch_version"]
+    for name in declared:
+        assert hasattr(lib, name), name
 
 
 @pytest.mark.skipif(not os.path.isdir("/root/reference/include"),
@@ -173,6 +179,28 @@ def test_shim_marshalling_rejects_malformed_arguments(tmpdir_mod):
     err = C.create_string_buffer(128)
     assert not be.ops.compile_primitive_pipeline(be.device(), V.OP_STATE_SPACE, err, 128)
     assert b"no primitive kernel" in err.value
+
+
+def test_linear_batch_extension_through_shim_on_host_mock(tmpdir_mod, host):
+    """The batched-linear extension (include/vbs_hip_batch.h) through the
+    shim over the host mock: B vectors equal B oracle tiles; bad batches,
+    strides and short buffers are refused."""
+    so = build_mock(tmpdir_mod, "mock_batch.so")
+    be, ok = fresh_shim(tmpdir_mod, so)
+    assert ok, be.last_error()
+    res = run_linear_batch(be, Oracle(), host, [(V.Q4_K, 40, 512), (V.Q8_0, 19, 256),
+                                                (V.F16, 9, 96)], [1, 3, 16])
+    bad = [r[0] for r in res if not r[1]]
+    assert not bad, bad
+
+
+@pytest.mark.gpu
+def test_linear_batch_extension_on_gfx950(backend, host):
+    res = run_linear_batch(backend, Oracle(), host,
+                           [(V.Q4_K, 4096, 4096), (V.Q6_K, 4096, 11008), (V.Q8_0, 1000, 4096),
+                            (V.Q4_0, 300, 512), (V.F32, 77, 1000)], [1, 5, 8, 16])
+    bad = [r[0] for r in res if not r[1]]
+    assert not bad, bad
 
 
 @pytest.mark.gpu

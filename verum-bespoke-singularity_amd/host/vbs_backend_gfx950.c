@@ -20,6 +20,7 @@
 #endif
 #include "vbs_abi.h"
 #include "vbs_gfx950.h"
+#include "vbs_hip_batch.h"
 
 #include <dlfcn.h>
 #include <stdarg.h>
@@ -47,6 +48,8 @@ typedef struct {
     int (*linear_supported)(int);
     int (*linear)(int, const void *, const float *, float *, uint32_t, uint32_t, uint32_t,
                   uint32_t, int);
+    int (*linear_batch)(int, const void *, const float *, uint32_t, float *, uint32_t, uint32_t,
+                        uint32_t, uint32_t);
     int (*embed)(int, const void *, uint32_t, float *, uint32_t);
     int (*rms_norm)(const float *, const float *, float *, uint32_t, float);
     int (*rope)(float *, uint32_t, uint32_t, uint32_t, float);
@@ -143,6 +146,7 @@ static bool gfx950_init(void) {
     BIND(synchronize, "vbs_gfx950_synchronize");
     BIND(linear_supported, "vbs_gfx950_linear_supported");
     BIND(linear, "vbs_gfx950_linear");
+    BIND(linear_batch, "vbs_gfx950_linear_batch");
     BIND(embed, "vbs_gfx950_embed");
     BIND(rms_norm, "vbs_gfx950_rms_norm");
     BIND(rope, "vbs_gfx950_rope");
@@ -355,6 +359,48 @@ static bool gfx950_dispatch_linear_tile(vbs_device_t *dev, void *pipeline, vbs_b
                       (float *)out->internal_handle, cols, rows, col_off, row_off,
                       accumulate ? 1 : 0))
         return lib_fail("linear tile");
+    return true;
+}
+
+/* ---- batched linear (extension, include/vbs_hip_batch.h) ------------------ */
+
+uint32_t vbs_hip_linear_batch_version(void) { return VBS_HIP_LINEAR_BATCH_VERSION; }
+
+bool vbs_hip_dispatch_linear_batch(vbs_device_t *dev, void *pipeline, vbs_buffer_t *w,
+                                   vbs_buffer_t *x, uint32_t x_stride, vbs_buffer_t *y,
+                                   uint32_t y_stride, uint32_t cols, uint32_t rows,
+                                   uint32_t batch) {
+    (void)dev;
+    gfx950_linear_pipe_t *p = (gfx950_linear_pipe_t *)pipeline;
+    if (!g_ready) {
+        set_err("linear batch before a successful init");
+        return false;
+    }
+    if (!p || !w || !x || !y || !w->internal_handle || !x->internal_handle || !y->internal_handle) {
+        set_err("linear batch: null pipeline or buffer");
+        return false;
+    }
+    if (batch == 0 || batch > 16u) {
+        set_err("linear batch: batch %u outside 1..16", batch);
+        return false;
+    }
+    if (x_stride < cols || y_stride < rows) {
+        set_err("linear batch: strides %u/%u below cols/rows %u/%u", x_stride, y_stride, cols,
+                rows);
+        return false;
+    }
+    const uint64_t need_w = packed_row_bytes(p->type, cols) * rows;
+    const uint64_t need_x = 4ull * ((uint64_t)(batch - 1u) * x_stride + cols);
+    const uint64_t need_y = 4ull * ((uint64_t)(batch - 1u) * y_stride + rows);
+    if ((w->size && w->size < need_w) || (x->size && x->size < need_x) ||
+        (y->size && y->size < need_y)) {
+        set_err("linear batch: a buffer is smaller than %s %ux%u at batch %u needs",
+                type_name(p->type), rows, cols, batch);
+        return false;
+    }
+    if (!g_lib.linear_batch((int)p->type, w->internal_handle, (const float *)x->internal_handle,
+                            x_stride, (float *)y->internal_handle, y_stride, cols, rows, batch))
+        return lib_fail("linear batch");
     return true;
 }
 
