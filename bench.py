@@ -59,9 +59,9 @@ SEED = 424242
 # HBM bytes per launch of the dominant kernel (11008x4096 Q4_K) from two
 # rocprofv3 --pmc passes over this program (FETCH_SIZE, WRITE_SIZE in KiB per
 # dispatch), each scaled by what the counter reads for a 256 MiB device copy
-# in the same run: FETCH_SIZE x 1.9997 + WRITE_SIZE x 1.0000
+# in the same run: FETCH_SIZE x (262144 / 131092.9) + WRITE_SIZE x 1.0000
 # (profiles/q4k_matvec_7b_layer_set.md).
-TRAFFIC_BYTES = round((12481.7 * 1.9997 + 43.0) * 1024)
+TRAFFIC_BYTES = round((12483.8 * 262144 / 131092.9 + 43.0) * 1024)
 
 
 def algo_bytes(t, rows, cols):
