@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the gfx950 quantized decode hot path (one MI355X).
 
-Metric (BASELINE.json): Q4_K matvec HBM GB/s (% of peak); decode tokens/sec
+Metric: Q4_K matvec HBM GB/s (% of peak); decode tokens/sec
 at 7B Q4_K_M, 1 GPU.
 
 A step is one pass of the Llama-7B layer matvec set at batch 1 (config 2):
@@ -360,7 +360,7 @@ def cpu_linear_s(t, w, rows, cols, max_seconds=2.0):
 
 
 def bench_configs(dev, host, cpu_work=None):
-    """The other BASELINE configs at batch 1 on the GPU: config 1 Q4_0
+    """The other benchmark configurations at batch 1 on the GPU: config 1 Q4_0
     4096x4096; config 2's Q8_0 repetition of the 7B layer set; config 3's
     Q6_K 32000x4096 head and the 64-id Q6_K embedding gather. The host copies
     of configs 1 and 3 go into `cpu_work` for the CPU baseline leg."""
@@ -709,7 +709,7 @@ def main():
     ap.add_argument("--decode-tokens", type=int, default=128)
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-configs", action="store_true",
-                    help="skip BASELINE configs 1, 2 (Q8_0) and 3")
+                    help="skip configs 1 (Q4_0), 2 (the Q8_0 layer set) and 3 (the Q6_K head)")
     ap.add_argument("--no-batch8", action="store_true",
                     help="skip the config 5 batch-8 layer matvec set")
     ap.add_argument("--decode-70b-tokens", type=int, default=32,

@@ -178,7 +178,7 @@ int vbs_gfx950_decoder_destroy(void *handle);
 
 /* ---- batched decode (extension) --------------------------------------------
  * The decode step above for `batch` (1..8) independent sequences over one copy
- * of the weights (BASELINE config 5 at batch 8): each sequence has its own
+ * of the weights (the Llama-70B case at batch 8): each sequence has its own
  * caches, m->kc / m->vc + b * kv_seq_stride elements (the model's layout per
  * sequence), its own token and position. Every matrix must be Q4_K or Q6_K
  * (the batched matrix-core kernels; q/k/v and gate/up pairwise of one type).

@@ -102,7 +102,7 @@ def test_batch_non_finite_vector(dev, host, oracle, mem, t):
                                          (V.Q6_K, 32000, 8192)],
                          ids=["q4k_70b_gate", "q6k_70b_down", "q6k_70b_head"])
 def test_batch_70b_shapes(dev, host, oracle, mem, t, rows, cols):
-    """BASELINE config 5 shapes at batch 8, the oracle on the first and last
+    """The Llama-70B layer shapes at batch 8, the oracle on the first and last
     192 rows (the packed rows are sliced out of the full matrix)."""
     w = V.synth_matrix(host, t, rows, cols, SEED, 75)
     X = vectors(host, 8, cols, 120)
