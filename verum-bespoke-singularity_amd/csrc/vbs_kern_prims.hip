@@ -61,12 +61,25 @@ __global__ __launch_bounds__(1024) void k_rms_norm(const float *__restrict__ in,
     __shared__ float s_scale;
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const uint32_t blocks = (n + 255u) / 256u;
+    // the wave's first block (x and the norm weights) is requested up front and
+    // kept in registers for the output; later blocks (n > 4096) are re-read
+    float xr[4] = {0.f, 0.f, 0.f, 0.f}, wr[4] = {0.f, 0.f, 0.f, 0.f};
+    if (wave < blocks) {
+#pragma unroll
+        for (uint32_t k = 0; k < 4u; k++) {
+            const uint32_t i = 256u * wave + 4u * lane + k;
+            if (i < n) {
+                xr[k] = in[i];
+                wr[k] = w[i];
+            }
+        }
+    }
     for (uint32_t b = wave; b < blocks; b += 16u) {
         double ss = 0.0;
         for (uint32_t k = 0; k < 4u; k++) {
             const uint32_t i = 256u * b + 4u * lane + k;
             if (i < n) {
-                const double v = in[i];
+                const double v = b == wave ? xr[k] : in[i];
                 ss = fma(v, v, ss);  // v*v is exact in double, so fusing changes nothing
             }
         }
@@ -81,8 +94,17 @@ __global__ __launch_bounds__(1024) void k_rms_norm(const float *__restrict__ in,
         s_scale = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, eps)));
     }
     __syncthreads();
-    float sc = s_scale;
-    for (uint32_t i = threadIdx.x; i < n; i += 1024u) out[i] = __fmul_rn(__fmul_rn(in[i], sc), w[i]);
+    const float sc = s_scale;
+    for (uint32_t b = wave; b < blocks; b += 16u) {
+#pragma unroll
+        for (uint32_t k = 0; k < 4u; k++) {
+            const uint32_t i = 256u * b + 4u * lane + k;
+            if (i < n) {
+                const float x = b == wave ? xr[k] : in[i], wv = b == wave ? wr[k] : w[i];
+                out[i] = __fmul_rn(__fmul_rn(x, sc), wv);
+            }
+        }
+    }
 }
 
 hipError_t launch_rms_norm(const float *in, const float *w, float *out, uint32_t n, float eps,
