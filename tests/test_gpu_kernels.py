@@ -100,6 +100,43 @@ def test_linear_full_size(dev, host, oracle, mem, t, rows, cols):
     assert rel_l2(got, want) <= LIN_TOL
 
 
+@pytest.mark.parametrize("t,rows,cols", [(V.Q4_K, 28672, 8192), (V.Q6_K, 8192, 28672),
+                                         (V.Q4_K, 11008, 4096), (V.Q8_0, 4096, 11008)],
+                         ids=["q4k_28672x8192", "q6k_8192x28672", "q4k_11008x4096",
+                              "q80_4096x11008"])
+def test_linear_full_size_properties(dev, host, oracle, mem, t, rows, cols):
+    """Size-independent properties over every row of the full matrices, where
+    the oracle checks a sample of rows. x travels as three balanced digit
+    planes of rint(x 2^(22-e)) per 32-element sub-block, so scaling x by a
+    power of two leaves every digit unchanged and scales every row value
+    exactly. Negating x negates each integer dot, but the digits of -X are not
+    the negated digits of X (they range over -128..127), and the two low
+    planes are added in int32 before one conversion to float: that sum stays
+    below 2^24, hence exact, only for Q4_K's 32 x 15-bounded groups, so the
+    negation is exact for Q4_K and within a few ulps otherwise. A row's value
+    depends only on its own bytes, so reversing the rows reverses y exactly.
+    The sampled rows match the oracle."""
+    w = V.synth_matrix(host, t, rows, cols, SEED, 41)
+    x = synth_x(host, cols, stream=42)
+    pw, pr = mem.up(w), mem.up(np.ascontiguousarray(w[::-1]))
+    ys = {}
+    for name, xv, wp in (("x", x, pw), ("4x", 4.0 * x, pw), ("-x", -x, pw), ("rev", x, pr)):
+        px, py = mem.up(xv.astype(np.float32)), mem.zeros(rows)
+        dev.linear(t, wp, px, py, cols, rows)
+        ys[name] = dev.download(py, rows, np.float32)
+    y = ys["x"]
+    assert np.all(np.isfinite(y))
+    assert np.array_equal(ys["4x"], 4.0 * y)
+    if t == V.Q4_K:
+        assert np.array_equal(ys["-x"].view(np.uint32), (-y).view(np.uint32))
+    else:
+        assert rel_l2(-ys["-x"], y) <= 1e-6
+    assert np.array_equal(ys["rev"].view(np.uint32), y[::-1].view(np.uint32))
+    sample = np.r_[0:96, rows // 2 - 48:rows // 2 + 48, rows - 96:rows]
+    want = oracle.linear(t, w[sample], x, cols, len(sample), threads=16)
+    assert rel_l2(y[sample], want) <= LIN_TOL
+
+
 @pytest.mark.parametrize("t", [V.Q4_K, V.Q6_K, V.Q8_0, V.Q4_0], ids=lambda t: V.TYPE_NAMES[t])
 def test_linear_activation_edge_cases(dev, host, oracle, mem, t):
     """x with all-zero sub-blocks, 1e4 outliers, subnormal-scale blocks and
