@@ -259,7 +259,13 @@ static void parallel_copy(void *dst, const void *src, size_t n) {
     unsigned used = 0;
     for (unsigned t = 1; t < nt && per * t < n; t++) {
         const size_t off = per * t, len = n - off < per ? n - off : per;
-        th[used++] = std::thread([=] { memcpy((char *)dst + off, (const char *)src + off, len); });
+        try {
+            th[used] = std::thread([=] { memcpy((char *)dst + off, (const char *)src + off, len); });
+            used++;
+        } catch (...) {  // no thread to spare: copy the rest here (no exception leaves the C ABI)
+            memcpy((char *)dst + off, (const char *)src + off, n - off);
+            break;
+        }
     }
     memcpy(dst, src, n < per ? n : per);
     for (unsigned i = 0; i < used; i++) th[i].join();
