@@ -79,11 +79,24 @@ __global__ __launch_bounds__(256) void k_xprep_b(const float *x, const float *x2
     const float *xt = x + (uint64_t)t * xs;
     float sc = 1.0f;
     if (MODE == XP_NORM) {
-        for (uint32_t k = wave; k < nblk; k += 4u) {
-            const float4 a = *reinterpret_cast<const f4u *>(xt + 256u * k + 4u * lane);
-            const float v[4] = {a.x, a.y, a.z, a.w};
-            const double ss = block_sumsq(v);
-            if (lane == 0) bsum[k] = ss;
+        // the wave's blocks wave, wave + 4, ...: eight requested at a time,
+        // then their sums of squares
+        for (uint32_t k0 = wave; k0 < nblk; k0 += 32u) {
+            float4 a[8];
+#pragma unroll
+            for (uint32_t j = 0; j < 8u; j++) {
+                const uint32_t k = min(k0 + 4u * j, nblk - 1u);
+                a[j] = *reinterpret_cast<const f4u *>(xt + 256u * k + 4u * lane);
+            }
+#pragma unroll
+            for (uint32_t j = 0; j < 8u; j++) {
+                const uint32_t k = k0 + 4u * j;
+                if (k < nblk) {  // (wave-uniform)
+                    const float v[4] = {a[j].x, a[j].y, a[j].z, a[j].w};
+                    const double ss = block_sumsq(v);
+                    if (lane == 0) bsum[k] = ss;
+                }
+            }
         }
         __syncthreads();
         double tot = 0.0;
