@@ -5,9 +5,9 @@
 
 The file holds the tensors in the decode order of the reference's graph
 (src/vbs_graph.c:61-96) and the llama.* metadata its profiler and CPU model
-require (src/vbs_profiler.c:328-352, src/vbs_cpu.c:396-476), so the
-reference's own tools open it (`verum-slice --inspect` / `--benchmark <file>`,
-src/main.c:810-860).
+require (src/vbs_profiler.c:328-352, src/vbs_cpu.c:396-476): the reference's
+GGUF parser and CPU model open it, and its `verum-slice --inspect` /
+`--benchmark <file>` modes (src/main.c:810-860) read the same keys.
 Weights are the same synthetic bytes the decode tests and bench.py use for
 the same seed; nothing is held in memory beyond a 32 MiB piece.
 """
