@@ -151,3 +151,16 @@ def test_7b_geometry_file_from_the_command_line(tmp_path):
         assert os.path.getsize(path) == end
     finally:
         lib.vbs_gguf_close(m)
+
+
+def test_writer_refuses_bad_geometry(host, tmp_path):
+    """Empty dimensions and rows that are not whole blocks of their type are
+    refused with the reason, and no file is left half-written as success."""
+    base = dict(n_layers=1, hidden=256, ffn=512, n_heads=4, n_kv_heads=2, head_dim=64, vocab=512,
+                context_length=2176)
+    with pytest.raises(RuntimeError, match="empty model dimension"):
+        V.write_gguf_geometry(host, str(tmp_path / "a.gguf"), **dict(base, n_layers=0))
+    with pytest.raises(RuntimeError, match="does not fit"):
+        V.write_gguf_geometry(host, str(tmp_path / "b.gguf"), **dict(base, hidden=100))
+    with pytest.raises(RuntimeError):
+        V.write_gguf_geometry(host, str(tmp_path / "missing_dir" / "c.gguf"), **base)

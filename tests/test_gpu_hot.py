@@ -219,3 +219,20 @@ def test_reference_cpu_model_on_the_module(dev, host, tmp_path, mix):
         assert lib.vbs_hot_rollback(err, 256), err.value
     for step, (a, b) in enumerate(zip(got, want)):
         assert same_bits(a, b), step
+
+
+def test_module_accepts_host_arrays_at_odd_addresses(dev, host, orc, hot_module):
+    """The table passes host pointers with no alignment promise (blocks are
+    2-byte fields at any address); the module stages them byte for byte."""
+    rows, cols = 37, 4096
+    w = V.synth_matrix(host, V.Q4_0, rows, cols, 97, 1)
+    x = V.synth_normal(host, cols, 98, 2)
+    xq, qd, _ = orc.quantize_q8(x)
+    raw = np.empty(w.nbytes + 1, np.uint8)
+    wo = raw[1:].reshape(w.shape)
+    wo[...] = w
+    xr = np.empty(cols + 3, np.int8)
+    xo = xr[3:]
+    xo[...] = xq
+    got = hot_module.matvec(V.Q4_0, wo, rows, cols, xq=xo, qd=qd)
+    assert same_bits(got, orc.hot_matvec(V.Q4_0, w, rows, cols, xq, qd))
