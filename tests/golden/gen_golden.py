@@ -268,7 +268,22 @@ def gen_tiny(host):
                    "last_logits_f32_bits": [int(v) for v in last.view(np.uint32)]}, fh)
 
 
+def write_provenance():
+    """Where the fixtures were computed: the libm behind the reference's powf,
+    cosf, sinf and expf (RoPE angles, softmax weights in prims.npz and
+    tiny_model.json) and the compiler that built the reference sources."""
+    import platform
+    import subprocess
+    cc = subprocess.run(["gcc", "--version"], capture_output=True, text=True).stdout.splitlines()
+    info = {"libc": " ".join(platform.libc_ver()), "cc": cc[0] if cc else "",
+            "machine": platform.machine(),
+            "reference_build": "gcc -std=c11 -O3 -D_GNU_SOURCE (oracle/Makefile, ref target)"}
+    with open(os.path.join(HERE, "provenance.json"), "w") as f:
+        json.dump(info, f, indent=1)
+
+
 if __name__ == "__main__":
+    write_provenance()
     lib = ref_lib()
     host = V.load_host()
     gen_dequant(lib, host)
