@@ -78,6 +78,20 @@ __host__ __device__ inline XqLayout xq_layout(uint32_t cols) {
     return L;
 }
 
+// Where the digits of one 256-element block live: plane p at base + p *
+// pstride, its xs (8 float2) and xs16 (16 floats), and a 16-byte zero pad.
+// Launches with one tile per workgroup give each wave a single slot that it
+// refills for every block (a wave's blocks are used once, in turn), so their
+// LDS does not grow with the row length; the others keep [3][cols] planes.
+struct DigitView {
+    uint8_t *base;
+    uint32_t pstride;
+    float2 *xs;
+    float *xs16;
+    const uint8_t *zero;
+};
+constexpr uint32_t kSlotBytes = 3u * 256u + 64u + 64u;  // planes | xs16 | xs
+
 
 // Group reductions over aligned lane groups with DPP (every lane of the group
 // gets the result): L = 4 (quads) or 8 (half rows).
@@ -101,8 +115,7 @@ __device__ __forceinline__ float half_row_other(float v) { return dpp_f<0x141>(v
 // sub-block a half row. Writes the three planes, xs and xs16 of the block.
 // Sums: per lane in element order, then the quad, then the two quads of a
 // sub-block (the same value in every lane of the group).
-__device__ __forceinline__ void prep_block(const float *v, uint32_t cols, uint32_t b,
-                                           uint32_t lane, uint8_t *xq, const XqLayout &L) {
+__device__ __forceinline__ void prep_block(const float *v, uint32_t lane, const DigitView &dv) {
     float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
     const float sum4 = ((v[0] + v[1]) + v[2]) + v[3];
     amax = quad_max(amax);
@@ -127,15 +140,15 @@ __device__ __forceinline__ void prep_block(const float *v, uint32_t cols, uint32
     const uint32_t lo23 = __builtin_amdgcn_perm(u[3], u[2], 0x05010400u);
     const uint32_t hi01 = __builtin_amdgcn_perm(u[1], u[0], 0x0c0c0602u);
     const uint32_t hi23 = __builtin_amdgcn_perm(u[3], u[2], 0x0c0c0602u);
-    const uint32_t off = 256u * b + 4u * lane;
-    *reinterpret_cast<uint32_t *>(xq + off) = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u) ^ 0x80808080u;
-    *reinterpret_cast<uint32_t *>(xq + cols + off) =
+    uint8_t *const at = dv.base + 4u * lane;
+    *reinterpret_cast<uint32_t *>(at) = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u) ^ 0x80808080u;
+    *reinterpret_cast<uint32_t *>(at + dv.pstride) =
         __builtin_amdgcn_perm(lo23, lo01, 0x07060302u) ^ 0x80808080u;
-    *reinterpret_cast<uint32_t *>(xq + 2u * cols + off) =
+    *reinterpret_cast<uint32_t *>(at + 2u * dv.pstride) =
         __builtin_amdgcn_perm(hi23, hi01, 0x05040100u) ^ 0x80808080u;
-    if ((lane & 3u) == 0) reinterpret_cast<float *>(xq + L.xs16)[16u * b + lane / 4u] = sum16;
+    if ((lane & 3u) == 0) dv.xs16[lane / 4u] = sum16;
     if ((lane & 7u) == 0)
-        reinterpret_cast<float2 *>(xq + L.xs)[8u * b + lane / 8u] =
+        dv.xs[lane / 8u] =
             make_float2(finite ? ldexpf(1.0f, e - 22) : __builtin_nanf(""), sum32);
 }
 
@@ -198,18 +211,18 @@ struct Q4K {
         r[1] = lda4(blk + 16u * g + 16u);
         r[2] = lda4(blk + 16u * g + 80u);
     }
-    __device__ static float dot(const u32x4 *r, uint8_t *, const Src &, const uint8_t *xq,
-                                const XqLayout &L, uint32_t cols, uint32_t b, uint32_t n,
-                                uint32_t g) {
+    __device__ static float dot(const u32x4 *r, uint8_t *, const Src &, const DigitView &dv,
+                                uint32_t b, uint32_t n, uint32_t g) {
+        (void)b;
         // A row n = 4t+p: lane group g carries sub-blocks 2(g>>1) (low nibbles,
         // t even) and 2(g>>1)+1 (high nibbles, t odd) at element offset 16(g&1)
         const uint32_t t = n >> 2, p = n & 3u;
         const bool on = p < 3u && (g >> 1) == (t >> 1);
-        const uint32_t ao = p * cols + 256u * b + 32u * t + 16u * (g & 1u);
-        const i32x4 A0l = lda(xq + (on && !(t & 1u) ? ao : L.zero));
-        const i32x4 A0h = lda(xq + (on && (t & 1u) ? ao : L.zero));
-        const i32x4 A1l = lda(xq + (on && !(t & 1u) ? ao + 128u : L.zero));
-        const i32x4 A1h = lda(xq + (on && (t & 1u) ? ao + 128u : L.zero));
+        const uint8_t *ao = dv.base + p * dv.pstride + 32u * t + 16u * (g & 1u);
+        const i32x4 A0l = lda(on && !(t & 1u) ? ao : dv.zero);
+        const i32x4 A0h = lda(on && (t & 1u) ? ao : dv.zero);
+        const i32x4 A1l = lda(on && !(t & 1u) ? ao + 128u : dv.zero);
+        const i32x4 A1h = lda(on && (t & 1u) ? ao + 128u : dv.zero);
         const uint32_t M4 = 0x0F0F0F0Fu;
         const u32x4 qa = r[1], qb = r[2];
         const i32x4 B0l = {(int)(qa.x & M4), (int)(qa.y & M4), (int)(qa.z & M4), (int)(qa.w & M4)};
@@ -223,8 +236,7 @@ struct Q4K {
         const float S1 = plane_sum(mfma(A1h, B1h, mfma(A1l, B1l, z)));
         // D group g: sub-blocks g (span 0) and 4 + g (span 1); scales and mins
         // as src/vbs_dequant.c:225-233
-        const float2 *xs = reinterpret_cast<const float2 *>(xq + L.xs);
-        const float2 xs0 = xs[8u * b + g], xs1 = xs[8u * b + 4u + g];
+        const float2 xs0 = dv.xs[g], xs1 = dv.xs[4u + g];
         const u32x4 hd = r[0];
         const uint32_t sh = 8u * g;
         const uint32_t sc0 = bfe(hd.y, sh, 6), m0 = bfe(hd.z, sh, 6);
@@ -288,8 +300,7 @@ struct Q6K {
         }
     }
     __device__ static float dot(const u32x4 *r, uint8_t *scratch, const Src &src,
-                                const uint8_t *xq, const XqLayout &L, uint32_t cols, uint32_t b,
-                                uint32_t n, uint32_t g) {
+                                const DigitView &dv, uint32_t b, uint32_t n, uint32_t g) {
         const uint32_t lane = 16u * g + n;
 #pragma unroll
         for (uint32_t i = 0; i < 4; i++) {
@@ -328,11 +339,9 @@ struct Q6K {
         // 8h + 2q + u; A row n = 4t+p carries plane p of the group of lane group t
         const uint32_t t = n >> 2, p = n & 3u;
         const bool on = p < 3u && t == g;
-        const float2 *xs = reinterpret_cast<const float2 *>(xq + L.xs);
-        const float *xs16 = reinterpret_cast<const float *>(xq + L.xs16);
         const uint32_t qew[4] = {qe.x, qe.y, qe.z, qe.w}, qow[4] = {qo.x, qo.y, qo.z, qo.w};
         const uint32_t qhw[4] = {qh.x, qh.y, qh.z, qh.w};
-        const uint32_t a0 = p * cols + 256u * b + 128u * (t >> 1) + 16u * (t & 1u);
+        const uint8_t *a0 = dv.base + p * dv.pstride + 128u * (t >> 1) + 16u * (t & 1u);
         float acc = 0.f;
 #pragma unroll
         for (uint32_t q = 0; q < 4; q++) {
@@ -347,15 +356,15 @@ struct Q6K {
                 bw[k] = (int)(((ql[k] >> (4u * (q >> 1))) & 0x0F0F0F0Fu) | hi);
             }
             const i32x4 B = {bw[0], bw[1], bw[2], bw[3]};
-            const i32x4 A = lda(xq + (on ? a0 + 32u * q : L.zero));
+            const i32x4 A = lda(on ? a0 + 32u * q : dv.zero);
             const i32x4 z = {0, 0, 0, 0};
             const float S = plane_sum(mfma(A, B, z));
             // scale 8h + 2q + u: dword 2h + (q >> 1), byte 2(q & 1) + u; the group
             // is half u of sub-block 4h + q
             const uint32_t scd = (q >> 1) ? sc_hi : sc_lo;
             const float sc = (float)(int)(int8_t)bfe(scd, 16u * (q & 1u) + 8u * u, 8);
-            const uint32_t j = 8u * b + 4u * h + q;
-            acc = fmaf(sc, fmaf(xs[j].x, S, -32.f * xs16[2u * j + u]), acc);
+            const uint32_t j = 4u * h + q;  // sub-block of the block
+            acc = fmaf(sc, fmaf(dv.xs[j].x, S, -32.f * dv.xs16[2u * j + u]), acc);
         }
         return cvt_h(dbits) * acc;
     }
@@ -410,8 +419,7 @@ struct KBlk {
         }
     }
     __device__ static float dot(const u32x4 *r, uint8_t *scratch, const Src &src,
-                                const uint8_t *xq, const XqLayout &L, uint32_t cols, uint32_t b,
-                                uint32_t n, uint32_t g) {
+                                const DigitView &dv, uint32_t b, uint32_t n, uint32_t g) {
         const uint32_t lane = 16u * g + n;
 #pragma unroll
         for (uint32_t i = 0; i < NLD; i++) {
@@ -434,7 +442,6 @@ struct KBlk {
         };
         const uint32_t t = n >> 2, p = n & 3u;
         const bool on = p < 3u && t == g;
-        const float2 *xs = reinterpret_cast<const float2 *>(xq + L.xs);
         const i32x4 z = {0, 0, 0, 0};
         float acc = 0.f;
 #pragma unroll
@@ -450,13 +457,13 @@ struct KBlk {
                 q0 = field(BB * j + QOFF);
                 q1 = field(BB * j + QOFF + 16u);
             }
-            const uint32_t ao = p * cols + 256u * b + 32u * (4u * c + t);
-            const i32x4 A0 = lda(xq + (on ? ao : L.zero));
-            const i32x4 A1 = lda(xq + (on ? ao + 16u : L.zero));
+            const uint8_t *ao = dv.base + p * dv.pstride + 32u * (4u * c + t);
+            const i32x4 A0 = lda(on ? ao : dv.zero);
+            const i32x4 A1 = lda(on ? ao + 16u : dv.zero);
             const i32x4 D = mfma(A1, __builtin_bit_cast(i32x4, q1),
                                  mfma(A0, __builtin_bit_cast(i32x4, q0), z));
             const float S = plane_sum(D);
-            const float2 x2 = xs[8u * b + j];
+            const float2 x2 = dv.xs[j];
             const float d = cvt_h(half16(BB * j));
             if (TYPE == kQ8_0) acc = fmaf(d * x2.x, S, acc);
             else if (TYPE == kQ4_0) acc = fmaf(d, fmaf(x2.x, S, -8.f * x2.y), acc);
@@ -573,14 +580,35 @@ __global__ __launch_bounds__(MAXT) void k_mvf(const MvArgs a) {
         const float mean = (float)(t / (double)cols);
         sc = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, a.eps)));
     }
-    if (lane < 4u) reinterpret_cast<uint32_t *>(xq + L.zero)[lane] = 0u;  // each wave's own pad
+    // digits: one slot per wave (TPW == 1: [16-byte zero pad][nw slots]) or
+    // [3][cols] planes with the pad after them
+    constexpr bool kRing = TPW == 1u;
+    const uint32_t zero_off = kRing ? 0u : L.zero;
+    const uint32_t digit_bytes = kRing ? 16u + nw * kSlotBytes : L.bytes;
+    if (lane < 4u) reinterpret_cast<uint32_t *>(xq + zero_off)[lane] = 0u;  // each wave's own pad
+    auto view = [&](uint32_t b) {
+        DigitView dv;
+        dv.zero = xq + zero_off;
+        if constexpr (kRing) {
+            dv.base = xq + 16u + wave * kSlotBytes;
+            dv.pstride = 256u;
+            dv.xs16 = reinterpret_cast<float *>(dv.base + 768u);
+            dv.xs = reinterpret_cast<float2 *>(dv.base + 832u);
+        } else {
+            dv.base = xq + 256u * b;
+            dv.pstride = cols;
+            dv.xs16 = reinterpret_cast<float *>(xq + L.xs16) + 16u * b;
+            dv.xs = reinterpret_cast<float2 *>(xq + L.xs) + 8u * b;
+        }
+        return dv;
+    };
 
     // 4. stream: issue item i + P, prepare x of a new block, compute item i
     // (loads return in issue order, so the wait is for item i alone)
-    uint8_t *scratch = xq + L.bytes + wave * T::SCRATCH;
+    uint8_t *scratch = xq + digit_bytes + wave * T::SCRATCH;
     // per-block row sums [TPW][nblk][16]: every row adds its blocks in index
     // order at the end, so a row's value does not depend on the work split
-    float *pb = reinterpret_cast<float *>(xq + L.bytes + nw * T::SCRATCH);
+    float *pb = reinterpret_cast<float *>(xq + digit_bytes + nw * T::SCRATCH);
 #pragma unroll
     for (uint32_t i = 0; i < NI; i++) {
 #pragma unroll
@@ -593,9 +621,10 @@ __global__ __launch_bounds__(MAXT) void k_mvf(const MvArgs a) {
 #pragma unroll
                 for (int k = 0; k < 4; k++) v[k] = __fmul_rn(__fmul_rn(v[k], sc), w4[k]);
             }
-            prep_block(v, cols, blk(i), lane, xq, L);
+            prep_block(v, lane, view(blk(i)));
         }
-        float part = T::dot(r[i], scratch, src[i / KS], xq, L, cols, min(blk(i), nblk - 1u), n, g);
+        const uint32_t bi = min(blk(i), nblk - 1u);
+        float part = T::dot(r[i], scratch, src[i / KS], view(bi), bi, n, g);
         // the four lane groups of a row hold different groups of the block
         part += __shfl_xor(part, 16, 64);
         part += __shfl_xor(part, 32, 64);
@@ -678,7 +707,8 @@ static MvPlan mv_plan(uint32_t cols, bool two_tiles, bool fused) {
 
 template <class T, uint32_t KS, uint32_t TPW, uint32_t MAXT, bool NORM, int EPI>
 static hipError_t launch_t(const MvArgs &a, uint32_t nw, uint32_t wgs, hipStream_t s) {
-    const size_t lds = xq_layout(a.cols).bytes + (size_t)nw * T::SCRATCH +
+    const size_t digits = TPW == 1u ? 16u + (size_t)nw * kSlotBytes : xq_layout(a.cols).bytes;
+    const size_t lds = digits + (size_t)nw * T::SCRATCH +
                        (size_t)TPW * (a.cols / 256u) * 16u * sizeof(float);
     if (lds > 65536u) {  // beyond the default per-workgroup LDS window: opt in once
         static size_t granted = 0;
