@@ -61,7 +61,7 @@ SEED = 424242
 # dispatch), each scaled by what the counter reads for a 256 MiB device copy
 # in the same run: FETCH_SIZE x (262144 / 131092.9) + WRITE_SIZE x 1.0000
 # (profiles/q4k_matvec_7b_layer_set.md).
-TRAFFIC_BYTES = round((12483.8 * 262144 / 131092.9 + 43.0) * 1024)
+TRAFFIC_BYTES = round((12481.8 * 262144 / 131092.9 + 43.0) * 1024)
 
 
 def algo_bytes(t, rows, cols):
