@@ -396,15 +396,18 @@ static hipError_t launch_mvb_t(const MbArgs &a, uint32_t nw, hipStream_t s) {
     return hipGetLastError();
 }
 
-// Tiles per workgroup and waves (measured at batch 8 on the 70B shapes): the
-// A operands of a block serve every tile of a wave, so they are shared as
-// widely as the grid still fills the chip; four tiles pair best with four
-// waves. Q6_K stops at two tiles (four would spill registers).
+// Tiles per workgroup and waves (measured at batch 8 on the 70B and 7B
+// shapes): the A operands of a block serve every tile of a wave, so they are
+// shared as widely as the grid still fills the chip; four tiles pair best
+// with four waves, or with eight waves of two blocks on rows of 16 blocks or
+// fewer (Q4_K 11008x4096: 18.8 -> 17.6 us; more waves with fewer tiles each
+// are slower at every shape). Q6_K stops at two tiles (four would spill
+// registers).
 template <class T, bool ACC>
 static hipError_t launch_mvb_plan(const MbArgs &a, hipStream_t s) {
     const uint32_t nblk = a.cols / 256u, tiles = a.tile_end[a.nmat - 1u];
     if constexpr (T::BYTES == 144u) {
-        if (tiles >= 640u) return launch_mvb_t<T, 4, ACC>(a, min(4u, nblk), s);
+        if (tiles >= 640u) return launch_mvb_t<T, 4, ACC>(a, min(nblk <= 16u ? 8u : 4u, nblk), s);
         if (tiles >= 256u) return launch_mvb_t<T, 2, ACC>(a, min(8u, nblk), s);
     } else {
         if (tiles >= 512u) return launch_mvb_t<T, 2, ACC>(a, nblk > 64u ? 8u : min(4u, nblk), s);
