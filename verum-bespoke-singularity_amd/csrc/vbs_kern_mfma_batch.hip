@@ -15,8 +15,11 @@ namespace vbs {
 //   2^s_tb so that its largest |x| lies in [2^14, 2^15), and each element
 //   x' = x 2^s_tb becomes hi + lo with hi = f16(x') and lo = f16(x' - hi): 22
 //   significant bits, each element represented to ~2^-23 of itself (or of
-//   2^-10 below its block's maximum). Plane 2t holds hi, plane 2t + 1 lo, in
-//   element order; A row n of an MFMA is plane n, so D row 2t + h is vector
+//   2^-10 below its block's maximum). Plane 2t holds hi, plane 2t + 1 lo,
+//   stored chunk-major: eight elements of plane 0, the same eight of plane
+//   1, ... of plane 15, then the next eight, so the sixteen A rows of an
+//   MFMA's k range are one contiguous 256-byte run per lane group (one load
+//   instruction reads whole cache lines); A row n of an MFMA is plane n, so D row 2t + h is vector
 //   t's dot with hi or lo, the two add up in fp32, and the block's sum is
 //   scaled back by 2^-s_tb. Rows past 2 batch re-read the last plane and are
 //   never stored. An inf or NaN in a block makes its lo plane NaN (inf - inf),
@@ -49,8 +52,8 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kBatchMax = 8;
 
-// Prepared x: [16 planes][cols] f16 | [16 planes][cols/32] f16 sub-block sums
-// of x'/32 | int s[cols/256][8] (block, vector).
+// Prepared x: [cols/8][16 planes][8] f16 | [cols/256][16 planes][8] f16
+// sub-block sums of x'/32 | int s[cols/256][8] (block, vector).
 struct XbLayout {
     uint32_t msum, expo, bytes;
 };
@@ -136,9 +139,10 @@ __global__ __launch_bounds__(256) void k_xprep_b(const float *x, const float *x2
     }
     const XbLayout L = xb_layout(cols);
     typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-    _Float16 *ph = reinterpret_cast<_Float16 *>(xp) + (uint64_t)(2u * t) * cols + e0;
+    // elements e0..e0+3: chunk e0 / 8, half lane & 1; planes 2t and 2t + 1
+    _Float16 *ph = reinterpret_cast<_Float16 *>(xp) + 128u * (e0 >> 3) + 8u * (2u * t) + 4u * (lane & 1u);
     *reinterpret_cast<u32x2 *>(ph) = u32x2{__builtin_bit_cast(uint32_t, hi[0]), __builtin_bit_cast(uint32_t, hi[1])};
-    *reinterpret_cast<u32x2 *>(ph + cols) = u32x2{__builtin_bit_cast(uint32_t, lo[0]), __builtin_bit_cast(uint32_t, lo[1])};
+    *reinterpret_cast<u32x2 *>(ph + 8u) = u32x2{__builtin_bit_cast(uint32_t, lo[0]), __builtin_bit_cast(uint32_t, lo[1])};
     // sub-block sums of x'/32: eight lanes per 32 elements
     sum += __shfl_xor(sum, 1, 64);
     sum += __shfl_xor(sum, 2, 64);
@@ -146,10 +150,9 @@ __global__ __launch_bounds__(256) void k_xprep_b(const float *x, const float *x2
     if ((lane & 7u) == 0) {
         const float m = sum * 0.03125f;
         const _Float16 h = (_Float16)m;
-        _Float16 *pm = reinterpret_cast<_Float16 *>(xp + L.msum) + (uint64_t)(2u * t) * (cols / 32u) +
-                       8u * b + lane / 8u;
+        _Float16 *pm = reinterpret_cast<_Float16 *>(xp + L.msum) + 128u * b + 8u * (2u * t) + lane / 8u;
         pm[0] = h;
-        pm[cols / 32u] = (_Float16)(m - (float)h);
+        pm[8] = (_Float16)(m - (float)h);
     }
     if (lane == 0) reinterpret_cast<int *>(xp + L.expo)[8u * b + t] = s;
 }
@@ -166,7 +169,9 @@ struct MbArgs {
     uint32_t cols, batch;
 };
 
-// This lane's A row: its plane and its sub-block-sum plane.
+// This lane's A row: its plane's first eight elements and first eight
+// sub-block sums; element chunk c of the plane is at plane + 128 c, block b's
+// sums at msum + 128 b.
 struct XbView {
     const _Float16 *plane, *msum;
     const int *expo;
@@ -199,13 +204,14 @@ struct Q4KB {
     // the block, j = 4 (m >> 2) + 2 (g >> 1) + ((m >> 1) & 1) (the nibbles of
     // qs byte 16 g + 8 (m & 1) + k, or of byte 64 + ..., low or high half).
     __device__ static void load_a(const XbView &v, uint32_t b, uint32_t g, A &a) {
-        const _Float16 *p = v.plane + 256u * b + 16u * (g & 1u);
+        // element 256 b + 32 j + 16 (g & 1) + 8 (m & 1): chunk 32 b + 4 j + 2 (g & 1) + (m & 1)
+        const _Float16 *p = v.plane + 128u * (32u * b + 2u * (g & 1u));
 #pragma unroll
         for (uint32_t m = 0; m < 8u; m++) {
             const uint32_t j = 4u * (m >> 2) + 2u * (g >> 1) + ((m >> 1) & 1u);
-            a.m[m] = *reinterpret_cast<const h8 *>(p + 32u * j + 8u * (m & 1u));
+            a.m[m] = *reinterpret_cast<const h8 *>(p + 128u * (4u * j + (m & 1u)));
         }
-        const h8 t = *reinterpret_cast<const h8 *>(v.msum + 8u * b), z = {};
+        const h8 t = *reinterpret_cast<const h8 *>(v.msum + 128u * b), z = {};
         a.mn = g == 0u ? t : z;
         a.s = *reinterpret_cast<const int2 *>(v.expo + 8u * b + 2u * g);
     }
@@ -261,11 +267,13 @@ struct Q6KB {
     // MFMA G = 8h + 2q + u (scale group G), lane group g, slot k: element
     // 128 h + 32 q + 16 u + 4 g + k (src/vbs_dequant.c:316-333)
     __device__ static void load_a(const XbView &v, uint32_t b, uint32_t g, A &a) {
-        const _Float16 *p = v.plane + 256u * b + 4u * g;
+        // element 256 b + 128 (G >> 3) + 32 ((G >> 1) & 3) + 16 (G & 1) + 4 g:
+        // chunk 32 b + 16 (G >> 3) + 4 ((G >> 1) & 3) + 2 (G & 1) + (g >> 1), half g & 1
+        const _Float16 *p = v.plane + 128u * (32u * b + (g >> 1)) + 4u * (g & 1u);
 #pragma unroll
         for (uint32_t G = 0; G < 16u; G++)
-            a.g[G] = *reinterpret_cast<const h4 *>(p + 128u * (G >> 3) + 32u * ((G >> 1) & 3u) +
-                                                   16u * (G & 1u));
+            a.g[G] = *reinterpret_cast<const h4 *>(p + 128u * (16u * (G >> 3) + 4u * ((G >> 1) & 3u) +
+                                                               2u * (G & 1u)));
         a.s = *reinterpret_cast<const int2 *>(v.expo + 8u * b + 2u * g);
     }
     __device__ static void dot(const u32x4 *r, const A &x, uint8_t *scratch, const Src &src,
@@ -320,8 +328,8 @@ __global__ __launch_bounds__(512) void k_mvb(const MbArgs a) {
     const uint32_t n = lane & 15u, g = lane >> 4;
     const XbLayout L = xb_layout(cols);
     const uint32_t p = min(n, 2u * a.batch - 1u);
-    const XbView xv{reinterpret_cast<const _Float16 *>(a.xp) + (uint64_t)p * cols,
-                    reinterpret_cast<const _Float16 *>(a.xp + L.msum) + (uint64_t)p * (cols / 32u),
+    const XbView xv{reinterpret_cast<const _Float16 *>(a.xp) + 8u * p,
+                    reinterpret_cast<const _Float16 *>(a.xp + L.msum) + 8u * p,
                     reinterpret_cast<const int *>(a.xp + L.expo)};
     const uint32_t total = a.tile_end[a.nmat - 1u];
     Src src[TPW];
