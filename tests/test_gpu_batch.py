@@ -114,11 +114,13 @@ def test_batch_70b_shapes(dev, host, oracle, mem, t, rows, cols):
             assert rel_l2(Y[b, lo:lo + k], oracle.linear(t, ws, X[b], cols, k)) <= LIN_TOL, (lo, b)
 
 
+@pytest.mark.parametrize("rows", [11008, 22016])
 @pytest.mark.parametrize("batch", [5, 8])
-def test_batch_7b_gate_shape(dev, host, oracle, mem, batch):
-    """Q4_K 11008x4096 (the Llama-7B gate/up shape): 688 tiles of 16-block rows,
-    the plan's eight-wave launch, every row against the oracle."""
-    rows, cols = 11008, 4096
+def test_batch_7b_gate_shape(dev, host, oracle, mem, batch, rows):
+    """Q4_K 11008x4096 and 22016x4096 (the Llama-7B gate, and gate/up as one
+    launch): 688 and 1376 tiles of 16-block rows, three tiles per workgroup
+    (the last workgroup partly idle), every row against the oracle."""
+    cols = 4096
     w = V.synth_matrix(host, V.Q4_K, rows, cols, SEED, 77)
     X = vectors(host, batch, cols, 130)
     Y = run_batch(dev, mem, V.Q4_K, w, X, rows, cols)

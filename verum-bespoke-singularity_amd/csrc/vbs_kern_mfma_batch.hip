@@ -406,16 +406,19 @@ static hipError_t launch_mvb_t(const MbArgs &a, uint32_t nw, hipStream_t s) {
 
 // Tiles per workgroup and waves (measured at batch 8 on the 70B and 7B
 // shapes): the A operands of a block serve every tile of a wave, so they are
-// shared as widely as the grid still fills the chip; four tiles pair best
-// with four waves, or with eight waves of two blocks on rows of 16 blocks or
-// fewer (Q4_K 11008x4096: 18.8 -> 17.6 us; more waves with fewer tiles each
-// are slower at every shape). Q6_K stops at two tiles (four would spill
-// registers).
+// shared as widely as the grid still fills the chip. From 1024 tiles of
+// rows wider than 16 blocks (70B gate/up) four tiles pair best with four
+// waves; otherwise from 640 tiles (70B Q/K/V, the 7B gate and gate/up)
+// three tiles and eight waves (Q4_K 10240x8192: 25.7 -> 22.6 us,
+// 11008x4096: 16.1 -> 14.4 us, 22016x4096: 27.9 -> 24.4 us against four
+// tiles); below that two tiles. Other splits were slower at every shape.
+// Q6_K stops at two tiles (four would spill registers).
 template <class T, bool ACC>
 static hipError_t launch_mvb_plan(const MbArgs &a, hipStream_t s) {
     const uint32_t nblk = a.cols / 256u, tiles = a.tile_end[a.nmat - 1u];
     if constexpr (T::BYTES == 144u) {
-        if (tiles >= 640u) return launch_mvb_t<T, 4, ACC>(a, min(nblk <= 16u ? 8u : 4u, nblk), s);
+        if (tiles >= 1024u && nblk > 16u) return launch_mvb_t<T, 4, ACC>(a, 4u, s);
+        if (tiles >= 640u) return launch_mvb_t<T, 3, ACC>(a, min(8u, nblk), s);
         if (tiles >= 256u) return launch_mvb_t<T, 2, ACC>(a, min(8u, nblk), s);
     } else {
         if (tiles >= 512u) return launch_mvb_t<T, 2, ACC>(a, nblk > 64u ? 8u : min(4u, nblk), s);
