@@ -49,6 +49,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "verum-bespoke-singularity_amd"))
 sys.path.insert(0, os.path.join(ROOT, "tests"))
 import vbs_gfx950 as V  # noqa: E402
+from vbs_gfx950 import Hip  # noqa: E402
 
 PEAK_HBM_GBS = 8000.0
 H, FF = 4096, 11008
@@ -66,63 +67,6 @@ TRAFFIC_BYTES = round((12481.8 * 262144 / 131092.9 + 43.0) * 1024)
 
 def algo_bytes(t, rows, cols):
     return V.row_bytes(t, cols) * rows + 4 * cols + 4 * rows
-
-
-class Hip:
-    """hipEvent timing and stream capture on the device library's stream."""
-
-    def __init__(self):
-        h = self.h = C.CDLL("libamdhip64.so")
-        vp, pvp = C.c_void_p, C.POINTER(C.c_void_p)
-        h.hipEventCreate.argtypes = [pvp]
-        h.hipEventRecord.argtypes = [vp, vp]
-        h.hipEventSynchronize.argtypes = [vp]
-        h.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), vp, vp]
-        h.hipEventDestroy.argtypes = [vp]
-        h.hipStreamBeginCapture.argtypes = [vp, C.c_int]
-        h.hipStreamEndCapture.argtypes = [vp, pvp]
-        h.hipGraphInstantiate.argtypes = [pvp, vp, vp, vp, C.c_size_t]
-        h.hipGraphLaunch.argtypes = [vp, vp]
-        h.hipGraphExecDestroy.argtypes = [vp]
-        h.hipGraphDestroy.argtypes = [vp]
-
-    def _ok(self, rc, what):
-        if rc != 0:
-            raise RuntimeError(f"{what} failed ({rc})")
-
-    def event(self):
-        e = C.c_void_p()
-        self._ok(self.h.hipEventCreate(C.byref(e)), "hipEventCreate")
-        return e
-
-    def record(self, ev, stream):
-        self._ok(self.h.hipEventRecord(ev, C.c_void_p(stream)), "hipEventRecord")
-
-    def elapsed_ms(self, a, b):
-        self._ok(self.h.hipEventSynchronize(b), "hipEventSynchronize")
-        ms = C.c_float()
-        self._ok(self.h.hipEventElapsedTime(C.byref(ms), a, b), "hipEventElapsedTime")
-        return ms.value
-
-    def capture(self, stream, enqueue):
-        """Graph of the work `enqueue()` puts on `stream` (thread-local capture)."""
-        self._ok(self.h.hipStreamBeginCapture(C.c_void_p(stream), 1), "hipStreamBeginCapture")
-        try:
-            enqueue()
-        finally:
-            g = C.c_void_p()
-            rc = self.h.hipStreamEndCapture(C.c_void_p(stream), C.byref(g))
-        self._ok(rc, "hipStreamEndCapture")
-        ex = C.c_void_p()
-        self._ok(self.h.hipGraphInstantiate(C.byref(ex), g, None, None, 0), "hipGraphInstantiate")
-        return g, ex
-
-    def launch(self, graph, stream):
-        self._ok(self.h.hipGraphLaunch(graph[1], C.c_void_p(stream)), "hipGraphLaunch")
-
-    def destroy(self, graph):
-        self.h.hipGraphExecDestroy(graph[1])
-        self.h.hipGraphDestroy(graph[0])
 
 
 def cpu_hot_q8_0_s(w, xq, qd, rows, cols, max_seconds=1.0):

@@ -133,7 +133,17 @@ int vbs_gfx950_linear_batch(int type, const void *w, const float *x, uint32_t x_
                             uint32_t batch);
 
 /* The library's stream (a hipStream_t), for callers that time kernels with
- * HIP events or capture the stream into a graph. */
+ * HIP events or capture the stream into a graph.
+ *
+ * Capture and the library's scratch: vbs_gfx950_linear_batch (Q4_K / Q6_K)
+ * and vbs_gfx950_attention keep intermediate results in a device scratch
+ * that the library owns. It only grows, and a buffer that a larger call
+ * replaces stays allocated until the process ends, so a captured graph keeps
+ * valid memory whatever is called after the capture. Growing allocates, so a
+ * call made while the stream is being captured fails (0, reason "operation
+ * not permitted when stream is capturing") if it needs more scratch than
+ * earlier uncaptured calls have sized: make one uncaptured call of the
+ * largest shape before capturing. */
 void *vbs_gfx950_stream(void);
 
 /* ---- graph-replayed decode step (extension) -------------------------------

@@ -5,6 +5,8 @@ src/vbs_specializer.c:353-357), so the oracle of vbs_gfx950_linear_batch is
 `batch` independent vbs_host_linear_tile calls (src/vbs_host_math.h:223-267):
 every vector must meet the single matvec's bar, relative L2 <= 1e-5.
 """
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -126,3 +128,54 @@ def test_batch_7b_gate_shape(dev, host, oracle, mem, batch, rows):
     Y = run_batch(dev, mem, V.Q4_K, w, X, rows, cols)
     for b in range(batch):
         assert rel_l2(Y[b], oracle.linear(V.Q4_K, w, X[b], cols, rows)) <= LIN_TOL, b
+
+
+def test_scratch_growth_keeps_captured_graphs(dev, host, oracle, mem):
+    """The batched matvec keeps its prepared x in the library's scratch. A
+    graph captured from the library's stream holds the scratch address of the
+    capture, so a later call that grows the scratch (a long attention: its
+    per-chunk partials live there too) must leave that memory valid: every
+    replay still meets the oracle. A call under capture that would need more
+    scratch fails with a reason and launches nothing (growing allocates)."""
+    hip, stream = V.Hip(), dev.stream()
+    t, rows, cols, batch = V.Q4_K, 96, 4096, 4
+    w = V.synth_matrix(host, t, rows, cols, SEED, 78)
+    X = vectors(host, batch, cols, 140)
+    pw, px, py = mem.up(w), mem.up(X), mem.zeros(batch * rows)
+    want = [oracle.linear(t, w, X[b], cols, rows) for b in range(batch)]
+    nqh, nkh, hd = 8, 1, 128
+    pq, po = mem.up(synth_x(host, nqh * hd, 141)), mem.zeros(nqh * hd)
+
+    # zero keys and values for the long attentions below, allocated before any capture
+    caches = {seq: (mem.zeros(seq * hd, np.uint16), mem.zeros(seq * hd, np.uint16))
+              for seq in (520_000, 1_100_000)}
+
+    def attention(seq):
+        """Attention over `seq` zero keys and values: per-chunk partials of
+        8 x seq/64 x 130 floats (32 MiB at 520,000 positions)."""
+        kc, vc = caches[seq]
+        return dev._attention(pq, kc, vc, po, seq, 0, seq, nqh, nkh, hd, ctypes.c_float(0.088))
+
+    dev.linear_batch(t, pw, px, cols, py, rows, cols, rows, batch)  # sizes the scratch
+    graph = hip.capture(stream, lambda: dev.linear_batch(t, pw, px, cols, py, rows, cols, rows,
+                                                         batch))
+    try:
+        for rep in range(3):
+            dev.write(py, np.zeros(batch * rows, np.float32))
+            if rep == 1:  # grows the scratch well past anything the other tests use
+                assert attention(520_000) == 1, dev.error()
+                assert np.all(dev.download(po, nqh * hd, np.float32) == 0.0)
+            hip.launch(graph, stream)
+            Y = dev.download(py, (batch, rows), np.float32)
+            for b in range(batch):
+                assert rel_l2(Y[b], want[b]) <= LIN_TOL, (rep, b)
+    finally:
+        hip.destroy(graph)
+    rc = []
+    failed = hip.capture(stream, lambda: rc.append(attention(1_100_000)))
+    hip.destroy(failed)
+    assert rc == [0] and "capturing" in dev.error(), dev.error()
+    # the stream works on after the refused call
+    dev.linear_batch(t, pw, px, cols, py, rows, cols, rows, batch)
+    Y = dev.download(py, (batch, rows), np.float32)
+    assert rel_l2(Y[0], want[0]) <= LIN_TOL

@@ -19,6 +19,8 @@
 
 namespace {
 
+constexpr int kMaxRetired = 48;
+
 struct Runtime {
     bool probed = false;
     bool ready = false;
@@ -27,6 +29,8 @@ struct Runtime {
     char name[128] = {0};
     void *scratch = nullptr;
     size_t scratch_bytes = 0;
+    void *retired[kMaxRetired] = {nullptr};  // superseded scratch buffers, kept (see rt_scratch)
+    int n_retired = 0;
     uint32_t *counters = nullptr;  // zeroed once; kernels that use one leave it at 0
 };
 
@@ -83,22 +87,41 @@ uint64_t row_bytes(int type, uint32_t cols) {
     }
 }
 
-void *scratch(size_t bytes, hipStream_t s) {
+// The scratch only grows, and a buffer that a larger one replaces stays
+// allocated until the process ends: a graph captured from the library's
+// stream keeps the address it was captured with, and a replay after a larger
+// call must still find valid memory there. Every growth at least doubles the
+// size, so the retired buffers together are smaller than the live one (and
+// 48 retirements are more than any 64-bit size allows). Growing allocates,
+// which a stream under capture must not do: such a call fails with
+// hipErrorStreamCaptureUnsupported and nothing is launched; one uncaptured
+// call of the same size first sizes the scratch for later captures.
+void *rt_scratch(size_t bytes, hipStream_t s, hipError_t *why) {
+    *why = hipSuccess;
     if (bytes <= g_rt.scratch_bytes) return g_rt.scratch;
-    size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
-    want = (want + 4095u) & ~(size_t)4095u;
-    if (g_rt.scratch) {
-        (void)hipStreamSynchronize(s);
-        (void)hipFree(g_rt.scratch);
-        g_rt.scratch = nullptr;
-        g_rt.scratch_bytes = 0;
-    }
-    if (hipMalloc(&g_rt.scratch, want) != hipSuccess) {
-        g_rt.scratch = nullptr;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) {
+        (void)hipGetLastError();
+        *why = hipErrorStreamCaptureUnsupported;
         return nullptr;
     }
+    if (g_rt.n_retired == kMaxRetired) {
+        *why = hipErrorOutOfMemory;
+        return nullptr;
+    }
+    size_t want = bytes < 2 * g_rt.scratch_bytes ? 2 * g_rt.scratch_bytes : bytes;
+    want = want < (1u << 20) ? (1u << 20) : want;
+    want = (want + 4095u) & ~(size_t)4095u;
+    void *p = nullptr;
+    if (hipMalloc(&p, want) != hipSuccess) {
+        (void)hipGetLastError();
+        *why = hipErrorOutOfMemory;
+        return nullptr;
+    }
+    if (g_rt.scratch) g_rt.retired[g_rt.n_retired++] = g_rt.scratch;
+    g_rt.scratch = p;
     g_rt.scratch_bytes = want;
-    return g_rt.scratch;
+    return p;
 }
 
 hipStream_t rt_stream() { return g_rt.stream; }
@@ -407,16 +430,24 @@ int vbs_gfx950_cache_store(const float *k, const float *v, uint16_t *kc, uint16_
     return hip_ok(launch_cache_store(k, v, kc, vc, base, kv_dim, g_rt.stream), "cache_store");
 }
 
+// Argument checks of the attention entry point; 0 with the reason set.
+static int attention_args_ok(const char *who, const float *q, const uint16_t *kc,
+                             const uint16_t *vc, const float *out, uint32_t seq_len,
+                             uint32_t max_ctx, uint32_t nqh, uint32_t nkh, uint32_t hd) {
+    if (!q || !kc || !vc || !out) return fail("%s: null pointer", who);
+    if (seq_len == 0 || nqh == 0 || nkh == 0 || hd == 0) return fail("%s: empty shape", who);
+    if (seq_len > max_ctx) return fail("%s: seq_len %u > max_ctx %u", who, seq_len, max_ctx);
+    if (nqh % nkh) return fail("%s: %u q heads not a multiple of %u kv heads", who, nqh, nkh);
+    if (nqh / nkh > 16) return fail("%s: group size %u exceeds 16", who, nqh / nkh);
+    if (hd > 256 || (hd & 1u)) return fail("%s: head_dim %u must be even and <= 256", who, hd);
+    return 1;
+}
+
 int vbs_gfx950_attention(const float *q, const uint16_t *kc, const uint16_t *vc, float *out,
                          uint32_t seq_len, uint32_t layer, uint32_t max_ctx, uint32_t nqh,
                          uint32_t nkh, uint32_t hd, float scale) {
     if (!ready_or_fail()) return 0;
-    if (!q || !kc || !vc || !out) return fail("attention: null pointer");
-    if (seq_len == 0 || nqh == 0 || nkh == 0 || hd == 0) return fail("attention: empty shape");
-    if (seq_len > max_ctx) return fail("attention: seq_len %u > max_ctx %u", seq_len, max_ctx);
-    if (nqh % nkh) return fail("attention: %u q heads not a multiple of %u kv heads", nqh, nkh);
-    if (nqh / nkh > 16) return fail("attention: group size %u exceeds 16", nqh / nkh);
-    if (hd > 256 || (hd & 1u)) return fail("attention: head_dim %u must be even and <= 256", hd);
+    if (!attention_args_ok("attention", q, kc, vc, out, seq_len, max_ctx, nqh, nkh, hd)) return 0;
     uint64_t layer_off = (uint64_t)layer * max_ctx * nkh * hd;
     return hip_ok(launch_attention(q, kc, vc, out, seq_len, nullptr, nullptr, layer_off, nqh, nkh,
                                    hd, scale, g_rt.stream),

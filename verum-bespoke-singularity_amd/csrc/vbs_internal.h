@@ -15,8 +15,12 @@ uint64_t row_bytes(int type, uint32_t cols);
 // Elements per block of `type`, 0 if not a hot-path type.
 uint32_t block_elems(int type);
 
-// Device scratch owned by the runtime (grown on demand, never shrunk).
-void *scratch(size_t bytes, hipStream_t s);
+// Device scratch owned by the runtime, at least `bytes` long. It only grows;
+// a replaced buffer stays allocated until the process ends, so graphs
+// captured with it stay valid. NULL with *why set when it cannot grow:
+// hipErrorStreamCaptureUnsupported while `s` is being captured (growing
+// allocates), hipErrorOutOfMemory otherwise.
+void *rt_scratch(size_t bytes, hipStream_t s, hipError_t *why);
 
 // The library's stream, and the last-error writer of the C ABI.
 hipStream_t rt_stream();

@@ -690,8 +690,11 @@ hipError_t launch_attention(const float *q, const uint16_t *kc, const uint16_t *
     if (group > kMaxGroup) return hipErrorInvalidValue;
     // with pos_dev, seq_len is the largest sequence the grid must cover
     const uint32_t stride = attn_max_chunks(seq_len, nkh);
-    if (!part) part = (float *)scratch(attention_partial_bytes(seq_len, nqh, nkh, hd), s);
-    if (!part) return hipErrorOutOfMemory;
+    if (!part) {
+        hipError_t why;
+        part = (float *)rt_scratch(attention_partial_bytes(seq_len, nqh, nkh, hd), s, &why);
+        if (!part) return why;
+    }
     const bool fast = (hd == 32u || hd == 64u || hd == 128u) && group <= 8u &&
                       ((uintptr_t)q & 15u) == 0 && ((uintptr_t)kc & 15u) == 0 &&
                       ((uintptr_t)vc & 15u) == 0;

@@ -473,8 +473,9 @@ hipError_t launch_kq_linear_batch(int type, const uint8_t *w, const float *x, ui
                                   hipStream_t s) {
     if (batch == 0 || batch > kBatchMax || rows == 0 || !mv_fits(type, w, x, cols, rows))
         return hipErrorNotSupported;
-    uint8_t *xp = static_cast<uint8_t *>(scratch(xb_layout(cols).bytes, s));
-    if (!xp) return hipErrorOutOfMemory;
+    hipError_t why;
+    uint8_t *xp = static_cast<uint8_t *>(rt_scratch(xb_layout(cols).bytes, s, &why));
+    if (!xp) return why;
     hipError_t e = launch_xprep(XP_PLAIN, x, nullptr, xs, nullptr, 0.f, cols, batch, xp, s);
     if (e != hipSuccess) return e;
     const uint8_t *wm[1] = {w};

@@ -54,6 +54,66 @@ def _cdll(path: str) -> C.CDLL:
 
 
 # --------------------------------------------------------------------------
+# HIP runtime: events and stream capture (timing and graph tests)
+# --------------------------------------------------------------------------
+class Hip:
+    """hipEvent timing and stream capture on the device library's stream."""
+
+    def __init__(self):
+        h = self.h = C.CDLL("libamdhip64.so")
+        vp, pvp = C.c_void_p, C.POINTER(C.c_void_p)
+        h.hipEventCreate.argtypes = [pvp]
+        h.hipEventRecord.argtypes = [vp, vp]
+        h.hipEventSynchronize.argtypes = [vp]
+        h.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), vp, vp]
+        h.hipEventDestroy.argtypes = [vp]
+        h.hipStreamBeginCapture.argtypes = [vp, C.c_int]
+        h.hipStreamEndCapture.argtypes = [vp, pvp]
+        h.hipGraphInstantiate.argtypes = [pvp, vp, vp, vp, C.c_size_t]
+        h.hipGraphLaunch.argtypes = [vp, vp]
+        h.hipGraphExecDestroy.argtypes = [vp]
+        h.hipGraphDestroy.argtypes = [vp]
+
+    def _ok(self, rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what} failed ({rc})")
+
+    def event(self):
+        e = C.c_void_p()
+        self._ok(self.h.hipEventCreate(C.byref(e)), "hipEventCreate")
+        return e
+
+    def record(self, ev, stream):
+        self._ok(self.h.hipEventRecord(ev, C.c_void_p(stream)), "hipEventRecord")
+
+    def elapsed_ms(self, a, b):
+        self._ok(self.h.hipEventSynchronize(b), "hipEventSynchronize")
+        ms = C.c_float()
+        self._ok(self.h.hipEventElapsedTime(C.byref(ms), a, b), "hipEventElapsedTime")
+        return ms.value
+
+    def capture(self, stream, enqueue):
+        """Graph of the work `enqueue()` puts on `stream` (thread-local capture)."""
+        self._ok(self.h.hipStreamBeginCapture(C.c_void_p(stream), 1), "hipStreamBeginCapture")
+        try:
+            enqueue()
+        finally:
+            g = C.c_void_p()
+            rc = self.h.hipStreamEndCapture(C.c_void_p(stream), C.byref(g))
+        self._ok(rc, "hipStreamEndCapture")
+        ex = C.c_void_p()
+        self._ok(self.h.hipGraphInstantiate(C.byref(ex), g, None, None, 0), "hipGraphInstantiate")
+        return g, ex
+
+    def launch(self, graph, stream):
+        self._ok(self.h.hipGraphLaunch(graph[1], C.c_void_p(stream)), "hipGraphLaunch")
+
+    def destroy(self, graph):
+        self.h.hipGraphExecDestroy(graph[1])
+        self.h.hipGraphDestroy(graph[0])
+
+
+# --------------------------------------------------------------------------
 # device library (include/vbs_gfx950.h)
 # --------------------------------------------------------------------------
 _P, _U32, _I, _SZ, _F, _U64 = C.c_void_p, C.c_uint32, C.c_int, C.c_size_t, C.c_float, C.c_uint64
