@@ -109,6 +109,21 @@ int vbs_gfx950_attention(const float *q, const uint16_t *kc, const uint16_t *vc,
                          uint32_t n_q_heads, uint32_t n_kv_heads, uint32_t head_dim,
                          float scale);
 
+/* vbs_gfx950_attention without any device allocation: no counterpart in the
+ * reference. For callers that cannot allocate (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). Same arguments and
+ * result as vbs_gfx950_attention; the per-chunk partial results live in a
+ * fixed 8 MiB device array of the library instead of the growable scratch, so
+ * calls whose partials exceed it (nqh x max(ceil(1024 / nkh), ceil(seq_len /
+ * 64)) x (head_dim + 2) x 4 bytes; e.g. 70B shapes up to seq_len 16128) fail
+ * with a reason and launch nothing. Every call on the device shares that
+ * array: calls that overlap on the device race (the library's own calls are
+ * ordered on its one stream and never overlap). */
+int vbs_gfx950_attention_noalloc(const float *q, const uint16_t *kc, const uint16_t *vc,
+                                 float *out, uint32_t seq_len, uint32_t layer, uint32_t max_ctx,
+                                 uint32_t n_q_heads, uint32_t n_kv_heads, uint32_t head_dim,
+                                 float scale);
+
 /* out = gate / (1 + expf(-gate)) * up (src/vbs_host_math.h:53-57; ACTIVATION). */
 int vbs_gfx950_silu_mul(const float *gate, const float *up, float *out, uint32_t n);
 

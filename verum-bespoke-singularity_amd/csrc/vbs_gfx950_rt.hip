@@ -17,6 +17,15 @@
 #include "vbs_gfx950.h"
 #include "vbs_internal.h"
 
+// Partial results of vbs_gfx950_attention_noalloc: a fixed device array, so
+// that entry point allocates nothing. Its device address is looked up once,
+// at vbs_gfx950_init with the library's device current; host code uses only
+// that address (the array's name is a host-side stand-in). Every call on the
+// device shares it, and calls that overlap on the device would race; the
+// library orders all its work on one stream, so its own calls never overlap.
+constexpr size_t kNoAllocScratchBytes = 8u << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
 namespace {
 
 constexpr int kMaxRetired = 48;
@@ -31,6 +40,7 @@ struct Runtime {
     size_t scratch_bytes = 0;
     void *retired[kMaxRetired] = {nullptr};  // superseded scratch buffers, kept (see rt_scratch)
     int n_retired = 0;
+    void *noalloc_scratch = nullptr;  // device address of `scratch` on the library's device
     uint32_t *counters = nullptr;  // zeroed once; kernels that use one leave it at 0
 };
 
@@ -172,6 +182,9 @@ int vbs_gfx950_init(void) {
     if (chosen < 0) return fail("no gfx950 (MI355X) device among %d visible GPUs", count);
     if (!hip_ok(hipSetDevice(chosen), "hipSetDevice")) return 0;
     if (!hip_ok(hipStreamCreateWithFlags(&g_rt.stream, hipStreamNonBlocking), "hipStreamCreate"))
+        return 0;
+    if (!hip_ok(hipGetSymbolAddress(&g_rt.noalloc_scratch, HIP_SYMBOL(scratch)),
+                "hipGetSymbolAddress(scratch)"))
         return 0;
     if (!hip_ok(hipMalloc(&g_rt.counters, kCounterSlots * sizeof(uint32_t)), "hipMalloc(counters)") ||
         !hip_ok(hipMemset(g_rt.counters, 0, kCounterSlots * sizeof(uint32_t)), "hipMemset(counters)") ||
@@ -430,7 +443,7 @@ int vbs_gfx950_cache_store(const float *k, const float *v, uint16_t *kc, uint16_
     return hip_ok(launch_cache_store(k, v, kc, vc, base, kv_dim, g_rt.stream), "cache_store");
 }
 
-// Argument checks of the attention entry point; 0 with the reason set.
+// Argument checks shared by both attention entry points; 0 with the reason set.
 static int attention_args_ok(const char *who, const float *q, const uint16_t *kc,
                              const uint16_t *vc, const float *out, uint32_t seq_len,
                              uint32_t max_ctx, uint32_t nqh, uint32_t nkh, uint32_t hd) {
@@ -452,6 +465,26 @@ int vbs_gfx950_attention(const float *q, const uint16_t *kc, const uint16_t *vc,
     return hip_ok(launch_attention(q, kc, vc, out, seq_len, nullptr, nullptr, layer_off, nqh, nkh,
                                    hd, scale, g_rt.stream),
                   "attention");
+}
+
+int vbs_gfx950_attention_noalloc(const float *q, const uint16_t *kc, const uint16_t *vc,
+                                 float *out, uint32_t seq_len, uint32_t layer, uint32_t max_ctx,
+                                 uint32_t nqh, uint32_t nkh, uint32_t hd, float scale) {
+    if (!ready_or_fail()) return 0;
+    if (!attention_args_ok("attention_noalloc", q, kc, vc, out, seq_len, max_ctx, nqh, nkh, hd))
+        return 0;
+    const size_t need = attention_partial_bytes(seq_len, nqh, nkh, hd);
+    if (need > kNoAllocScratchBytes)
+        return fail("attention_noalloc: %zu bytes of partial results (seq_len %u, %u q heads, "
+                    "%u kv heads, head_dim %u) exceed its fixed %zu-byte scratch",
+                    need, seq_len, nqh, nkh, hd, kNoAllocScratchBytes);
+    // every partial the merge reads is written by the same call's chunk
+    // kernels first, so the scratch needs no clearing between calls
+    uint64_t layer_off = (uint64_t)layer * max_ctx * nkh * hd;
+    return hip_ok(launch_attention(q, kc, vc, out, seq_len, nullptr,
+                                   static_cast<float *>(g_rt.noalloc_scratch), layer_off, nqh,
+                                   nkh, hd, scale, g_rt.stream),
+                  "attention_noalloc");
 }
 
 int vbs_gfx950_silu_mul(const float *g, const float *u, float *out, uint32_t n) {

@@ -139,6 +139,7 @@ _DEVICE_SIGS = {
     "rope": (_I, [_P, _U32, _U32, _U32, _F]),
     "cache_store": (_I, [_P, _P, _P, _P, _U32, _U32, _U32, _U32]),
     "attention": (_I, [_P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, _U32, _F]),
+    "attention_noalloc": (_I, [_P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, _U32, _F]),
     "silu_mul": (_I, [_P, _P, _P, _U32]),
     "add": (_I, [_P, _P, _P, _U32]),
     "dequant_rows": (_I, [_I, _P, _P, _U32, _U32, _P]),
