@@ -223,6 +223,8 @@ def bench_matvec(dev, host, steps, warmup, ncopy, roof_reps):
     per_launch = ncopy * len(big)
     big_ms = hip.elapsed_ms(evs[0], evs[-1]) / (roof_reps * per_launch)
     rep_ms = sorted(hip.elapsed_ms(evs[i], evs[i + 1]) / per_launch for i in range(roof_reps))
+    ceiling = bench_ceiling(dev, hip, stream, [copies[k][i] for k in range(ncopy) for i in big],
+                            algo_bytes(t, FF, H) - 4 * (FF + H), roof_reps)
     # a replay of copy 0's step graph against the same launches issued eagerly
     hip.launch(step_graphs[0], stream)
     y_graph = [dev.download(py[i], (r,), np.float32) for i, (_, r, _) in enumerate(LAYER_SET)]
@@ -235,7 +237,7 @@ def bench_matvec(dev, host, steps, warmup, ncopy, roof_reps):
     step_bytes = sum(algo_bytes(t, r, c) for _, r, c in LAYER_SET)
     res = {"step_bytes": step_bytes, "wall_s": wall, "gpu_ms": gpu_ms,
            "big_bytes": algo_bytes(t, FF, H), "avg_big_ms": big_ms, "rep_big_ms": rep_ms,
-           "replay_equals_eager": replay_equal,
+           "replay_equals_eager": replay_equal, "ceiling": ceiling,
            "weights_host": weights_host, "xs_host": xs_host}
     for k_ in copies:
         for p in k_:
@@ -243,6 +245,64 @@ def bench_matvec(dev, host, steps, warmup, ncopy, roof_reps):
     for p in px + py:
         dev.free(p)
     return res
+
+
+def bench_ceiling(dev, hip, stream, regions, region_bytes, reps):
+    """What a launch of this size can reach on this part, measured the way the
+    roofline is (graph replays between HIP events on the library's stream):
+    vbs_gfx950_checksum reading the same weight regions the dominant matvec
+    reads (every byte once, nothing else: the read floor), the same over
+    1 GiB (the streaming rate), a 16-byte checksum (the cost of one launch
+    back to back), and device-to-device copies of 25.4 MB and 1 GiB."""
+    n_part = int(dev._checksum_partials(1 << 30))
+    part = dev.alloc(4 * n_part)
+
+    def per_launch_us(enqueue, launches, rep):
+        g = hip.capture(stream, enqueue)
+        hip.launch(g, stream)
+        dev.sync()
+        e0, e1 = hip.event(), hip.event()
+        hip.record(e0, stream)
+        for _ in range(rep):
+            hip.launch(g, stream)
+        hip.record(e1, stream)
+        dev.sync()
+        hip.destroy(g)
+        return hip.elapsed_ms(e0, e1) * 1e3 / (rep * launches)
+
+    out = {}
+    read_us = per_launch_us(lambda: [dev.check(dev._checksum(r, region_bytes, part), "checksum")
+                                     for r in regions], len(regions), reps)
+    gib = 1 << 30
+    big = dev.alloc(gib)
+    try:
+        stream_us = per_launch_us(lambda: [dev.check(dev._checksum(big, gib, part), "checksum")
+                                           for _ in range(2)], 2, 4)
+        one_us = per_launch_us(lambda: [dev.check(dev._checksum(big, 16, part), "checksum")
+                                        for _ in range(100)], 100, 4)
+        dst = dev.alloc(region_bytes)
+        try:
+            cp_us = per_launch_us(lambda: [dev.check(dev._copy_d2d(dst, r, region_bytes), "copy")
+                                           for r in regions], len(regions), 8)
+        finally:
+            dev.free(dst)
+        half = gib // 2
+        cpg_us = per_launch_us(lambda: [dev.check(dev._copy_d2d(big + half, big, half), "copy")
+                                        for _ in range(2)], 2, 4)
+    finally:
+        dev.free(big)
+        dev.free(part)
+    gbs = lambda b, us: round(b / us / 1e3, 1)
+    out = {"read_floor": {"us_per_launch": round(read_us, 3),
+                          "GB_per_s": gbs(region_bytes, read_us),
+                          "frac": round(region_bytes / read_us / 1e3 / PEAK_HBM_GBS, 4),
+                          "bytes": region_bytes,
+                          "kernel": "vbs_gfx950_checksum over the same weight copies"},
+           "stream_1GiB_GB_per_s": gbs(gib, stream_us),
+           "launch_floor_us": round(one_us, 3),
+           "copy_d2d_GB_per_s": {"25.4MB_read_plus_write": gbs(2 * region_bytes, cp_us),
+                                 "512MiB_read_plus_write": gbs(2 * half, cpg_us)}}
+    return out
 
 
 def gpu_matvec_us(dev, host, t, rows, cols, rotate_bytes=400e6, reps=3):
@@ -709,6 +769,9 @@ def main():
                      "kernel": "k_mvf<Q4K> (matrix-core Q4_K matvec), 11008x4096 and 4096x11008",
                      "algorithmic_bytes_per_launch": r["big_bytes"],
                      "avg_launch_us": round(1e3 * r["avg_big_ms"], 3),
+                     "ceiling": r["ceiling"],
+                     "frac_of_read_floor": round(r["ceiling"]["read_floor"]["us_per_launch"]
+                                                 / (1e3 * r["avg_big_ms"]), 4),
                      "per_replay_GB_per_s": {
                          "median": round(r["big_bytes"] / (rep[len(rep) // 2] * 1e-3) / 1e9, 1),
                          "min": round(r["big_bytes"] / (rep[-1] * 1e-3) / 1e9, 1),

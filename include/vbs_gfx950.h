@@ -147,6 +147,17 @@ int vbs_gfx950_linear_batch(int type, const void *w, const float *x, uint32_t x_
                             float *y, uint32_t y_stride, uint32_t cols, uint32_t rows,
                             uint32_t batch);
 
+/* XOR checksum of a device region, as partial words: partials[i] is the XOR
+ * of the 32-bit words of one span of the region (consecutive spans of up to
+ * 112 KB), for i < vbs_gfx950_checksum_partials(bytes); their XOR is the
+ * region's. p is 16-byte aligned and bytes a multiple of 16; partials is
+ * device memory.
+ * Verifies uploads (the host XORs the same words) and, reading every byte
+ * exactly once and nothing else, it is the read floor beside the matvec
+ * roofline. No counterpart in the reference. */
+uint32_t vbs_gfx950_checksum_partials(size_t bytes);
+int vbs_gfx950_checksum(const void *p, size_t bytes, uint32_t *partials);
+
 /* The library's stream (a hipStream_t), for callers that time kernels with
  * HIP events or capture the stream into a graph.
  *

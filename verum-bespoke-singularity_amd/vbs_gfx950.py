@@ -145,6 +145,8 @@ _DEVICE_SIGS = {
     "dequant_rows": (_I, [_I, _P, _P, _U32, _U32, _P]),
     "linear_batch": (_I, [_I, _P, _P, _U32, _P, _U32, _U32, _U32, _U32]),
     "stream": (_P, []),
+    "checksum_partials": (_U32, [_SZ]),
+    "checksum": (_I, [_P, _SZ, _P]),
     "decoder_create": (_I, [_P, _U32, C.POINTER(C.c_void_p)]),
     "decoder_step": (_I, [_P, _U32, _U32, _P]),
     "decoder_greedy": (_I, [_P, _U32, _U32, _U32, _P, _P]),
@@ -237,6 +239,19 @@ class DeviceLib:
     def hot_matvec(self, t, w, rows, cols, act, qd, qsum, y):
         self.check(self._hot_matvec(t, w, rows, cols, act, qd or None, qsum or None, y),
                    "hot_matvec")
+
+    def checksum(self, p, nbytes: int) -> int:
+        """XOR of the 32-bit words of device bytes [p, p + nbytes) (16-byte
+        aligned, a multiple of 16 bytes), from the per-workgroup partials."""
+        n = int(self._checksum_partials(nbytes))
+        if n == 0:
+            return 0
+        part = self.alloc(4 * n)
+        try:
+            self.check(self._checksum(p, nbytes, part), "checksum")
+            return int(np.bitwise_xor.reduce(self.download(part, n, np.uint32)))
+        finally:
+            self.free(part)
 
     def dequant_rows(self, t, w, ids, n_rows, dim, out):
         self.check(self._dequant_rows(t, w, ids or None, n_rows, dim, out), "dequant_rows")
