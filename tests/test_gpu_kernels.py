@@ -87,9 +87,9 @@ def test_linear_parity(dev, host, oracle, mem, t, rows, cols):
 
 @pytest.mark.parametrize("t,rows,cols", [(V.Q4_K, 4096, 11008), (V.Q4_K, 11008, 4096),
                                          (V.Q6_K, 4096, 11008), (V.Q8_0, 11008, 4096),
-                                         (V.Q4_0, 4096, 4096)],
+                                         (V.Q4_0, 4096, 4096), (V.Q6_K, 32000, 4096)],
                          ids=["q4k_4096x11008", "q4k_11008x4096", "q6k_4096x11008",
-                              "q80_11008x4096", "q40_4096x4096"])
+                              "q80_11008x4096", "q40_4096x4096", "q6k_32000x4096_head"])
 def test_linear_full_size(dev, host, oracle, mem, t, rows, cols):
     w = V.synth_matrix(host, t, rows, cols, SEED, 31)
     x = synth_x(host, cols)

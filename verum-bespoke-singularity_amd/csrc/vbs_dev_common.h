@@ -33,6 +33,24 @@ __device__ __forceinline__ uint16_t ld16(const uint8_t *p) {
 }
 __device__ __forceinline__ float h2f(uint16_t h) { return vbs_h2f(h); }
 
+// The reference's dequantiser runs on the host's SSE arithmetic, whose NaN
+// results follow two rules: a NaN operand comes back quieted with its sign and
+// payload (the first operand when both are NaN), and an invalid operation
+// (0 x inf, inf - inf) gives the negative default NaN 0xFFC00000. The VALU
+// differs on both (a subtraction adds the negated operand, so a NaN
+// subtrahend changes sign; its default NaN is positive), so the block
+// decoders rebuild NaN results by the host's rules: NaN scales in a GGUF block
+// then dequantise to the same words as on the host.
+__device__ __forceinline__ float nan_as_host(float r, float a, float b) {
+    if (!__builtin_isnan(r)) return r;
+    if (__builtin_isnan(a)) return vbs_half_bits_to_float(vbs_float_to_bits(a) | 0x00400000u);
+    if (__builtin_isnan(b)) return vbs_half_bits_to_float(vbs_float_to_bits(b) | 0x00400000u);
+    return vbs_half_bits_to_float(0xFFC00000u);
+}
+__device__ __forceinline__ float hmul(float a, float b) { return nan_as_host(__fmul_rn(a, b), a, b); }
+__device__ __forceinline__ float hadd(float a, float b) { return nan_as_host(__fadd_rn(a, b), a, b); }
+__device__ __forceinline__ float hsub(float a, float b) { return nan_as_host(__fsub_rn(a, b), a, b); }
+
 // 6-bit scale and min of sub-block j of a Q4_K super-block
 // (src/vbs_dequant.c:225-233).
 __device__ __forceinline__ void q4k_scale_min(const uint8_t *s, int j, int &sc, int &mn) {
@@ -58,16 +76,16 @@ template <> __device__ __forceinline__ float deq_elem<kQ4_0>(const uint8_t *b, u
     float d = h2f(ld16(b));
     uint8_t byte = b[2 + (e & 15)];
     int nib = e < 16 ? (byte & 15) : (byte >> 4);
-    return __fmul_rn((float)nib - 8.0f, d);
+    return hmul(__fsub_rn((float)nib, 8.0f), d);
 }
 template <> __device__ __forceinline__ float deq_elem<kQ4_1>(const uint8_t *b, uint32_t e) {
     float d = h2f(ld16(b)), m = h2f(ld16(b + 2));
     uint8_t byte = b[4 + (e & 15)];
     int nib = e < 16 ? (byte & 15) : (byte >> 4);
-    return __fadd_rn(__fmul_rn(d, (float)nib), m);
+    return hadd(hmul(d, (float)nib), m);
 }
 template <> __device__ __forceinline__ float deq_elem<kQ8_0>(const uint8_t *b, uint32_t e) {
-    return __fmul_rn(h2f(ld16(b)), (float)(int8_t)b[2 + e]);
+    return hmul(h2f(ld16(b)), (float)(int8_t)b[2 + e]);
 }
 template <> __device__ __forceinline__ float deq_elem<kQ4_K>(const uint8_t *b, uint32_t e) {
     float d = h2f(ld16(b)), dmin = h2f(ld16(b + 2));
@@ -75,7 +93,7 @@ template <> __device__ __forceinline__ float deq_elem<kQ4_K>(const uint8_t *b, u
     q4k_scale_min(b + 4, (int)(e >> 5), sc, mn);
     uint8_t byte = b[16 + 32 * (e >> 6) + (e & 31)];
     int nib = (e & 32) ? (byte >> 4) : (byte & 15);
-    return __fsub_rn(__fmul_rn(__fmul_rn(d, (float)sc), (float)nib), __fmul_rn(dmin, (float)mn));
+    return hsub(hmul(hmul(d, (float)sc), (float)nib), hmul(dmin, (float)mn));
 }
 template <> __device__ __forceinline__ float deq_elem<kQ6_K>(const uint8_t *b, uint32_t e) {
     uint32_t h = e >> 7, q = (e >> 5) & 3, l = e & 31;
@@ -84,7 +102,7 @@ template <> __device__ __forceinline__ float deq_elem<kQ6_K>(const uint8_t *b, u
     int v = (lo | (hi << 4)) - 32;
     float d = h2f(ld16(b + 208));
     float sc = (float)(int8_t)b[192 + 8 * h + 2 * q + (l >> 4)];
-    return __fmul_rn(__fmul_rn(d, sc), (float)v);
+    return hmul(hmul(d, sc), (float)v);
 }
 // LNS8 (src/vbs_host_math.h:111-121): 32 log-codes then an f32 scale at byte
 // 32; value = exp2f(q) * scale. exp2f of an integer code is the exact power
@@ -93,7 +111,7 @@ template <> __device__ __forceinline__ float deq_elem<kLNS8>(const uint8_t *b, u
     uint32_t q = b[e];
     float p = q < 128u ? vbs_half_bits_to_float((q + 127u) << 23) : INFINITY;
     float scale = *reinterpret_cast<const float *>(b + 32);
-    return __fmul_rn(p, scale);
+    return hmul(p, scale);
 }
 
 // Sum over the 64 lanes of a wavefront; every lane receives the total.
