@@ -214,17 +214,32 @@ static void dq_q4_k(const uint8_t *b, float *y) {
  * low 4 bits from ql[64h + 32(q&1) + l] (shifted by 4 for q >= 2), high 2
  * bits from qh[32h + l] >> 2q; scale index 8h + 2q + l/16.
  * value = ((d * sc) * (q6 - 32)). */
+/* quarter q (0..3) of half h: constant shifts, so the 32-element loop
+ * vectorises; element l takes scale 8h + 2q + l/16, formed as d * scale once
+ * per 16 elements (the same product the reference forms per element) */
+#define DQ_Q6K_QUARTER(Q)                                                          \
+    do {                                                                           \
+        const uint8_t *lq = ql + 64 * h + 32 * ((Q) & 1);                          \
+        const uint8_t *hq = qh + 32 * h;                                           \
+        float *yq = y + 128 * h + 32 * (Q);                                        \
+        float a0 = d * (float)sc[8 * h + 2 * (Q)], a1 = d * (float)sc[8 * h + 2 * (Q) + 1]; \
+        for (int l = 0; l < 32; l++) {                                             \
+            int lo = (lq[l] >> ((Q) >= 2 ? 4 : 0)) & 15;                           \
+            int hi2 = (hq[l] >> (2 * (Q))) & 3;                                    \
+            int v = (lo | (hi2 << 4)) - 32;                                        \
+            yq[l] = (l < 16 ? a0 : a1) * (float)v;                                 \
+        }                                                                          \
+    } while (0)
+
 static void dq_q6_k(const uint8_t *b, float *y) {
     const uint8_t *ql = b, *qh = b + 128;
     const int8_t *sc = (const int8_t *)(b + 192);
     float d = vbs_oracle_f16_to_f32(rd16(b + 208));
-    for (int e = 0; e < 256; e++) {
-        int h = e >> 7, q = (e >> 5) & 3, l = e & 31;
-        int lo = (ql[64 * h + 32 * (q & 1) + l] >> (q >= 2 ? 4 : 0)) & 15;
-        int hi2 = (qh[32 * h + l] >> (2 * q)) & 3;
-        int v = (lo | (hi2 << 4)) - 32;
-        float a = d * (float)sc[8 * h + 2 * q + (l >> 4)];
-        y[e] = a * (float)v;
+    for (int h = 0; h < 2; h++) {
+        DQ_Q6K_QUARTER(0);
+        DQ_Q6K_QUARTER(1);
+        DQ_Q6K_QUARTER(2);
+        DQ_Q6K_QUARTER(3);
     }
 }
 
@@ -280,9 +295,36 @@ static int linear_rows(int type, const uint8_t *w, const float *x, float *y, uin
     uint32_t epb, bpb;
     if (!vbs_oracle_geometry(type, &epb, &bpb) || cols % epb) return 0;
     uint64_t rb = (uint64_t)(cols / epb) * bpb;
-    float vals[256];
+    float vals[4][256];
     const float *xs = x + col_off;
-    for (uint32_t r = r0; r < r1; r++) {
+    /* four rows at a time: each keeps its own double sum over its elements in
+     * order (the rows' sums are independent chains, so they overlap in the
+     * pipeline; no row's arithmetic changes) */
+    uint32_t r = r0;
+    if (type != T_F32 && type != T_F16) {
+        for (; r + 4 <= r1; r += 4) {
+            double acc[4] = {0.0, 0.0, 0.0, 0.0};
+            for (uint32_t b = 0; b < cols / epb; b++) {
+                const float *xb = xs + (size_t)b * epb;
+                for (int k = 0; k < 4; k++) {
+                    const uint8_t *blk = w + (uint64_t)(r + k) * rb + (uint64_t)b * bpb;
+                    if (vbs_oracle_dequant_block(type, blk, vals[k]) != (int)epb) return 0;
+                }
+                for (uint32_t i = 0; i < epb; i++) {
+                    double xi = xb[i];
+                    acc[0] += (double)vals[0][i] * xi;
+                    acc[1] += (double)vals[1][i] * xi;
+                    acc[2] += (double)vals[2][i] * xi;
+                    acc[3] += (double)vals[3][i] * xi;
+                }
+            }
+            for (int k = 0; k < 4; k++) {
+                float *dst = y + row_off + r + k;
+                *dst = accumulate ? *dst + (float)acc[k] : (float)acc[k];
+            }
+        }
+    }
+    for (; r < r1; r++) {
         const uint8_t *row = w + (uint64_t)r * rb;
         double acc = 0.0;
         for (uint32_t b = 0; b < cols / epb; b++) {
@@ -295,8 +337,8 @@ static int linear_rows(int type, const uint8_t *w, const float *x, float *y, uin
             } else if (type == T_F16) {
                 acc += (double)vbs_oracle_f16_to_f32(rd16(blk)) * xb[0];
             } else {
-                if (vbs_oracle_dequant_block(type, blk, vals) != (int)epb) return 0;
-                for (uint32_t i = 0; i < epb; i++) acc += (double)vals[i] * xb[i];
+                if (vbs_oracle_dequant_block(type, blk, vals[0]) != (int)epb) return 0;
+                for (uint32_t i = 0; i < epb; i++) acc += (double)vals[0][i] * xb[i];
             }
         }
         float *dst = y + row_off + r;
@@ -414,17 +456,25 @@ void vbs_oracle_cache_store(const float *k, const float *v, uint16_t *kc, uint16
     }
 }
 
-/* src/vbs_host_math.h:170-209: for each q head h (kv head h / group):
- * sequential online softmax over s < seq_len with score = (float)(double
- * dot) * scale, m starting at -FLT_MAX, r = expf(m - m'), e = expf(score -
- * m'), l = l*r + e, acc = acc*r + e*v; out = acc * (1 / l). */
-void vbs_oracle_attention(const float *q, const uint16_t *kc, const uint16_t *vc, float *out,
-                          uint32_t seq_len, uint32_t layer, uint32_t max_ctx, uint32_t nqh,
-                          uint32_t nkh, uint32_t hd, float scale) {
-    if (!nkh || !nqh || !hd) return;
-    uint32_t group = nqh / nkh ? nqh / nkh : 1;
-    uint64_t lbase = (uint64_t)layer * max_ctx * nkh * hd;
-    for (uint32_t h = 0; h < nqh; h++) {
+/* Every half as a float, built once by vbs_oracle_f16_to_f32 itself: the
+ * attention below reads keys and values through it (the same values, without
+ * a call and its branches per cached element). */
+static float g_half_table[65536];
+static pthread_once_t g_half_once = PTHREAD_ONCE_INIT;
+static void half_table_init(void) {
+    for (uint32_t h = 0; h < 65536u; h++) g_half_table[h] = vbs_oracle_f16_to_f32((uint16_t)h);
+}
+
+/* src/vbs_host_math.h:170-209 for q heads [h0, h1): for each q head h (kv
+ * head h / group): sequential online softmax over s < seq_len with score =
+ * (float)(double dot) * scale, m starting at -FLT_MAX, r = expf(m - m'),
+ * e = expf(score - m'), l = l*r + e, acc = acc*r + e*v; out = acc * (1 / l).
+ * Heads are independent, so splitting them over threads changes no result. */
+static void attention_heads(const float *q, const uint16_t *kc, const uint16_t *vc, float *out,
+                            uint32_t seq_len, uint64_t lbase, uint32_t nkh, uint32_t hd,
+                            uint32_t group, float scale, uint32_t h0, uint32_t h1) {
+    const float *f16 = g_half_table;
+    for (uint32_t h = h0; h < h1; h++) {
         const float *qh = q + (size_t)h * hd;
         float *acc = out + (size_t)h * hd;
         uint32_t kvh = h / group;
@@ -433,8 +483,7 @@ void vbs_oracle_attention(const float *q, const uint16_t *kc, const uint16_t *vc
         for (uint32_t s = 0; s < seq_len; s++) {
             uint64_t at = lbase + ((uint64_t)s * nkh + kvh) * hd;
             double dot = 0.0;
-            for (uint32_t d = 0; d < hd; d++)
-                dot += (double)qh[d] * (double)vbs_oracle_f16_to_f32(kc[at + d]);
+            for (uint32_t d = 0; d < hd; d++) dot += (double)qh[d] * (double)f16[kc[at + d]];
             float score = (float)dot * scale;
             float mn = score > m ? score : m;
             float r = expf(m - mn);
@@ -443,7 +492,7 @@ void vbs_oracle_attention(const float *q, const uint16_t *kc, const uint16_t *vc
             l = lr + e;
             m = mn;
             for (uint32_t d = 0; d < hd; d++) {
-                float vv = vbs_oracle_f16_to_f32(vc[at + d]);
+                float vv = f16[vc[at + d]];
                 float ar = acc[d] * r, ev = e * vv;
                 acc[d] = ar + ev;
             }
@@ -451,6 +500,54 @@ void vbs_oracle_attention(const float *q, const uint16_t *kc, const uint16_t *vc
         float inv = 1.0f / l;
         for (uint32_t d = 0; d < hd; d++) acc[d] *= inv;
     }
+}
+
+typedef struct {
+    const float *q; const uint16_t *kc, *vc; float *out;
+    uint32_t seq_len; uint64_t lbase; uint32_t nkh, hd, group; float scale; uint32_t h0, h1;
+} attn_job_t;
+
+static void *attn_worker(void *a) {
+    attn_job_t *j = (attn_job_t *)a;
+    attention_heads(j->q, j->kc, j->vc, j->out, j->seq_len, j->lbase, j->nkh, j->hd, j->group,
+                    j->scale, j->h0, j->h1);
+    return NULL;
+}
+
+void vbs_oracle_attention_mt(const float *q, const uint16_t *kc, const uint16_t *vc, float *out,
+                             uint32_t seq_len, uint32_t layer, uint32_t max_ctx, uint32_t nqh,
+                             uint32_t nkh, uint32_t hd, float scale, int nthreads) {
+    if (!nkh || !nqh || !hd) return;
+    pthread_once(&g_half_once, half_table_init);
+    uint32_t group = nqh / nkh ? nqh / nkh : 1;
+    uint64_t lbase = (uint64_t)layer * max_ctx * nkh * hd;
+    if (nthreads > 64) nthreads = 64;
+    if (nthreads > (int)nqh) nthreads = (int)nqh;
+    if (nthreads <= 1) {
+        attention_heads(q, kc, vc, out, seq_len, lbase, nkh, hd, group, scale, 0, nqh);
+        return;
+    }
+    pthread_t th[64];
+    attn_job_t jobs[64];
+    uint32_t per = (nqh + (uint32_t)nthreads - 1) / (uint32_t)nthreads;
+    int n = 0;
+    for (int t = 0; t < nthreads; t++) {
+        uint32_t h0 = (uint32_t)t * per, h1 = h0 + per < nqh ? h0 + per : nqh;
+        if (h0 >= h1) break;
+        jobs[n] = (attn_job_t){q, kc, vc, out, seq_len, lbase, nkh, hd, group, scale, h0, h1};
+        if (pthread_create(&th[n], NULL, attn_worker, &jobs[n]) != 0) {
+            attention_heads(q, kc, vc, out, seq_len, lbase, nkh, hd, group, scale, h0, h1);
+            continue;
+        }
+        n++;
+    }
+    for (int t = 0; t < n; t++) pthread_join(th[t], NULL);
+}
+
+void vbs_oracle_attention(const float *q, const uint16_t *kc, const uint16_t *vc, float *out,
+                          uint32_t seq_len, uint32_t layer, uint32_t max_ctx, uint32_t nqh,
+                          uint32_t nkh, uint32_t hd, float scale) {
+    vbs_oracle_attention_mt(q, kc, vc, out, seq_len, layer, max_ctx, nqh, nkh, hd, scale, 1);
 }
 
 /* ------------------------------------------------------------------ */
@@ -481,8 +578,8 @@ int vbs_oracle_forward_token(const vbs_oracle_model_t *m, uint32_t token, uint32
         vbs_oracle_rope(kb, pos, hd, m->n_kv_heads, m->rope_theta);
         ok &= vbs_oracle_linear_tile_mt(t[2], w[2], normed, vb, H, kvd, 0, 0, 0, nt);
         vbs_oracle_cache_store(kb, vb, m->kc, m->vc, pos, L, m->max_ctx, kvd);
-        vbs_oracle_attention(qb, m->kc, m->vc, ab, pos + 1, L, m->max_ctx, m->n_heads,
-                             m->n_kv_heads, hd, scale);
+        vbs_oracle_attention_mt(qb, m->kc, m->vc, ab, pos + 1, L, m->max_ctx, m->n_heads,
+                                m->n_kv_heads, hd, scale, nt);
         ok &= vbs_oracle_linear_tile_mt(t[3], w[3], ab, tmp, qd, H, 0, 0, 0, nt);
         vbs_oracle_add(stream, tmp, stream, H);
         vbs_oracle_rms_norm(stream, m->ffn_norm[L], normed, H, m->rms_eps);

@@ -62,6 +62,10 @@ void vbs_oracle_cache_store(const float *k, const float *v, uint16_t *kc, uint16
 void vbs_oracle_attention(const float *q, const uint16_t *kc, const uint16_t *vc, float *out,
                           uint32_t seq_len, uint32_t layer, uint32_t max_ctx, uint32_t n_q_heads,
                           uint32_t n_kv_heads, uint32_t head_dim, float scale);
+/* The same, its q heads split over up to nthreads threads (identical results). */
+void vbs_oracle_attention_mt(const float *q, const uint16_t *kc, const uint16_t *vc, float *out,
+                             uint32_t seq_len, uint32_t layer, uint32_t max_ctx, uint32_t nqh,
+                             uint32_t nkh, uint32_t hd, float scale, int nthreads);
 
 /* ---- one decode step in the specializer's order ----
  * src/vbs_specializer.c:270-349 (sequence) with the bridge's scalar
