@@ -23,8 +23,11 @@ import numpy as np
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 LIB_DIR = os.path.join(PKG_DIR, "lib")
 DEVICE_LIB = os.path.join(LIB_DIR, "libvbs_gfx950.so")
-HOST_LIB = os.path.join(LIB_DIR, "libvbs_backend_gfx950.so")
-HOT_LIB = os.path.join(LIB_DIR, "libvbs_hot_gfx950.so")
+# The two host libraries can be taken from another directory, such as the
+# sanitizer build of `make sanitize` (lib-san/); the device library cannot.
+HOST_LIB_DIR = os.environ.get("VBS_GFX950_HOST_LIB_DIR") or LIB_DIR
+HOST_LIB = os.path.join(HOST_LIB_DIR, "libvbs_backend_gfx950.so")
+HOT_LIB = os.path.join(HOST_LIB_DIR, "libvbs_hot_gfx950.so")
 
 # GGUF type ids (include/vbs_abi.h, reference include/vbs_gguf.h:13-48)
 F32, F16, Q4_0, Q4_1, Q8_0, Q8_K, Q4_K, Q5_K, Q6_K, LNS8 = 0, 1, 2, 3, 8, 15, 12, 13, 14, 40
