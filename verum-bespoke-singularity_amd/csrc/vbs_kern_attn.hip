@@ -397,6 +397,26 @@ __global__ __launch_bounds__(64 * kWaves) void k_attn_chunk(
 // The chunk's (m, l, acc) go to the same partials as the vector-ALU kernel.
 constexpr uint32_t kMfmaGran = 32, kMfmaTiles = 8, kMfmaLmax = kMfmaGran * kMfmaTiles;
 
+// The most chunks the matrix-core split gives any sequence of at most max_seq
+// positions: the chunk count grows with the sequence while the chunk length
+// stays put, so the maximum lies at the longest sequence of some chunk length
+// (32 k positions for sequences of at most 32 k * target / nkh, the last
+// length open-ended) or at max_seq itself. The chunk launch's grid: a graph
+// replay reads the position on the device, so the grid covers every
+// position up to max_seq, and workgroups beyond the current split exit at
+// once (each costs dispatch time, so the grid is no larger than this).
+inline uint32_t mfma_grid_chunks(uint32_t max_seq, uint32_t nkh) {
+    uint32_t best = 0;
+    for (uint32_t k = 1; k <= kMfmaTiles; k++) {
+        const uint64_t hi = k < kMfmaTiles ? (uint64_t)kMfmaGran * k * kMfmaTargetWgs / nkh : max_seq;
+        const uint32_t s = (uint32_t)(hi < max_seq ? hi : max_seq);
+        if (s == 0) continue;
+        const uint32_t c = attn_split(s, nkh, kMfmaGran, kMfmaLmax, kMfmaTargetWgs).n;
+        best = c > best ? c : best;
+    }
+    return best;
+}
+
 typedef _Float16 ah8 __attribute__((ext_vector_type(8)));
 typedef float af4 __attribute__((ext_vector_type(4)));
 typedef uint32_t au4 __attribute__((ext_vector_type(4)));
@@ -426,39 +446,6 @@ __global__ __launch_bounds__(64) void k_attn_mfma(const float *__restrict__ q,
     const uint64_t rstride = (uint64_t)nkh * HD;
     const uint64_t base = layer_off + (uint64_t)s0 * rstride + (uint64_t)kvh * HD;
 
-    // ---- q' of head n & 7 (heads past the group repeat head 0 and are not stored)
-    const uint32_t h = n & 7u, hq = h < group ? h : 0u;
-    float qv[4][8];
-    {
-        const float4 *qp = reinterpret_cast<const float4 *>(q + ((uint64_t)kvh * group + hq) * HD);
-#pragma unroll
-        for (uint32_t kk = 0; kk < 4; kk++) {
-            const float4 a = qp[(32u * kk + 8u * g) / 4u], b = qp[(32u * kk + 8u * g) / 4u + 1u];
-            qv[kk][0] = a.x; qv[kk][1] = a.y; qv[kk][2] = a.z; qv[kk][3] = a.w;
-            qv[kk][4] = b.x; qv[kk][5] = b.y; qv[kk][6] = b.z; qv[kk][7] = b.w;
-        }
-    }
-    float amax = 0.f;
-#pragma unroll
-    for (uint32_t kk = 0; kk < 4; kk++)
-#pragma unroll
-        for (uint32_t j = 0; j < 8; j++) amax = fmaxf(amax, fabsf(qv[kk][j]));
-    amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
-    int e2 = 0;
-    (void)frexpf(amax, &e2);  // amax < 2^e2
-    const int sq = amax > 0.f ? 15 - e2 : 0;
-    const float csc = ldexpf(scale, -sq);
-    ah8 Qb[4];
-#pragma unroll
-    for (uint32_t kk = 0; kk < 4; kk++)
-#pragma unroll
-        for (uint32_t j = 0; j < 8; j++) {
-            const float x = ldexpf(qv[kk][j], sq);
-            const _Float16 hi = (_Float16)x;
-            Qb[kk][j] = n < 8u ? hi : (_Float16)(x - (float)hi);
-        }
-
     // ---- tile loads: K rows (A operand: position 16 hf + n, dims 32 kk + 8 g ..),
     // V rows (position p_j of this lane group, dims 8 n ..); positions past the
     // chunk re-read its last row and are masked
@@ -480,14 +467,51 @@ __global__ __launch_bounds__(64) void k_attn_mfma(const float *__restrict__ q,
             vr[j] = *reinterpret_cast<const au4 *>(
                 vc + base + (uint64_t)min(pos_of(t, j), valid - 1u) * rstride + 8u * n);
     };
+    // ---- q' of head n & 7 (heads past the group repeat head 0 and are not stored)
+    const uint32_t h = n & 7u, hq = h < group ? h : 0u;
+    float qv[4][8];
+    {
+        const float4 *qp = reinterpret_cast<const float4 *>(q + ((uint64_t)kvh * group + hq) * HD);
+#pragma unroll
+        for (uint32_t kk = 0; kk < 4; kk++) {
+            const float4 a = qp[(32u * kk + 8u * g) / 4u], b = qp[(32u * kk + 8u * g) / 4u + 1u];
+            qv[kk][0] = a.x; qv[kk][1] = a.y; qv[kk][2] = a.z; qv[kk][3] = a.w;
+            qv[kk][4] = b.x; qv[kk][5] = b.y; qv[kk][6] = b.z; qv[kk][7] = b.w;
+        }
+    }
+    // the first tile's K and V rows go out with q's loads: one memory round
+    // trip before the first MMA instead of two (the scheduler may not sink
+    // them below q's arithmetic)
     load_k(0);
     load_v(0);
+    __builtin_amdgcn_sched_barrier(0);
+    float amax = 0.f;
+#pragma unroll
+    for (uint32_t kk = 0; kk < 4; kk++)
+#pragma unroll
+        for (uint32_t j = 0; j < 8; j++) amax = fmaxf(amax, fabsf(qv[kk][j]));
+    amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+    int e2 = 0;
+    (void)frexpf(amax, &e2);  // amax < 2^e2
+    const int sq = amax > 0.f ? 15 - e2 : 0;
+    const float csc = ldexpf(scale, -sq);
+    ah8 Qb[4];
+#pragma unroll
+    for (uint32_t kk = 0; kk < 4; kk++)
+#pragma unroll
+        for (uint32_t j = 0; j < 8; j++) {
+            const float x = ldexpf(qv[kk][j], sq);
+            const _Float16 hi = (_Float16)x;
+            Qb[kk][j] = n < 8u ? hi : (_Float16)(x - (float)hi);
+        }
+
 
     float m = -INFINITY, l = 0.f;
     af4 acc[8];
 #pragma unroll
     for (uint32_t t = 0; t < 8; t++) acc[t] = af4{0.f, 0.f, 0.f, 0.f};
-    for (uint32_t t = 0; t < nt; t++) {
+    auto tile = [&](uint32_t t) {
         af4 S[2];
 #pragma unroll
         for (uint32_t hf = 0; hf < 2; hf++) {
@@ -541,7 +565,9 @@ __global__ __launch_bounds__(64) void k_attn_mfma(const float *__restrict__ q,
             acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(P, __builtin_bit_cast(ah8, b), a, 0, 0, 0);
         }
         if (t + 1u < nt) load_v(t + 1u);
-    }
+    };
+    tile(0);  // peeled, so that its loads and uses share the entry block with q's
+    for (uint32_t t = 1; t < nt; t++) tile(t);
 
     // ---- the chunk's partial: l summed over the lane groups of a head, rows
     // hi + lo of acc (lane groups g and g + 2), stored by lane groups 0 and 1
@@ -657,6 +683,80 @@ __global__ __launch_bounds__(kMergeThreads) void k_attn_merge(const float *__res
     }
 }
 
+// Merge for head_dim 128 (the matrix-core chunk kernel's partials): one
+// workgroup of four waves per q head (grid y: the sequences of a batch). Every
+// wave loads all chunks' (m, l) (lanes c, c + 64, ...) and forms M = max m_c,
+// w_c = e^(m_c - M) and L = sum l_c w_c itself; wave w then takes chunks
+// w, w + 4, ... for head dims 2 lane and 2 lane + 1 (their acc rows loaded at
+// once), and one LDS pass adds the four waves' sums in order. No loads wait
+// on a reduction and one barrier ends it (the general merge above has four).
+constexpr uint32_t kMerge4Waves = 4, kMerge4Batch = 32;  // chunks per wave held in registers
+
+__global__ __launch_bounds__(64 * kMerge4Waves) void k_attn_merge_h128(
+    const float *__restrict__ part, float *__restrict__ out, uint32_t stride_chunks,
+    const uint32_t *__restrict__ pos_dev, uint32_t seq_len, uint32_t nkh, uint32_t q_bstride,
+    uint64_t part_bstride) {
+    constexpr uint32_t HD = 128, RS = HD + 2u;  // partial row: m, l, acc[HD]
+    __shared__ float2 red[kMerge4Waves][64];
+    const uint32_t h = blockIdx.x, bz = blockIdx.y, lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    part += bz * part_bstride;
+    out += (uint64_t)bz * q_bstride;
+    if (pos_dev) seq_len = pos_dev[bz] + 1u;  // seq = pos + 1
+    const uint32_t nc = attn_split(seq_len, nkh, kMfmaGran, kMfmaLmax, kMfmaTargetWgs).n;
+    const float *ph = part + (uint64_t)h * stride_chunks * RS;
+    float2 av[kMerge4Batch];
+#pragma unroll
+    for (uint32_t k = 0; k < kMerge4Batch; k++) {
+        const uint32_t c = wave + kMerge4Waves * k;
+        av[k] = c < nc ? *reinterpret_cast<const float2 *>(ph + (uint64_t)c * RS + 2u + 2u * lane)
+                       : make_float2(0.f, 0.f);
+    }
+    float M = -INFINITY;
+    for (uint32_t c = lane; c < nc; c += 64u) M = fmaxf(M, ph[(uint64_t)c * RS]);
+    M = wave_max(M);
+    float L = 0.f, w_lane = 0.f;  // w_lane: weight of chunk `lane` (the first 64 chunks)
+    for (uint32_t c = lane; c < nc; c += 64u) {
+        const float mc = ph[(uint64_t)c * RS];
+        const float wc = mc == -INFINITY ? 0.f : fast_exp(__fsub_rn(mc, M));
+        if (c == lane) w_lane = wc;
+        L = fmaf(ph[(uint64_t)c * RS + 1u], wc, L);
+    }
+    L = wave_sum(L);
+    float ox = 0.f, oy = 0.f;
+    auto add = [&](uint32_t c, float2 a) {
+        float wc;
+        if (c < 64u) {
+            wc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w_lane),
+                                                                     (int)c));
+        } else {
+            const float mc = ph[(uint64_t)c * RS];
+            wc = mc == -INFINITY ? 0.f : fast_exp(__fsub_rn(mc, M));
+        }
+        ox = fmaf(a.x, wc, ox);
+        oy = fmaf(a.y, wc, oy);
+    };
+#pragma unroll
+    for (uint32_t k = 0; k < kMerge4Batch; k++) {
+        const uint32_t c = wave + kMerge4Waves * k;
+        if (c < nc) add(c, av[k]);
+    }
+    for (uint32_t c = wave + kMerge4Waves * kMerge4Batch; c < nc; c += kMerge4Waves)
+        add(c, *reinterpret_cast<const float2 *>(ph + (uint64_t)c * RS + 2u + 2u * lane));
+    red[wave][lane] = make_float2(ox, oy);
+    __syncthreads();
+    if (wave == 0) {
+        float2 a = red[0][lane];
+#pragma unroll
+        for (uint32_t w = 1; w < kMerge4Waves; w++) {
+            a.x += red[w][lane].x;
+            a.y += red[w][lane].y;
+        }
+        const float inv = __fdiv_rn(1.0f, L);
+        *reinterpret_cast<float2 *>(out + (uint64_t)h * HD + 2u * lane) =
+            make_float2(__fmul_rn(a.x, inv), __fmul_rn(a.y, inv));
+    }
+}
+
 size_t attention_partial_bytes(uint32_t max_seq, uint32_t nqh, uint32_t nkh, uint32_t hd) {
     return (size_t)nqh * attn_max_chunks(max_seq, nkh) * (hd + 2u) * sizeof(float);
 }
@@ -702,10 +802,12 @@ hipError_t launch_attention(const float *q, const uint16_t *kc, const uint16_t *
     uint32_t gran = kChunk, lmax = kChunk, target = kTargetWgs;
     const dim3 grid(stride, nkh);
     if (fast && hd == 128u) {
-        gran = kMfmaGran, lmax = kMfmaLmax, target = kMfmaTargetWgs;
-        k_attn_mfma<<<grid, 64, 0, s>>>(q, kc, vc, part, seq_len, pos_dev, layer_off, nkh, group,
-                                        scale, stride, 0u, 0ull, 0ull);
-        e = hipGetLastError();
+        k_attn_mfma<<<dim3(mfma_grid_chunks(seq_len, nkh), nkh), 64, 0, s>>>(
+            q, kc, vc, part, seq_len, pos_dev, layer_off, nkh, group, scale, stride, 0u, 0ull, 0ull);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        k_attn_merge_h128<<<nqh, 64 * kMerge4Waves, 0, s>>>(part, out, stride, pos_dev, seq_len, nkh,
+                                                            0u, 0ull);
+        return hipGetLastError();
     } else if (fast && hd == 32u) {
         gran = ChunkShape<32>::GRAN, lmax = ChunkShape<32>::LMAX;
         e = launch_chunk_hd<32>(grid, s, q, kc, vc, part, seq_len, pos_dev, layer_off, nkh, group,
@@ -756,16 +858,13 @@ hipError_t launch_attention_batch(const float *q, const uint16_t *kc, const uint
         return hipSuccess;
     }
     const uint32_t stride = attn_max_chunks(max_seq, nkh);
-    k_attn_mfma<<<dim3(stride, nkh, batch), 64, 0, s>>>(q, kc, vc, part, max_seq, pos_dev, layer_off,
-                                                        nkh, group, scale, stride, q_stride,
-                                                        kv_stride, pstride);
+    k_attn_mfma<<<dim3(mfma_grid_chunks(max_seq, nkh), nkh, batch), 64, 0, s>>>(
+        q, kc, vc, part, max_seq, pos_dev, layer_off, nkh, group, scale, stride, q_stride, kv_stride,
+        pstride);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const uint32_t n_chunks = attn_split(max_seq, nkh, kMfmaGran, kMfmaLmax, kMfmaTargetWgs).n;
-    const size_t mlds = ((size_t)stride + kMergeThreads) * sizeof(float);
-    k_attn_merge<<<dim3(nqh, batch), kMergeThreads, mlds, s>>>(part, out, hd, n_chunks, stride,
-                                                               pos_dev, nkh, kMfmaGran, kMfmaLmax,
-                                                               kMfmaTargetWgs, q_stride, pstride);
+    k_attn_merge_h128<<<dim3(nqh, batch), 64 * kMerge4Waves, 0, s>>>(part, out, stride, pos_dev,
+                                                                     max_seq, nkh, q_stride, pstride);
     return hipGetLastError();
 }
 
