@@ -15,8 +15,10 @@
 //     the host fills with the reference's own expressions and libm;
 //   * the KV store and attention compute their offsets / sequence length from
 //     the device position;
-//   * the argmax kernel writes the next token, records it, and advances the
-//     position.
+//   * the argmax kernel writes the next token, records it, advances the
+//     position and gathers the next token's embedding into the residual
+//     stream, so the graph starts at the first layer (the host gathers the
+//     first token's embedding before the first replay).
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -86,17 +88,27 @@ __device__ __forceinline__ Top2 top2_merge(Top2 a, Top2 b) {
 
 // One workgroup per sequence b of a batch (gridDim.x sequences): logits row b,
 // state token_dev[b], pos_dev[b], step_dev[b], outputs tokens[step * nb + b].
+// It then writes the next step's input, row `token` of the embedding table
+// (type T, src/vbs_host_math.h:94-142, as k_dequant_rows computes it), to
+// x + b * dim: the gather that would otherwise open the next step's graph.
+constexpr uint32_t kArgVec = 8, kArgScalar = 16;  // loads per thread in flight per pass
+
+template <int T>
 __global__ __launch_bounds__(1024) void k_argmax_advance(const float *__restrict__ logits,
                                                          uint32_t n, uint32_t *token_dev,
                                                          uint32_t *pos_dev, uint32_t *step_dev,
                                                          uint32_t *tokens, float *margins,
-                                                         uint32_t max_steps) {
+                                                         uint32_t max_steps,
+                                                         const uint8_t *__restrict__ embd,
+                                                         uint64_t embd_rb, uint32_t dim,
+                                                         float *__restrict__ x) {
     __shared__ Top2 red[16];
     const uint32_t sb = blockIdx.x, nb = gridDim.x;
     logits += (uint64_t)sb * n;
     token_dev += sb;
     pos_dev += sb;
     step_dev += sb;
+    x += (uint64_t)sb * dim;
     Top2 t{-INFINITY, 0xFFFFFFFFu, -INFINITY};
     auto consider = [&](float v, uint32_t i) {
         if (v != v && i != 0u) return;  // a NaN never beats anything after index 0
@@ -109,20 +121,43 @@ __global__ __launch_bounds__(1024) void k_argmax_advance(const float *__restrict
         }
     };
     // each thread scans its indices in increasing order: 16-byte chunks
-    // c, c + 1024, ... when the logits allow it, single floats otherwise
-    const bool vec = (n % 4u) == 0 && ((uintptr_t)logits & 15u) == 0;
-    if (vec) {
+    // c, c + 1024, ... when the logits allow it, single floats otherwise; a
+    // pass requests all of its loads before it looks at any value
+    if ((n % 4u) == 0 && ((uintptr_t)logits & 15u) == 0) {
         const float4 *l4 = reinterpret_cast<const float4 *>(logits);
-#pragma unroll 8
-        for (uint32_t c = threadIdx.x; c < n / 4u; c += 1024u) {
-            const float4 f = l4[c];
-            consider(f.x, 4u * c);
-            consider(f.y, 4u * c + 1u);
-            consider(f.z, 4u * c + 2u);
-            consider(f.w, 4u * c + 3u);
+        const uint32_t n4 = n / 4u;
+        for (uint32_t c0 = threadIdx.x; c0 < n4; c0 += 1024u * kArgVec) {
+            float4 f[kArgVec];
+#pragma unroll
+            for (uint32_t k = 0; k < kArgVec; k++) {
+                const uint32_t c = c0 + 1024u * k;
+                f[k] = c < n4 ? l4[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (uint32_t k = 0; k < kArgVec; k++) {
+                const uint32_t c = c0 + 1024u * k;
+                if (c < n4) {
+                    consider(f[k].x, 4u * c);
+                    consider(f[k].y, 4u * c + 1u);
+                    consider(f[k].z, 4u * c + 2u);
+                    consider(f[k].w, 4u * c + 3u);
+                }
+            }
         }
     } else {
-        for (uint32_t i = threadIdx.x; i < n; i += 1024u) consider(logits[i], i);
+        for (uint32_t i0 = threadIdx.x; i0 < n; i0 += 1024u * kArgScalar) {
+            float f[kArgScalar];
+#pragma unroll
+            for (uint32_t k = 0; k < kArgScalar; k++) {
+                const uint32_t i = i0 + 1024u * k;
+                f[k] = i < n ? logits[i] : 0.f;
+            }
+#pragma unroll
+            for (uint32_t k = 0; k < kArgScalar; k++) {
+                const uint32_t i = i0 + 1024u * k;
+                if (i < n) consider(f[k], i);
+            }
+        }
     }
     // wave butterflies, then the 16 wave results in one wave
     auto wave_merge = [](Top2 v, uint32_t width) {
@@ -145,16 +180,48 @@ __global__ __launch_bounds__(1024) void k_argmax_advance(const float *__restrict
         if (lane == 0) red[0] = w;
     }
     __syncthreads();
+    const uint32_t tok = red[0].i1;
     if (threadIdx.x == 0) {
         const uint32_t step = step_dev[0];
         if (step < max_steps) {
-            tokens[step * nb + sb] = red[0].i1;
+            tokens[step * nb + sb] = tok;
             margins[step * nb + sb] = red[0].v1 - red[0].v2;
         }
-        token_dev[0] = red[0].i1;
+        token_dev[0] = tok;
         pos_dev[0] = pos_dev[0] + 1u;
         step_dev[0] = step + 1u;
     }
+    if (tok < n) {  // (always: index 0 is taken even when every logit is NaN)
+        const uint8_t *row = embd + (uint64_t)tok * embd_rb;
+        for (uint32_t e = threadIdx.x; e < dim; e += 1024u)
+            x[e] = deq_elem<T>(row + (uint64_t)(e / Geo<T>::E) * Geo<T>::B, e % Geo<T>::E);
+    }
+}
+
+// The argmax of `nb` logit rows of n (the vocabulary) and, for each, the
+// embedding of the chosen token into x + b * dim (table of type `type`).
+static hipError_t launch_argmax_embed(int type, const float *logits, uint32_t n, uint32_t nb,
+                                      uint32_t *token_dev, uint32_t *pos_dev, uint32_t *step_dev,
+                                      uint32_t *tokens, float *margins, uint32_t max_steps,
+                                      const void *embd, uint32_t dim, float *x, hipStream_t s) {
+    const uint64_t rb = row_bytes(type, dim);
+    const uint8_t *e = (const uint8_t *)embd;
+#define VBS_ARGMAX(TT)                                                                             \
+    k_argmax_advance<TT><<<nb, 1024, 0, s>>>(logits, n, token_dev, pos_dev, step_dev, tokens,      \
+                                             margins, max_steps, e, rb, dim, x)
+    switch (type) {
+        case kF32: VBS_ARGMAX(kF32); break;
+        case kF16: VBS_ARGMAX(kF16); break;
+        case kQ4_0: VBS_ARGMAX(kQ4_0); break;
+        case kQ4_1: VBS_ARGMAX(kQ4_1); break;
+        case kQ8_0: VBS_ARGMAX(kQ8_0); break;
+        case kQ4_K: VBS_ARGMAX(kQ4_K); break;
+        case kQ6_K: VBS_ARGMAX(kQ6_K); break;
+        case kLNS8: VBS_ARGMAX(kLNS8); break;
+        default: return hipErrorInvalidValue;
+    }
+#undef VBS_ARGMAX
+    return hipGetLastError();
 }
 
 // ---- decoder -------------------------------------------------------------------
@@ -188,8 +255,8 @@ static hipError_t enqueue_step(const Decoder &d, hipStream_t s) {
         hipError_t e_ = (expr);           \
         if (e_ != hipSuccess) return e_;  \
     } while (0)
-    VBS_TRY(launch_dequant_rows(m.embd_type, (const uint8_t *)m.tok_embd, token_dev, 0, 1, H,
-                                d.stream, s));
+    // the stream holds the token's embedding already (written by the previous
+    // step's argmax, or by decoder_start for the first step)
     for (uint32_t L = 0; L < m.n_layers; L++) {
         const int *t = d.wtype.data() + 7 * L;
         const uint8_t *const *w = (const uint8_t *const *)d.wdata.data() + 7 * L;
@@ -258,9 +325,8 @@ static hipError_t enqueue_step(const Decoder &d, hipStream_t s) {
     } else {
         VBS_TRY(e);
     }
-    k_argmax_advance<<<1, 1024, 0, s>>>(d.logits, m.vocab, token_dev, pos_dev, step_dev,
-                                        d.tokens, d.margins, d.max_steps);
-    VBS_TRY(hipGetLastError());
+    VBS_TRY(launch_argmax_embed(m.embd_type, d.logits, m.vocab, 1, token_dev, pos_dev, step_dev,
+                                d.tokens, d.margins, d.max_steps, m.tok_embd, H, d.stream, s));
 #undef VBS_TRY
     return hipSuccess;
 }
@@ -386,6 +452,9 @@ static int set_state(Decoder *d, uint32_t token, uint32_t pos) {
     hipStream_t s = rt_stream();
     return rt_hip_ok(hipMemcpyAsync(d->state, st, sizeof(st), hipMemcpyHostToDevice, s),
                      "decoder: state") &&
+           rt_hip_ok(launch_dequant_rows(d->m.embd_type, (const uint8_t *)d->m.tok_embd, d->state,
+                                         0, 1, d->m.hidden, d->stream, s),
+                     "decoder: first embedding") &&
            rt_hip_ok(hipStreamSynchronize(s), "decoder: state");
 }
 
@@ -537,7 +606,8 @@ static hipError_t enqueue_step_batch(const BDecoder &d, hipStream_t s) {
         hipError_t e_ = (expr);           \
         if (e_ != hipSuccess) return e_;  \
     } while (0)
-    VBS_TRY(launch_dequant_rows(m.embd_type, (const uint8_t *)m.tok_embd, token_dev, 0, B, H, d.x, s));
+    // x holds every sequence's token embedding already (the previous step's
+    // argmax, or bdecoder_run for the first step)
     const uint32_t units = qd / 2u + kvd;
     for (uint32_t L = 0; L < m.n_layers; L++) {
         const int *t = d.wtype.data() + 7 * L;
@@ -580,9 +650,8 @@ static hipError_t enqueue_step_batch(const BDecoder &d, hipStream_t s) {
         float *const y[1] = {d.logits};
         VBS_TRY(launch_mvb(m.head_type, 1, wh, rows, y, ys, 0, d.xp, H, B, s));
     }
-    k_argmax_advance<<<B, 1024, 0, s>>>(d.logits, V, token_dev, pos_dev, step_dev, d.tokens,
-                                        d.margins, d.max_steps);
-    VBS_TRY(hipGetLastError());
+    VBS_TRY(launch_argmax_embed(m.embd_type, d.logits, V, B, token_dev, pos_dev, step_dev,
+                                d.tokens, d.margins, d.max_steps, m.tok_embd, H, d.x, s));
 #undef VBS_TRY
     return hipSuccess;
 }
@@ -731,7 +800,10 @@ static int bdecoder_run(void *handle, const uint32_t *tokens0, const uint32_t *p
     }
     hipStream_t s = rt_stream();
     if (!rt_hip_ok(hipMemcpyAsync(d->state, st.data(), st.size() * 4, hipMemcpyHostToDevice, s),
-                   "bdecoder_greedy: state"))
+                   "bdecoder_greedy: state") ||
+        !rt_hip_ok(launch_dequant_rows(d->m.embd_type, (const uint8_t *)d->m.tok_embd, d->state, 0,
+                                       B, d->m.hidden, d->x, s),
+                   "bdecoder_greedy: first embeddings"))
         return 0;
     for (uint32_t i = 0; i < n; i++) {
         if (!rt_hip_ok(eager ? enqueue_step_batch(*d, s) : hipGraphLaunch(d->exec, s),
