@@ -747,6 +747,10 @@ static hipError_t launch_ks(const MvArgs &a, const MvPlan &p, uint32_t wgs, hipS
         if (p.ks == 14u) VBS_MV(14, 512);
         if (p.ks == 1u) VBS_MV(1, 1024);
     }
+    if constexpr (EPI == E_QKV) {  // the Q/K/V plans of launch_plan
+        if (TPW == 2u && p.ks == 1u) VBS_MV(1, 1024);
+        if (TPW == 1u && p.ks == 8u && p.nw <= 4u) VBS_MV(8, 256);
+    }
     VBS_MV(8, 1024);
 #undef VBS_MV
 }
@@ -768,6 +772,23 @@ static hipError_t launch_plan(const MvArgs &a, hipStream_t s) {
         if (nblk <= 16u && (total <= 384u || (T::BYTES == 210u && total < 1024u))) {
             p.ks = 1u;
             p.nw = nblk;
+        }
+    }
+    // Fused RMSNorm + Q/K/V launches (measured over the tile and block splits
+    // this kernel offers, weights streamed from HBM): rows of at most 16
+    // blocks (7B) take two tiles per workgroup on sixteen waves of one block
+    // (8.4 -> 7.6 us at 6144 x 4096); rows of 17-32 blocks (70B) eight
+    // blocks per wave (18.2 -> 17.0 us at 10240 x 8192).
+    if constexpr (EPI == E_QKV) {
+        const uint32_t nblk = a.cols / 256u;
+        if (nblk <= 16u) {
+            p.ks = 1u;
+            p.nw = nblk;
+            return launch_ks<T, NORM, EPI, 2>(a, p, (total + 1u) / 2u, s);
+        }
+        if (nblk <= 32u) {
+            p.ks = 8u;
+            p.nw = (nblk + 7u) / 8u;
         }
     }
     if (p.nw > 16u) return hipErrorNotSupported;
