@@ -147,6 +147,19 @@ int vbs_gfx950_linear_batch(int type, const void *w, const float *x, uint32_t x_
                             float *y, uint32_t y_stride, uint32_t cols, uint32_t rows,
                             uint32_t batch);
 
+/* Up to three matrices of one type and column count over the same vectors
+ * (Q, K and V, or gate and up): for m < n_mat, Y_m[b*y_stride[m] + r] =
+ * sum_c deq(W_m[r,c]) * X[b*x_stride + c], b < batch (<= 16). Equal to n_mat
+ * calls of vbs_gfx950_linear_batch; for Q4_K and Q6_K the vectors are
+ * prepared once and every matrix shares one matrix-core launch, as the
+ * batched decoder runs a layer's Q/K/V and gate/up. w, rows, y and y_stride
+ * are host arrays of n_mat entries (w[m] and y[m] device pointers). No
+ * counterpart in the reference (it has no batched matvec). */
+int vbs_gfx950_linear_batch_multi(int type, uint32_t n_mat, const void *const *w,
+                                  const uint32_t *rows, const float *x, uint32_t x_stride,
+                                  float *const *y, const uint32_t *y_stride, uint32_t cols,
+                                  uint32_t batch);
+
 /* XOR checksum of a device region, as partial words: partials[i] is the XOR
  * of the 32-bit words of one span of the region (consecutive spans of up to
  * 112 KB), for i < vbs_gfx950_checksum_partials(bytes); their XOR is the

@@ -130,6 +130,37 @@ def test_batch_7b_gate_shape(dev, host, oracle, mem, batch, rows):
         assert rel_l2(Y[b], oracle.linear(V.Q4_K, w, X[b], cols, rows)) <= LIN_TOL, b
 
 
+@pytest.mark.parametrize("t,shapes,cols", [
+    (V.Q4_K, [8192, 1024, 1024], 8192), (V.Q4_K, [4096, 1024, 1024], 4096),
+    (V.Q4_K, [28672, 28672], 8192), (V.Q6_K, [4096, 1000, 13], 4096), (V.Q4_K, [37], 512)],
+    ids=["q4k_70b_qkv", "q4k_7b_qkv", "q4k_70b_gate_up", "q6k_ragged", "q4k_one"])
+@pytest.mark.parametrize("batch", [5, 8, 11])
+def test_batch_multi_matrix_launch(dev, host, oracle, mem, t, shapes, cols, batch):
+    """vbs_gfx950_linear_batch_multi: Q/K/V (or gate/up) of one layer over the
+    same vectors in one launch. Workgroups of several tiles span the
+    boundaries between the matrices (70B Q/K/V: 640 tiles, three per
+    workgroup, the last one partly idle). The first and last 64 rows of every
+    matrix (so the rows on both sides of each boundary, and the last
+    workgroup's) against the oracle, per vector; entries past each matrix's
+    rows untouched."""
+    ws = [V.synth_matrix(host, t, r, cols, SEED, 140 + m) for m, r in enumerate(shapes)]
+    X = vectors(host, batch, cols, 150)
+    px = mem.up(X)
+    pad = 7
+    pws = [mem.up(w) for w in ws]
+    pys = [mem.up(np.full(batch * (r + pad), -3.0, np.float32)) for r in shapes]
+    dev.linear_batch_multi(t, pws, shapes, px, cols, pys, [r + pad for r in shapes], cols, batch)
+    for m, (w, r) in enumerate(zip(ws, shapes)):
+        Y = dev.download(pys[m], (batch, r + pad), np.float32)
+        assert np.all(Y[:, r:] == -3.0), m
+        spans = sorted({(0, min(64, r)), (max(0, r - 64), r)})
+        for lo, hi in spans:
+            wsl = np.ascontiguousarray(w[lo:hi])
+            for b in range(batch):
+                want = oracle.linear(t, wsl, X[b], cols, hi - lo)
+                assert rel_l2(Y[b, lo:hi], want) <= LIN_TOL, (m, lo, b)
+
+
 def test_scratch_growth_keeps_captured_graphs(dev, host, oracle, mem):
     """The batched matvec keeps its prepared x in the library's scratch. A
     graph captured from the library's stream holds the scratch address of the

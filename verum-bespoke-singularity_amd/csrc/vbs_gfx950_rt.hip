@@ -389,6 +389,34 @@ int vbs_gfx950_linear_batch(int type, const void *w, const float *x, uint32_t x_
                   "linear_batch");
 }
 
+int vbs_gfx950_linear_batch_multi(int type, uint32_t n_mat, const void *const *w,
+                                  const uint32_t *rows, const float *x, uint32_t x_stride,
+                                  float *const *y, const uint32_t *y_stride, uint32_t cols,
+                                  uint32_t batch) {
+    if (!ready_or_fail()) return 0;
+    uint32_t e = block_elems(type);
+    if (!e) return fail("linear_batch_multi: no gfx950 kernel for weight type %d", type);
+    if (cols % e) return fail("linear_batch_multi: cols %u not a multiple of %u", cols, e);
+    if (n_mat == 0 || n_mat > 3) return fail("linear_batch_multi: %u matrices (1-3)", n_mat);
+    if (batch > 16) return fail("linear_batch_multi: batch %u exceeds 16", batch);
+    if (!w || !rows || !x || !y || !y_stride) return fail("linear_batch_multi: null pointer");
+    if (x_stride < cols) return fail("linear_batch_multi: x stride smaller than a row");
+    const uint8_t *wm[3];
+    float *ym[3];
+    uint32_t rm[3], ysm[3];
+    for (uint32_t m = 0; m < n_mat; m++) {
+        if (!w[m] || !y[m]) return fail("linear_batch_multi: null pointer for matrix %u", m);
+        if (y_stride[m] < rows[m]) return fail("linear_batch_multi: y stride of matrix %u smaller than its rows", m);
+        wm[m] = (const uint8_t *)w[m];
+        ym[m] = y[m];
+        rm[m] = rows[m];
+        ysm[m] = y_stride[m];
+    }
+    return hip_ok(launch_linear_batch_multi(type, n_mat, wm, rm, x, x_stride, ym, ysm, cols, batch,
+                                            g_rt.stream),
+                  "linear_batch_multi");
+}
+
 int vbs_gfx950_embed(int type, const void *w, uint32_t token, float *out, uint32_t dim) {
     if (!ready_or_fail()) return 0;
     uint32_t e = block_elems(type);

@@ -89,6 +89,13 @@ hipError_t launch_linear(int type, const uint8_t *w, const float *x, float *y, u
 hipError_t launch_linear_batch(int type, const uint8_t *w, const float *x, uint32_t x_stride,
                                float *y, uint32_t y_stride, uint32_t cols, uint32_t rows,
                                uint32_t batch, hipStream_t s);
+// n_mat (<= 3) matrices of one type over the same vectors: x prepared once per
+// eight vectors and one matrix-core launch for Q4_K / Q6_K, else n_mat
+// launch_linear_batch calls.
+hipError_t launch_linear_batch_multi(int type, uint32_t n_mat, const uint8_t *const w[],
+                                     const uint32_t rows[], const float *x, uint32_t xs,
+                                     float *const y[], const uint32_t ys[], uint32_t cols,
+                                     uint32_t batch, hipStream_t s);
 hipError_t launch_dequant_rows(int type, const uint8_t *w, const uint32_t *ids, uint32_t token,
                                uint32_t n_rows, uint32_t dim, float *out, hipStream_t s);
 hipError_t launch_rms_norm(const float *in, const float *w, float *out, uint32_t n, float eps,

@@ -484,4 +484,37 @@ hipError_t launch_kq_linear_batch(int type, const uint8_t *w, const float *x, ui
     return launch_mvb(type, 1, wm, rm, ym, ysm, 0, xp, cols, batch, s);
 }
 
+hipError_t launch_linear_batch_multi(int type, uint32_t n_mat, const uint8_t *const w[],
+                                     const uint32_t rows[], const float *x, uint32_t xs,
+                                     float *const y[], const uint32_t ys[], uint32_t cols,
+                                     uint32_t batch, hipStream_t s) {
+    if (n_mat == 0 || n_mat > 3u) return hipErrorInvalidValue;
+    if (batch == 0) return hipSuccess;
+    bool mfma = type == kQ4_K || type == kQ6_K;
+    for (uint32_t m = 0; m < n_mat && mfma; m++)
+        mfma = rows[m] != 0 && mv_fits(type, w[m], x, cols, rows[m]);
+    if (!mfma) {
+        for (uint32_t m = 0; m < n_mat; m++) {
+            const hipError_t e = launch_linear_batch(type, w[m], x, xs, y[m], ys[m], cols, rows[m],
+                                                     batch, s);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
+    hipError_t why;
+    uint8_t *xp = static_cast<uint8_t *>(rt_scratch(xb_layout(cols).bytes, s, &why));
+    if (!xp) return why;
+    for (uint32_t b0 = 0; b0 < batch; b0 += kBatchMax) {
+        const uint32_t nb = min(kBatchMax, batch - b0);
+        hipError_t e = launch_xprep(XP_PLAIN, x + (uint64_t)b0 * xs, nullptr, xs, nullptr, 0.f, cols,
+                                    nb, xp, s);
+        if (e != hipSuccess) return e;
+        float *yb[3];
+        for (uint32_t m = 0; m < n_mat; m++) yb[m] = y[m] + (uint64_t)b0 * ys[m];
+        e = launch_mvb(type, n_mat, w, rows, yb, ys, 0, xp, cols, nb, s);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
 }  // namespace vbs

@@ -147,6 +147,7 @@ _DEVICE_SIGS = {
     "add": (_I, [_P, _P, _P, _U32]),
     "dequant_rows": (_I, [_I, _P, _P, _U32, _U32, _P]),
     "linear_batch": (_I, [_I, _P, _P, _U32, _P, _U32, _U32, _U32, _U32]),
+    "linear_batch_multi": (_I, [_I, _U32, _P, _P, _P, _U32, _P, _P, _U32, _U32]),
     "stream": (_P, []),
     "checksum_partials": (_U32, [_SZ]),
     "checksum": (_I, [_P, _SZ, _P]),
@@ -232,6 +233,14 @@ class DeviceLib:
 
     def linear_batch(self, t, w, x, xs, y, ys, cols, rows, batch):
         self.check(self._linear_batch(t, w, x, xs, y, ys, cols, rows, batch), "linear_batch")
+
+    def linear_batch_multi(self, t, ws, rows, x, xs, ys, y_strides, cols, batch):
+        """Up to three matrices (device pointers ws, outputs ys) over the same vectors."""
+        n = len(ws)
+        arr = lambda ctype, v: (ctype * n)(*v)
+        self.check(self._linear_batch_multi(t, n, arr(C.c_void_p, ws), arr(C.c_uint32, rows), x, xs,
+                                            arr(C.c_void_p, ys), arr(C.c_uint32, y_strides), cols,
+                                            batch), "linear_batch_multi")
 
     def embed(self, t, w, token, out, dim):
         self.check(self._embed(t, w, token, out, dim), "embed")
