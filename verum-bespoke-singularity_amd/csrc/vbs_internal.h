@@ -79,6 +79,11 @@ hipError_t launch_kq_linear_batch(int type, const uint8_t *w, const float *x, ui
                                   uint32_t ys, uint32_t cols, uint32_t rows, uint32_t batch,
                                   hipStream_t s);
 
+// Q4_K matvec with each workgroup's whole row range in flight (rows of 16
+// blocks, 4096-12288 rows, 16-byte aligned w and x); hipErrorNotSupported
+// outside that range (k_mvf then runs). Bit-identical to k_mvf.
+hipError_t launch_q4k_mvl(const uint8_t *w, const float *x, float *y, uint32_t cols, uint32_t rows,
+                          int accumulate, hipStream_t s);
 // Specialised Q4_K matvec; hipErrorNotSupported when the shape/alignment is
 // outside its range (the generic kernel then runs).
 hipError_t launch_q4k_fast(const uint8_t *w, const float *x, float *y, uint32_t cols,
