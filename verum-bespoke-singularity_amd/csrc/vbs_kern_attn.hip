@@ -31,6 +31,7 @@
 //
 // Other shapes use the generic chunk kernel (double dot, one position per
 // four threads).
+#include "vbs_attn_common.h"
 #include "vbs_dev_common.h"
 #include "vbs_internal.h"
 
@@ -39,21 +40,8 @@ namespace vbs {
 constexpr uint32_t kChunk = 64;  // positions per workgroup of the generic kernel
 constexpr uint32_t kMaxGroup = 16;
 constexpr uint32_t kTargetWgs = 512;      // workgroups the vector-ALU split aims for
-constexpr uint32_t kMfmaTargetWgs = 1024; // one-wave workgroups of the matrix-core split
 
-// Sequence split: chunks of `len` positions (a multiple of gran, at most lmax)
-// sized so that about `target` workgroups cover seq x nkh; n chunks per kv
-// head. The chunk kernel, the merge and the host compute it identically.
-struct AttnSplit {
-    uint32_t len, n;
-};
-__host__ __device__ inline AttnSplit attn_split(uint32_t seq, uint32_t nkh, uint32_t gran,
-                                                uint32_t lmax, uint32_t target) {
-    const uint32_t per = (uint32_t)(((uint64_t)seq * nkh + target - 1u) / target);
-    uint32_t len = (per + gran - 1u) / gran * gran;
-    len = len < gran ? gran : len > lmax ? lmax : len;
-    return {len, (seq + len - 1u) / len};
-}
+// (attn_split, the matrix-core split's constants and fast_exp: vbs_attn_common.h)
 // Chunks per kv head of any split of a sequence of at most max_seq (every
 // len >= 64 or len >= seq * nkh / target, target <= kMfmaTargetWgs).
 inline uint32_t attn_max_chunks(uint32_t max_seq, uint32_t nkh) {
@@ -179,11 +167,6 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
-// e^x as 2^(x log2 e) on the hardware exponential (a few ulp; the scores
-// themselves differ from the reference's double dots by ~1e-7 relative).
-__device__ __forceinline__ float fast_exp(float x) {
-    return __builtin_amdgcn_exp2f(x * 1.44269504088896341f);
-}
 
 // Shape of the fast kernel: four waves; LPP lanes per position (8 head dims
 // each), so a wave step covers PPW positions ("slots"); a wave loads kSteps
@@ -395,8 +378,6 @@ __global__ __launch_bounds__(64 * kWaves) void k_attn_chunk(
 //   itself (dims 8n..8n+7 of its eight positions) and no transpose is needed.
 //   D rows 0-7 (hi) and 8-15 (lo) add up at the end.
 // The chunk's (m, l, acc) go to the same partials as the vector-ALU kernel.
-constexpr uint32_t kMfmaGran = 32, kMfmaTiles = 8, kMfmaLmax = kMfmaGran * kMfmaTiles;
-
 // The most chunks the matrix-core split gives any sequence of at most max_seq
 // positions: the chunk count grows with the sequence while the chunk length
 // stays put, so the maximum lies at the longest sequence of some chunk length
@@ -604,7 +585,7 @@ __global__ __launch_bounds__(64) void k_attn_mfma(const float *__restrict__ q,
 // ... and thread t also m_t and l_t. Then M = max_c m_c (block maximum),
 // weights w_c = e^(m_c - M) in LDS, L = sum_c l_c w_c, and the slices'
 // weighted sums are added in LDS in a fixed order.
-constexpr uint32_t kMergeBatch = 32;     // chunks per thread held in registers at once
+constexpr uint32_t kMergeThreadBatch = 32;     // chunks per thread held in registers at once
 constexpr uint32_t kMergeThreads = 512;  // (measured 2-8% faster than 1024 and than 256)
 
 __global__ __launch_bounds__(kMergeThreads) void k_attn_merge(const float *__restrict__ part,
@@ -626,9 +607,9 @@ __global__ __launch_bounds__(kMergeThreads) void k_attn_merge(const float *__res
     const float *ph = part + (uint64_t)h * stride_chunks * (hd + 2u);
     const uint32_t ns = kMergeThreads / hd;
     const uint32_t d = t % hd, s = t / hd;
-    float av[kMergeBatch];
+    float av[kMergeThreadBatch];
 #pragma unroll
-    for (uint32_t k = 0; k < kMergeBatch; k++) {
+    for (uint32_t k = 0; k < kMergeThreadBatch; k++) {
         const uint32_t c = s + k * ns;
         av[k] = (s < ns && c < n_chunks) ? ph[(uint64_t)c * (hd + 2u) + 2u + d] : 0.f;
     }
@@ -667,11 +648,11 @@ __global__ __launch_bounds__(kMergeThreads) void k_attn_merge(const float *__res
     float a = 0.f;
     if (s < ns) {
 #pragma unroll
-        for (uint32_t k = 0; k < kMergeBatch; k++) {
+        for (uint32_t k = 0; k < kMergeThreadBatch; k++) {
             const uint32_t c = s + k * ns;
             if (c < n_chunks) a = fmaf(av[k], w[c], a);
         }
-        for (uint32_t c = s + kMergeBatch * ns; c < n_chunks; c += ns)
+        for (uint32_t c = s + kMergeThreadBatch * ns; c < n_chunks; c += ns)
             a = fmaf(ph[(uint64_t)c * (hd + 2u) + 2u + d], w[c], a);
     }
     sl[t] = a;
@@ -685,75 +666,31 @@ __global__ __launch_bounds__(kMergeThreads) void k_attn_merge(const float *__res
 
 // Merge for head_dim 128 (the matrix-core chunk kernel's partials): one
 // workgroup of four waves per q head (grid y: the sequences of a batch). Every
-// wave loads all chunks' (m, l) (lanes c, c + 64, ...) and forms M = max m_c,
-// w_c = e^(m_c - M) and L = sum l_c w_c itself; wave w then takes chunks
-// w, w + 4, ... for head dims 2 lane and 2 lane + 1 (their acc rows loaded at
-// once), and one LDS pass adds the four waves' sums in order. No loads wait
-// on a reduction and one barrier ends it (the general merge above has four).
-constexpr uint32_t kMerge4Waves = 4, kMerge4Batch = 32;  // chunks per wave held in registers
-
-__global__ __launch_bounds__(64 * kMerge4Waves) void k_attn_merge_h128(
+// wave forms M, L and the chunk weights itself from all chunks' (m, l); wave r
+// takes residue r of the chunks (vbs_attn_common.h), its acc rows loaded at
+// once, and one LDS pass adds the four sums in order. No loads wait on a
+// reduction and one barrier ends it (the general merge above has four).
+__global__ __launch_bounds__(64 * kMergeRes) void k_attn_merge_h128(
     const float *__restrict__ part, float *__restrict__ out, uint32_t stride_chunks,
     const uint32_t *__restrict__ pos_dev, uint32_t seq_len, uint32_t nkh, uint32_t q_bstride,
     uint64_t part_bstride) {
-    constexpr uint32_t HD = 128, RS = HD + 2u;  // partial row: m, l, acc[HD]
-    __shared__ float2 red[kMerge4Waves][64];
+    __shared__ float2 red[kMergeRes][64];
     const uint32_t h = blockIdx.x, bz = blockIdx.y, lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     part += bz * part_bstride;
     out += (uint64_t)bz * q_bstride;
     if (pos_dev) seq_len = pos_dev[bz] + 1u;  // seq = pos + 1
-    const uint32_t nc = attn_split(seq_len, nkh, kMfmaGran, kMfmaLmax, kMfmaTargetWgs).n;
-    const float *ph = part + (uint64_t)h * stride_chunks * RS;
-    float2 av[kMerge4Batch];
-#pragma unroll
-    for (uint32_t k = 0; k < kMerge4Batch; k++) {
-        const uint32_t c = wave + kMerge4Waves * k;
-        av[k] = c < nc ? *reinterpret_cast<const float2 *>(ph + (uint64_t)c * RS + 2u + 2u * lane)
-                       : make_float2(0.f, 0.f);
-    }
-    float M = -INFINITY;
-    for (uint32_t c = lane; c < nc; c += 64u) M = fmaxf(M, ph[(uint64_t)c * RS]);
-    M = wave_max(M);
-    float L = 0.f, w_lane = 0.f;  // w_lane: weight of chunk `lane` (the first 64 chunks)
-    for (uint32_t c = lane; c < nc; c += 64u) {
-        const float mc = ph[(uint64_t)c * RS];
-        const float wc = mc == -INFINITY ? 0.f : fast_exp(__fsub_rn(mc, M));
-        if (c == lane) w_lane = wc;
-        L = fmaf(ph[(uint64_t)c * RS + 1u], wc, L);
-    }
-    L = wave_sum(L);
-    float ox = 0.f, oy = 0.f;
-    auto add = [&](uint32_t c, float2 a) {
-        float wc;
-        if (c < 64u) {
-            wc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w_lane),
-                                                                     (int)c));
-        } else {
-            const float mc = ph[(uint64_t)c * RS];
-            wc = mc == -INFINITY ? 0.f : fast_exp(__fsub_rn(mc, M));
-        }
-        ox = fmaf(a.x, wc, ox);
-        oy = fmaf(a.y, wc, oy);
-    };
-#pragma unroll
-    for (uint32_t k = 0; k < kMerge4Batch; k++) {
-        const uint32_t c = wave + kMerge4Waves * k;
-        if (c < nc) add(c, av[k]);
-    }
-    for (uint32_t c = wave + kMerge4Waves * kMerge4Batch; c < nc; c += kMerge4Waves)
-        add(c, *reinterpret_cast<const float2 *>(ph + (uint64_t)c * RS + 2u + 2u * lane));
-    red[wave][lane] = make_float2(ox, oy);
+    const uint32_t nc = mfma_chunks(seq_len, nkh);
+    const float *ph = part + (uint64_t)h * stride_chunks * kPartRow;
+    float2 av[kMergeBatch];
+    merge_residue_load(ph, nc, wave, lane, av);  // with the (m, l) loads: one round trip
+    const MergeStats st = merge_stats(ph, nc, lane, merge_ml_load(ph, nc, lane));
+    red[wave][lane] = merge_residue_sum(ph, nc, st, wave, lane, av);
     __syncthreads();
     if (wave == 0) {
-        float2 a = red[0][lane];
+        float2 a[kMergeRes];
 #pragma unroll
-        for (uint32_t w = 1; w < kMerge4Waves; w++) {
-            a.x += red[w][lane].x;
-            a.y += red[w][lane].y;
-        }
-        const float inv = __fdiv_rn(1.0f, L);
-        *reinterpret_cast<float2 *>(out + (uint64_t)h * HD + 2u * lane) =
-            make_float2(__fmul_rn(a.x, inv), __fmul_rn(a.y, inv));
+        for (uint32_t r = 0; r < kMergeRes; r++) a[r] = red[r][lane];
+        *reinterpret_cast<float2 *>(out + (uint64_t)h * 128u + 2u * lane) = merge_finish(a, st.L);
     }
 }
 
@@ -805,7 +742,7 @@ hipError_t launch_attention(const float *q, const uint16_t *kc, const uint16_t *
         k_attn_mfma<<<dim3(mfma_grid_chunks(seq_len, nkh), nkh), 64, 0, s>>>(
             q, kc, vc, part, seq_len, pos_dev, layer_off, nkh, group, scale, stride, 0u, 0ull, 0ull);
         if ((e = hipGetLastError()) != hipSuccess) return e;
-        k_attn_merge_h128<<<nqh, 64 * kMerge4Waves, 0, s>>>(part, out, stride, pos_dev, seq_len, nkh,
+        k_attn_merge_h128<<<nqh, 64 * kMergeRes, 0, s>>>(part, out, stride, pos_dev, seq_len, nkh,
                                                             0u, 0ull);
         return hipGetLastError();
     } else if (fast && hd == 32u) {
@@ -863,7 +800,7 @@ hipError_t launch_attention_batch(const float *q, const uint16_t *kc, const uint
         pstride);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    k_attn_merge_h128<<<dim3(nqh, batch), 64 * kMerge4Waves, 0, s>>>(part, out, stride, pos_dev,
+    k_attn_merge_h128<<<dim3(nqh, batch), 64 * kMergeRes, 0, s>>>(part, out, stride, pos_dev,
                                                                      max_seq, nkh, q_stride, pstride);
     return hipGetLastError();
 }
