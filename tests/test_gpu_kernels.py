@@ -179,6 +179,38 @@ def test_kquant_odd_shapes(dev, host, oracle, mem, t, rows, cols):
     assert rel_l2(got[5:], want[5:]) <= LIN_TOL
 
 
+@pytest.mark.parametrize("t", [V.Q6_K, V.Q4_0, V.Q4_1, V.Q8_0], ids=lambda t: V.TYPE_NAMES[t])
+@pytest.mark.parametrize("rows,cols", [(3, 768), (37, 4352), (4096, 11008)])
+@pytest.mark.parametrize("off", [2, 6, 14])
+def test_kquant_matrix_base_off_16_bytes(dev, host, oracle, mem, t, rows, cols, off):
+    """A matrix whose first byte is only 2-byte aligned (these types' blocks
+    are, so a matrix may start anywhere even): the matrix-core kernels read it
+    as 16-byte chunks counted from the address rounded down to 16, never
+    before that granule or past the matrix's last one. The batched kernel
+    (Q6_K) reads it the same way."""
+    w = V.synth_matrix(host, t, rows, cols, SEED, 27)
+    x = synth_x(host, cols, 28)
+    base = dev.alloc(w.nbytes + 32)
+    mem.ptrs.append(base)
+    pw = base + off
+    dev.write(pw, w)
+    px, py = mem.up(x), mem.zeros(rows)
+    dev.linear(t, pw, px, py, cols, rows)
+    got = dev.download(py, rows, np.float32)
+    sample = np.unique(np.r_[0:min(rows, 48), max(rows - 48, 0):rows])
+    want = oracle.linear(t, w[sample], x, cols, len(sample), threads=16)
+    assert rel_l2(got[sample], want) <= LIN_TOL
+    if t == V.Q6_K:
+        batch = 5
+        xb = np.stack([synth_x(host, cols, 29 + b) for b in range(batch)])
+        pxb, pyb = mem.up(xb), mem.zeros(batch * rows)
+        dev.linear_batch(t, pw, pxb, cols, pyb, rows, cols, rows, batch)
+        gotb = dev.download(pyb, (batch, rows), np.float32)
+        for b in range(batch):
+            wantb = oracle.linear(t, w[sample], xb[b], cols, len(sample), threads=16)
+            assert rel_l2(gotb[b][sample], wantb) <= LIN_TOL
+
+
 def test_linear_offsets_accumulate(dev, host, oracle, mem):
     """Two column tiles into one output window: offsets index x and y, the
     second tile accumulates (src/vbs_backend_test.c:888-948)."""

@@ -275,28 +275,32 @@ struct Q6K {
     static constexpr uint32_t BYTES = 210, NLD = 4, SCRATCH = 16u * 224u;
     __device__ static void load(const Src &src, uint32_t b, uint32_t n, uint32_t g, u32x4 *r) {
         const uint32_t lane = 16u * g + n;
-        // only the last block of the matrix's last row has chunks that reach
-        // past its end (by at most 14 bytes); those loads are bounded
+        // Offsets are taken from w16, w rounded down to 16 bytes (w itself may
+        // be only 2-byte aligned): chunk k of a block at byte s of the matrix
+        // starts at ((s + wlo) & ~15) + 16 k from w16. Only the last block of
+        // the matrix's last row has chunks that reach past its end (by at most
+        // 14 bytes); those loads are bounded.
         const uint32_t wlo = (uint32_t)(uintptr_t)src.w & 15u;
+        const uint8_t *const w16 = src.w - wlo;
         const uint32_t last = src.row(15u) + b * BYTES;
         const bool edge = __builtin_amdgcn_readfirstlane(
-                              (uint32_t)(last - ((last + wlo) & 15u) + 224u > src.bytes)) != 0u;
+                              (uint32_t)(((last + wlo) & ~15u) + 224u > src.bytes + wlo)) != 0u;
         uint32_t a[4];
 #pragma unroll
         for (uint32_t i = 0; i < 4; i++) {
             // chunk c of the tile: 16 aligned bytes
             const uint32_t c = min(lane + 64u * i, 223u);
             const uint32_t s = src.row(c / 14u) + b * BYTES;
-            a[i] = s - ((s + wlo) & 15u) + 16u * (c % 14u);
+            a[i] = ((s + wlo) & ~15u) + 16u * (c % 14u);
         }
         if (!edge) {
 #pragma unroll
-            for (uint32_t i = 0; i < 4; i++) r[i] = lda4(src.w + a[i]);
+            for (uint32_t i = 0; i < 4; i++) r[i] = lda4(w16 + a[i]);
         } else {
             const uint8_t *end = src.w + src.bytes;
 #pragma unroll
             for (uint32_t i = 0; i < 4; i++)
-                r[i] = a[i] + 16u <= src.bytes ? lda4(src.w + a[i]) : ld_tail(src.w + a[i], end);
+                r[i] = a[i] + 16u <= src.bytes + wlo ? lda4(w16 + a[i]) : ld_tail(w16 + a[i], end);
         }
     }
     __device__ static float dot(const u32x4 *r, uint8_t *scratch, const Src &src,
@@ -307,6 +311,12 @@ struct Q6K {
             const uint32_t c = lane + 64u * i;
             if (i < 3u || c < 224u) *reinterpret_cast<u32x4 *>(scratch + 16u * c) = r[i];
         }
+        return dot_staged(scratch, src, dv, b, n, g);
+    }
+    // The same from a scratch that already holds the tile's 224 chunks (chunk
+    // 14 n + k at 16 (14 n + k): row n's aligned 16-byte chunk k).
+    __device__ static float dot_staged(const uint8_t *scratch, const Src &src, const DigitView &dv,
+                                       uint32_t b, uint32_t n, uint32_t g) {
         // row n's block starts o = (its address mod 16) into its 224 scratch
         // bytes; rw is the 4-byte aligned word at or below the start and sh
         // (0 or 2) the byte shift from there. Every word read lies in the row.
@@ -396,26 +406,28 @@ struct KBlk {
     static constexpr uint32_t NLD = (NCHUNK + 63u) / 64u, SCRATCH = 16u * NCHUNK;
     __device__ static void load(const Src &src, uint32_t b, uint32_t n, uint32_t g, u32x4 *r) {
         const uint32_t lane = 16u * g + n;
-        // only the last block of the matrix's last row has chunks past its end
+        // offsets from w16 = w rounded down to 16 bytes, as for Q6_K; only the
+        // last block of the matrix's last row has chunks past its end
         const uint32_t wlo = (uint32_t)(uintptr_t)src.w & 15u;
+        const uint8_t *const w16 = src.w - wlo;
         const uint32_t last = src.row(15u) + b * BYTES;
         const bool edge = __builtin_amdgcn_readfirstlane(
-                              (uint32_t)(last - ((last + wlo) & 15u) + 16u * CH > src.bytes)) != 0u;
+                              (uint32_t)(((last + wlo) & ~15u) + 16u * CH > src.bytes + wlo)) != 0u;
         uint32_t a[NLD];
 #pragma unroll
         for (uint32_t i = 0; i < NLD; i++) {
             const uint32_t c = min(lane + 64u * i, NCHUNK - 1u);
             const uint32_t s0 = src.row(c / CH) + b * BYTES;
-            a[i] = s0 - ((s0 + wlo) & 15u) + 16u * (c % CH);
+            a[i] = ((s0 + wlo) & ~15u) + 16u * (c % CH);
         }
         if (!edge) {
 #pragma unroll
-            for (uint32_t i = 0; i < NLD; i++) r[i] = lda4(src.w + a[i]);
+            for (uint32_t i = 0; i < NLD; i++) r[i] = lda4(w16 + a[i]);
         } else {
             const uint8_t *end = src.w + src.bytes;
 #pragma unroll
             for (uint32_t i = 0; i < NLD; i++)
-                r[i] = a[i] + 16u <= src.bytes ? lda4(src.w + a[i]) : ld_tail(src.w + a[i], end);
+                r[i] = a[i] + 16u <= src.bytes + wlo ? lda4(w16 + a[i]) : ld_tail(w16 + a[i], end);
         }
     }
     __device__ static float dot(const u32x4 *r, uint8_t *scratch, const Src &src,
@@ -811,13 +823,14 @@ static hipError_t launch_plan(const MvArgs &a, hipStream_t s) {
 static inline bool mv_fits_blk(int type, const uint8_t *w, const float *x, uint32_t cols, uint32_t rows) {
     if (type != kQ4_0 && type != kQ4_1 && type != kQ8_0) return false;
     if (cols % 256u || cols / 256u > 128u || ((uintptr_t)x & 3u) || ((uintptr_t)w & 1u)) return false;
-    return (uint64_t)rows * row_bytes(type, cols) < (1ull << 32);
+    return (uint64_t)rows * row_bytes(type, cols) + 256u < (1ull << 32);
 }
 
 static inline bool mv_fits(int type, const uint8_t *w, const float *x, uint32_t cols, uint32_t rows) {
     if (type != kQ4_K && type != kQ6_K) return false;
     if (cols % 256u || cols / 256u > 128u || ((uintptr_t)x & 3u)) return false;
-    if ((uint64_t)rows * (cols / 256u) * (type == kQ4_K ? 144u : 210u) >= (1ull << 32)) return false;
+    // (32-bit offsets: the matrix and the 16-byte chunks around it)
+    if ((uint64_t)rows * (cols / 256u) * (type == kQ4_K ? 144u : 210u) + 256u >= (1ull << 32)) return false;
     return ((uintptr_t)w & (type == kQ4_K ? 15u : 1u)) == 0;
 }
 
