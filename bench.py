@@ -34,7 +34,11 @@ Also reported: configs 1-3 on the GPU; the CPU hot-kernel table
 decode tokens/sec of the synthetic 7B Q4_K_M model (config 4:
 32 layers, KV prefilled to 2048, greedy from position 2048) through the graph
 decoder (vbs_gfx950_decoder_*), and through the g_vbs_hip_backend ops table
-with one dispatch per bridge call.
+with one dispatch per bridge call. The decode entry's `checked` block comes
+from the CPU leg, after every GPU timing: the decoded tokens against the
+reference CPU backend's 128 for the same model and start
+(tests/golden/decode_7b_greedy.npz), and the first four against the oracle's
+forward pass run on the host.
 """
 import argparse
 import ctypes as C
@@ -56,13 +60,17 @@ H, FF = 4096, 11008
 LAYER_SET = [("q", H, H), ("k", H, H), ("v", H, H), ("o", H, H),
              ("gate", FF, H), ("up", FF, H), ("down", H, FF)]  # (name, rows, cols)
 SEED = 424242
+# Config 4's synthetic model seed: the one the reference CPU backend's 128
+# greedy tokens in tests/golden/decode_7b_greedy.npz were decoded with.
+DECODE_SEED = 7
+DECODE_FIXTURE = os.path.join(ROOT, "tests", "golden", "decode_7b_greedy.npz")
 
-# HBM bytes per launch of the dominant kernel (11008x4096 Q4_K) from two
-# rocprofv3 --pmc passes over this program (FETCH_SIZE, WRITE_SIZE in KiB per
-# dispatch), each scaled by what the counter reads for a 256 MiB device copy
-# in the same run: FETCH_SIZE x (262144 / 131092.9) + WRITE_SIZE x 1.0000
+# HBM bytes per launch of the dominant kernel (11008x4096 Q4_K, k_mvl) from
+# two rocprofv3 --pmc passes over this program (FETCH_SIZE, WRITE_SIZE in KiB
+# per dispatch), each scaled by what the counter reads for a 256 MiB device
+# copy in the same run: FETCH_SIZE x (262144 / 131093.1) + WRITE_SIZE x 1.0000
 # (profiles/q4k_matvec_7b_layer_set.md).
-TRAFFIC_BYTES = round((12481.8 * 262144 / 131092.9 + 43.0) * 1024)
+TRAFFIC_BYTES = round((12487.8 * 262144 / 131093.1 + 50.0) * 1024)
 
 
 def algo_bytes(t, rows, cols):
@@ -555,10 +563,12 @@ LAYER_SET_70B = [("q", V.Q4_K, 8192, 8192), ("k", V.Q4_K, 1024, 8192), ("v", V.Q
 
 def bench_batch8_70b(dev, host, steps=20, batch=8, ncopy=2):
     """Config 5 at batch 8: the 70B layer matvec set through
-    vbs_gfx950_linear_batch (x prepared, then the f16 matrix-core kernel), one
-    HIP graph per step, `ncopy` resident copies (1.08 GB) rotated so the
-    Infinity Cache cannot serve the weights; beside it the same vectors as
-    `batch` batch-1 matvec launches each."""
+    vbs_gfx950_linear_batch_multi as the batched decoder groups it (Q/K/V over
+    one prepared x and one launch, O, gate/up over one prepared x, down: four
+    preparations and four f16 matrix-core launches), one HIP graph per step,
+    `ncopy` resident copies (1.08 GB) rotated so the Infinity Cache cannot
+    serve the weights; beside it the same vectors as `batch` batch-1 matvec
+    launches each."""
     hip, stream = Hip(), dev.stream()
     copies = [[dev.upload(V.synth_matrix(host, t, r, c, SEED + k, 200 + i))
                for i, (_, t, r, c) in enumerate(LAYER_SET_70B)] for k in range(ncopy)]
@@ -567,12 +577,16 @@ def bench_batch8_70b(dev, host, steps=20, batch=8, ncopy=2):
     py = [dev.upload(np.zeros(batch * r, np.float32)) for _, _, r, _ in LAYER_SET_70B]
 
     def step(k, batched):
+        if batched:  # Q/K/V and gate/up over one prepared x each, as the batched decoder runs them
+            for group in ((0, 1, 2), (3,), (4, 5), (6,)):
+                t, c = LAYER_SET_70B[group[0]][1], LAYER_SET_70B[group[0]][3]
+                rows = [LAYER_SET_70B[i][2] for i in group]
+                dev.linear_batch_multi(t, [copies[k][i] for i in group], rows, px[c], c,
+                                       [py[i] for i in group], rows, c, batch)
+            return
         for i, (_, t, r, c) in enumerate(LAYER_SET_70B):
-            if batched:
-                dev.linear_batch(t, copies[k][i], px[c], c, py[i], r, c, r, batch)
-            else:
-                for b in range(batch):
-                    dev.linear(t, copies[k][i], px[c] + 4 * b * c, py[i] + 4 * b * r, c, r)
+            for b in range(batch):
+                dev.linear(t, copies[k][i], px[c] + 4 * b * c, py[i] + 4 * b * r, c, r)
 
     out = {}
     for batched in (True, False):
@@ -599,13 +613,14 @@ def bench_batch8_70b(dev, host, steps=20, batch=8, ncopy=2):
         dev.free(p)
     return {"workload": "Llama-70B layer matvec set (Q4_K_M mix), batch 8 (config 5)",
             "batch": batch, "weight_bytes_per_step": wbytes, "weight_copies": ncopy,
+            "launches": "Q/K/V, O, gate/up, down: each one x preparation + one matrix-core launch",
             "ms_per_step": round(out["batched"], 4),
             "weight_GB_per_s": round(wbytes / (out["batched"] * 1e-3) / 1e9, 1),
             "roofline_frac": round(wbytes / (out["batched"] * 1e-3) / (PEAK_HBM_GBS * 1e9), 4),
             "vector_matvecs_per_s": round(batch * len(LAYER_SET_70B) / (out["batched"] * 1e-3)),
             "batch1_x8_ms_per_step": round(out["batch1_x8"], 4),
             "speedup_vs_batch1_x8": round(out["batch1_x8"] / out["batched"], 2),
-            "path": "vbs_gfx950_linear_batch: k_xprep_b + k_mvb (f16 MFMA) per matrix"}
+            "path": "vbs_gfx950_linear_batch_multi: k_xprep_b + k_mvb (f16 MFMA) per matrix group"}
 
 
 GEO_7B = dict(hidden=4096, ffn=11008, n_heads=32, n_kv_heads=8, head_dim=128, vocab=32000)
@@ -613,14 +628,14 @@ GEO_70B = dict(hidden=8192, ffn=28672, n_heads=64, n_kv_heads=8, head_dim=128, v
 
 
 def bench_decode(dev, host, n_tokens, path="both", geo=GEO_7B, n_layers=32, ctx=2048,
-                 n_dispatch_tokens=16, batch=0, batch_tokens=16):
+                 n_dispatch_tokens=16, batch=0, batch_tokens=16, seed=SEED):
     """Greedy decode of a Q4_K_M synthetic Llama model (config 4: 7B, 32 layers,
     ctx 2048; config 5: 70B, 80 layers, ctx 8192) from position `ctx` with the
     KV cache prefilled N(0,1): the graph decoder (one graph launch per token)
     and, for comparison, the per-dispatch ops-table path."""
     n_dispatch_tokens = min(n_dispatch_tokens, n_tokens)
     t_build = time.perf_counter()
-    model = V.SynthModel(host, n_layers=n_layers, **geo, max_ctx=ctx + n_tokens + 1, seed=SEED)
+    model = V.SynthModel(host, n_layers=n_layers, **geo, max_ctx=ctx + n_tokens + 1, seed=seed)
     kc, vc = model.kv_prefill(host, ctx)
     be = V.gfx950_backend()
     if not be.init():
@@ -670,7 +685,44 @@ def bench_decode(dev, host, n_tokens, path="both", geo=GEO_7B, n_layers=32, ctx=
             "paths_agree": bool(np.array_equal(toks[:n_dispatch_tokens], dtoks)),
             "first_tokens": [int(x) for x in toks[:8]],
             "min_margin": float(np.min(margins)),
+            "_tokens": toks, "_margins": margins,
             **({"batch_decode": batched} if batched else {})}
+
+
+def decode_vs_checkers(host, toks, margins, n_oracle=4, ctx=2048):
+    """Checker leg of the config-4 decode (graph decoder, seed DECODE_SEED,
+    token 1 at position `ctx`): its tokens and top-1 minus top-2 margins
+    against the reference CPU backend's 128 (the fixture), and its first
+    `n_oracle` tokens against the oracle's forward pass, run here on the
+    host's cores over a fresh copy of the same synthetic model."""
+    from oracle_lib import Oracle
+    out = {}
+    if os.path.exists(DECODE_FIXTURE):
+        fx = np.load(DECODE_FIXTURE)
+        n = min(len(toks), len(fx["tokens"]))
+        want_m = fx["top2"][:n, 0].astype(np.float64) - fx["top2"][:n, 1]
+        out["reference_tokens_compared"] = n
+        out["reference_tokens_equal"] = bool(np.array_equal(toks[:n], fx["tokens"][:n]))
+        out["max_abs_margin_diff"] = float(np.abs(np.asarray(margins[:n]) - want_m).max())
+    t0 = time.perf_counter()
+    model = V.SynthModel(host, n_layers=32, **GEO_7B, max_ctx=ctx + n_oracle + 1,
+                         seed=DECODE_SEED)
+    kc_p, vc_p = model.kv_prefill(host, ctx)
+    kvd = GEO_7B["n_kv_heads"] * GEO_7B["head_dim"]
+    shape = (32, ctx + n_oracle + 1, kvd)
+    kc, vc = np.zeros(shape, np.uint16), np.zeros(shape, np.uint16)
+    kc[:, :ctx], vc[:, :ctx] = kc_p.reshape(32, ctx, kvd), vc_p.reshape(32, ctx, kvd)
+    del kc_p, vc_p
+    orc = Oracle()
+    om = orc.model(model, kc, vc)
+    threads, tok, want = min(16, os.cpu_count() or 1), 1, []
+    for i in range(n_oracle):
+        tok = int(np.argmax(orc.forward(om, tok, ctx + i, GEO_7B["vocab"], threads)))
+        want.append(tok)
+    out["oracle_tokens_compared"] = n_oracle
+    out["oracle_agree"] = bool(np.array_equal(np.asarray(toks[:n_oracle]), want))
+    out["oracle_s"] = round(time.perf_counter() - t0, 1)
+    return out
 
 
 def bench_batch_decode(dev, d, model, kc, vc, ctx, batch, n_tokens, eager=False):
@@ -766,7 +818,7 @@ def main():
                      "traffic": TRAFFIC_BYTES,
                      "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, scaled by a "
                                        "256 MiB copy (profiles/q4k_matvec_7b_layer_set.md)",
-                     "kernel": "k_mvf<Q4K> (matrix-core Q4_K matvec), 11008x4096 and 4096x11008",
+                     "kernel": "Q4_K matvec: k_mvl (whole row range in flight) at 11008x4096, k_mvf at 4096x11008",
                      "algorithmic_bytes_per_launch": r["big_bytes"],
                      "avg_launch_us": round(1e3 * r["avg_big_ms"], 3),
                      "ceiling": r["ceiling"],
@@ -792,13 +844,19 @@ def main():
                                      n_layers=80, ctx=8192, n_dispatch_tokens=4, batch=8,
                                      batch_tokens=a.decode_tokens)
     elif not a.no_decode:
-        out["decode"] = bench_decode(dev, host, a.decode_tokens, a.decode_path)
+        out["decode"] = bench_decode(dev, host, a.decode_tokens, a.decode_path, seed=DECODE_SEED)
         if a.decode_70b_tokens and a.decode_path == "both":
             out["decode_70b"] = bench_decode(dev, host, a.decode_70b_tokens, geo=GEO_70B,
                                              n_layers=80, ctx=8192, n_dispatch_tokens=4,
                                              batch=8, batch_tokens=16)
+    dec = out.get("decode", {})
+    toks, margins = dec.pop("_tokens", None), dec.pop("_margins", None)
+    out.get("decode_70b", {}).pop("_tokens", None)
+    out.get("decode_70b", {}).pop("_margins", None)
     if not a.no_cpu:
         out["cpu_baseline"] = cpu_baseline(host, r["weights_host"], r["xs_host"], beside=cpu_work)
+        if toks is not None and a.decode_geometry == "7b" and "tokens_per_s" in dec:
+            dec["checked"] = decode_vs_checkers(host, toks, margins)
     print(json.dumps(out))
 
 

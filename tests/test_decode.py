@@ -11,7 +11,14 @@ vbs_oracle_forward_token, following src/vbs_specializer.c:231-349).
 * GPU: the graph-replayed decoder (vbs_gfx950_decoder_*) runs the same kernels
   with device-resident token/position, so its logits and KV stores must equal
   the per-dispatch driver's bit for bit, and its greedy tokens the oracle's.
+* Config 4 at full length (32 layers of the 7B geometry, KV prefilled to
+  2048): 128 greedy tokens against the reference CPU backend's own 128
+  (tests/golden/decode_7b_greedy.npz), to whose first step the oracle is
+  pinned bit for bit on the CPU, and 32 teacher-forced positions against the
+  oracle's logits.
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -126,6 +133,124 @@ def test_gpu_llama_shape_greedy(host, backend, dev, geo, n_layers, ctx, n_tok):
     assert np.array_equal(toks, want), (toks, want, margins)
 
 
+def top2_margin(logits):
+    """top-1 minus top-2 logit (the greedy decision's distance from a tie)."""
+    part = np.partition(logits.astype(np.float64), -2)
+    return float(part[-1] - part[-2])
+
+
+@pytest.fixture(scope="module")
+def model_7b(host):
+    """The full 7B-shaped Q4_K_M model of config 4 with its KV cache prefilled
+    N(0,1) to position 2048 (room for 129 more positions)."""
+    ctx = 2048
+    model = V.SynthModel(host, n_layers=32, **GEO_7B, max_ctx=ctx + 129, seed=7)
+    kc_p, vc_p = model.kv_prefill(host, ctx)
+    return model, kc_p, vc_p, ctx
+
+
+DECODE_7B = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                         "decode_7b_greedy.npz")
+
+
+def decode_7b_fixture():
+    """The reference CPU backend's 128 greedy steps of config 4 (written by
+    tests/golden/gen_decode_7b.py): tokens, per-step top-1/top-2 logits and
+    the first and last steps' logits."""
+    g = np.load(DECODE_7B)
+    ctx, n_tok, seed, start, n_layers = (int(v) for v in g["config"])
+    assert (ctx, n_tok, seed, start, n_layers) == (2048, 128, 7, 1, 32)
+    return g
+
+
+def test_oracle_7b_first_step_matches_reference_fixture(host):
+    """The oracle's full 7B forward at position 2048 reproduces the reference
+    CPU backend's first-step logits bit for bit (and so its first token)."""
+    g = decode_7b_fixture()
+    ctx = 2048
+    model = V.SynthModel(host, n_layers=32, **GEO_7B, max_ctx=ctx + 129, seed=7)
+    kc_p, vc_p = model.kv_prefill(host, ctx)
+    kc, vc = full_cache(model, kc_p, vc_p, ctx)
+    del kc_p, vc_p
+    oracle = Oracle()
+    lg = oracle.forward(oracle.model(model, kc, vc), 1, ctx, GEO_7B["vocab"], 8)
+    assert int(np.argmax(lg)) == int(g["tokens"][0])
+    assert np.array_equal(lg.view(np.uint32), g["logits_first"].view(np.uint32))
+
+
+@pytest.mark.gpu
+def test_gpu_7b_128_greedy_tokens_vs_oracle_and_reference(backend, dev, host, model_7b):
+    """Config 4 at its stated length: 128 greedy tokens from position 2048
+    through the graph decoder against the oracle's 128, run here (first
+    maximum, src/main.c:929-932), and against the reference CPU backend's
+    128 (the fixture the oracle is pinned to above); every step's top-1 minus
+    top-2 margin within 1e-3 + 1e-4 |margin| of both."""
+    model, kc_p, vc_p, ctx = model_7b
+    fx = decode_7b_fixture()
+    ref_toks = fx["tokens"]
+    ref_margins = fx["top2"][:, 0].astype(np.float64) - fx["top2"][:, 1]
+    n_tok = len(ref_toks)
+    d = V.Decoder(host, backend, model)
+    d.load_kv(kc_p, vc_p, ctx)
+    g = V.GraphDecoder(dev, d, max_steps=n_tok)
+    toks, margins = g.greedy(1, ctx, n_tok)
+    g.close()
+    d.close()
+    kc, vc = full_cache(model, kc_p, vc_p, ctx)
+    oracle = Oracle()
+    om = oracle.model(model, kc, vc)
+    want, want_margins, tok = [], [], 1
+    for i in range(n_tok):
+        lg = oracle.forward(om, tok, ctx + i, model.cfg["vocab"], 16)
+        tok = int(np.argmax(lg))
+        want.append(tok)
+        want_margins.append(top2_margin(lg))
+        if i % 32 == 31:
+            print(f"oracle: {i + 1} of {n_tok} tokens", flush=True)
+    want, want_margins = np.array(want, np.uint32), np.array(want_margins)
+    print(f"128 greedy tokens: {len(set(want.tolist()))} distinct, first {want[:6].tolist()}; "
+          f"min oracle margin {want_margins.min():.4f}; max |margin - oracle| "
+          f"{np.abs(margins - want_margins).max():.2e}, - reference "
+          f"{np.abs(margins - ref_margins).max():.2e}")
+    assert np.array_equal(want, ref_toks)
+    assert np.array_equal(toks, want), (np.nonzero(toks != want)[0][:4], toks[:8], want[:8])
+    for m in (want_margins, ref_margins):
+        assert np.all(np.abs(margins - m) <= 1e-3 + 1e-4 * np.abs(m))
+
+
+@pytest.mark.gpu
+def test_gpu_7b_teacher_forced_logits_vs_oracle(backend, dev, host, model_7b):
+    """The synthetic model's greedy stream settles on a repeated token within
+    a few steps, so equal greedy tokens say little after that. Here 32
+    positions (2048..2079) are fed a fixed pseudo-random token stream through
+    the graph decoder and the oracle alike: every step's logits within 1e-4
+    relative L2 of the oracle's, with the same first-maximum argmax."""
+    model, kc_p, vc_p, ctx = model_7b
+    stream = np.random.default_rng(2048).integers(0, model.cfg["vocab"], 32)
+    d = V.Decoder(host, backend, model)
+    d.load_kv(kc_p, vc_p, ctx)
+    g = V.GraphDecoder(dev, d, max_steps=4)
+    kc, vc = full_cache(model, kc_p, vc_p, ctx)
+    oracle = Oracle()
+    om = oracle.model(model, kc, vc)
+    errs, margins = [], []
+    try:
+        for i, tok in enumerate(stream.tolist()):
+            got = g.step(tok, ctx + i)
+            want = oracle.forward(om, tok, ctx + i, model.cfg["vocab"], 16)
+            errs.append(rel_l2(got, want))
+            margins.append(top2_margin(want))
+            print(f"position {ctx + i}: token {tok} rel L2 {errs[-1]:.2e} "
+                  f"oracle margin {margins[-1]:.4f}", flush=True)
+            assert errs[-1] <= 1e-4, (i, errs[-1])
+            assert int(np.argmax(got)) == int(np.argmax(want)), (i, margins[-1])
+    finally:
+        g.close()
+        d.close()
+    print(f"teacher-forced 32 steps: max rel L2 {max(errs):.2e}, "
+          f"oracle margins min {min(margins):.4f} median {float(np.median(margins)):.4f}")
+
+
 @pytest.mark.gpu
 def test_gpu_graph_decoder_equals_dispatch_path(host, backend, dev, tiny):
     """Logits and KV stores of graph replays equal the per-dispatch driver's."""
@@ -157,6 +282,34 @@ def test_gpu_graph_decoder_equals_dispatch_path(host, backend, dev, tiny):
         assert margins[i] == np.float32(top2[1] - top2[0])
     g.close()
     d.close()
+
+
+@pytest.mark.gpu
+def test_gpu_graph_decoder_7b_width_equals_dispatch_path(host, backend, dev):
+    """At the 7B width (4096, 32 q heads of 128: the fused Q/K/V launch with
+    two tiles per workgroup, the matrix-core attention, k_mvl's O projection
+    with the residual add) the graph decoder's logits and KV rows equal the
+    per-dispatch path's bit for bit, over 2 layers of the 7B geometry and 8
+    teacher-forced positions from 333."""
+    model = V.SynthModel(host, n_layers=2, **GEO_7B, max_ctx=400, seed=11)
+    ctx, n = 333, 8
+    kc_p, vc_p = model.kv_prefill(host, ctx)
+    d = V.Decoder(host, backend, model)
+    d.load_kv(kc_p, vc_p, ctx)
+    stream = np.random.default_rng(333).integers(0, model.cfg["vocab"], n).tolist()
+    want = [d.step(tok, ctx + i) for i, tok in enumerate(stream)]
+    want_kc, want_vc = d.read_kv(ctx + n)
+    d.load_kv(kc_p, vc_p, ctx)
+    g = V.GraphDecoder(dev, d, max_steps=n)
+    try:
+        for i, tok in enumerate(stream):
+            got = g.step(tok, ctx + i)
+            assert np.array_equal(got.view(np.uint32), want[i].view(np.uint32)), i
+        gk, gv = d.read_kv(ctx + n)
+        assert np.array_equal(gk, want_kc) and np.array_equal(gv, want_vc)
+    finally:
+        g.close()
+        d.close()
 
 
 @pytest.mark.gpu

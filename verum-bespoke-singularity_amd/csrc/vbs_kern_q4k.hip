@@ -1,4 +1,6 @@
-// vbs_kern_q4k.hip — batch-1 Q4_K matvec tuned for gfx950 (the metric kernel).
+// vbs_kern_q4k.hip — batch-1 Q4_K matvec on the vector ALUs (v_dot4), for the
+// matrices the matrix-core kernels do not take: 4 GiB of weights or more (their
+// offsets are 32-bit). Rows up to 32768 columns, 16-byte aligned weights.
 //
 // y[r] (+)= sum_c deq(W[r,c]) * x[c], W in native GGUF Q4_K super-blocks
 // (144 B: f16 d, f16 dmin, 12 B of 6-bit scales/mins, 128 B of nibbles;
