@@ -84,6 +84,10 @@ hipError_t launch_kq_linear_batch(int type, const uint8_t *w, const float *x, ui
 // outside that range (k_mvf then runs). Bit-identical to k_mvf.
 hipError_t launch_q4k_mvl(const uint8_t *w, const float *x, float *y, uint32_t cols, uint32_t rows,
                           int accumulate, hipStream_t s);
+// The ring variant (vbs_kern_mvl.hip) for Q6_K rows of 33-48 blocks over
+// 2049-4096 rows (7B down); hipErrorNotSupported elsewhere.
+hipError_t launch_q6k_mvr(const uint8_t *w, const float *x, float *y, uint32_t cols, uint32_t rows,
+                          int accumulate, hipStream_t s);
 // Specialised Q4_K matvec; hipErrorNotSupported when the shape/alignment is
 // outside its range (the generic kernel then runs).
 hipError_t launch_q4k_fast(const uint8_t *w, const float *x, float *y, uint32_t cols,

@@ -18,8 +18,9 @@ hipError_t launch_kq_linear(int type, const uint8_t *w, const float *x, float *y
     if (mv_fits_blk(type, w, x, cols, rows))
         return launch_blk_linear(type, w, x, y, cols, rows, accumulate, s);
     if (!mv_fits(type, w, x, cols, rows)) return hipErrorNotSupported;
-    if (type == kQ4_K) {
-        const hipError_t e = launch_q4k_mvl(w, x, y, cols, rows, accumulate, s);
+    {
+        const hipError_t e = type == kQ4_K ? launch_q4k_mvl(w, x, y, cols, rows, accumulate, s)
+                                           : launch_q6k_mvr(w, x, y, cols, rows, accumulate, s);
         if (e != hipErrorNotSupported) return e;
     }
     MvArgs a{};

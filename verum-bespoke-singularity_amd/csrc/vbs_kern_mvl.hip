@@ -1,5 +1,7 @@
-// vbs_kern_mvl.hip — Q4_K matvec with the whole row range of a workgroup in
-// flight at once (rows of 16 super-blocks, 4096-12288 rows).
+// vbs_kern_mvl.hip — batch-1 K-quant matvecs that keep a CU's weights in
+// flight through LDS DMA: k_mvl (Q4_K, the whole row range of a workgroup at
+// once: rows of 16 super-blocks, 4096-12288 rows) and k_mvr (Q6_K, a ring of
+// slots per wave: rows of 33-48 super-blocks, 2049-4096 rows).
 //
 // One 16-wave workgroup per CU owns an even range of at most 48 rows (T tiles
 // of 16). Wave w owns super-block w of every row: before it computes anything
@@ -16,7 +18,9 @@
 // The DMA is issued by inline assembly (M0 = the wave-uniform LDS address):
 // the compiler's builtin makes it insert waits for all loads before every
 // LDS access. The compiler does not see these loads, so each wait for them is
-// an explicit s_waitcnt; nothing else in this kernel uses M0.
+// an explicit s_waitcnt; nothing else in these kernels uses M0.
+#include <type_traits>
+
 #include "vbs_mfma.h"
 
 namespace vbs {
@@ -157,6 +161,183 @@ static hipError_t launch_mvl_t(const MvArgs &a, uint32_t wgs, uint32_t rpw, hipS
     }
     k_mvl<T, EPI><<<wgs, 64 * kMvlWaves, lds, s>>>(a, rpw);
     return hipGetLastError();
+}
+
+// ---- ring variant for Q6_K: more items per wave than the LDS holds at once ---------------
+// k_mvr: a workgroup per CU owns an even range of at most 16 T rows; wave w
+// owns blocks w, w + 16, ... (NB of them; slots past the row re-read its last
+// block and add nothing). Its items -- T tiles of each of its blocks -- stream
+// by LDS DMA through a ring of R slots: R items are requested before anything
+// is computed and item i + R as soon as item i is done, so a CU keeps ~115 KB
+// of weights in flight for the whole launch. An item is the tile's 16 rows of
+// the block as 14 aligned 16-byte chunks each (224 bytes covering the 210 at
+// any 2-byte offset), in the layout Q6K::dot_staged reads. x comes by DMA as
+// well, a block ahead (two slots per wave); the digits of a block are written
+// over its x. Arithmetic and per-(row, block) sums are k_mvf's, so the results
+// equal k_mvf's bit for bit. Every wait is an explicit s_waitcnt on the number
+// of DMAs issued after the awaited one (the loads return in issue order).
+// Measured at 4096 x 11008 (7B down, weights streamed from HBM): 11.0-11.4
+// against k_mvf's 12.1-12.8 us.
+constexpr uint32_t kMvrItem = 16u * 224u, kMvrDma = 4u;
+
+template <uint32_t I, uint32_t N, class F>
+__device__ __forceinline__ void mvr_for(F &&f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<uint32_t, I>{});
+        mvr_for<I + 1u, N>(f);
+    }
+}
+
+template <uint32_t NB, uint32_t T, uint32_t R>
+struct MvrPlan {
+    static constexpr uint32_t NI = NB * T, D = kMvrDma;
+    static constexpr uint32_t XS = NB > 1u ? 2u : 1u;  // x slots per wave
+    static_assert(R >= 1u && R <= NI && (NB == 1u || R <= T + 1u), "ring");
+    // DMAs that item i brings: its own, after x when it opens a block
+    static constexpr uint32_t with(uint32_t i) { return D + (i % T == 0u ? 1u : 0u); }
+    // DMAs issued after item i's last one at the time item i is computed
+    // (items up to i + R - 1 are out)
+    static constexpr uint32_t after_item(uint32_t i) {
+        uint32_t c = 0;
+        for (uint32_t j = i + 1u; j < i + R && j < NI; j++) c += with(j);
+        return c;
+    }
+    // ... and after the x of the block item i opens
+    static constexpr uint32_t after_x(uint32_t i) { return D + after_item(i); }
+    static constexpr size_t lds(uint32_t nblk) {
+        return 16u * (size_t)R * kMvrItem + 16u + 16u * (size_t)XS * 1024u +
+               16u * (size_t)T * nblk * sizeof(float);
+    }
+};
+
+template <uint32_t NB, uint32_t T, uint32_t R, int EPI>
+__global__ __launch_bounds__(1024) void k_mvr(const MvArgs a, uint32_t rpw) {
+    using P = MvrPlan<NB, T, R>;
+    constexpr uint32_t NI = P::NI;
+    extern __shared__ __align__(16) uint8_t lds[];
+    const uint32_t cols = a.cols, nblk = cols >> 8, rb = nblk * Q6K::BYTES;
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const uint32_t n = lane & 15u, g = lane >> 4;
+    const uint32_t r0 = blockIdx.x * rpw, r1 = min(r0 + rpw, a.rows[0]);
+    if (r0 >= r1) return;
+    // LDS: [16 waves][R slots] | 16 zero bytes | [16 waves][XS x slots] | pb [16 T rows][nblk]
+    const uint32_t lds0 = (uint32_t)(uintptr_t)lds;
+    const uint32_t ring = lds0 + wave * R * kMvrItem;
+    uint8_t *const zero = lds + 16u * R * kMvrItem;
+    uint8_t *const xs0 = zero + 16u + wave * P::XS * 1024u;
+    float *const pb = reinterpret_cast<float *>(zero + 16u + 16u * P::XS * 1024u);
+    // offsets are taken from w rounded down to 16 bytes (as in Q6K::load)
+    const uint8_t *const w = a.w[0];
+    const uint32_t wlo = (uint32_t)(uintptr_t)w & 15u;
+
+    auto issue = [&](auto ic) {
+        constexpr uint32_t i = decltype(ic)::value;
+        constexpr uint32_t k = i / T, j = i % T;
+        const uint32_t b = min(wave + 16u * k, nblk - 1u);
+        if constexpr (j == 0u)
+            mvl_dma16(a.x + 256u * b + 4u * lane, (uint32_t)(uintptr_t)(xs0 + (k % P::XS) * 1024u));
+        const uint32_t dst = ring + (i % R) * kMvrItem;
+#pragma unroll
+        for (uint32_t q = 0; q < kMvrDma; q++) {
+            const uint32_t c = min(64u * q + lane, 223u);  // chunk 14 n' + k' of the tile
+            const uint32_t st = min(r0 + 16u * j + c / 14u, r1 - 1u) * rb + b * 210u;
+            const uint32_t off = ((st + wlo) & ~15u) + 16u * (c % 14u);
+            if (q < 3u || lane < 32u) mvl_dma16(w - wlo + off, dst + 1024u * q);
+        }
+    };
+    mvr_for<0u, R>(issue);
+    if (lane < 4u) reinterpret_cast<uint32_t *>(zero)[lane] = 0u;
+
+    mvr_for<0u, NI>([&](auto ic) {
+        constexpr uint32_t i = decltype(ic)::value;
+        constexpr uint32_t k = i / T, j = i % T;
+        const uint32_t bw = wave + 16u * k;
+        const bool own = bw < nblk;
+        const uint32_t b = min(bw, nblk - 1u);
+        uint8_t *const slot = xs0 + (k % P::XS) * 1024u;
+        DigitView dv;
+        dv.zero = zero;
+        dv.base = slot;
+        dv.pstride = 256u;
+        dv.xs16 = reinterpret_cast<float *>(slot + 768u);
+        dv.xs = reinterpret_cast<float2 *>(slot + 832u);
+        if constexpr (j == 0u) {  // x of block b has landed: its digits, over it
+            mvl_vmcnt_le<P::after_x(i)>();
+            asm volatile("" ::: "memory");
+            const float4 xv = *reinterpret_cast<const float4 *>(slot + 16u * lane);
+            const float v[4] = {xv.x, xv.y, xv.z, xv.w};
+            if (own) prep_block(v, lane, dv);
+        }
+        mvl_vmcnt_le<P::after_item(i)>();
+        asm volatile("" ::: "memory");
+        if (own) {
+            const Src src{w, a.rows[0] * rb, rb, r0 + 16u * j, r1};
+            float part = Q6K::dot_staged(lds + (ring - lds0) + (i % R) * kMvrItem, src, dv, b, n, g);
+            part += __shfl_xor(part, 16, 64);
+            part += __shfl_xor(part, 32, 64);
+            const uint32_t rr = 16u * j + n;
+            if (lane < 16u && rr < rpw) pb[rr * nblk + b] = part;
+            asm volatile("" ::"v"(part));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (i + R < NI) issue(std::integral_constant<uint32_t, i + R>{});
+    });
+
+    // row t of the range: its blocks' sums in block order
+    __syncthreads();
+    const uint32_t t = threadIdx.x;
+    if (t < r1 - r0) {
+        float s = 0.f;
+        const float *p = pb + t * nblk;
+        for (uint32_t k = 0; k < nblk; k++) s += p[k];
+        float *y = a.y[0] + r0 + t;
+        *y = EPI == E_ACC ? __fadd_rn(*y, s) : s;
+    }
+}
+
+template <uint32_t NB, uint32_t T, uint32_t R, int EPI>
+static hipError_t launch_mvr_t(const MvArgs &a, uint32_t wgs, uint32_t rpw, hipStream_t s) {
+    const size_t lds = MvrPlan<NB, T, R>::lds(a.cols / 256u);
+    static size_t granted = 0;
+    if (lds > granted) {
+        if (hipFuncSetAttribute((const void *)k_mvr<NB, T, R, EPI>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
+            (void)hipGetLastError();
+            return hipErrorNotSupported;
+        }
+        granted = lds;
+    }
+    k_mvr<NB, T, R, EPI><<<wgs, 1024, lds, s>>>(a, rpw);
+    return hipGetLastError();
+}
+
+// Q6_K rows of 33-48 blocks over 2049-4096 rows (7B down: 4096 x 11008): one
+// tile per workgroup, three blocks per wave, two items in flight per wave.
+hipError_t launch_q6k_mvr(const uint8_t *w, const float *x, float *y, uint32_t cols, uint32_t rows,
+                          int accumulate, hipStream_t s) {
+    const uint32_t nblk = cols / 256u;
+    if (cols % 256u || nblk <= 32u || nblk > 48u || rows <= 2048u || ((uintptr_t)w & 1u) ||
+        ((uintptr_t)x & 15u))
+        return hipErrorNotSupported;
+    const uint32_t wgs = mvl_cus();
+    const uint32_t rpw = (rows + wgs - 1u) / wgs;
+    if (rpw > 16u) return hipErrorNotSupported;
+    // the last row's last block read as aligned chunks must end inside the
+    // matrix (the DMA has no bounded form); offsets are 32-bit
+    const uint64_t rb = (uint64_t)nblk * 210u, bytes = rb * rows, wlo = (uintptr_t)w & 15u;
+    const uint64_t last = bytes - 210u;
+    if (((last + wlo) & ~(uint64_t)15u) + 224u > bytes + wlo || bytes + 256u >= (1ull << 32))
+        return hipErrorNotSupported;
+    MvArgs a{};
+    a.w[0] = w;
+    a.y[0] = y;
+    a.rows[0] = rows;
+    a.nmat = 1;
+    a.cols = cols;
+    a.x = x;
+    const uint32_t g = (rows + rpw - 1u) / rpw;
+    return accumulate ? launch_mvr_t<3, 1, 2, E_ACC>(a, g, rpw, s)
+                      : launch_mvr_t<3, 1, 2, E_STORE>(a, g, rpw, s);
 }
 
 hipError_t launch_q4k_mvl(const uint8_t *w, const float *x, float *y, uint32_t cols, uint32_t rows,
