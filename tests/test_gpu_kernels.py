@@ -211,6 +211,32 @@ def test_kquant_matrix_base_off_16_bytes(dev, host, oracle, mem, t, rows, cols, 
             assert rel_l2(gotb[b][sample], wantb) <= LIN_TOL
 
 
+@pytest.mark.parametrize("rows,cols,off", [(4096, 11008, 0), (3000, 8448, 0), (2100, 12288, 0),
+                                          (3001, 11008, 10), (8192, 28672, 0), (4100, 28672, 0),
+                                          (5000, 25088, 0)])
+@pytest.mark.parametrize("accumulate", [False, True])
+def test_q6k_ring_kernel_shapes(dev, host, oracle, mem, rows, cols, off, accumulate):
+    """Q6_K rows of 33-48 blocks over 2049-4096 rows and of 97-112 blocks
+    over 4097-8192 rows take the LDS-DMA ring kernel: full row ranges (16 and
+    32 rows per workgroup), short ones (12, 9, 17 and 20), 33, 48, 98 and 112
+    blocks, and a matrix starting 10 bytes past a 16-byte boundary whose last
+    block still ends inside its last aligned chunk; every row against the
+    oracle."""
+    w = V.synth_matrix(host, V.Q6_K, rows, cols, SEED, 31)
+    x = synth_x(host, cols, 32)
+    base = dev.alloc(w.nbytes + 32)
+    mem.ptrs.append(base)
+    pw = base + off
+    dev.write(pw, w)
+    y0 = synth_x(host, rows, 33)
+    px, py = mem.up(x), mem.up(y0)
+    dev.linear(V.Q6_K, pw, px, py, cols, rows, accumulate=accumulate)
+    got = dev.download(py, rows, np.float32)
+    want = oracle.linear(V.Q6_K, w, x, cols, rows, y=y0.copy() if accumulate else None,
+                         accumulate=accumulate, threads=16)
+    assert rel_l2(got, want) <= LIN_TOL
+
+
 def test_linear_offsets_accumulate(dev, host, oracle, mem):
     """Two column tiles into one output window: offsets index x and y, the
     second tile accumulates (src/vbs_backend_test.c:888-948)."""

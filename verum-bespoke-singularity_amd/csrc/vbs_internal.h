@@ -85,7 +85,8 @@ hipError_t launch_kq_linear_batch(int type, const uint8_t *w, const float *x, ui
 hipError_t launch_q4k_mvl(const uint8_t *w, const float *x, float *y, uint32_t cols, uint32_t rows,
                           int accumulate, hipStream_t s);
 // The ring variant (vbs_kern_mvl.hip) for Q6_K rows of 33-48 blocks over
-// 2049-4096 rows (7B down); hipErrorNotSupported elsewhere.
+// 2049-4096 rows (7B down) and of 97-112 blocks over 4097-8192 rows (70B
+// down); hipErrorNotSupported elsewhere.
 hipError_t launch_q6k_mvr(const uint8_t *w, const float *x, float *y, uint32_t cols, uint32_t rows,
                           int accumulate, hipStream_t s);
 // Specialised Q4_K matvec; hipErrorNotSupported when the shape/alignment is

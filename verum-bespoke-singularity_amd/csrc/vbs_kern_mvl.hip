@@ -176,8 +176,9 @@ static hipError_t launch_mvl_t(const MvArgs &a, uint32_t wgs, uint32_t rpw, hipS
 // over its x. Arithmetic and per-(row, block) sums are k_mvf's, so the results
 // equal k_mvf's bit for bit. Every wait is an explicit s_waitcnt on the number
 // of DMAs issued after the awaited one (the loads return in issue order).
-// Measured at 4096 x 11008 (7B down, weights streamed from HBM): 11.0-11.4
-// against k_mvf's 12.1-12.8 us.
+// Measured with the weights streamed from HBM: 4096 x 11008 (7B down)
+// 10.9-11.2 against k_mvf's 11.9-12.4 us, 8192 x 28672 (70B down) 41.1-42.1
+// against 47.3-52.2 us.
 constexpr uint32_t kMvrItem = 16u * 224u, kMvrDma = 4u;
 
 template <uint32_t I, uint32_t N, class F>
@@ -312,16 +313,18 @@ static hipError_t launch_mvr_t(const MvArgs &a, uint32_t wgs, uint32_t rpw, hipS
 }
 
 // Q6_K rows of 33-48 blocks over 2049-4096 rows (7B down: 4096 x 11008): one
-// tile per workgroup, three blocks per wave, two items in flight per wave.
+// tile per workgroup, three blocks per wave; rows of 97-112 blocks over
+// 4097-8192 rows (70B down: 8192 x 28672): two tiles, seven blocks per wave.
+// Two items in flight per wave.
 hipError_t launch_q6k_mvr(const uint8_t *w, const float *x, float *y, uint32_t cols, uint32_t rows,
                           int accumulate, hipStream_t s) {
     const uint32_t nblk = cols / 256u;
-    if (cols % 256u || nblk <= 32u || nblk > 48u || rows <= 2048u || ((uintptr_t)w & 1u) ||
-        ((uintptr_t)x & 15u))
+    const bool narrow = nblk > 32u && nblk <= 48u, wide = nblk > 96u && nblk <= 112u;
+    if (cols % 256u || !(narrow || wide) || ((uintptr_t)w & 1u) || ((uintptr_t)x & 15u))
         return hipErrorNotSupported;
     const uint32_t wgs = mvl_cus();
     const uint32_t rpw = (rows + wgs - 1u) / wgs;
-    if (rpw > 16u) return hipErrorNotSupported;
+    if (narrow ? rows <= 2048u || rpw > 16u : rows <= 4096u || rpw > 32u) return hipErrorNotSupported;
     // the last row's last block read as aligned chunks must end inside the
     // matrix (the DMA has no bounded form); offsets are 32-bit
     const uint64_t rb = (uint64_t)nblk * 210u, bytes = rb * rows, wlo = (uintptr_t)w & 15u;
@@ -336,6 +339,9 @@ hipError_t launch_q6k_mvr(const uint8_t *w, const float *x, float *y, uint32_t c
     a.cols = cols;
     a.x = x;
     const uint32_t g = (rows + rpw - 1u) / rpw;
+    if (wide)
+        return accumulate ? launch_mvr_t<7, 2, 2, E_ACC>(a, g, rpw, s)
+                          : launch_mvr_t<7, 2, 2, E_STORE>(a, g, rpw, s);
     return accumulate ? launch_mvr_t<3, 1, 2, E_ACC>(a, g, rpw, s)
                       : launch_mvr_t<3, 1, 2, E_STORE>(a, g, rpw, s);
 }
