@@ -116,6 +116,20 @@ def test_batch_70b_shapes(dev, host, oracle, mem, t, rows, cols):
             assert rel_l2(Y[b, lo:lo + k], oracle.linear(t, ws, X[b], cols, k)) <= LIN_TOL, (lo, b)
 
 
+@pytest.mark.parametrize("rows,cols", [(4096, 11008), (3000, 8448), (4100, 28672), (5000, 25088)])
+@pytest.mark.parametrize("batch", [3, 8, 11])
+def test_batch_q6k_ring_shapes(dev, host, oracle, mem, rows, cols, batch):
+    """Q6_K rows of 33-48 blocks over 2049-4096 rows and of 97-112 blocks
+    over 4097-8192 rows take the batched LDS-DMA ring kernel: whole and short
+    row ranges per workgroup, 33-112 blocks, one and two launches of eight
+    vectors; every row of every vector against the oracle."""
+    w = V.synth_matrix(host, V.Q6_K, rows, cols, SEED, 77)
+    X = vectors(host, batch, cols, 130)
+    Y = run_batch(dev, mem, V.Q6_K, w, X, rows, cols)
+    for b in range(batch):
+        assert rel_l2(Y[b], oracle.linear(V.Q6_K, w, X[b], cols, rows, threads=16)) <= LIN_TOL, b
+
+
 @pytest.mark.parametrize("rows", [11008, 22016])
 @pytest.mark.parametrize("batch", [5, 8])
 def test_batch_7b_gate_shape(dev, host, oracle, mem, batch, rows):

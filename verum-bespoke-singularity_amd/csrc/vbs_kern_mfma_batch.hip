@@ -1,6 +1,7 @@
 // vbs_kern_mfma_batch.hip — batched (skinny) K-quant matvec on the gfx950 f16
 // matrix cores: x preparation (k_xprep_b) and the k_mvb kernel, with the weight
 // loads of the batch-1 kernel (vbs_mfma.h).
+#include "vbs_lds_dma.h"
 #include "vbs_mfma.h"
 
 namespace vbs {
@@ -284,6 +285,12 @@ struct Q6KB {
             const uint32_t c = lane + 64u * i;
             if (i < 3u || c < 224u) *reinterpret_cast<u32x4 *>(scratch + 16u * c) = r[i];
         }
+        dot_staged(scratch, x, src, b, n, g, acc);
+    }
+    // The same from a scratch that already holds the tile's 224 chunks (chunk
+    // 14 n + k at 16 (14 n + k): row n's aligned 16-byte chunk k).
+    __device__ static void dot_staged(const uint8_t *scratch, const A &x, const Src &src, uint32_t b,
+                                      uint32_t n, uint32_t g, float acc[2]) {
         // row n's block starts o = (its address mod 16) into its 224 scratch bytes
         const uint32_t o = ((uint32_t)(uintptr_t)src.w + src.row(n) + b * BYTES) & 15u;
         const uint32_t *rw = reinterpret_cast<const uint32_t *>(scratch + 224u * n + (o & 12u));
@@ -396,6 +403,168 @@ __global__ __launch_bounds__(512) void k_mvb(const MbArgs a) {
     }
 }
 
+// ---- ring form of the batched Q6_K launch ----------------------------------------------
+// k_mvbr6: the batch-1 ring kernel's structure (k_mvr, vbs_kern_mvl.hip) with
+// Q6KB's arithmetic. One 16-wave workgroup per CU owns an even range of at
+// most 16 T rows; wave w owns blocks w, w + 16, ... (NB of them; slots past the
+// row re-read its last block and add nothing). Its items -- T tiles of each of
+// its blocks -- come by LDS DMA into a ring of R slots, item i + R requested
+// as soon as item i is computed, and the A operands of a block (the prepared
+// x planes and exponents) come into registers from inline assembly with the
+// block's first item, a block ahead of their use. Per tile a wave adds its
+// blocks in order, and the waves' sums are added in wave order at the end.
+typedef int vi2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ void q6kb_load_a_async(const XbView &v, uint32_t b, uint32_t g, h4 (&ag)[16],
+                                                  vi2 &as) {
+    const _Float16 *p = v.plane + 128u * (32u * b + (g >> 1)) + 4u * (g & 1u);
+#pragma unroll
+    for (uint32_t G = 0; G < 16u; G++)
+        asm volatile("global_load_dwordx2 %0, %1, off"
+                     : "=v"(ag[G])
+                     : "v"(p + 128u * (16u * (G >> 3) + 4u * ((G >> 1) & 3u) + 2u * (G & 1u))));
+    asm volatile("global_load_dwordx2 %0, %1, off" : "=v"(as) : "v"(v.expo + 8u * b + 2u * g));
+}
+
+template <uint32_t NB, uint32_t T, uint32_t R>
+struct MvbrPlan {
+    static constexpr uint32_t NI = NB * T, D = 4u, ISZ = 16u * 224u;
+    static_assert(R >= 1u && R <= NI && (NB == 1u || R <= T + 1u), "ring");
+    // loads that item i brings: its four DMAs, after the block's 17 A loads
+    // when it opens a block
+    static constexpr uint32_t with(uint32_t i) { return D + (i % T == 0u ? 17u : 0u); }
+    // loads issued after item i's last one when item i is computed
+    static constexpr uint32_t after_item(uint32_t i) {
+        uint32_t c = 0;
+        for (uint32_t j = i + 1u; j < i + R && j < NI; j++) c += with(j);
+        return c;
+    }
+    static constexpr size_t lds() { return 16u * (size_t)R * ISZ + (size_t)T * 16u * 128u * sizeof(float); }
+};
+
+template <uint32_t NB, uint32_t T, uint32_t R, bool ACC>
+__global__ __launch_bounds__(1024) void k_mvbr6(const MbArgs a, uint32_t rpw) {
+    using P = MvbrPlan<NB, T, R>;
+    constexpr uint32_t NI = P::NI, ISZ = P::ISZ;
+    extern __shared__ __align__(16) uint8_t lds[];
+    const uint32_t cols = a.cols, nblk = cols >> 8, rb = nblk * 210u;
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const uint32_t n = lane & 15u, g = lane >> 4;
+    const uint32_t r0 = blockIdx.x * rpw, r1 = min(r0 + rpw, a.rows[0]);
+    if (r0 >= r1) return;
+    const XbLayout L = xb_layout(cols);
+    const uint32_t pl = min(n, 2u * a.batch - 1u);
+    const XbView xv{reinterpret_cast<const _Float16 *>(a.xp) + 8u * pl,
+                    reinterpret_cast<const _Float16 *>(a.xp + L.msum) + 8u * pl,
+                    reinterpret_cast<const int *>(a.xp + L.expo)};
+    const uint32_t lds0 = (uint32_t)(uintptr_t)lds, ring = lds0 + wave * R * ISZ;
+    float *const red = reinterpret_cast<float *>(lds + 16u * R * ISZ);
+    // offsets are taken from w rounded down to 16 bytes (as in Q6K::load)
+    const uint8_t *const w = a.w[0];
+    const uint32_t wlo = (uint32_t)(uintptr_t)w & 15u;
+    h4 ag[2][16];
+    vi2 as[2];
+    float acc[T][2];
+#pragma unroll
+    for (uint32_t j = 0; j < T; j++) acc[j][0] = acc[j][1] = 0.f;
+
+    auto issue = [&](auto ic) {
+        constexpr uint32_t i = decltype(ic)::value;
+        constexpr uint32_t k = i / T, j = i % T;
+        const uint32_t b = min(wave + 16u * k, nblk - 1u);
+        if constexpr (j == 0u) q6kb_load_a_async(xv, b, g, ag[k % 2u], as[k % 2u]);
+        const uint32_t dst = ring + (i % R) * ISZ;
+#pragma unroll
+        for (uint32_t q = 0; q < 4u; q++) {
+            const uint32_t c = min(64u * q + lane, 223u);  // chunk 14 n' + k' of the tile
+            const uint32_t st = min(r0 + 16u * j + c / 14u, r1 - 1u) * rb + b * 210u;
+            const uint32_t off = ((st + wlo) & ~15u) + 16u * (c % 14u);
+            if (q < 3u || lane < 32u) dma16(w - wlo + off, dst + 1024u * q);
+        }
+    };
+    unroll_for<0u, R>(issue);
+
+    unroll_for<0u, NI>([&](auto ic) {
+        constexpr uint32_t i = decltype(ic)::value;
+        constexpr uint32_t k = i / T, j = i % T;
+        vmcnt_le<P::after_item(i)>();  // (the block's A loads precede its first item)
+        asm volatile("" ::: "memory");
+        if constexpr (j == 0u) {
+#pragma unroll
+            for (uint32_t G = 0; G < 16u; G++) asm volatile("" : "+v"(ag[k % 2u][G]));
+            asm volatile("" : "+v"(as[k % 2u]));
+        }
+        const uint32_t bw = wave + 16u * k;
+        if (bw < nblk) {
+            Q6KB::A x;
+#pragma unroll
+            for (uint32_t G = 0; G < 16u; G++) x.g[G] = ag[k % 2u][G];
+            x.s = make_int2(as[k % 2u].x, as[k % 2u].y);
+            const Src src{w, a.rows[0] * rb, rb, r0 + 16u * j, r1};
+            Q6KB::dot_staged(lds + (ring - lds0) + (i % R) * ISZ, x, src, bw, n, g, acc[j]);
+            asm volatile("" ::"v"(acc[j][0]), "v"(acc[j][1]));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (i + R < NI) issue(std::integral_constant<uint32_t, i + R>{});
+    });
+
+    // per tile: lane (n, g) holds row n for vectors 2g and 2g + 1; the waves'
+    // sums added in wave order
+#pragma unroll
+    for (uint32_t j = 0; j < T; j++) {
+        red[(j * 16u + wave) * 128u + 2u * lane] = acc[j][0];
+        red[(j * 16u + wave) * 128u + 2u * lane + 1u] = acc[j][1];
+    }
+    __syncthreads();
+    for (uint32_t q = threadIdx.x; q < T * 128u; q += 1024u) {
+        const uint32_t j = q >> 7, l = (q >> 1) & 63u, tk = q & 1u;
+        float sum = 0.f;
+        for (uint32_t v = 0; v < 16u; v++) sum += red[(j * 16u + v) * 128u + 2u * l + tk];
+        const uint32_t row = r0 + 16u * j + (l & 15u), t = 2u * (l >> 4) + tk;
+        if (row < r1 && t < a.batch) {
+            float *dst = a.y[0] + (uint64_t)t * a.ys[0] + row;
+            *dst = ACC ? __fadd_rn(*dst, sum) : sum;
+        }
+    }
+}
+
+template <uint32_t NB, uint32_t T, uint32_t R, bool ACC>
+static hipError_t launch_mvbr6_t(const MbArgs &a, uint32_t wgs, uint32_t rpw, hipStream_t s) {
+    const size_t lds = MvbrPlan<NB, T, R>::lds();
+    static bool granted = false;
+    if (!granted) {
+        if (hipFuncSetAttribute((const void *)k_mvbr6<NB, T, R, ACC>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
+            (void)hipGetLastError();
+            return hipErrorNotSupported;
+        }
+        granted = true;
+    }
+    k_mvbr6<NB, T, R, ACC><<<wgs, 1024, lds, s>>>(a, rpw);
+    return hipGetLastError();
+}
+
+// One Q6_K matrix of rows of 33-48 blocks over 2049-4096 rows (three blocks
+// per wave, one tile) or of 97-112 blocks over 4097-8192 rows (seven blocks,
+// two tiles); the matrix's last block read as aligned chunks must end inside
+// it (the DMA has no bounded form).
+static hipError_t launch_mvbr6(const MbArgs &a, bool acc, hipStream_t s) {
+    const uint32_t nblk = a.cols / 256u, rows = a.rows[0];
+    const bool narrow = nblk > 32u && nblk <= 48u, wide = nblk > 96u && nblk <= 112u;
+    if (a.nmat != 1u || a.cols % 256u || !(narrow || wide) || ((uintptr_t)a.w[0] & 1u))
+        return hipErrorNotSupported;
+    const uint32_t wgs = device_cus();
+    const uint32_t rpw = (rows + wgs - 1u) / wgs;
+    if (narrow ? rows <= 2048u || rpw > 16u : rows <= 4096u || rpw > 32u) return hipErrorNotSupported;
+    const uint64_t rb = (uint64_t)nblk * 210u, bytes = rb * rows, wlo = (uintptr_t)a.w[0] & 15u;
+    const uint64_t last = bytes - 210u;
+    if (((last + wlo) & ~(uint64_t)15u) + 224u > bytes + wlo || bytes + 256u >= (1ull << 32))
+        return hipErrorNotSupported;
+    const uint32_t g = (rows + rpw - 1u) / rpw;
+    if (wide) return acc ? launch_mvbr6_t<7, 2, 2, true>(a, g, rpw, s) : launch_mvbr6_t<7, 2, 2, false>(a, g, rpw, s);
+    return acc ? launch_mvbr6_t<3, 1, 2, true>(a, g, rpw, s) : launch_mvbr6_t<3, 1, 2, false>(a, g, rpw, s);
+}
+
 template <class T, uint32_t TPW, bool ACC>
 static hipError_t launch_mvb_t(const MbArgs &a, uint32_t nw, hipStream_t s) {
     const uint32_t tiles = a.tile_end[a.nmat - 1u];
@@ -463,6 +632,10 @@ hipError_t launch_mvb(int type, uint32_t nmat, const uint8_t *const w[], const u
     a.xp = xp;
     a.cols = cols;
     a.batch = batch;
+    if (type == kQ6_K) {
+        const hipError_t e = launch_mvbr6(a, accumulate != 0, s);
+        if (e != hipErrorNotSupported) return e;
+    }
     if (type == kQ4_K)
         return accumulate ? launch_mvb_plan<Q4KB, true>(a, s) : launch_mvb_plan<Q4KB, false>(a, s);
     return accumulate ? launch_mvb_plan<Q6KB, true>(a, s) : launch_mvb_plan<Q6KB, false>(a, s);

@@ -19,24 +19,12 @@
 // the compiler's builtin makes it insert waits for all loads before every
 // LDS access. The compiler does not see these loads, so each wait for them is
 // an explicit s_waitcnt; nothing else in these kernels uses M0.
-#include <type_traits>
-
+#include "vbs_lds_dma.h"
 #include "vbs_mfma.h"
 
 namespace vbs {
 
 constexpr uint32_t kMvlWaves = 16, kMvlItem = 16u * 144u, kMvlSlot = 1024u, kMvlMaxT = 3;
-
-__device__ __forceinline__ void mvl_dma16(const void *g, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g),
-                 "s"(__builtin_amdgcn_readfirstlane(lds))
-                 : "memory");
-}
-template <uint32_t N>
-__device__ __forceinline__ void mvl_vmcnt_le() {  // vmcnt <= N, other counters untouched
-    static_assert(N < 64, "vmcnt");
-    __builtin_amdgcn_s_waitcnt((N & 15u) | ((N >> 4) << 14) | (7u << 4) | (15u << 8));
-}
 
 // EPI: E_STORE (y = W x) or E_ACC (y += W x). T tiles of 16 rows per workgroup,
 // rpw <= 16 T rows each (the last workgroup's range may be shorter or empty).
@@ -60,7 +48,7 @@ __global__ __launch_bounds__(64 * kMvlWaves) void k_mvl(const MvArgs a, uint32_t
 
     // 1. all loads: x block b (one DMA), then the T items (three DMAs each:
     // chunk c = 9 n' + p is piece p of row n' of the tile, at item + 16 c)
-    mvl_dma16(a.x + 256u * b + 4u * lane, (uint32_t)(uintptr_t)slot);
+    dma16(a.x + 256u * b + 4u * lane, (uint32_t)(uintptr_t)slot);
 #pragma unroll
     for (uint32_t j = 0; j < T; j++) {
 #pragma unroll
@@ -68,7 +56,7 @@ __global__ __launch_bounds__(64 * kMvlWaves) void k_mvl(const MvArgs a, uint32_t
             const uint32_t c = 64u * q + lane;
             const uint32_t row = min(r0 + 16u * j + c / 9u, r1 - 1u);
             const uint8_t *src = w + ((uint64_t)row * rb + b * 144u + 16u * (c % 9u));
-            if (q < 2u || lane < 16u) mvl_dma16(src, stage + j * kMvlItem + 1024u * q);
+            if (q < 2u || lane < 16u) dma16(src, stage + j * kMvlItem + 1024u * q);
         }
     }
     if (lane < 4u) reinterpret_cast<uint32_t *>(xq)[lane] = 0u;
@@ -81,7 +69,7 @@ __global__ __launch_bounds__(64 * kMvlWaves) void k_mvl(const MvArgs a, uint32_t
 
     // 2. x has landed (the 3 T item DMAs after it may still be in flight):
     // its digits, written over it in the same slot
-    mvl_vmcnt_le<3u * T>();
+    vmcnt_le<3u * T>();
     asm volatile("" ::: "memory");
     {
         const float4 xv = *reinterpret_cast<const float4 *>(slot + 16u * lane);
@@ -105,16 +93,16 @@ __global__ __launch_bounds__(64 * kMvlWaves) void k_mvl(const MvArgs a, uint32_t
         asm volatile("" ::"v"(part));
         __builtin_amdgcn_sched_barrier(0);
     };
-    mvl_vmcnt_le<3u * (T - 1u)>();
+    vmcnt_le<3u * (T - 1u)>();
     asm volatile("" ::: "memory");
     item(0);
     if constexpr (T > 1u) {
-        mvl_vmcnt_le<3u * (T - 2u)>();
+        vmcnt_le<3u * (T - 2u)>();
         asm volatile("" ::: "memory");
         item(1);
     }
     if constexpr (T > 2u) {
-        mvl_vmcnt_le<0u>();
+        vmcnt_le<0u>();
         asm volatile("" ::: "memory");
         item(2);
     }
@@ -181,14 +169,6 @@ static hipError_t launch_mvl_t(const MvArgs &a, uint32_t wgs, uint32_t rpw, hipS
 // against 47.3-52.2 us.
 constexpr uint32_t kMvrItem = 16u * 224u, kMvrDma = 4u;
 
-template <uint32_t I, uint32_t N, class F>
-__device__ __forceinline__ void mvr_for(F &&f) {
-    if constexpr (I < N) {
-        f(std::integral_constant<uint32_t, I>{});
-        mvr_for<I + 1u, N>(f);
-    }
-}
-
 template <uint32_t NB, uint32_t T, uint32_t R>
 struct MvrPlan {
     static constexpr uint32_t NI = NB * T, D = kMvrDma;
@@ -236,20 +216,20 @@ __global__ __launch_bounds__(1024) void k_mvr(const MvArgs a, uint32_t rpw) {
         constexpr uint32_t k = i / T, j = i % T;
         const uint32_t b = min(wave + 16u * k, nblk - 1u);
         if constexpr (j == 0u)
-            mvl_dma16(a.x + 256u * b + 4u * lane, (uint32_t)(uintptr_t)(xs0 + (k % P::XS) * 1024u));
+            dma16(a.x + 256u * b + 4u * lane, (uint32_t)(uintptr_t)(xs0 + (k % P::XS) * 1024u));
         const uint32_t dst = ring + (i % R) * kMvrItem;
 #pragma unroll
         for (uint32_t q = 0; q < kMvrDma; q++) {
             const uint32_t c = min(64u * q + lane, 223u);  // chunk 14 n' + k' of the tile
             const uint32_t st = min(r0 + 16u * j + c / 14u, r1 - 1u) * rb + b * 210u;
             const uint32_t off = ((st + wlo) & ~15u) + 16u * (c % 14u);
-            if (q < 3u || lane < 32u) mvl_dma16(w - wlo + off, dst + 1024u * q);
+            if (q < 3u || lane < 32u) dma16(w - wlo + off, dst + 1024u * q);
         }
     };
-    mvr_for<0u, R>(issue);
+    unroll_for<0u, R>(issue);
     if (lane < 4u) reinterpret_cast<uint32_t *>(zero)[lane] = 0u;
 
-    mvr_for<0u, NI>([&](auto ic) {
+    unroll_for<0u, NI>([&](auto ic) {
         constexpr uint32_t i = decltype(ic)::value;
         constexpr uint32_t k = i / T, j = i % T;
         const uint32_t bw = wave + 16u * k;
@@ -263,13 +243,13 @@ __global__ __launch_bounds__(1024) void k_mvr(const MvArgs a, uint32_t rpw) {
         dv.xs16 = reinterpret_cast<float *>(slot + 768u);
         dv.xs = reinterpret_cast<float2 *>(slot + 832u);
         if constexpr (j == 0u) {  // x of block b has landed: its digits, over it
-            mvl_vmcnt_le<P::after_x(i)>();
+            vmcnt_le<P::after_x(i)>();
             asm volatile("" ::: "memory");
             const float4 xv = *reinterpret_cast<const float4 *>(slot + 16u * lane);
             const float v[4] = {xv.x, xv.y, xv.z, xv.w};
             if (own) prep_block(v, lane, dv);
         }
-        mvl_vmcnt_le<P::after_item(i)>();
+        vmcnt_le<P::after_item(i)>();
         asm volatile("" ::: "memory");
         if (own) {
             const Src src{w, a.rows[0] * rb, rb, r0 + 16u * j, r1};
