@@ -565,6 +565,228 @@ static hipError_t launch_mvbr6(const MbArgs &a, bool acc, hipStream_t s) {
     return acc ? launch_mvbr6_t<3, 1, 2, true>(a, g, rpw, s) : launch_mvbr6_t<3, 1, 2, false>(a, g, rpw, s);
 }
 
+// Q4KB's A operands of block b requested from inline assembly (vbs_lds_dma.h):
+// the eight k-slices, the mins' sums and the two exponents.
+__device__ __forceinline__ void q4kb_load_a_async(const XbView &v, uint32_t b, uint32_t g, h8 (&am)[8],
+                                                  h8 &mn, vi2 &es) {
+    const _Float16 *p = v.plane + 128u * (32u * b + 2u * (g & 1u));
+#pragma unroll
+    for (uint32_t m = 0; m < 8u; m++) {
+        const uint32_t j = 4u * (m >> 2) + 2u * (g >> 1) + ((m >> 1) & 1u);
+        asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(am[m]) : "v"(p + 128u * (4u * j + (m & 1u))));
+    }
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(mn) : "v"(v.msum + 128u * b));
+    asm volatile("global_load_dwordx2 %0, %1, off" : "=v"(es) : "v"(v.expo + 8u * b + 2u * g));
+}
+
+// ---- ring form of the batched Q4_K launch ----------------------------------------------
+// k_mvbr4: one 16-wave workgroup per CU owns T consecutive tiles (of up to three
+// matrices); wave w owns blocks w, w + 16, ... (NB of them) and for each of them
+// all T tiles, so a block's A operands (Q4KB's, 10 loads from inline assembly)
+// serve T items. The items -- for each of the wave's blocks, its T tiles'
+// 16 x 144 bytes -- come by LDS DMA into a ring of R slots, item i + R requested
+// as soon as item i is computed; the next block's A operands are requested
+// after the current block's last item, into the same registers. Per tile a wave
+// adds its blocks in order; the waves' sums meet in LDS (the ring's space, a
+// pass of up to kMvbr4Pass tiles at a time) and are added in wave order.
+template <uint32_t NB, uint32_t T, uint32_t R>
+struct Mvbr4Plan {
+    static constexpr uint32_t NI = NB * T, ISZ = 16u * 144u;
+    static_assert(R >= 1u && R <= NI, "ring");
+    // Loads issued after the awaited one when item i is computed: the awaited
+    // one is item i's last DMA, or for the first item of a later block that
+    // block's A. Issue order: A(0), items 0 .. R - 1; after computing item s,
+    // A(k) when s is the last item of block k - 1, then item s + R.
+    static constexpr uint32_t wait_count(uint32_t i) {
+        const bool await_a = i % T == 0u && i >= T;
+        uint32_t count = 0;
+        bool after = false;
+        auto visit = [&](bool is_a, uint32_t idx, uint32_t n) {
+            if (after)
+                count += n;
+            else if (await_a ? (is_a && idx == i / T) : (!is_a && idx == i))
+                after = true;
+        };
+        visit(true, 0u, 10u);
+        for (uint32_t q = 0; q < R; q++) visit(false, q, 3u);
+        for (uint32_t st = 0; st < i; st++) {
+            if ((st + 1u) % T == 0u && (st + 1u) / T < NB) visit(true, (st + 1u) / T, 10u);
+            if (st + R < NI) visit(false, st + R, 3u);
+        }
+        return count;
+    }
+    static constexpr size_t lds() { return 16u * (size_t)R * ISZ; }
+};
+constexpr uint32_t kMvbr4Pass = 12;  // tiles per reduction pass (12 x 8 KB in the ring's 110 KB)
+
+template <uint32_t NB, uint32_t T, uint32_t R, bool ACC>
+__global__ __launch_bounds__(1024) void k_mvbr4(const MbArgs a) {
+    using P = Mvbr4Plan<NB, T, R>;
+    constexpr uint32_t NI = P::NI, ISZ = P::ISZ;
+    static_assert(16u * R * ISZ >= (T < kMvbr4Pass ? T : kMvbr4Pass) * 16u * 128u * sizeof(float), "pass");
+    extern __shared__ __align__(16) uint8_t lds[];
+    const uint32_t cols = a.cols, nblk = cols >> 8, rb = nblk * 144u;
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const uint32_t n = lane & 15u, g = lane >> 4;
+    const uint32_t total = a.tile_end[a.nmat - 1u], gt0 = blockIdx.x * T;
+    if (gt0 >= total) return;
+    const XbLayout L = xb_layout(cols);
+    const uint32_t pl = min(n, 2u * a.batch - 1u);
+    const XbView xv{reinterpret_cast<const _Float16 *>(a.xp) + 8u * pl,
+                    reinterpret_cast<const _Float16 *>(a.xp + L.msum) + 8u * pl,
+                    reinterpret_cast<const int *>(a.xp + L.expo)};
+    const uint32_t lds0 = (uint32_t)(uintptr_t)lds, ring = lds0 + wave * R * ISZ;
+    // tile j of the workgroup: matrix, local tile and row count (tiles past
+    // the last one repeat it and are not stored)
+    auto tile = [&](uint32_t j, uint32_t &m, uint32_t &lt, uint32_t &rows) {
+        const uint32_t gt = min(gt0 + j, total - 1u);
+        m = (gt >= a.tile_end[0]) + (a.nmat > 2u && gt >= a.tile_end[1]);
+        lt = gt - (m == 0u ? 0u : m == 1u ? a.tile_end[0] : a.tile_end[1]);  // (no dynamic index
+        rows = m == 0u ? a.rows[0] : m == 1u ? a.rows[1] : a.rows[2];      // into the arguments)
+    };
+    // every tile's matrix and this lane's three chunk offsets in it, computed
+    // before the first DMA (argument reads inside the stream would wait for it)
+    const uint8_t *tw[T];
+    uint32_t toff[T][3];
+#pragma unroll
+    for (uint32_t j = 0; j < T; j++) {
+        uint32_t m, lt, rows;
+        tile(j, m, lt, rows);
+        tw[j] = m == 0u ? a.w[0] : m == 1u ? a.w[1] : a.w[2];
+#pragma unroll
+        for (uint32_t q = 0; q < 3u; q++) {
+            const uint32_t c = min(64u * q + lane, 143u);  // chunk 9 n' + p of the tile
+            toff[j][q] = min(16u * lt + c / 9u, rows - 1u) * rb + 16u * (c % 9u);
+        }
+    }
+    auto issue = [&](auto ic) {
+        constexpr uint32_t i = decltype(ic)::value;
+        constexpr uint32_t k = i / T, j = i % T;
+        const uint32_t b = min(wave + 16u * k, nblk - 1u);
+        const uint32_t dst = ring + (i % R) * ISZ;
+#pragma unroll
+        for (uint32_t q = 0; q < 3u; q++)
+            if (q < 2u || lane < 16u) dma16(tw[j] + toff[j][q] + b * 144u, dst + 1024u * q);
+    };
+    h8 am[8], mn;
+    vi2 es;
+    float acc[T][2];
+#pragma unroll
+    for (uint32_t j = 0; j < T; j++) acc[j][0] = acc[j][1] = 0.f;
+    q4kb_load_a_async(xv, min(wave, nblk - 1u), g, am, mn, es);
+    unroll_for<0u, R>(issue);
+
+    unroll_for<0u, NI>([&](auto ic) {
+        constexpr uint32_t i = decltype(ic)::value;
+        constexpr uint32_t k = i / T, j = i % T;
+        vmcnt_le<P::wait_count(i)>();
+        asm volatile("" ::: "memory");
+        if constexpr (j == 0u) {
+#pragma unroll
+            for (uint32_t q = 0; q < 8u; q++) asm volatile("" : "+v"(am[q]));
+            asm volatile("" : "+v"(mn), "+v"(es));
+        }
+        const uint32_t bw = wave + 16u * k;
+        if (bw < nblk) {
+            Q4KB::A x;
+#pragma unroll
+            for (uint32_t q = 0; q < 8u; q++) x.m[q] = am[q];
+            const h8 z = {};
+            x.mn = g == 0u ? mn : z;
+            x.s = make_int2(es.x, es.y);
+            const uint8_t *row = lds + (ring - lds0) + (i % R) * ISZ + 144u * n;
+            u32x4 r[3];
+            r[0] = lda4(row);
+            r[1] = lda4(row + 16u + 16u * g);
+            r[2] = lda4(row + 80u + 16u * g);
+            const Src src{a.w[0], 0u, rb, 0u, 1u};  // (Q4KB::dot reads nothing through it)
+            Q4KB::dot(r, x, nullptr, src, bw, n, g, acc[j]);
+            asm volatile("" ::"v"(acc[j][0]), "v"(acc[j][1]));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (j == T - 1u && k + 1u < NB)
+            q4kb_load_a_async(xv, min(wave + 16u * (k + 1u), nblk - 1u), g, am, mn, es);
+        if constexpr (i + R < NI) issue(std::integral_constant<uint32_t, i + R>{});
+    });
+
+    // per tile: lane (n, g) holds row n for vectors 2g and 2g + 1; the waves'
+    // sums meet in the ring's space and are added in wave order
+    __syncthreads();
+    float *const red = reinterpret_cast<float *>(lds);
+    unroll_for<0u, (T + kMvbr4Pass - 1u) / kMvbr4Pass>([&](auto pc) {
+        constexpr uint32_t j0 = decltype(pc)::value * kMvbr4Pass;
+        constexpr uint32_t jn = T - j0 < kMvbr4Pass ? T - j0 : kMvbr4Pass;
+#pragma unroll
+        for (uint32_t jj = 0; jj < jn; jj++) {
+            red[(jj * 16u + wave) * 128u + 2u * lane] = acc[j0 + jj][0];
+            red[(jj * 16u + wave) * 128u + 2u * lane + 1u] = acc[j0 + jj][1];
+        }
+        __syncthreads();
+        for (uint32_t q = threadIdx.x; q < jn * 128u; q += 1024u) {
+            const uint32_t jj = q >> 7, l = (q >> 1) & 63u, tk = q & 1u;
+            float sum = 0.f;
+            for (uint32_t v = 0; v < 16u; v++) sum += red[(jj * 16u + v) * 128u + 2u * l + tk];
+            uint32_t m, lt, rows;
+            tile(j0 + jj, m, lt, rows);
+            const uint32_t row = 16u * lt + (l & 15u), t = 2u * (l >> 4) + tk;
+            if (gt0 + j0 + jj < total && row < rows && t < a.batch) {
+                float *const y = m == 0u ? a.y[0] : m == 1u ? a.y[1] : a.y[2];
+                const uint32_t ys = m == 0u ? a.ys[0] : m == 1u ? a.ys[1] : a.ys[2];
+                float *dst = y + (uint64_t)t * ys + row;
+                *dst = ACC ? __fadd_rn(*dst, sum) : sum;
+            }
+        }
+        __syncthreads();
+    });
+}
+
+template <uint32_t NB, uint32_t T, bool ACC>
+static hipError_t launch_mvbr4_t(const MbArgs &a, uint32_t wgs, hipStream_t s) {
+    constexpr uint32_t R = NB * T < 3u ? NB * T : 3u;
+    const size_t lds = Mvbr4Plan<NB, T, R>::lds();
+    static bool granted = false;
+    if (!granted) {
+        if (hipFuncSetAttribute((const void *)k_mvbr4<NB, T, R, ACC>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
+            (void)hipGetLastError();
+            return hipErrorNotSupported;
+        }
+        granted = true;
+    }
+    k_mvbr4<NB, T, R, ACC><<<wgs, 1024, lds, s>>>(a);
+    return hipGetLastError();
+}
+
+// Rows of 16 or 17-32 blocks; tiles per workgroup: the tiles per CU rounded up
+// to 1, 2, 3 or 6, or 7 with as many rounds of workgroups as that takes (more
+// tiles per workgroup would not fit the registers); w 16-byte aligned, 32-bit
+// offsets.
+static hipError_t launch_mvbr4(const MbArgs &a, bool acc, hipStream_t s) {
+    const uint32_t nblk = a.cols / 256u, total = a.tile_end[a.nmat - 1u], cus = device_cus();
+    if (a.cols % 256u || nblk == 0u || nblk > 32u) return hipErrorNotSupported;
+    for (uint32_t m = 0; m < a.nmat; m++)
+        if (((uintptr_t)a.w[m] & 15u) || (uint64_t)a.rows[m] * nblk * 144u + 256u >= (1ull << 32))
+            return hipErrorNotSupported;
+    const uint32_t per = (total + cus - 1u) / cus;
+    const uint32_t T = per <= 1u ? 1u : per <= 2u ? 2u : per <= 3u ? 3u : per <= 6u ? 6u : 7u;
+    const uint32_t wgs = (total + T - 1u) / T;
+#define VBS_MVBR4(NB_, T_)                                                                  \
+    return acc ? launch_mvbr4_t<NB_, T_, true>(a, wgs, s) : launch_mvbr4_t<NB_, T_, false>(a, wgs, s)
+    if (nblk <= 16u) {
+        if (T == 1u) VBS_MVBR4(1, 1);
+        if (T == 2u) VBS_MVBR4(1, 2);
+        if (T == 3u) VBS_MVBR4(1, 3);
+        if (T == 6u) VBS_MVBR4(1, 6);
+        VBS_MVBR4(1, 7);
+    }
+    if (T == 1u) VBS_MVBR4(2, 1);
+    if (T == 2u) VBS_MVBR4(2, 2);
+    if (T == 3u) VBS_MVBR4(2, 3);
+    if (T == 6u) VBS_MVBR4(2, 6);
+    VBS_MVBR4(2, 7);
+#undef VBS_MVBR4
+}
+
 template <class T, uint32_t TPW, bool ACC>
 static hipError_t launch_mvb_t(const MbArgs &a, uint32_t nw, hipStream_t s) {
     const uint32_t tiles = a.tile_end[a.nmat - 1u];
@@ -632,8 +854,9 @@ hipError_t launch_mvb(int type, uint32_t nmat, const uint8_t *const w[], const u
     a.xp = xp;
     a.cols = cols;
     a.batch = batch;
-    if (type == kQ6_K) {
-        const hipError_t e = launch_mvbr6(a, accumulate != 0, s);
+    {
+        const hipError_t e = type == kQ6_K ? launch_mvbr6(a, accumulate != 0, s)
+                                           : launch_mvbr4(a, accumulate != 0, s);
         if (e != hipErrorNotSupported) return e;
     }
     if (type == kQ4_K)
