@@ -613,15 +613,24 @@ static hipError_t enqueue_step_batch(const BDecoder &d, hipStream_t s) {
         const int *t = d.wtype.data() + 7 * L;
         const uint8_t *const *w = (const uint8_t *const *)d.wdata.data() + 7 * L;
         const uint64_t layer_off = (uint64_t)L * m.max_ctx * kvd;
-        {  // attn_norm, Q, K, V
+        {  // attn_norm, Q, K, V, RoPE and the cache stores: one launch after the
+           // preparation when q, k and v are Q4_K, else the store kernel after them
             VBS_TRY(launch_xprep(XP_NORM, d.x, nullptr, H, d.attn_norm[L], m.rms_eps, H, B, d.xp, s));
             const uint32_t rows[3] = {qd, kvd, kvd}, ys[3] = {qd, kvd, kvd};
-            float *const y[3] = {d.q, d.k, d.v};
-            VBS_TRY(launch_mvb(t[0], 3, w, rows, y, ys, 0, d.xp, H, B, s));
+            hipError_t e = t[0] == t[1] && t[1] == t[2]
+                               ? launch_mvb_qkv(t[0], w, rows, d.q, qd, d.xp, H, B, d.rope, pos_dev, m.kc,
+                                                m.vc, d.kv_seq, layer_off, hd, kvd, m.max_ctx, s)
+                               : hipErrorNotSupported;
+            if (e == hipErrorNotSupported) {
+                float *const y[3] = {d.q, d.k, d.v};
+                VBS_TRY(launch_mvb(t[0], 3, w, rows, y, ys, 0, d.xp, H, B, s));
+                k_rope_store_b<<<dim3((units + 255u) / 256u, B), 256, 0, s>>>(
+                    d.q, d.k, d.v, qd, kvd, hd, d.rope, pos_dev, m.kc, m.vc, d.kv_seq, layer_off,
+                    m.max_ctx);
+                e = hipGetLastError();
+            }
+            VBS_TRY(e);
         }
-        k_rope_store_b<<<dim3((units + 255u) / 256u, B), 256, 0, s>>>(
-            d.q, d.k, d.v, qd, kvd, hd, d.rope, pos_dev, m.kc, m.vc, d.kv_seq, layer_off, m.max_ctx);
-        VBS_TRY(hipGetLastError());
         VBS_TRY(launch_attention_batch(d.q, m.kc, m.vc, d.attn, m.max_ctx, pos_dev, d.part, layer_off,
                                        nq, nkv, hd, scale, B, qd, d.kv_seq, s));
         {  // O, added into the residual stream

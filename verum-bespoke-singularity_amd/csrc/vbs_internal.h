@@ -72,6 +72,15 @@ hipError_t launch_xprep(int mode, const float *x, const float *x2, uint32_t xs,
 hipError_t launch_mvb(int type, uint32_t nmat, const uint8_t *const w[], const uint32_t rows[],
                       float *const y[], const uint32_t ys[], int accumulate, const uint8_t *xp,
                       uint32_t cols, uint32_t batch, hipStream_t s);
+// The batched decoder's Q/K/V launch with the RoPE and the f16 cache store of
+// every sequence in its epilogue (q, k, v of Q4_K, rows of 16-row multiples, at
+// most 32 blocks; hipErrorNotSupported otherwise): q rows to q + t q_stride,
+// k and v rows to kc / vc + t kv_seq + layer_off + pos[t] kvd.
+hipError_t launch_mvb_qkv(int type, const uint8_t *const w[3], const uint32_t rows[3], float *q,
+                          uint32_t q_stride, const uint8_t *xp, uint32_t cols, uint32_t batch,
+                          const float2 *rope, const uint32_t *pos, uint16_t *kc, uint16_t *vc,
+                          uint64_t kv_seq, uint64_t layer_off, uint32_t hd, uint32_t kvd,
+                          uint32_t max_ctx, hipStream_t s);
 // Y[t] = W * X[t] for t < batch <= 8 (Q4_K / Q6_K) on the f16 matrix cores,
 // W read once; x prepared into the runtime scratch first. hipErrorNotSupported
 // (before anything is launched) outside the matrix-core shape range.

@@ -168,6 +168,15 @@ struct MbArgs {
     uint32_t nmat;
     const uint8_t *xp;
     uint32_t cols, batch;
+    // E_QKV (the batched decoder's Q/K/V launch, matrices q, k, v): RoPE of the
+    // q and k rows at sequence t's device position pos[t] (table rope[pos][hd/2]),
+    // q rows to y[0], k and v rows as f16 to the caches at t * kv_seq +
+    // layer_off + pos[t] * kvd (src/vbs_host_math.h:38-51, 150-159)
+    const float2 *rope;
+    const uint32_t *pos;
+    uint16_t *kc, *vc;
+    uint64_t kv_seq, layer_off;
+    uint32_t hd, kvd, max_ctx;
 };
 
 // This lane's A row: its plane's first eight elements and first eight
@@ -619,7 +628,7 @@ struct Mvbr4Plan {
 };
 constexpr uint32_t kMvbr4Pass = 12;  // tiles per reduction pass (12 x 8 KB in the ring's 110 KB)
 
-template <uint32_t NB, uint32_t T, uint32_t R, bool ACC>
+template <uint32_t NB, uint32_t T, uint32_t R, int EPI>
 __global__ __launch_bounds__(1024) void k_mvbr4(const MbArgs a) {
     using P = Mvbr4Plan<NB, T, R>;
     constexpr uint32_t NI = P::NI, ISZ = P::ISZ;
@@ -729,31 +738,51 @@ __global__ __launch_bounds__(1024) void k_mvbr4(const MbArgs a) {
             uint32_t m, lt, rows;
             tile(j0 + jj, m, lt, rows);
             const uint32_t row = 16u * lt + (l & 15u), t = 2u * (l >> 4) + tk;
-            if (gt0 + j0 + jj < total && row < rows && t < a.batch) {
+            const bool st = gt0 + j0 + jj < total && row < rows && t < a.batch;
+            if constexpr (EPI == E_QKV) {
+                // the RoPE partner (row ^ 1, same vector) is thread q ^ 2
+                const float other = __shfl_xor(sum, 2, 64);
+                if (st) {
+                    const uint32_t pos = a.pos[t];
+                    float v = sum;
+                    if (m < 2u && pos < a.max_ctx) {
+                        const float2 cs = a.rope[(uint64_t)pos * (a.hd / 2u) + (row % a.hd) / 2u];
+                        const bool even = (row & 1u) == 0u;
+                        const float x0 = even ? sum : other, x1 = even ? other : sum;
+                        v = even ? __fsub_rn(__fmul_rn(x0, cs.x), __fmul_rn(x1, cs.y))
+                                 : __fadd_rn(__fmul_rn(x0, cs.y), __fmul_rn(x1, cs.x));
+                    }
+                    if (m == 0u)
+                        a.y[0][(uint64_t)t * a.ys[0] + row] = v;
+                    else if (pos < a.max_ctx)  // (the host bounds every greedy run by max_ctx)
+                        (m == 1u ? a.kc : a.vc)[(uint64_t)t * a.kv_seq + a.layer_off + (uint64_t)pos * a.kvd +
+                                                row] = vbs_f2h(v);
+                }
+            } else if (st) {
                 float *const y = m == 0u ? a.y[0] : m == 1u ? a.y[1] : a.y[2];
                 const uint32_t ys = m == 0u ? a.ys[0] : m == 1u ? a.ys[1] : a.ys[2];
                 float *dst = y + (uint64_t)t * ys + row;
-                *dst = ACC ? __fadd_rn(*dst, sum) : sum;
+                *dst = EPI == E_ACC ? __fadd_rn(*dst, sum) : sum;
             }
         }
         __syncthreads();
     });
 }
 
-template <uint32_t NB, uint32_t T, bool ACC>
+template <uint32_t NB, uint32_t T, int EPI>
 static hipError_t launch_mvbr4_t(const MbArgs &a, uint32_t wgs, hipStream_t s) {
     constexpr uint32_t R = NB * T < 3u ? NB * T : 3u;
     const size_t lds = Mvbr4Plan<NB, T, R>::lds();
     static bool granted = false;
     if (!granted) {
-        if (hipFuncSetAttribute((const void *)k_mvbr4<NB, T, R, ACC>,
+        if (hipFuncSetAttribute((const void *)k_mvbr4<NB, T, R, EPI>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
             (void)hipGetLastError();
             return hipErrorNotSupported;
         }
         granted = true;
     }
-    k_mvbr4<NB, T, R, ACC><<<wgs, 1024, lds, s>>>(a);
+    k_mvbr4<NB, T, R, EPI><<<wgs, 1024, lds, s>>>(a);
     return hipGetLastError();
 }
 
@@ -761,7 +790,7 @@ static hipError_t launch_mvbr4_t(const MbArgs &a, uint32_t wgs, hipStream_t s) {
 // to 1, 2, 3 or 6, or 7 with as many rounds of workgroups as that takes (more
 // tiles per workgroup would not fit the registers); w 16-byte aligned, 32-bit
 // offsets.
-static hipError_t launch_mvbr4(const MbArgs &a, bool acc, hipStream_t s) {
+static hipError_t launch_mvbr4(const MbArgs &a, int epi, hipStream_t s) {
     const uint32_t nblk = a.cols / 256u, total = a.tile_end[a.nmat - 1u], cus = device_cus();
     if (a.cols % 256u || nblk == 0u || nblk > 32u) return hipErrorNotSupported;
     for (uint32_t m = 0; m < a.nmat; m++)
@@ -771,7 +800,9 @@ static hipError_t launch_mvbr4(const MbArgs &a, bool acc, hipStream_t s) {
     const uint32_t T = per <= 1u ? 1u : per <= 2u ? 2u : per <= 3u ? 3u : per <= 6u ? 6u : 7u;
     const uint32_t wgs = (total + T - 1u) / T;
 #define VBS_MVBR4(NB_, T_)                                                                  \
-    return acc ? launch_mvbr4_t<NB_, T_, true>(a, wgs, s) : launch_mvbr4_t<NB_, T_, false>(a, wgs, s)
+    return epi == E_QKV   ? launch_mvbr4_t<NB_, T_, E_QKV>(a, wgs, s)                           \
+           : epi == E_ACC ? launch_mvbr4_t<NB_, T_, E_ACC>(a, wgs, s)                           \
+                          : launch_mvbr4_t<NB_, T_, E_STORE>(a, wgs, s)
     if (nblk <= 16u) {
         if (T == 1u) VBS_MVBR4(1, 1);
         if (T == 2u) VBS_MVBR4(1, 2);
@@ -856,12 +887,48 @@ hipError_t launch_mvb(int type, uint32_t nmat, const uint8_t *const w[], const u
     a.batch = batch;
     {
         const hipError_t e = type == kQ6_K ? launch_mvbr6(a, accumulate != 0, s)
-                                           : launch_mvbr4(a, accumulate != 0, s);
+                                           : launch_mvbr4(a, accumulate ? E_ACC : E_STORE, s);
         if (e != hipErrorNotSupported) return e;
     }
     if (type == kQ4_K)
         return accumulate ? launch_mvb_plan<Q4KB, true>(a, s) : launch_mvb_plan<Q4KB, false>(a, s);
     return accumulate ? launch_mvb_plan<Q6KB, true>(a, s) : launch_mvb_plan<Q6KB, false>(a, s);
+}
+
+hipError_t launch_mvb_qkv(int type, const uint8_t *const w[3], const uint32_t rows[3], float *q,
+                          uint32_t q_stride, const uint8_t *xp, uint32_t cols, uint32_t batch,
+                          const float2 *rope, const uint32_t *pos, uint16_t *kc, uint16_t *vc,
+                          uint64_t kv_seq, uint64_t layer_off, uint32_t hd, uint32_t kvd,
+                          uint32_t max_ctx, hipStream_t s) {
+    if (type != kQ4_K || batch == 0 || batch > kBatchMax || hd == 0u || (hd & 1u))
+        return hipErrorNotSupported;
+    MbArgs a{};
+    uint32_t tiles = 0;
+    for (uint32_t m = 0; m < 3u; m++) {
+        if (rows[m] == 0 || rows[m] % 16u ||
+            !mv_fits(type, w[m], reinterpret_cast<const float *>(xp), cols, rows[m]))
+            return hipErrorNotSupported;
+        a.w[m] = w[m];
+        a.rows[m] = rows[m];
+        tiles += rows[m] / 16u;
+        a.tile_end[m] = tiles;
+    }
+    a.y[0] = q;
+    a.ys[0] = q_stride;
+    a.nmat = 3;
+    a.xp = xp;
+    a.cols = cols;
+    a.batch = batch;
+    a.rope = rope;
+    a.pos = pos;
+    a.kc = kc;
+    a.vc = vc;
+    a.kv_seq = kv_seq;
+    a.layer_off = layer_off;
+    a.hd = hd;
+    a.kvd = kvd;
+    a.max_ctx = max_ctx;
+    return launch_mvbr4(a, E_QKV, s);
 }
 
 hipError_t launch_kq_linear_batch(int type, const uint8_t *w, const float *x, uint32_t xs, float *y,
