@@ -631,10 +631,23 @@ static hipError_t enqueue_step_batch(const BDecoder &d, hipStream_t s) {
             }
             VBS_TRY(e);
         }
-        VBS_TRY(launch_attention_batch(d.q, m.kc, m.vc, d.attn, m.max_ctx, pos_dev, d.part, layer_off,
-                                       nq, nkv, hd, scale, B, qd, d.kv_seq, s));
+        // attention; its merge writes O's prepared x when the matrix-core
+        // chunk kernel runs (else the merge, then the preparation)
+        hipError_t ea = launch_attention_batch(d.q, m.kc, m.vc, nullptr, m.max_ctx, pos_dev, d.part,
+                                               layer_off, nq, nkv, hd, scale, B, qd, d.kv_seq, s);
+        if (ea == hipSuccess) {
+            ea = launch_attn_merge_prep(d.part, d.xp, attention_chunk_stride(m.max_ctx, nkv), pos_dev,
+                                        nq, nkv,
+                                        attention_partial_bytes(m.max_ctx, nq, nkv, hd) / sizeof(float),
+                                        B, s);
+        } else if (ea == hipErrorNotSupported) {
+            ea = launch_attention_batch(d.q, m.kc, m.vc, d.attn, m.max_ctx, pos_dev, d.part, layer_off,
+                                        nq, nkv, hd, scale, B, qd, d.kv_seq, s);
+            if (ea == hipSuccess)
+                ea = launch_xprep(XP_PLAIN, d.attn, nullptr, qd, nullptr, 0.f, qd, B, d.xp, s);
+        }
+        VBS_TRY(ea);
         {  // O, added into the residual stream
-            VBS_TRY(launch_xprep(XP_PLAIN, d.attn, nullptr, qd, nullptr, 0.f, qd, B, d.xp, s));
             const uint32_t rows[1] = {H}, ys[1] = {H};
             float *const y[1] = {d.x};
             VBS_TRY(launch_mvb(t[3], 1, w + 3, rows, y, ys, 1, d.xp, qd, B, s));

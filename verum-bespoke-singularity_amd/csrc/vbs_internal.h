@@ -72,6 +72,13 @@ hipError_t launch_xprep(int mode, const float *x, const float *x2, uint32_t xs,
 hipError_t launch_mvb(int type, uint32_t nmat, const uint8_t *const w[], const uint32_t rows[],
                       float *const y[], const uint32_t ys[], int accumulate, const uint8_t *xp,
                       uint32_t cols, uint32_t batch, hipStream_t s);
+// The head_dim-128 merge of the batched attention partials (chunk stride
+// attn_max_chunks(max_seq, nkh), part_bstride floats per sequence) written as
+// O's prepared x (xprep layout, nqh x 128 columns), pairs of q heads per block.
+hipError_t launch_attn_merge_prep(const float *part, uint8_t *xp, uint32_t stride_chunks,
+                                  const uint32_t *pos_dev, uint32_t nqh, uint32_t nkh,
+                                  uint64_t part_bstride, uint32_t batch, hipStream_t s);
+uint32_t attention_chunk_stride(uint32_t max_seq, uint32_t nkh);
 // The batched decoder's Q/K/V launch with the RoPE and the f16 cache store of
 // every sequence in its epilogue (q, k, v of Q4_K, rows of 16-row multiples, at
 // most 32 blocks; hipErrorNotSupported otherwise): q rows to q + t q_stride,
@@ -134,7 +141,11 @@ hipError_t launch_attention(const float *q, const uint16_t *kc, const uint16_t *
 // The same for `batch` sequences with their own caches and positions:
 // sequence b reads q + b q_stride, writes out + b q_stride, uses the caches at
 // + b kv_stride elements, the position pos_dev[b] and the partials at
-// part + b * attention_partial_bytes(max_seq, ...) bytes.
+// part + b * attention_partial_bytes(max_seq, ...) bytes. With out NULL only the
+// matrix-core chunk launch runs (attn_mfma_batch_fits; hipErrorNotSupported
+// otherwise) and the caller merges the partials (launch_attn_merge_prep).
+bool attn_mfma_batch_fits(const float *q, const uint16_t *kc, const uint16_t *vc, uint32_t nqh,
+                          uint32_t nkh, uint32_t hd, uint32_t q_stride, uint64_t kv_stride);
 hipError_t launch_attention_batch(const float *q, const uint16_t *kc, const uint16_t *vc,
                                   float *out, uint32_t max_seq, const uint32_t *pos_dev,
                                   float *part, uint64_t layer_off, uint32_t nqh, uint32_t nkh,

@@ -772,18 +772,27 @@ hipError_t launch_attention(const float *q, const uint16_t *kc, const uint16_t *
     return hipGetLastError();
 }
 
+uint32_t attention_chunk_stride(uint32_t max_seq, uint32_t nkh) { return attn_max_chunks(max_seq, nkh); }
+
+bool attn_mfma_batch_fits(const float *q, const uint16_t *kc, const uint16_t *vc, uint32_t nqh,
+                          uint32_t nkh, uint32_t hd, uint32_t q_stride, uint64_t kv_stride) {
+    return nkh != 0u && nqh % nkh == 0u && hd == 128u && nqh / nkh <= 8u && ((uintptr_t)q & 15u) == 0 &&
+           ((uintptr_t)kc & 15u) == 0 && ((uintptr_t)vc & 15u) == 0 && (q_stride % 4u) == 0 &&
+           (kv_stride % 8u) == 0;
+}
+
 hipError_t launch_attention_batch(const float *q, const uint16_t *kc, const uint16_t *vc,
                                   float *out, uint32_t max_seq, const uint32_t *pos_dev,
                                   float *part, uint64_t layer_off, uint32_t nqh, uint32_t nkh,
                                   uint32_t hd, float scale, uint32_t batch, uint32_t q_stride,
                                   uint64_t kv_stride, hipStream_t s) {
     if (batch == 0 || !part || !pos_dev) return hipErrorInvalidValue;
+    if (!out && !attn_mfma_batch_fits(q, kc, vc, nqh, nkh, hd, q_stride, kv_stride))
+        return hipErrorNotSupported;
     if (max_seq == 0 || nkh == 0 || nqh % nkh != 0) return hipErrorInvalidValue;
     const uint64_t pstride = attention_partial_bytes(max_seq, nqh, nkh, hd) / sizeof(float);
     const uint32_t group = nqh / nkh;
-    const bool mfma = hd == 128u && group <= 8u && ((uintptr_t)q & 15u) == 0 &&
-                      ((uintptr_t)kc & 15u) == 0 && ((uintptr_t)vc & 15u) == 0 &&
-                      (q_stride % 4u) == 0 && (kv_stride % 8u) == 0;
+    const bool mfma = attn_mfma_batch_fits(q, kc, vc, nqh, nkh, hd, q_stride, kv_stride);
     if (!mfma) {  // one sequence at a time through the single-sequence path
         for (uint32_t b = 0; b < batch; b++) {
             const hipError_t e = launch_attention(q + (uint64_t)b * q_stride, kc + b * kv_stride,
@@ -799,7 +808,7 @@ hipError_t launch_attention_batch(const float *q, const uint16_t *kc, const uint
         q, kc, vc, part, max_seq, pos_dev, layer_off, nkh, group, scale, stride, q_stride, kv_stride,
         pstride);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    if (e != hipSuccess || !out) return e;  // (no out: the caller merges the partials itself)
     k_attn_merge_h128<<<dim3(nqh, batch), 64 * kMergeRes, 0, s>>>(part, out, stride, pos_dev,
                                                                      max_seq, nkh, q_stride, pstride);
     return hipGetLastError();

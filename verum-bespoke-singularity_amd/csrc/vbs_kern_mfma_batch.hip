@@ -1,6 +1,7 @@
 // vbs_kern_mfma_batch.hip — batched (skinny) K-quant matvec on the gfx950 f16
 // matrix cores: x preparation (k_xprep_b) and the k_mvb kernel, with the weight
 // loads of the batch-1 kernel (vbs_mfma.h).
+#include "vbs_attn_common.h"
 #include "vbs_lds_dma.h"
 #include "vbs_mfma.h"
 
@@ -72,6 +73,46 @@ __host__ __device__ inline XbLayout xb_layout(uint32_t cols) {
 // One wave per (256-element block, vector): lane l holds elements 4l..4l+3.
 // XP_NORM: the workgroup first sums the squares of the whole vector (blocks
 // split over its waves, added in block order).
+// Block b of vector t (one wave, lane l: elements 4l..4l+3 of the block in v)
+// into the prepared form: its exponent, f16 hi/lo planes 2t and 2t + 1 and the
+// sub-block sums of x'/32.
+__device__ __forceinline__ void xprep_block(const float v[4], uint32_t lane, uint32_t t, uint32_t b,
+                                            uint32_t cols, uint8_t *xp) {
+    const uint32_t e0 = 256u * b + 4u * lane;
+    const float amax = wave_max(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+    int e = 0;
+    (void)frexpf(amax, &e);  // amax < 2^e
+    const int s = amax > 0.f ? 15 - e : 0;
+    h2 hi[2], lo[2];
+    float sum = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const float xs2 = ldexpf(v[k], s);
+        const _Float16 h = (_Float16)xs2;
+        hi[k >> 1][k & 1] = h;
+        lo[k >> 1][k & 1] = (_Float16)(xs2 - (float)h);
+        sum += xs2;
+    }
+    const XbLayout L = xb_layout(cols);
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    // elements e0..e0+3: chunk e0 / 8, half lane & 1; planes 2t and 2t + 1
+    _Float16 *ph = reinterpret_cast<_Float16 *>(xp) + 128u * (e0 >> 3) + 8u * (2u * t) + 4u * (lane & 1u);
+    *reinterpret_cast<u32x2 *>(ph) = u32x2{__builtin_bit_cast(uint32_t, hi[0]), __builtin_bit_cast(uint32_t, hi[1])};
+    *reinterpret_cast<u32x2 *>(ph + 8u) = u32x2{__builtin_bit_cast(uint32_t, lo[0]), __builtin_bit_cast(uint32_t, lo[1])};
+    // sub-block sums of x'/32: eight lanes per 32 elements
+    sum += __shfl_xor(sum, 1, 64);
+    sum += __shfl_xor(sum, 2, 64);
+    sum += __shfl_xor(sum, 4, 64);
+    if ((lane & 7u) == 0) {
+        const float m = sum * 0.03125f;
+        const _Float16 h = (_Float16)m;
+        _Float16 *pm = reinterpret_cast<_Float16 *>(xp + L.msum) + 128u * b + 8u * (2u * t) + lane / 8u;
+        pm[0] = h;
+        pm[8] = (_Float16)(m - (float)h);
+    }
+    if (lane == 0) reinterpret_cast<int *>(xp + L.expo)[8u * b + t] = s;
+}
+
 template <int MODE>
 __global__ __launch_bounds__(256) void k_xprep_b(const float *x, const float *x2, uint32_t xs,
                                                  const float *norm_w, float eps, uint32_t cols,
@@ -124,38 +165,7 @@ __global__ __launch_bounds__(256) void k_xprep_b(const float *x, const float *x2
         for (int k = 0; k < 4; k++)
             v[k] = __fmul_rn(__fdiv_rn(v[k], __fadd_rn(1.0f, expf(-v[k]))), u4[k]);
     }
-    const float amax = wave_max(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
-    int e = 0;
-    (void)frexpf(amax, &e);  // amax < 2^e
-    const int s = amax > 0.f ? 15 - e : 0;
-    h2 hi[2], lo[2];
-    float sum = 0.f;
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const float xs2 = ldexpf(v[k], s);
-        const _Float16 h = (_Float16)xs2;
-        hi[k >> 1][k & 1] = h;
-        lo[k >> 1][k & 1] = (_Float16)(xs2 - (float)h);
-        sum += xs2;
-    }
-    const XbLayout L = xb_layout(cols);
-    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-    // elements e0..e0+3: chunk e0 / 8, half lane & 1; planes 2t and 2t + 1
-    _Float16 *ph = reinterpret_cast<_Float16 *>(xp) + 128u * (e0 >> 3) + 8u * (2u * t) + 4u * (lane & 1u);
-    *reinterpret_cast<u32x2 *>(ph) = u32x2{__builtin_bit_cast(uint32_t, hi[0]), __builtin_bit_cast(uint32_t, hi[1])};
-    *reinterpret_cast<u32x2 *>(ph + 8u) = u32x2{__builtin_bit_cast(uint32_t, lo[0]), __builtin_bit_cast(uint32_t, lo[1])};
-    // sub-block sums of x'/32: eight lanes per 32 elements
-    sum += __shfl_xor(sum, 1, 64);
-    sum += __shfl_xor(sum, 2, 64);
-    sum += __shfl_xor(sum, 4, 64);
-    if ((lane & 7u) == 0) {
-        const float m = sum * 0.03125f;
-        const _Float16 h = (_Float16)m;
-        _Float16 *pm = reinterpret_cast<_Float16 *>(xp + L.msum) + 128u * b + 8u * (2u * t) + lane / 8u;
-        pm[0] = h;
-        pm[8] = (_Float16)(m - (float)h);
-    }
-    if (lane == 0) reinterpret_cast<int *>(xp + L.expo)[8u * b + t] = s;
+    xprep_block(v, lane, t, b, cols, xp);
 }
 
 // Up to three matrices of the same type and column count over one prepared x
@@ -846,6 +856,53 @@ static hipError_t launch_mvb_plan(const MbArgs &a, hipStream_t s) {
         if (tiles >= 512u) return launch_mvb_t<T, 2, ACC>(a, nblk > 64u ? 8u : min(4u, nblk), s);
     }
     return launch_mvb_t<T, 1, ACC>(a, min(8u, nblk), s);
+}
+
+// ---- attention merge into the prepared form ------------------------------------------
+// The batched decoder's attention merge (head_dim 128, the matrix-core chunk
+// kernel's partials) writing O's prepared x directly: workgroup (pair p,
+// sequence t) merges q heads 2p and 2p + 1 -- block p of the attention output
+// -- as k_attn_merge_h128 does (four waves per head, the same vbs_attn_common.h
+// pieces), then one wave prepares the block with xprep_block: the values and
+// the prepared bytes equal the merge launch followed by k_xprep_b's.
+__global__ __launch_bounds__(512) void k_attn_merge_prep(const float *__restrict__ part,
+                                                         uint8_t *__restrict__ xp, uint32_t stride_chunks,
+                                                         const uint32_t *__restrict__ pos_dev,
+                                                         uint32_t nkh, uint64_t part_bstride,
+                                                         uint32_t cols) {
+    __shared__ float2 red[2][kMergeRes][64];
+    __shared__ float4 outv[64];
+    const uint32_t pb = blockIdx.x, bz = blockIdx.y, lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t hh = wave / kMergeRes, r = wave % kMergeRes, h = 2u * pb + hh;
+    part += bz * part_bstride;
+    const uint32_t nc = mfma_chunks(pos_dev[bz] + 1u, nkh);  // seq = pos + 1
+    const float *ph = part + (uint64_t)h * stride_chunks * kPartRow;
+    float2 av[kMergeBatch];
+    merge_residue_load(ph, nc, r, lane, av);
+    const MergeStats st = merge_stats(ph, nc, lane, merge_ml_load(ph, nc, lane));
+    red[hh][r][lane] = merge_residue_sum(ph, nc, st, r, lane, av);
+    __syncthreads();
+    if (r == 0u) {
+        float2 a[kMergeRes];
+#pragma unroll
+        for (uint32_t k = 0; k < kMergeRes; k++) a[k] = red[hh][k][lane];
+        reinterpret_cast<float2 *>(outv)[64u * hh + lane] = merge_finish(a, st.L);
+    }
+    __syncthreads();
+    if (wave == 0u) {
+        const float4 x = outv[lane];
+        const float v[4] = {x.x, x.y, x.z, x.w};
+        xprep_block(v, lane, bz, pb, cols, xp);
+    }
+}
+
+hipError_t launch_attn_merge_prep(const float *part, uint8_t *xp, uint32_t stride_chunks,
+                                  const uint32_t *pos_dev, uint32_t nqh, uint32_t nkh,
+                                  uint64_t part_bstride, uint32_t batch, hipStream_t s) {
+    if (nqh % 2u || batch == 0 || batch > kBatchMax || !pos_dev) return hipErrorNotSupported;
+    k_attn_merge_prep<<<dim3(nqh / 2u, batch), 512, 0, s>>>(part, xp, stride_chunks, pos_dev, nkh,
+                                                           part_bstride, nqh * 128u);
+    return hipGetLastError();
 }
 
 size_t xprep_bytes(uint32_t cols) { return xb_layout(cols).bytes; }
