@@ -9,11 +9,15 @@
 // block's 16 x 144 bytes of each of its T tiles, as contiguous 144-byte row
 // runs. Nothing waits on anything else, so a CU has all of its ~110 KB of
 // weights in flight from the start; the items are then computed in arrival
-// order with the batch-1 kernel's arithmetic (Q4K::dot on the digits of x,
-// vbs_mfma.h), and every row adds its blocks' partial sums in block order at
+// order with the batch-1 kernel's arithmetic (Q4K::dot_x on the digits of x,
+// vbs_mfma.h; the x operands of the wave's block are read from LDS once, not
+// per tile), and every row adds its blocks' partial sums in block order at
 // the end, as k_mvf does: the results equal k_mvf's bit for bit. Measured
-// against k_mvf (weights streamed from HBM): 11008 x 4096 7.8 against 8.4 us
-// per launch, 12288 x 4096 8.0 against 8.7 us, 4096 x 4096 4.8 against 4.9 us.
+// against k_mvf (weights streamed from HBM): 11008 x 4096 7.4 against 8.4 us
+// per launch, 4096 x 4096 4.9 against 5.0 us. Of the 11008 x 4096 launch,
+// the arithmetic alone (no weight loads) takes 4.1 us and the loads alone
+// (no arithmetic) 5.9 us; the x operands read per tile cost 0.2 us more, and
+// a row sum that waited for each partial in turn another 0.3 us.
 //
 // The DMA is issued by inline assembly (M0 = the wave-uniform LDS address):
 // the compiler's builtin makes it insert waits for all loads before every
@@ -77,19 +81,20 @@ __global__ __launch_bounds__(64 * kMvlWaves) void k_mvl(const MvArgs a, uint32_t
         if (own) prep_block(v, lane, dv);
     }
 
-    // 3. the items in arrival order
+    // 3. the items in arrival order, the x operands of block b read once
+    const Q4K::X xo = Q4K::x_operands(dv, n, g);
+    const uint32_t ps = part_stride(nblk);
     auto item = [&](uint32_t j) {
         const uint8_t *row = lds + (stage - lds0) + j * kMvlItem + 144u * n;
         u32x4 r[3];
         r[0] = lda4(row);
         r[1] = lda4(row + 16u + 16u * g);
         r[2] = lda4(row + 80u + 16u * g);
-        const Src src{w, a.rows[0] * rb, rb, r0 + 16u * j, r1};
-        float part = Q4K::dot(r, nullptr, src, dv, b, n, g);
+        float part = Q4K::dot_x(r, xo, g);
         part += __shfl_xor(part, 16, 64);
         part += __shfl_xor(part, 32, 64);
         const uint32_t rr = 16u * j + n;
-        if (lane < 16u && own && rr < rpw) pb[rr * nblk + b] = part;
+        if (lane < 16u && own && rr < rpw) pb[rr * ps + b] = part;
         asm volatile("" ::"v"(part));
         __builtin_amdgcn_sched_barrier(0);
     };
@@ -111,9 +116,7 @@ __global__ __launch_bounds__(64 * kMvlWaves) void k_mvl(const MvArgs a, uint32_t
     __syncthreads();
     const uint32_t t = threadIdx.x;
     if (t < r1 - r0) {
-        float s = 0.f;
-        const float *p = pb + t * nblk;
-        for (uint32_t k = 0; k < nblk; k++) s += p[k];
+        const float s = ordered_sum(pb + t * ps, kMvlWaves);
         float *y = a.y[0] + r0 + t;
         *y = EPI == E_ACC ? __fadd_rn(*y, s) : s;
     }
@@ -135,13 +138,14 @@ template <uint32_t T, int EPI>
 static hipError_t launch_mvl_t(const MvArgs &a, uint32_t wgs, uint32_t rpw, hipStream_t s) {
     const uint32_t nblk = a.cols / 256u;
     const size_t lds = (size_t)kMvlWaves * T * kMvlItem + 16u + (size_t)kMvlWaves * kMvlSlot +
-                       (size_t)rpw * nblk * sizeof(float);
+                       (size_t)rpw * part_stride(nblk) * sizeof(float);
     static bool granted = false;
     if (!granted) {
         if (hipFuncSetAttribute((const void *)k_mvl<T, EPI>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)(kMvlWaves * kMvlMaxT * kMvlItem + 16u + kMvlWaves * kMvlSlot +
-                                      16u * kMvlMaxT * 16u * sizeof(float))) != hipSuccess) {
+                                      16u * kMvlMaxT * part_stride(kMvlWaves) * sizeof(float))) !=
+            hipSuccess) {
             (void)hipGetLastError();
             return hipErrorNotSupported;
         }
@@ -164,9 +168,12 @@ static hipError_t launch_mvl_t(const MvArgs &a, uint32_t wgs, uint32_t rpw, hipS
 // over its x. Arithmetic and per-(row, block) sums are k_mvf's, so the results
 // equal k_mvf's bit for bit. Every wait is an explicit s_waitcnt on the number
 // of DMAs issued after the awaited one (the loads return in issue order).
+// A block's x operands are read once for its T items, and the row sums read
+// the partials 16 at a time (padded with +0.0 to a multiple of 16).
 // Measured with the weights streamed from HBM: 4096 x 11008 (7B down)
-// 10.9-11.2 against k_mvf's 11.9-12.4 us, 8192 x 28672 (70B down) 41.1-42.1
-// against 47.3-52.2 us.
+// 10.7 against k_mvf's 11.9-12.4 us, 8192 x 28672 (70B down) 38.7-38.8
+// against 47.3-52.2 us (11.0-11.3 and 39.6-39.8 with the x operands read per
+// item and a row sum that waited for each partial in turn).
 constexpr uint32_t kMvrItem = 16u * 224u, kMvrDma = 4u;
 
 template <uint32_t NB, uint32_t T, uint32_t R>
@@ -187,7 +194,7 @@ struct MvrPlan {
     static constexpr uint32_t after_x(uint32_t i) { return D + after_item(i); }
     static constexpr size_t lds(uint32_t nblk) {
         return 16u * (size_t)R * kMvrItem + 16u + 16u * (size_t)XS * 1024u +
-               16u * (size_t)T * nblk * sizeof(float);
+               16u * (size_t)T * part_stride(nblk) * sizeof(float);
     }
 };
 
@@ -201,7 +208,8 @@ __global__ __launch_bounds__(1024) void k_mvr(const MvArgs a, uint32_t rpw) {
     const uint32_t n = lane & 15u, g = lane >> 4;
     const uint32_t r0 = blockIdx.x * rpw, r1 = min(r0 + rpw, a.rows[0]);
     if (r0 >= r1) return;
-    // LDS: [16 waves][R slots] | 16 zero bytes | [16 waves][XS x slots] | pb [16 T rows][nblk]
+    // LDS: [16 waves][R slots] | 16 zero bytes | [16 waves][XS x slots] |
+    // pb [16 T rows][part_stride(nblk)] (the 16 NB >= part_slots(nblk) block slots)
     const uint32_t lds0 = (uint32_t)(uintptr_t)lds;
     const uint32_t ring = lds0 + wave * R * kMvrItem;
     uint8_t *const zero = lds + 16u * R * kMvrItem;
@@ -229,6 +237,7 @@ __global__ __launch_bounds__(1024) void k_mvr(const MvArgs a, uint32_t rpw) {
     unroll_for<0u, R>(issue);
     if (lane < 4u) reinterpret_cast<uint32_t *>(zero)[lane] = 0u;
 
+    Q6K::X xo;  // block k's x operands, read once for its T items
     unroll_for<0u, NI>([&](auto ic) {
         constexpr uint32_t i = decltype(ic)::value;
         constexpr uint32_t k = i / T, j = i % T;
@@ -248,17 +257,21 @@ __global__ __launch_bounds__(1024) void k_mvr(const MvArgs a, uint32_t rpw) {
             const float4 xv = *reinterpret_cast<const float4 *>(slot + 16u * lane);
             const float v[4] = {xv.x, xv.y, xv.z, xv.w};
             if (own) prep_block(v, lane, dv);
+            xo = Q6K::x_operands(dv, n, g);
         }
         vmcnt_le<P::after_item(i)>();
         asm volatile("" ::: "memory");
         if (own) {
             const Src src{w, a.rows[0] * rb, rb, r0 + 16u * j, r1};
-            float part = Q6K::dot_staged(lds + (ring - lds0) + (i % R) * kMvrItem, src, dv, b, n, g);
+            float part = Q6K::dot_staged_x(lds + (ring - lds0) + (i % R) * kMvrItem, src, xo, b, n, g);
             part += __shfl_xor(part, 16, 64);
             part += __shfl_xor(part, 32, 64);
             const uint32_t rr = 16u * j + n;
-            if (lane < 16u && rr < rpw) pb[rr * nblk + b] = part;
+            if (lane < 16u && rr < rpw) pb[rr * part_stride(nblk) + b] = part;
             asm volatile("" ::"v"(part));
+        } else {  // a slot past the row: +0.0 for the row sums
+            const uint32_t rr = 16u * j + n;
+            if (lane < 16u && rr < rpw) pb[rr * part_stride(nblk) + bw] = 0.f;
         }
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (i + R < NI) issue(std::integral_constant<uint32_t, i + R>{});
@@ -268,9 +281,7 @@ __global__ __launch_bounds__(1024) void k_mvr(const MvArgs a, uint32_t rpw) {
     __syncthreads();
     const uint32_t t = threadIdx.x;
     if (t < r1 - r0) {
-        float s = 0.f;
-        const float *p = pb + t * nblk;
-        for (uint32_t k = 0; k < nblk; k++) s += p[k];
+        const float s = ordered_sum(pb + t * part_stride(nblk), nblk);
         float *y = a.y[0] + r0 + t;
         *y = EPI == E_ACC ? __fadd_rn(*y, s) : s;
     }
@@ -305,6 +316,8 @@ hipError_t launch_q6k_mvr(const uint8_t *w, const float *x, float *y, uint32_t c
     const uint32_t wgs = mvl_cus();
     const uint32_t rpw = (rows + wgs - 1u) / wgs;
     if (narrow ? rows <= 2048u || rpw > 16u : rows <= 4096u || rpw > 32u) return hipErrorNotSupported;
+    // every row-sum slot, the padding included, belongs to a wave's block slot
+    if (16u * (wide ? 7u : 3u) < part_slots(nblk)) return hipErrorNotSupported;
     // the last row's last block read as aligned chunks must end inside the
     // matrix (the DMA has no bounded form); offsets are 32-bit
     const uint64_t rb = (uint64_t)nblk * 210u, bytes = rb * rows, wlo = (uintptr_t)w & 15u;

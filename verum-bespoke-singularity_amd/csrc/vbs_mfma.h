@@ -211,18 +211,34 @@ struct Q4K {
         r[1] = lda4(blk + 16u * g + 16u);
         r[2] = lda4(blk + 16u * g + 80u);
     }
-    __device__ static float dot(const u32x4 *r, uint8_t *, const Src &, const DigitView &dv,
-                                uint32_t b, uint32_t n, uint32_t g) {
-        (void)b;
-        // A row n = 4t+p: lane group g carries sub-blocks 2(g>>1) (low nibbles,
-        // t even) and 2(g>>1)+1 (high nibbles, t odd) at element offset 16(g&1)
+    // The x side of a block's dot, the same for every tile of rows: the digit
+    // planes as MFMA A operands and the sub-block x scales of lane group g.
+    // A row n = 4t+p: lane group g carries sub-blocks 2(g>>1) (low nibbles,
+    // t even) and 2(g>>1)+1 (high nibbles, t odd) at element offset 16(g&1).
+    struct X {
+        i32x4 A0l, A0h, A1l, A1h;
+        float2 xs0, xs1;
+    };
+    __device__ static X x_operands(const DigitView &dv, uint32_t n, uint32_t g) {
         const uint32_t t = n >> 2, p = n & 3u;
         const bool on = p < 3u && (g >> 1) == (t >> 1);
         const uint8_t *ao = dv.base + p * dv.pstride + 32u * t + 16u * (g & 1u);
-        const i32x4 A0l = lda(on && !(t & 1u) ? ao : dv.zero);
-        const i32x4 A0h = lda(on && (t & 1u) ? ao : dv.zero);
-        const i32x4 A1l = lda(on && !(t & 1u) ? ao + 128u : dv.zero);
-        const i32x4 A1h = lda(on && (t & 1u) ? ao + 128u : dv.zero);
+        X x;
+        x.A0l = lda(on && !(t & 1u) ? ao : dv.zero);
+        x.A0h = lda(on && (t & 1u) ? ao : dv.zero);
+        x.A1l = lda(on && !(t & 1u) ? ao + 128u : dv.zero);
+        x.A1h = lda(on && (t & 1u) ? ao + 128u : dv.zero);
+        x.xs0 = dv.xs[g];
+        x.xs1 = dv.xs[4u + g];
+        return x;
+    }
+    __device__ static float dot(const u32x4 *r, uint8_t *, const Src &, const DigitView &dv,
+                                uint32_t b, uint32_t n, uint32_t g) {
+        (void)b;
+        return dot_x(r, x_operands(dv, n, g), g);
+    }
+    __device__ static float dot_x(const u32x4 *r, const X &x, uint32_t g) {
+        const i32x4 A0l = x.A0l, A0h = x.A0h, A1l = x.A1l, A1h = x.A1h;
         const uint32_t M4 = 0x0F0F0F0Fu;
         const u32x4 qa = r[1], qb = r[2];
         const i32x4 B0l = {(int)(qa.x & M4), (int)(qa.y & M4), (int)(qa.z & M4), (int)(qa.w & M4)};
@@ -236,7 +252,7 @@ struct Q4K {
         const float S1 = plane_sum(mfma(A1h, B1h, mfma(A1l, B1l, z)));
         // D group g: sub-blocks g (span 0) and 4 + g (span 1); scales and mins
         // as src/vbs_dequant.c:225-233
-        const float2 xs0 = dv.xs[g], xs1 = dv.xs[4u + g];
+        const float2 xs0 = x.xs0, xs1 = x.xs1;
         const u32x4 hd = r[0];
         const uint32_t sh = 8u * g;
         const uint32_t sc0 = bfe(hd.y, sh, 6), m0 = bfe(hd.z, sh, 6);
@@ -313,10 +329,36 @@ struct Q6K {
         }
         return dot_staged(scratch, src, dv, b, n, g);
     }
+    // The x side of a block's dot, the same for every tile of rows: MFMA q's A
+    // operand (row n = 4t+p carries plane p of the scale group of lane group
+    // t), and the x scale and -32 x sum of lane group g's scale group 8h + 2q + u.
+    struct X {
+        i32x4 A[4];
+        float xs[4], m32[4];
+    };
+    __device__ static X x_operands(const DigitView &dv, uint32_t n, uint32_t g) {
+        const uint32_t h = g >> 1, u = g & 1u;
+        const uint32_t t = n >> 2, p = n & 3u;
+        const bool on = p < 3u && t == g;
+        const uint8_t *a0 = dv.base + p * dv.pstride + 128u * (t >> 1) + 16u * (t & 1u);
+        X x;
+#pragma unroll
+        for (uint32_t q = 0; q < 4; q++) {
+            const uint32_t j = 4u * h + q;  // sub-block of the block
+            x.A[q] = lda(on ? a0 + 32u * q : dv.zero);
+            x.xs[q] = dv.xs[j].x;
+            x.m32[q] = -32.f * dv.xs16[2u * j + u];
+        }
+        return x;
+    }
     // The same from a scratch that already holds the tile's 224 chunks (chunk
     // 14 n + k at 16 (14 n + k): row n's aligned 16-byte chunk k).
     __device__ static float dot_staged(const uint8_t *scratch, const Src &src, const DigitView &dv,
                                        uint32_t b, uint32_t n, uint32_t g) {
+        return dot_staged_x(scratch, src, x_operands(dv, n, g), b, n, g);
+    }
+    __device__ static float dot_staged_x(const uint8_t *scratch, const Src &src, const X &x,
+                                         uint32_t b, uint32_t n, uint32_t g) {
         // row n's block starts o = (its address mod 16) into its 224 scratch
         // bytes; rw is the 4-byte aligned word at or below the start and sh
         // (0 or 2) the byte shift from there. Every word read lies in the row.
@@ -346,12 +388,9 @@ struct Q6K {
         const uint32_t sc_hi = __builtin_amdgcn_alignbyte(s2, s1, sh);
         const uint32_t dbits = (rw[52] >> (8u * sh)) & 0xFFFFu;
         // MFMA q (quarter q of both halves): lane group g holds scale group
-        // 8h + 2q + u; A row n = 4t+p carries plane p of the group of lane group t
-        const uint32_t t = n >> 2, p = n & 3u;
-        const bool on = p < 3u && t == g;
+        // 8h + 2q + u
         const uint32_t qew[4] = {qe.x, qe.y, qe.z, qe.w}, qow[4] = {qo.x, qo.y, qo.z, qo.w};
         const uint32_t qhw[4] = {qh.x, qh.y, qh.z, qh.w};
-        const uint8_t *a0 = dv.base + p * dv.pstride + 128u * (t >> 1) + 16u * (t & 1u);
         float acc = 0.f;
 #pragma unroll
         for (uint32_t q = 0; q < 4; q++) {
@@ -366,15 +405,13 @@ struct Q6K {
                 bw[k] = (int)(((ql[k] >> (4u * (q >> 1))) & 0x0F0F0F0Fu) | hi);
             }
             const i32x4 B = {bw[0], bw[1], bw[2], bw[3]};
-            const i32x4 A = lda(on ? a0 + 32u * q : dv.zero);
             const i32x4 z = {0, 0, 0, 0};
-            const float S = plane_sum(mfma(A, B, z));
+            const float S = plane_sum(mfma(x.A[q], B, z));
             // scale 8h + 2q + u: dword 2h + (q >> 1), byte 2(q & 1) + u; the group
             // is half u of sub-block 4h + q
             const uint32_t scd = (q >> 1) ? sc_hi : sc_lo;
             const float sc = (float)(int)(int8_t)bfe(scd, 16u * (q & 1u) + 8u * u, 8);
-            const uint32_t j = 4u * h + q;  // sub-block of the block
-            acc = fmaf(sc, fmaf(dv.xs[j].x, S, -32.f * dv.xs16[2u * j + u]), acc);
+            acc = fmaf(sc, fmaf(x.xs[q], S, x.m32[q]), acc);
         }
         return cvt_h(dbits) * acc;
     }
@@ -501,6 +538,32 @@ using Q80 = KBlk<kQ8_0>;
 //   E_SILU   gate and up: y[0][row] = gate / (1 + expf(-gate)) * up
 //            (src/vbs_host_math.h:53-57)
 enum : int { E_STORE = 0, E_ACC = 1, E_QKV = 2, E_SILU = 3 };
+
+// A row's per-block partial sums, kept in LDS by the kernels that split a
+// row's blocks over waves: part_slots(nblk) of them, nblk rounded up to 16
+// (the slots past the row hold +0.0), row t's at pb + t * part_stride(nblk)
+// floats (16-byte aligned; the threads of 16 rows read distinct banks).
+__host__ __device__ constexpr uint32_t part_slots(uint32_t nblk) { return (nblk + 15u) & ~15u; }
+__host__ __device__ constexpr uint32_t part_stride(uint32_t nblk) { return part_slots(nblk) + 4u; }
+// Their sum in block order, s = ((0 + p[0]) + p[1]) + ..., read 16 at a time.
+// The padding's +0.0 leaves s unchanged: s starts at +0.0 and never becomes
+// -0.0 (an exactly cancelling sum is +0.0 when rounding to nearest).
+__device__ __forceinline__ float ordered_sum(const float *p, uint32_t nblk) {
+    float s = 0.f;
+    for (uint32_t k0 = 0; k0 < nblk; k0 += 16u) {
+        float4 v[4];
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; i++) v[i] = *reinterpret_cast<const float4 *>(p + k0 + 4u * i);
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; i++) {
+            s += v[i].x;
+            s += v[i].y;
+            s += v[i].z;
+            s += v[i].w;
+        }
+    }
+    return s;
+}
 
 struct MvArgs {
     const uint8_t *w[3];
