@@ -681,9 +681,11 @@ __global__ __launch_bounds__(MAXT) void k_mvf(const MvArgs a) {
     // 4. stream: issue item i + P, prepare x of a new block, compute item i
     // (loads return in issue order, so the wait is for item i alone)
     uint8_t *scratch = xq + digit_bytes + wave * T::SCRATCH;
-    // per-block row sums [TPW][nblk][16]: every row adds its blocks in index
-    // order at the end, so a row's value does not depend on the work split
+    // per-block row sums, [TPW * 16 rows][part_stride(nblk)]: every row adds
+    // its blocks in index order at the end, so a row's value does not depend
+    // on the work split
     float *pb = reinterpret_cast<float *>(xq + digit_bytes + nw * T::SCRATCH);
+    const uint32_t ps = part_stride(nblk), slots = part_slots(nblk);
 #pragma unroll
     for (uint32_t i = 0; i < NI; i++) {
 #pragma unroll
@@ -703,12 +705,18 @@ __global__ __launch_bounds__(MAXT) void k_mvf(const MvArgs a) {
         // the four lane groups of a row hold different groups of the block
         part += __shfl_xor(part, 16, 64);
         part += __shfl_xor(part, 32, 64);
-        if (lane < 16u && blk(i) < nblk) pb[((i / KS) * nblk + blk(i)) * 16u + n] = part;
+        // (slots past the row: +0.0)
+        if (lane < 16u && blk(i) < slots) pb[((i / KS) * 16u + n) * ps + blk(i)] = blk(i) < nblk ? part : 0.f;
         // finish item i here: otherwise its arithmetic may sink past later
         // items and hold their registers
         asm volatile("" ::"v"(part));
         __builtin_amdgcn_sched_barrier(0);
     }
+
+    // the slots no wave covers: +0.0
+    const uint32_t covered = min(nw * KS, slots), pad = slots - covered;
+    for (uint32_t e = threadIdx.x; e < TPW * 16u * pad; e += nth)
+        pb[(e / pad) * ps + covered + e % pad] = 0.f;
 
     // 5. tile j finished by wave j % nw (both tiles by wave 0 for E_SILU)
     __syncthreads();
@@ -716,8 +724,7 @@ __global__ __launch_bounds__(MAXT) void k_mvf(const MvArgs a) {
 #pragma unroll
     for (uint32_t j = 0; j < TPW; j++) {
         if (wave != (EPI == E_SILU ? 0u : j % nw)) continue;
-        float t = 0.f;
-        for (uint32_t b = 0; b < nblk; b++) t += pb[(j * nblk + b) * 16u + n];
+        const float t = ordered_sum(pb + (j * 16u + n) * ps, nblk);
         // every lane holds the value of row n of the tile
         const uint32_t m = mt[j];
         const bool own = (EPI == E_SILU || blockIdx.x * TPW + j < total);
@@ -784,7 +791,7 @@ template <class T, uint32_t KS, uint32_t TPW, uint32_t MAXT, bool NORM, int EPI>
 static hipError_t launch_t(const MvArgs &a, uint32_t nw, uint32_t wgs, hipStream_t s) {
     const size_t digits = TPW == 1u ? 16u + (size_t)nw * kSlotBytes : xq_layout(a.cols).bytes;
     const size_t lds = digits + (size_t)nw * T::SCRATCH +
-                       (size_t)TPW * (a.cols / 256u) * 16u * sizeof(float);
+                       (size_t)TPW * 16u * part_stride(a.cols / 256u) * sizeof(float);
     if (lds > 65536u) {  // beyond the default per-workgroup LDS window: opt in once
         static size_t granted = 0;
         if (lds > granted) {
