@@ -12,7 +12,13 @@
 
 namespace vbs {
 
-constexpr uint32_t kMfmaTargetWgs = 1024;  // one-wave workgroups of the matrix-core split
+// One-wave workgroups the matrix-core split aims for per sequence. The chunk
+// kernel holds 88 VGPRs (five waves per SIMD, 5120 on the chip); at batch 8
+// a target of 1024 made ~5500 of them, a second round of waves late in the
+// launch. Measured chunk + merge with 640 against 1024: 70B batch 8 51.2
+// against 52.3-55.7 us, 70B batch 1 12.9 against 13.2-13.5 us, 7B batch 1
+// 8.3 either way.
+constexpr uint32_t kMfmaTargetWgs = 640;
 constexpr uint32_t kMfmaGran = 32, kMfmaTiles = 8, kMfmaLmax = kMfmaGran * kMfmaTiles;
 
 // Sequence split: chunks of `len` positions (a multiple of gran, at most lmax)
