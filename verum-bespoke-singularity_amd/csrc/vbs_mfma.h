@@ -55,6 +55,8 @@
 // d*sc*(q - 32) summed: d*sc*(2^(e-22)*S - 32*sum16(x)).
 #pragma once
 
+#include <type_traits>
+
 #include "vbs_dev_common.h"
 #include "vbs_internal.h"
 
@@ -237,6 +239,10 @@ struct Q4K {
         (void)b;
         return dot_x(r, x_operands(dv, n, g), g);
     }
+    __device__ static float dot_x(const u32x4 *r, uint8_t *, const Src &, const X &x, uint32_t,
+                                  uint32_t, uint32_t g) {
+        return dot_x(r, x, g);
+    }
     __device__ static float dot_x(const u32x4 *r, const X &x, uint32_t g) {
         const i32x4 A0l = x.A0l, A0h = x.A0h, A1l = x.A1l, A1h = x.A1h;
         const uint32_t M4 = 0x0F0F0F0Fu;
@@ -319,14 +325,17 @@ struct Q6K {
                 r[i] = a[i] + 16u <= src.bytes + wlo ? lda4(w16 + a[i]) : ld_tail(w16 + a[i], end);
         }
     }
-    __device__ static float dot(const u32x4 *r, uint8_t *scratch, const Src &src,
-                                const DigitView &dv, uint32_t b, uint32_t n, uint32_t g) {
+    __device__ static void stage(const u32x4 *r, uint8_t *scratch, uint32_t n, uint32_t g) {
         const uint32_t lane = 16u * g + n;
 #pragma unroll
         for (uint32_t i = 0; i < 4; i++) {
             const uint32_t c = lane + 64u * i;
             if (i < 3u || c < 224u) *reinterpret_cast<u32x4 *>(scratch + 16u * c) = r[i];
         }
+    }
+    __device__ static float dot(const u32x4 *r, uint8_t *scratch, const Src &src,
+                                const DigitView &dv, uint32_t b, uint32_t n, uint32_t g) {
+        stage(r, scratch, n, g);
         return dot_staged(scratch, src, dv, b, n, g);
     }
     // The x side of a block's dot, the same for every tile of rows: MFMA q's A
@@ -581,6 +590,18 @@ struct MvArgs {
     uint64_t kv_layer;  // layer * max_ctx * kvd
 };
 
+// The register set that holds a block's x operands when k_mvf reads them once
+// for its tiles: Q4_K only (Q6_K's 24 registers would take its four-tile
+// head launches past 128 VGPRs, one workgroup per CU instead of two).
+template <class T, bool>
+struct XOf {
+    using type = char;
+};
+template <class T>
+struct XOf<T, true> {
+    using type = typename T::X;
+};
+
 template <class T, uint32_t KS, uint32_t TPW, uint32_t MAXT, bool NORM, int EPI>
 __global__ __launch_bounds__(MAXT) void k_mvf(const MvArgs a) {
     extern __shared__ __align__(16) uint8_t xq[];
@@ -615,23 +636,29 @@ __global__ __launch_bounds__(MAXT) void k_mvf(const MvArgs a) {
         src[j] = Src{w, a.rows[mt[j]] * rb, rb, lt[j] * 16u, a.rows[mt[j]]};
     }
     // Block k of this wave: wave + nw * k (at each step the workgroup's waves
-    // read adjacent blocks of the same rows); item i is block i % KS of tile
-    // i / KS. Slots past the row re-read its last block and contribute zero.
-    // A wave prepares the digits of its own blocks only, so the waves share
-    // no x data and need no barrier before the matrix work.
-    auto blk = [&](uint32_t i) { return wave + nw * (i % KS); };
+    // read adjacent blocks of the same rows). Item i is block slot i % KS of
+    // tile i / KS, or, where a block's x operands are read once for its tiles
+    // (Q4_K with several tiles), tile i % TPW of block slot i / TPW. Slots
+    // past the row re-read its last block and contribute zero. A wave
+    // prepares the digits of its own blocks only, so the waves share no x
+    // data and need no barrier before the matrix work.
+    constexpr bool kHoist = std::is_same<T, Q4K>::value && TPW > 1u;
+    auto slot = [&](uint32_t i) { return kHoist ? i / TPW : i % KS; };
+    auto tile = [&](uint32_t i) { return kHoist ? i % TPW : i / KS; };
+    auto bk = [&](uint32_t k) { return wave + nw * k; };
+    auto blk = [&](uint32_t i) { return bk(slot(i)); };
 
     // x of this wave's blocks, lane l: elements 4l..4l+3 (x may be only
     // 4-byte aligned), and with the RMSNorm its weights: all requested first.
     typedef float4 __attribute__((aligned(4))) f4u;
     float4 xv[KS], wv[NORM ? KS : 1];
     auto load_x = [&](uint32_t k) {
-        const uint32_t e0 = 256u * min(blk(k), nblk - 1u) + 4u * lane;
+        const uint32_t e0 = 256u * min(bk(k), nblk - 1u) + 4u * lane;
         xv[k] = *reinterpret_cast<const f4u *>(a.x + e0);
         if (NORM) wv[k] = *reinterpret_cast<const f4u *>(a.norm_w + e0);
     };
     u32x4 r[NI][T::NLD];
-    auto issue = [&](uint32_t i) { T::load(src[i / KS], min(blk(i), nblk - 1u), n, g, r[i]); };
+    auto issue = [&](uint32_t i) { T::load(src[tile(i)], min(blk(i), nblk - 1u), n, g, r[i]); };
 
     // 1-2. x, then the first items
 #pragma unroll
@@ -647,7 +674,7 @@ __global__ __launch_bounds__(MAXT) void k_mvf(const MvArgs a) {
         for (uint32_t k = 0; k < KS; k++) {
             const float v[4] = {xv[k].x, xv[k].y, xv[k].z, xv[k].w};
             const double ss = block_sumsq(v);
-            if (lane == 0 && blk(k) < nblk) bsum[blk(k)] = ss;
+            if (lane == 0 && bk(k) < nblk) bsum[bk(k)] = ss;
         }
         __syncthreads();
         double t = 0.0;
@@ -686,27 +713,36 @@ __global__ __launch_bounds__(MAXT) void k_mvf(const MvArgs a) {
     // on the work split
     float *pb = reinterpret_cast<float *>(xq + digit_bytes + nw * T::SCRATCH);
     const uint32_t ps = part_stride(nblk), slots = part_slots(nblk);
+    // a block's x operands, read once for its TPW tiles
+    typename XOf<T, kHoist>::type xo{};
 #pragma unroll
     for (uint32_t i = 0; i < NI; i++) {
 #pragma unroll
         for (uint32_t j = i == 0 ? P0 : max(P0, i + P); j <= i + P && j < NI; j++) issue(j);
         __builtin_amdgcn_sched_barrier(0);
-        if (i < KS && blk(i) < nblk) {
-            float v[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+        const uint32_t k = slot(i), tl = tile(i);
+        if (tl == 0u && blk(i) < nblk) {
+            float v[4] = {xv[k].x, xv[k].y, xv[k].z, xv[k].w};
             if (NORM) {
-                const float w4[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
+                const float w4[4] = {wv[k].x, wv[k].y, wv[k].z, wv[k].w};
 #pragma unroll
                 for (int k = 0; k < 4; k++) v[k] = __fmul_rn(__fmul_rn(v[k], sc), w4[k]);
             }
             prep_block(v, lane, view(blk(i)));
         }
         const uint32_t bi = min(blk(i), nblk - 1u);
-        float part = T::dot(r[i], scratch, src[i / KS], view(bi), bi, n, g);
+        float part;
+        if constexpr (kHoist) {
+            if (tl == 0u) xo = T::x_operands(view(bi), n, g);
+            part = T::dot_x(r[i], scratch, src[tl], xo, bi, n, g);
+        } else {
+            part = T::dot(r[i], scratch, src[tl], view(bi), bi, n, g);
+        }
         // the four lane groups of a row hold different groups of the block
         part += __shfl_xor(part, 16, 64);
         part += __shfl_xor(part, 32, 64);
         // (slots past the row: +0.0)
-        if (lane < 16u && blk(i) < slots) pb[((i / KS) * 16u + n) * ps + blk(i)] = blk(i) < nblk ? part : 0.f;
+        if (lane < 16u && blk(i) < slots) pb[(tl * 16u + n) * ps + blk(i)] = blk(i) < nblk ? part : 0.f;
         // finish item i here: otherwise its arithmetic may sink past later
         // items and hold their registers
         asm volatile("" ::"v"(part));
