@@ -68,9 +68,9 @@ DECODE_FIXTURE = os.path.join(ROOT, "tests", "golden", "decode_7b_greedy.npz")
 # HBM bytes per launch of the dominant kernel (11008x4096 Q4_K, k_mvl) from
 # two rocprofv3 --pmc passes over this program (FETCH_SIZE, WRITE_SIZE in KiB
 # per dispatch), each scaled by what the counter reads for a 256 MiB device
-# copy in the same run: FETCH_SIZE x (262144 / 131093.1) + WRITE_SIZE x 1.0000
+# copy in the same run: FETCH_SIZE x (262144 / 131092.9) + WRITE_SIZE x 1.0000
 # (profiles/q4k_matvec_7b_layer_set.md).
-TRAFFIC_BYTES = round((12487.8 * 262144 / 131093.1 + 50.0) * 1024)
+TRAFFIC_BYTES = round((12479.5 * 262144 / 131092.9 + 50.0) * 1024)
 
 
 def algo_bytes(t, rows, cols):
@@ -620,7 +620,7 @@ def bench_batch8_70b(dev, host, steps=20, batch=8, ncopy=2):
             "vector_matvecs_per_s": round(batch * len(LAYER_SET_70B) / (out["batched"] * 1e-3)),
             "batch1_x8_ms_per_step": round(out["batch1_x8"], 4),
             "speedup_vs_batch1_x8": round(out["batch1_x8"] / out["batched"], 2),
-            "path": "vbs_gfx950_linear_batch_multi: k_xprep_b + k_mvb (f16 MFMA) per matrix group"}
+            "path": "vbs_gfx950_linear_batch_multi: k_xprep_b + one f16-MFMA launch per matrix group (k_mvbr4 Q4_K, k_mvbr6 Q6_K)"}
 
 
 GEO_7B = dict(hidden=4096, ffn=11008, n_heads=32, n_kv_heads=8, head_dim=128, vocab=32000)
