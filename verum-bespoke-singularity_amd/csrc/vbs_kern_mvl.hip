@@ -122,18 +122,6 @@ __global__ __launch_bounds__(64 * kMvlWaves) void k_mvl(const MvArgs a, uint32_t
     }
 }
 
-static uint32_t mvl_cus() {
-    static int cus = 0;
-    if (!cus) {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            cus <= 0)
-            cus = 256;
-    }
-    return (uint32_t)cus;
-}
-
 template <uint32_t T, int EPI>
 static hipError_t launch_mvl_t(const MvArgs &a, uint32_t wgs, uint32_t rpw, hipStream_t s) {
     const uint32_t nblk = a.cols / 256u;
@@ -313,7 +301,7 @@ hipError_t launch_q6k_mvr(const uint8_t *w, const float *x, float *y, uint32_t c
     const bool narrow = nblk > 32u && nblk <= 48u, wide = nblk > 96u && nblk <= 112u;
     if (cols % 256u || !(narrow || wide) || ((uintptr_t)w & 1u) || ((uintptr_t)x & 15u))
         return hipErrorNotSupported;
-    const uint32_t wgs = mvl_cus();
+    const uint32_t wgs = device_cus();
     const uint32_t rpw = (rows + wgs - 1u) / wgs;
     if (narrow ? rows <= 2048u || rpw > 16u : rows <= 4096u || rpw > 32u) return hipErrorNotSupported;
     // every row-sum slot, the padding included, belongs to a wave's block slot
@@ -348,7 +336,7 @@ hipError_t launch_q4k_mvl(const uint8_t *w, const float *x, float *y, uint32_t c
     if (cols % 256u || nblk != kMvlWaves || rows < 4096u || ((uintptr_t)w & 15u) ||
         ((uintptr_t)x & 15u))
         return hipErrorNotSupported;
-    const uint32_t wgs = mvl_cus();
+    const uint32_t wgs = device_cus();
     const uint32_t rpw = (rows + wgs - 1u) / wgs, tiles = (rpw + 15u) / 16u;
     if (tiles > kMvlMaxT) return hipErrorNotSupported;
     MvArgs a{};

@@ -59,6 +59,7 @@
 
 #include "vbs_dev_common.h"
 #include "vbs_internal.h"
+#include "vbs_lds_dma.h"
 
 namespace vbs {
 
@@ -912,6 +913,14 @@ static hipError_t launch_plan(const MvArgs &a, hipStream_t s) {
     if (p.nw > 16u) return hipErrorNotSupported;
     if constexpr (EPI == E_SILU)  // a gate tile and the same up tile
         return launch_ks<T, NORM, EPI, 2>(a, p, a.tile_end[0], s);
+    // Unfused Q4_K launches of rows of 17-32 blocks with at least two tiles
+    // per CU: two tiles per workgroup, a block's x operands serving both
+    // (measured at 8192 x 8192: 11.2-11.5 -> 10.4-10.7 us; four tiles, which
+    // leave half the CUs idle there, and the fused Q/K/V launch were slower)
+    if constexpr ((EPI == E_STORE || EPI == E_ACC) && !NORM && std::is_same<T, Q4K>::value) {
+        if (p.ks == 4u && total >= 2u * device_cus() && total < 1024u)
+            return launch_ks<T, NORM, EPI, 2>(a, p, (total + 1u) / 2u, s);
+    }
     // Launches that would need several rounds of resident workgroups give each
     // workgroup four tiles instead: x (and the RMSNorm) is prepared once per
     // four tiles and every workgroup is resident from the start.
