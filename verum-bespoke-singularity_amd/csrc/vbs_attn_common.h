@@ -13,11 +13,11 @@
 namespace vbs {
 
 // One-wave workgroups the matrix-core split aims for per sequence. The chunk
-// kernel holds 88 VGPRs (five waves per SIMD, 5120 on the chip); at batch 8
-// a target of 1024 made ~5500 of them, a second round of waves late in the
-// launch. Measured chunk + merge with 640 against 1024: 70B batch 8 51.2
-// against 52.3-55.7 us, 70B batch 1 12.9 against 13.2-13.5 us, 7B batch 1
-// 8.3 either way.
+// kernel holds 192 registers (157 VGPRs and the MFMA accumulators): two waves
+// per SIMD, 2048 on the chip at once. At 70B, batch 8, a target of 1024 made
+// 5504 of them (2.7 rounds of waves), 640 makes 4160 (2.03). Measured chunk +
+// merge with 640 against 1024: 70B batch 8 51.2 against 52.3-55.7 us, 70B
+// batch 1 12.9 against 13.2-13.5 us, 7B batch 1 8.3 either way.
 constexpr uint32_t kMfmaTargetWgs = 640;
 constexpr uint32_t kMfmaGran = 32, kMfmaTiles = 8, kMfmaLmax = kMfmaGran * kMfmaTiles;
 
