@@ -137,6 +137,25 @@ def test_linear_full_size_properties(dev, host, oracle, mem, t, rows, cols):
     assert rel_l2(y[sample], want) <= LIN_TOL
 
 
+@pytest.mark.parametrize("rows,cols", [(8192, 8192), (9000, 6144)], ids=["8192x8192", "9000x6144"])
+@pytest.mark.parametrize("accumulate", [False, True], ids=["store", "acc"])
+def test_q4k_two_tile_plan(dev, host, oracle, mem, rows, cols, accumulate):
+    """Q4_K rows of 17-32 blocks with two or more 16-row tiles per CU and
+    fewer than 1024 tiles take two tiles per workgroup, the block's x
+    operands serving both (the 70B O projection, 512 tiles). 9000 rows end in
+    a workgroup whose second tile lies past the matrix. Every row against the
+    oracle, store and accumulate."""
+    w = V.synth_matrix(host, V.Q4_K, rows, cols, SEED, 61)
+    x = synth_x(host, cols, stream=62)
+    y0 = synth_x(host, rows, 63)
+    pw, px, py = mem.up(w), mem.up(x), mem.up(y0)
+    dev.linear(V.Q4_K, pw, px, py, cols, rows, accumulate=accumulate)
+    got = dev.download(py, rows, np.float32)
+    want = oracle.linear(V.Q4_K, w, x, cols, rows, y=y0.copy() if accumulate else None,
+                         accumulate=accumulate, threads=16)
+    assert rel_l2(got, want) <= LIN_TOL
+
+
 @pytest.mark.parametrize("t", [V.Q4_K, V.Q6_K, V.Q8_0, V.Q4_0], ids=lambda t: V.TYPE_NAMES[t])
 def test_linear_activation_edge_cases(dev, host, oracle, mem, t):
     """x with all-zero sub-blocks, 1e4 outliers, subnormal-scale blocks and
