@@ -286,11 +286,11 @@ def test_gpu_graph_decoder_equals_dispatch_path(host, backend, dev, tiny):
 
 @pytest.mark.gpu
 def test_gpu_graph_decoder_7b_width_equals_dispatch_path(host, backend, dev):
-    """At the 7B width (4096, 32 q heads of 128: the fused Q/K/V launch with
-    two tiles per workgroup, the matrix-core attention, k_mvl's O projection
-    with the residual add) the graph decoder's logits and KV rows equal the
-    per-dispatch path's bit for bit, over 2 layers of the 7B geometry and 8
-    teacher-forced positions from 333."""
+    """At the 7B width (4096, 32 q heads of 128: k_mvl's fused attn_norm +
+    Q/K/V + RoPE + KV store launch over 6144 rows, the matrix-core attention,
+    k_mvl's O projection with the residual add) the graph decoder's logits
+    and KV rows equal the per-dispatch path's bit for bit, over 2 layers of
+    the 7B geometry and 8 teacher-forced positions from 333."""
     model = V.SynthModel(host, n_layers=2, **GEO_7B, max_ctx=400, seed=11)
     ctx, n = 333, 8
     kc_p, vc_p = model.kv_prefill(host, ctx)

@@ -115,20 +115,63 @@ template <> __device__ __forceinline__ float deq_elem<kLNS8>(const uint8_t *b, u
 }
 
 // Sum over the 64 lanes of a wavefront; every lane receives the total.
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+// Wave reductions: the butterfly v = op(v, v of lane l ^ m) for m = 32, 16,
+// 8, 4, 2, 1, so that every lane ends with the same value and the adds happen
+// in one fixed order whatever kernel runs them. The partners come without
+// LDS: m = 32 and 16 from the gfx950 lane swaps (v_permlane32_swap,
+// v_permlane16_swap); from m = 8 on, a value depends on lane mod 2m only, so
+// the row rotation by m (DPP row_ror: lane l reads lane (l - m) mod 16 of its
+// row) reads a lane holding the value of lane l ^ m. The whole wave must be
+// active.
+template <int M>
+__device__ __forceinline__ uint32_t bfly_partner(uint32_t v, uint32_t lane) {
+    if constexpr (M == 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return lane < 32u ? r[1] : r[0];
+    } else if constexpr (M == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return (lane & 16u) ? r[0] : r[1];
+    } else {
+        static_assert(M == 8 || M == 4 || M == 2 || M == 1, "butterfly step");
+        return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x120 + M, 0xF, 0xF, false);
+    }
+}
+template <int M>
+__device__ __forceinline__ float bfly_partner(float v, uint32_t lane) {
+    return __builtin_bit_cast(float, bfly_partner<M>(__builtin_bit_cast(uint32_t, v), lane));
+}
+template <int M>
+__device__ __forceinline__ double bfly_partner(double v, uint32_t lane) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = bfly_partner<M>((uint32_t)u, lane), hi = bfly_partner<M>((uint32_t)(u >> 32), lane);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+// The value that lane l ^ M holds, for any values: M = 16 or 32, by the lane
+// swaps (no LDS round trip). The whole wave must be active.
+template <int M, class T>
+__device__ __forceinline__ T lane_xor(T v) {
+    static_assert(M == 16 || M == 32, "lane_xor: 16 or 32");
+    return bfly_partner<M>(v, __lane_id());
+}
+template <class T, class Op>
+__device__ __forceinline__ T wave_butterfly(T v, Op op) {
+    const uint32_t lane = __lane_id();
+    v = op(v, bfly_partner<32>(v, lane));
+    v = op(v, bfly_partner<16>(v, lane));
+    v = op(v, bfly_partner<8>(v, lane));
+    v = op(v, bfly_partner<4>(v, lane));
+    v = op(v, bfly_partner<2>(v, lane));
+    v = op(v, bfly_partner<1>(v, lane));
     return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    return wave_butterfly(v, [](float a, float b) { return a + b; });
 }
 __device__ __forceinline__ double wave_sum_d(double v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
+    return wave_butterfly(v, [](double a, double b) { return a + b; });
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
+    return wave_butterfly(v, [](float a, float b) { return fmaxf(a, b); });
 }
 
 }  // namespace vbs

@@ -471,8 +471,8 @@ __global__ __launch_bounds__(64) void k_attn_mfma(const float *__restrict__ q,
     for (uint32_t kk = 0; kk < 4; kk++)
 #pragma unroll
         for (uint32_t j = 0; j < 8; j++) amax = fmaxf(amax, fabsf(qv[kk][j]));
-    amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+    amax = fmaxf(amax, lane_xor<16>(amax));
+    amax = fmaxf(amax, lane_xor<32>(amax));
     int e2 = 0;
     (void)frexpf(amax, &e2);  // amax < 2^e2
     const int sq = amax > 0.f ? 15 - e2 : 0;
@@ -514,8 +514,8 @@ __global__ __launch_bounds__(64) void k_attn_mfma(const float *__restrict__ q,
             sc[j] = pos_of(t, j) < valid ? __fmul_rn(w, csc) : -INFINITY;
             mt = fmaxf(mt, sc[j]);
         }
-        mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+        mt = fmaxf(mt, lane_xor<16>(mt));
+        mt = fmaxf(mt, lane_xor<32>(mt));
         const float mn = fmaxf(m, mt);
         const float rs = m == -INFINITY ? 0.f : fast_exp(__fsub_rn(m, mn));
         m = mn;
@@ -552,13 +552,13 @@ __global__ __launch_bounds__(64) void k_attn_mfma(const float *__restrict__ q,
 
     // ---- the chunk's partial: l summed over the lane groups of a head, rows
     // hi + lo of acc (lane groups g and g + 2), stored by lane groups 0 and 1
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
+    l += lane_xor<16>(l);
+    l += lane_xor<32>(l);
     float a[8][4];
 #pragma unroll
     for (uint32_t dt = 0; dt < 8; dt++)
 #pragma unroll
-        for (uint32_t r = 0; r < 4; r++) a[dt][r] = acc[dt][r] + __shfl_xor(acc[dt][r], 32, 64);
+        for (uint32_t r = 0; r < 4; r++) a[dt][r] = acc[dt][r] + lane_xor<32>(acc[dt][r]);
     float *const pk = part + (uint64_t)kvh * group * stride_chunks * (HD + 2u);
     if (g < 2u) {
 #pragma unroll

@@ -78,6 +78,10 @@ hipError_t launch_kq_qkv(int type, const uint8_t *const wqkv[3], uint32_t n_mat,
     a.kc = kc;
     a.vc = vc;
     a.kv_layer = kv_layer;
+    if (type == kQ4_K) {
+        const hipError_t e = launch_q4k_mvl_qkv(a, s);
+        if (e != hipErrorNotSupported) return e;
+    }
     set_tiles(a);
     return norm_w ? launch_type<true, E_QKV>(type, a, s) : launch_type<false, E_QKV>(type, a, s);
 }

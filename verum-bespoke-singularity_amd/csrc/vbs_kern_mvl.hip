@@ -1,7 +1,8 @@
 // vbs_kern_mvl.hip — batch-1 K-quant matvecs that keep a CU's weights in
 // flight through LDS DMA: k_mvl (Q4_K, the whole row range of a workgroup at
-// once: rows of 16 super-blocks, 4096-12288 rows) and k_mvr (Q6_K, a ring of
-// slots per wave: rows of 33-48 super-blocks, 2049-4096 rows).
+// once: rows of 16 super-blocks, 4096-12288 rows; also the decoder's fused
+// attn_norm + Q/K/V + RoPE + KV store launch over such rows) and k_mvr (Q6_K,
+// a ring of slots per wave: rows of 33-48 super-blocks, 2049-4096 rows).
 //
 // One 16-wave workgroup per CU owns an even range of at most 48 rows (T tiles
 // of 16). Wave w owns super-block w of every row: before it computes anything
@@ -29,40 +30,75 @@
 namespace vbs {
 
 constexpr uint32_t kMvlWaves = 16, kMvlItem = 16u * 144u, kMvlSlot = 1024u, kMvlMaxT = 3;
+constexpr uint32_t kMvlQkvBytes = 16u + 1024u;  // E_QKV: position, RoPE row of hd <= 256
 
-// EPI: E_STORE (y = W x) or E_ACC (y += W x). T tiles of 16 rows per workgroup,
+// EPI: E_STORE (y = W x), E_ACC (y += W x) or E_QKV (the nmat matrices' rows
+// one after another, RoPE and the f16 cache stores of k_mvf's E_QKV). NORM:
+// x is RMS-normalised first, as in k_mvf (each wave's block sum of squares,
+// the sixteen added in block order). T tiles of 16 rows per workgroup,
 // rpw <= 16 T rows each (the last workgroup's range may be shorter or empty).
-template <uint32_t T, int EPI>
+template <uint32_t T, bool NORM, int EPI>
 __global__ __launch_bounds__(64 * kMvlWaves) void k_mvl(const MvArgs a, uint32_t rpw) {
     extern __shared__ __align__(16) uint8_t lds[];
+    __shared__ double bsum[NORM ? kMvlWaves : 1];
     const uint32_t cols = a.cols, nblk = cols >> 8, rb = nblk * 144u;
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const uint32_t n = lane & 15u, g = lane >> 4;
-    const uint32_t r0 = blockIdx.x * rpw, r1 = min(r0 + rpw, a.rows[0]);
+    // the launch's rows: matrix 0's, then matrix 1's, then matrix 2's
+    const uint32_t e0 = a.rows[0], e1 = EPI == E_QKV && a.nmat > 1u ? e0 + a.rows[1] : e0;
+    const uint32_t total = EPI == E_QKV && a.nmat > 2u ? e1 + a.rows[2] : e1;
+    const uint32_t r0 = blockIdx.x * rpw, r1 = min(r0 + rpw, total);
     if (r0 >= r1) return;
     const uint32_t b = min(wave, nblk - 1u);  // this wave's block (waves past the row re-read the last)
     const bool own = wave < nblk;
-    // LDS: [16 waves][T items of 2304 B] | 16 zero bytes | [16 waves][x / digit slot] | pb
+    // LDS: [16 waves][T items of 2304 B] | 16 zero bytes | [16 waves][x / digit slot] |
+    // (NORM) [16 waves][RMSNorm weights of the block] | (E_QKV) the position
+    // (16 B) and its RoPE row (hd / 2 float2) | pb
     const uint32_t lds0 = (uint32_t)(uintptr_t)lds;
     const uint32_t stage = lds0 + wave * T * kMvlItem;
     uint8_t *const xq = lds + kMvlWaves * T * kMvlItem;
     uint8_t *const slot = xq + 16u + wave * kMvlSlot;
-    float *const pb = reinterpret_cast<float *>(xq + 16u + kMvlWaves * kMvlSlot);
-    const uint8_t *const w = a.w[0];
+    uint8_t *const nslot = xq + 16u + kMvlWaves * kMvlSlot + wave * 1024u;
+    uint8_t *const qpos = xq + 16u + kMvlWaves * kMvlSlot + (NORM ? kMvlWaves * 1024u : 0u);
+    uint8_t *const qrope = qpos + 16u;
+    float *const pb = reinterpret_cast<float *>(qpos + (EPI == E_QKV ? kMvlQkvBytes : 0u));
+    // E_QKV: wave 0 (the one that finishes the rows) requests the position
+    // before anything else and its RoPE row once the position is in: the
+    // epilogue's operands arrive during the matrix work, not after it
+    const bool w0 = EPI == E_QKV && __builtin_amdgcn_readfirstlane(wave) == 0u;
+    // matrix m of row gr (E_QKV) and gr's first byte
+    auto mat = [&](uint32_t gr) { return (uint32_t)(gr >= e0) + (uint32_t)(gr >= e1); };
+    auto wrow = [&](uint32_t gr) {
+        if constexpr (EPI == E_QKV) {
+            const uint32_t m = mat(gr);
+            const uint8_t *w = m == 0u ? a.w[0] : m == 1u ? a.w[1] : a.w[2];
+            return w + (uint64_t)(gr - (m == 0u ? 0u : m == 1u ? e0 : e1)) * rb;
+        } else {
+            return a.w[0] + (uint64_t)gr * rb;
+        }
+    };
 
-    // 1. all loads: x block b (one DMA), then the T items (three DMAs each:
-    // chunk c = 9 n' + p is piece p of row n' of the tile, at item + 16 c)
+    // 1. all loads: x block b (one DMA) and its RMSNorm weights, then the T
+    // items (three DMAs each: chunk c = 9 n' + p is piece p of row n' of the
+    // tile, at item + 16 c)
+    if (w0 && lane == 0u) dma4(a.pos, (uint32_t)(uintptr_t)qpos);
     dma16(a.x + 256u * b + 4u * lane, (uint32_t)(uintptr_t)slot);
-#pragma unroll
-    for (uint32_t j = 0; j < T; j++) {
+    if constexpr (NORM) dma16(a.norm_w + 256u * b + 4u * lane, (uint32_t)(uintptr_t)nslot);
+    auto issue_tile = [&](uint32_t j) {
 #pragma unroll
         for (uint32_t q = 0; q < 3; q++) {
             const uint32_t c = 64u * q + lane;
             const uint32_t row = min(r0 + 16u * j + c / 9u, r1 - 1u);
-            const uint8_t *src = w + ((uint64_t)row * rb + b * 144u + 16u * (c % 9u));
+            const uint8_t *src = wrow(row) + (b * 144u + 16u * (c % 9u));
             if (q < 2u || lane < 16u) dma16(src, stage + j * kMvlItem + 1024u * q);
         }
-    }
+    };
+    // With the RMSNorm, tiles from kPre on are requested after the barrier
+    // that shares the block sums: a barrier waits until every wave has issued
+    // everything before it, and issuing all of a CU's DMAs takes ~0.8 us.
+    constexpr uint32_t kPre = NORM ? 1u : T;
+#pragma unroll
+    for (uint32_t j = 0; j < kPre; j++) issue_tile(j);
     if (lane < 4u) reinterpret_cast<uint32_t *>(xq)[lane] = 0u;
     DigitView dv;
     dv.zero = xq;
@@ -71,15 +107,44 @@ __global__ __launch_bounds__(64 * kMvlWaves) void k_mvl(const MvArgs a, uint32_t
     dv.xs16 = reinterpret_cast<float *>(slot + 768u);
     dv.xs = reinterpret_cast<float2 *>(slot + 832u);
 
-    // 2. x has landed (the 3 T item DMAs after it may still be in flight):
-    // its digits, written over it in the same slot
-    vmcnt_le<3u * T>();
+    // 2. x has landed (the item DMAs after it may still be in flight): its
+    // digits, written over it in the same slot
+    vmcnt_le<3u * kPre>();
     asm volatile("" ::: "memory");
     {
         const float4 xv = *reinterpret_cast<const float4 *>(slot + 16u * lane);
-        const float v[4] = {xv.x, xv.y, xv.z, xv.w};
+        float v[4] = {xv.x, xv.y, xv.z, xv.w};
+        if constexpr (NORM) {
+            const double ss = block_sumsq(v);
+            if (lane == 0u && own) bsum[wave] = ss;
+            __syncthreads();
+#pragma unroll
+            for (uint32_t j = kPre; j < T; j++) issue_tile(j);
+            double t = 0.0;
+            for (uint32_t k = 0; k < nblk; k++) t += bsum[k];
+            const float mean = (float)(t / (double)cols);
+            const float sc = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, a.eps)));
+            const float4 wv = *reinterpret_cast<const float4 *>(nslot + 16u * lane);
+            const float w4[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+            for (int k = 0; k < 4; k++) v[k] = __fmul_rn(__fmul_rn(v[k], sc), w4[k]);
+        }
         if (own) prep_block(v, lane, dv);
     }
+    if (w0) {  // (the position landed before x)
+        const uint32_t p = *reinterpret_cast<const uint32_t *>(qpos);
+        if (lane < a.hd / 4u)
+            dma16(a.rope + (uint64_t)p * (a.hd / 2u) + 2u * lane, (uint32_t)(uintptr_t)qrope);
+    }
+    // the wait for the items issued before the last N (wave 0 of E_QKV has
+    // the RoPE DMA after them)
+    auto wait_items = [&](auto N) {
+        if (w0)
+            vmcnt_le<decltype(N)::value + 1u>();
+        else
+            vmcnt_le<decltype(N)::value>();
+        asm volatile("" ::: "memory");
+    };
 
     // 3. the items in arrival order, the x operands of block b read once
     const Q4K::X xo = Q4K::x_operands(dv, n, g);
@@ -91,55 +156,69 @@ __global__ __launch_bounds__(64 * kMvlWaves) void k_mvl(const MvArgs a, uint32_t
         r[1] = lda4(row + 16u + 16u * g);
         r[2] = lda4(row + 80u + 16u * g);
         float part = Q4K::dot_x(r, xo, g);
-        part += __shfl_xor(part, 16, 64);
-        part += __shfl_xor(part, 32, 64);
+        part += lane_xor<16>(part);
+        part += lane_xor<32>(part);
         const uint32_t rr = 16u * j + n;
         if (lane < 16u && own && rr < rpw) pb[rr * ps + b] = part;
         asm volatile("" ::"v"(part));
         __builtin_amdgcn_sched_barrier(0);
     };
-    vmcnt_le<3u * (T - 1u)>();
-    asm volatile("" ::: "memory");
+    wait_items(std::integral_constant<uint32_t, 3u * (T - 1u)>{});
     item(0);
     if constexpr (T > 1u) {
-        vmcnt_le<3u * (T - 2u)>();
-        asm volatile("" ::: "memory");
+        wait_items(std::integral_constant<uint32_t, 3u * (T - 2u)>{});
         item(1);
     }
     if constexpr (T > 2u) {
-        vmcnt_le<0u>();
-        asm volatile("" ::: "memory");
+        wait_items(std::integral_constant<uint32_t, 0u>{});
         item(2);
     }
 
     // 4. row t of the range: its blocks' sums in block order
     __syncthreads();
     const uint32_t t = threadIdx.x;
-    if (t < r1 - r0) {
+    if constexpr (EPI == E_QKV) {
+        // (ranges start and end on even rows: a row's RoPE partner t ^ 1 is in
+        // the range and in the same wave)
+        // (rows live in wave 0: rpw <= 48)
+        if (w0) {
+            vmcnt_le<0u>();
+            asm volatile("" ::: "memory");
+        }
+        float s = 0.f;
+        if (t < r1 - r0) s = ordered_sum(pb + t * ps, kMvlWaves);
+        const float other = __shfl_xor(s, 1, 64);
+        if (t < r1 - r0) {
+            const uint32_t gr = r0 + t, m = mat(gr);
+            const float2 *rp = reinterpret_cast<const float2 *>(qrope);
+            qkv_store(a, m, gr - (m == 0u ? 0u : m == 1u ? e0 : e1), s, other,
+                      *reinterpret_cast<const uint32_t *>(qpos), [&](uint32_t i) { return rp[i]; });
+        }
+    } else if (t < r1 - r0) {
         const float s = ordered_sum(pb + t * ps, kMvlWaves);
         float *y = a.y[0] + r0 + t;
         *y = EPI == E_ACC ? __fadd_rn(*y, s) : s;
     }
 }
 
-template <uint32_t T, int EPI>
+template <uint32_t T, bool NORM, int EPI>
 static hipError_t launch_mvl_t(const MvArgs &a, uint32_t wgs, uint32_t rpw, hipStream_t s) {
     const uint32_t nblk = a.cols / 256u;
-    const size_t lds = (size_t)kMvlWaves * T * kMvlItem + 16u + (size_t)kMvlWaves * kMvlSlot +
-                       (size_t)rpw * part_stride(nblk) * sizeof(float);
+    const size_t fixed = (size_t)kMvlWaves * T * kMvlItem + 16u + (size_t)kMvlWaves * kMvlSlot +
+                         (NORM ? (size_t)kMvlWaves * 1024u : 0u) + (EPI == E_QKV ? kMvlQkvBytes : 0u);
+    const size_t lds = fixed + (size_t)rpw * part_stride(nblk) * sizeof(float);
     static bool granted = false;
     if (!granted) {
-        if (hipFuncSetAttribute((const void *)k_mvl<T, EPI>,
+        if (hipFuncSetAttribute((const void *)k_mvl<T, NORM, EPI>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)(kMvlWaves * kMvlMaxT * kMvlItem + 16u + kMvlWaves * kMvlSlot +
-                                      16u * kMvlMaxT * part_stride(kMvlWaves) * sizeof(float))) !=
+                                (int)(fixed + 16u * T * part_stride(kMvlWaves) * sizeof(float))) !=
             hipSuccess) {
             (void)hipGetLastError();
             return hipErrorNotSupported;
         }
         granted = true;
     }
-    k_mvl<T, EPI><<<wgs, 64 * kMvlWaves, lds, s>>>(a, rpw);
+    k_mvl<T, NORM, EPI><<<wgs, 64 * kMvlWaves, lds, s>>>(a, rpw);
     return hipGetLastError();
 }
 
@@ -252,8 +331,8 @@ __global__ __launch_bounds__(1024) void k_mvr(const MvArgs a, uint32_t rpw) {
         if (own) {
             const Src src{w, a.rows[0] * rb, rb, r0 + 16u * j, r1};
             float part = Q6K::dot_staged_x(lds + (ring - lds0) + (i % R) * kMvrItem, src, xo, b, n, g);
-            part += __shfl_xor(part, 16, 64);
-            part += __shfl_xor(part, 32, 64);
+            part += lane_xor<16>(part);
+            part += lane_xor<32>(part);
             const uint32_t rr = 16u * j + n;
             if (lane < 16u && rr < rpw) pb[rr * part_stride(nblk) + b] = part;
             asm volatile("" ::"v"(part));
@@ -348,7 +427,37 @@ hipError_t launch_q4k_mvl(const uint8_t *w, const float *x, float *y, uint32_t c
     a.x = x;
     const uint32_t g = (rows + rpw - 1u) / rpw;  // workgroups with rows
 #define VBS_MVL(TT)                                                                              \
-    return accumulate ? launch_mvl_t<TT, E_ACC>(a, g, rpw, s) : launch_mvl_t<TT, E_STORE>(a, g, rpw, s)
+    return accumulate ? launch_mvl_t<TT, false, E_ACC>(a, g, rpw, s)                             \
+                      : launch_mvl_t<TT, false, E_STORE>(a, g, rpw, s)
+    if (tiles == 1u) VBS_MVL(1);
+    if (tiles == 2u) VBS_MVL(2);
+    VBS_MVL(3);
+#undef VBS_MVL
+}
+
+hipError_t launch_q4k_mvl_qkv(const MvArgs &a, hipStream_t s) {
+    // the fused attn_norm + Q/K/V + RoPE + KV store launch over rows of exactly
+    // 16 blocks and 4096 or more rows in all: every CU takes an even range
+    // (k_mvf's two tiles per workgroup leave a quarter of the CUs idle at
+    // 6144 rows)
+    const uint32_t nblk = a.cols / 256u;
+    if (a.cols % 256u || nblk != kMvlWaves || a.nmat == 0u || a.nmat > 3u || ((uintptr_t)a.x & 15u) ||
+        ((uintptr_t)a.norm_w & 15u) || ((uintptr_t)a.rope & 15u) || ((uintptr_t)a.pos & 3u) ||
+        a.hd % 4u || a.hd > 256u)
+        return hipErrorNotSupported;
+    uint32_t total = 0;
+    for (uint32_t m = 0; m < a.nmat; m++) {
+        if (((uintptr_t)a.w[m] & 15u) || (a.rows[m] & 1u)) return hipErrorNotSupported;
+        total += a.rows[m];
+    }
+    if (total < 4096u) return hipErrorNotSupported;
+    const uint32_t wgs = device_cus();
+    const uint32_t rpw = ((total + wgs - 1u) / wgs + 1u) & ~1u, tiles = (rpw + 15u) / 16u;
+    if (tiles > kMvlMaxT) return hipErrorNotSupported;
+    const uint32_t g = (total + rpw - 1u) / rpw;
+#define VBS_MVL(TT)                                                                              \
+    return a.norm_w ? launch_mvl_t<TT, true, E_QKV>(a, g, rpw, s)                                \
+                    : launch_mvl_t<TT, false, E_QKV>(a, g, rpw, s)
     if (tiles == 1u) VBS_MVL(1);
     if (tiles == 2u) VBS_MVL(2);
     VBS_MVL(3);

@@ -25,6 +25,12 @@ __device__ __forceinline__ void dma16(const void *g, uint32_t lds) {
                  "s"(__builtin_amdgcn_readfirstlane(lds))
                  : "memory");
 }
+// 4 bytes per lane from g to LDS at lds + 4 lane (lds wave-uniform, in M0).
+__device__ __forceinline__ void dma4(const void *g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g),
+                 "s"(__builtin_amdgcn_readfirstlane(lds))
+                 : "memory");
+}
 template <uint32_t N>
 __device__ __forceinline__ void vmcnt_le() {  // vmcnt <= N, other counters untouched
     static_assert(N < 64, "vmcnt");

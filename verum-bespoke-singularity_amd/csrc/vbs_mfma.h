@@ -591,6 +591,33 @@ struct MvArgs {
     uint64_t kv_layer;  // layer * max_ctx * kvd
 };
 
+// The fused attn_norm + Q/K/V + RoPE + KV store launch of k_mvl
+// (vbs_kern_mvl.hip) for Q4_K rows of 16 blocks and 4096 or more rows in all;
+// hipErrorNotSupported elsewhere (k_mvf then runs). Bit-identical to k_mvf.
+hipError_t launch_q4k_mvl_qkv(const MvArgs &a, hipStream_t s);
+
+// E_QKV: row `row` of matrix m (role role0 + m) with value t, its RoPE
+// partner row (row ^ 1) holding `other`: q rows and k rows rotated at the
+// device position p by rope(i) = (cos, sin) of pair i, q stored as f32, k and
+// v into the f16 caches.
+template <class Rope>
+__device__ __forceinline__ void qkv_store(const MvArgs &a, uint32_t m, uint32_t row, float t,
+                                          float other, uint32_t p, Rope rope) {
+    const uint32_t role = a.role0 + m;
+    float v = t;
+    if (role < 2u) {
+        const float2 cs = rope((row % a.hd) / 2u);
+        const bool even = (row & 1u) == 0u;
+        const float x0 = even ? t : other, x1 = even ? other : t;
+        v = even ? __fsub_rn(__fmul_rn(x0, cs.x), __fmul_rn(x1, cs.y))
+                 : __fadd_rn(__fmul_rn(x0, cs.y), __fmul_rn(x1, cs.x));
+    }
+    if (role == 0u)
+        a.y[0][row] = v;
+    else
+        (role == 1u ? a.kc : a.vc)[a.kv_layer + (uint64_t)p * a.kvd + row] = vbs_f2h(v);
+}
+
 // The register set that holds a block's x operands when k_mvf reads them once
 // for its tiles: Q4_K only (Q6_K's 24 registers would take its four-tile
 // head launches past 128 VGPRs, one workgroup per CU instead of two).
@@ -740,8 +767,8 @@ __global__ __launch_bounds__(MAXT) void k_mvf(const MvArgs a) {
             part = T::dot(r[i], scratch, src[tl], view(bi), bi, n, g);
         }
         // the four lane groups of a row hold different groups of the block
-        part += __shfl_xor(part, 16, 64);
-        part += __shfl_xor(part, 32, 64);
+        part += lane_xor<16>(part);
+        part += lane_xor<32>(part);
         // (slots past the row: +0.0)
         if (lane < 16u && blk(i) < slots) pb[(tl * 16u + n) * ps + blk(i)] = blk(i) < nblk ? part : 0.f;
         // finish item i here: otherwise its arithmetic may sink past later
@@ -779,22 +806,11 @@ __global__ __launch_bounds__(MAXT) void k_mvf(const MvArgs a) {
                 a.y[0][row] = __fmul_rn(__fdiv_rn(prev, den), t);
             }
         } else {  // E_QKV
-            const uint32_t role = a.role0 + m;
             const float other = __shfl_xor(t, 1, 64);  // the RoPE partner row
-            const uint32_t p = a.pos[0];
-            float v = t;
-            if (role < 2u) {
-                const float2 cs = a.rope[(uint64_t)p * (a.hd / 2u) + (row % a.hd) / 2u];
-                const bool even = (row & 1u) == 0u;
-                const float x0 = even ? t : other, x1 = even ? other : t;
-                v = even ? __fsub_rn(__fmul_rn(x0, cs.x), __fmul_rn(x1, cs.y))
-                         : __fadd_rn(__fmul_rn(x0, cs.y), __fmul_rn(x1, cs.x));
-            }
             if (st) {
-                if (role == 0u)
-                    a.y[0][row] = v;
-                else
-                    (role == 1u ? a.kc : a.vc)[a.kv_layer + (uint64_t)p * a.kvd + row] = vbs_f2h(v);
+                const uint32_t p = a.pos[0];
+                qkv_store(a, m, row, t, other, p,
+                          [&](uint32_t i) { return a.rope[(uint64_t)p * (a.hd / 2u) + i]; });
             }
         }
     }
