@@ -589,6 +589,9 @@ struct MvArgs {
     uint32_t hd, kvd, role0;
     uint16_t *kc, *vc;
     uint64_t kv_layer;  // layer * max_ctx * kvd
+    // ranged launches: workgroups of matrix m end at rwg_end[m] (cumulative),
+    // each taking rpw[m] rows of it (the last one of a matrix fewer)
+    uint32_t rwg_end[3], rpw[3];
 };
 
 // The fused attn_norm + Q/K/V + RoPE + KV store launch of k_mvl
@@ -630,7 +633,10 @@ struct XOf<T, true> {
     using type = typename T::X;
 };
 
-template <class T, uint32_t KS, uint32_t TPW, uint32_t MAXT, bool NORM, int EPI>
+// RANGED: workgroup b takes rows [r0, r1) of one matrix (MvArgs::rwg_end,
+// rpw) as TPW tiles from r0, rows past r1 re-reading row r1 - 1, so that every
+// CU streams an even share when the tiles do not divide evenly over the CUs.
+template <class T, uint32_t KS, uint32_t TPW, uint32_t MAXT, bool NORM, int EPI, bool RANGED = false>
 __global__ __launch_bounds__(MAXT) void k_mvf(const MvArgs a) {
     extern __shared__ __align__(16) uint8_t xq[];
     __shared__ double bsum[128];
@@ -650,8 +656,20 @@ __global__ __launch_bounds__(MAXT) void k_mvf(const MvArgs a) {
     // matrix and local tile of this workgroup's tile j
     uint32_t mt[TPW], lt[TPW];
     Src src[TPW];
+    uint32_t rm = 0, r0 = 0, r1 = 0;  // RANGED: the workgroup's matrix and rows
+    if constexpr (RANGED) {
+        rm = (uint32_t)(blockIdx.x >= a.rwg_end[0]) + (uint32_t)(blockIdx.x >= a.rwg_end[1]);
+        r0 = (blockIdx.x - (rm ? a.rwg_end[rm - 1u] : 0u)) * a.rpw[rm];
+        r1 = min(r0 + a.rpw[rm], a.rows[rm]);
+    }
 #pragma unroll
     for (uint32_t j = 0; j < TPW; j++) {
+        if constexpr (RANGED) {
+            mt[j] = rm;
+            lt[j] = 0u;
+            src[j] = Src{a.w[rm], a.rows[rm] * rb, rb, r0 + 16u * j, r1};
+            continue;
+        }
         if (EPI == E_SILU) {
             mt[j] = j;
             lt[j] = blockIdx.x;
@@ -791,9 +809,9 @@ __global__ __launch_bounds__(MAXT) void k_mvf(const MvArgs a) {
         const float t = ordered_sum(pb + (j * 16u + n) * ps, nblk);
         // every lane holds the value of row n of the tile
         const uint32_t m = mt[j];
-        const bool own = (EPI == E_SILU || blockIdx.x * TPW + j < total);
-        const uint32_t row = lt[j] * 16u + n;
-        const bool st = lane < 16u && own && row < a.rows[m];
+        const bool own = (RANGED || EPI == E_SILU || blockIdx.x * TPW + j < total);
+        const uint32_t row = RANGED ? r0 + 16u * j + n : lt[j] * 16u + n;
+        const bool st = lane < 16u && own && row < (RANGED ? r1 : a.rows[m]);
         if (EPI == E_STORE) {
             if (st) a.y[m][row] = t;
         } else if (EPI == E_ACC) {
@@ -821,6 +839,27 @@ struct MvPlan {
     uint32_t ks, tpw, nw;
 };
 
+// The ranged split of a launch's matrices: the smallest even row count per
+// workgroup (at most three tiles) whose workgroups, every one with rows, fit
+// one per CU; false if none does.
+static inline bool ranged_split(MvArgs &a, uint32_t cus) {
+    uint32_t total = 0;
+    for (uint32_t m = 0; m < a.nmat; m++) {
+        if (a.rows[m] & 1u) return false;  // (RoPE pairs stay in one workgroup)
+        total += a.rows[m];
+    }
+    for (uint32_t rpw = ((total + cus - 1u) / cus + 1u) & ~1u; rpw <= 48u; rpw += 2u) {
+        uint32_t wgs = 0;
+        for (uint32_t m = 0; m < 3u; m++) {
+            if (m < a.nmat) wgs += (a.rows[m] + rpw - 1u) / rpw;
+            a.rwg_end[m] = wgs;
+            a.rpw[m] = rpw;
+        }
+        if (wgs <= cus) return true;
+    }
+    return false;
+}
+
 // Blocks per wave (KS) and waves per tile: enough waves to split the row and
 // enough items per wave that the stream runs ahead of the arithmetic.
 // (The gate/up launch, two tiles per workgroup, keeps four blocks per wave:
@@ -840,7 +879,7 @@ static MvPlan mv_plan(uint32_t cols, bool two_tiles, bool fused) {
     return p;
 }
 
-template <class T, uint32_t KS, uint32_t TPW, uint32_t MAXT, bool NORM, int EPI>
+template <class T, uint32_t KS, uint32_t TPW, uint32_t MAXT, bool NORM, int EPI, bool RANGED = false>
 static hipError_t launch_t(const MvArgs &a, uint32_t nw, uint32_t wgs, hipStream_t s) {
     const size_t digits = TPW == 1u ? 16u + (size_t)nw * kSlotBytes : xq_layout(a.cols).bytes;
     const size_t lds = digits + (size_t)nw * T::SCRATCH +
@@ -848,7 +887,7 @@ static hipError_t launch_t(const MvArgs &a, uint32_t nw, uint32_t wgs, hipStream
     if (lds > 65536u) {  // beyond the default per-workgroup LDS window: opt in once
         static size_t granted = 0;
         if (lds > granted) {
-            if (hipFuncSetAttribute((const void *)k_mvf<T, KS, TPW, MAXT, NORM, EPI>,
+            if (hipFuncSetAttribute((const void *)k_mvf<T, KS, TPW, MAXT, NORM, EPI, RANGED>,
                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
                 hipSuccess) {
                 (void)hipGetLastError();
@@ -857,7 +896,7 @@ static hipError_t launch_t(const MvArgs &a, uint32_t nw, uint32_t wgs, hipStream
             granted = lds;
         }
     }
-    k_mvf<T, KS, TPW, MAXT, NORM, EPI><<<wgs, 64u * nw, lds, s>>>(a);
+    k_mvf<T, KS, TPW, MAXT, NORM, EPI, RANGED><<<wgs, 64u * nw, lds, s>>>(a);
     return hipGetLastError();
 }
 
@@ -916,6 +955,17 @@ static hipError_t launch_plan(const MvArgs &a, hipStream_t s) {
     // blocks per wave (18.2 -> 17.0 us at 10240 x 8192).
     if constexpr (EPI == E_QKV) {
         const uint32_t nblk = a.cols / 256u;
+        // Q4_K rows of 17-32 blocks (70B: 8192 + 1024 + 1024 rows of 32): an
+        // even range of at most three tiles per workgroup on sixteen waves of
+        // two blocks, so that no CU streams three tiles while others stream
+        // two (640 tiles over 256 CUs)
+        if constexpr (std::is_same<T, Q4K>::value) {
+            if (nblk > 16u && nblk <= 32u) {
+                MvArgs r = a;
+                if (ranged_split(r, device_cus()))
+                    return launch_t<T, 2, 3, 1024, NORM, EPI, true>(r, 16u, r.rwg_end[2], s);
+            }
+        }
         if (nblk <= 16u) {
             p.ks = 1u;
             p.nw = nblk;
