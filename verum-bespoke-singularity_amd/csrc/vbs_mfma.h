@@ -635,7 +635,8 @@ struct XOf<T, true> {
 
 // RANGED: workgroup b takes rows [r0, r1) of one matrix (MvArgs::rwg_end,
 // rpw) as TPW tiles from r0, rows past r1 re-reading row r1 - 1, so that every
-// CU streams an even share when the tiles do not divide evenly over the CUs.
+// CU streams an even share when the tiles do not divide evenly over the CUs
+// (E_SILU: the same rows of gate, tiles 0 .. TPW/2 - 1, and of up, the rest).
 template <class T, uint32_t KS, uint32_t TPW, uint32_t MAXT, bool NORM, int EPI, bool RANGED = false>
 __global__ __launch_bounds__(MAXT) void k_mvf(const MvArgs a) {
     extern __shared__ __align__(16) uint8_t xq[];
@@ -665,9 +666,10 @@ __global__ __launch_bounds__(MAXT) void k_mvf(const MvArgs a) {
 #pragma unroll
     for (uint32_t j = 0; j < TPW; j++) {
         if constexpr (RANGED) {
-            mt[j] = rm;
+            constexpr uint32_t H = EPI == E_SILU ? TPW / 2u : TPW;
+            mt[j] = EPI == E_SILU ? (uint32_t)(j >= H) : rm;
             lt[j] = 0u;
-            src[j] = Src{a.w[rm], a.rows[rm] * rb, rb, r0 + 16u * j, r1};
+            src[j] = Src{a.w[mt[j]], a.rows[mt[j]] * rb, rb, r0 + 16u * (j % H), r1};
             continue;
         }
         if (EPI == E_SILU) {
@@ -802,6 +804,21 @@ __global__ __launch_bounds__(MAXT) void k_mvf(const MvArgs a) {
 
     // 5. tile j finished by wave j % nw (both tiles by wave 0 for E_SILU)
     __syncthreads();
+    if constexpr (RANGED && EPI == E_SILU) {  // row tile j: gate tile j, up tile j + TPW / 2
+        constexpr uint32_t H = TPW / 2u;
+#pragma unroll
+        for (uint32_t j = 0; j < H; j++) {
+            if (wave != j % nw) continue;
+            const float gate = ordered_sum(pb + (j * 16u + n) * ps, nblk);
+            const float up = ordered_sum(pb + ((j + H) * 16u + n) * ps, nblk);
+            const uint32_t row = r0 + 16u * j + n;
+            if (lane < 16u && row < r1) {
+                const float den = __fadd_rn(1.0f, expf(-gate));
+                a.y[0][row] = __fmul_rn(__fdiv_rn(gate, den), up);
+            }
+        }
+        return;
+    }
     float prev = 0.f;  // E_SILU: the gate row value
 #pragma unroll
     for (uint32_t j = 0; j < TPW; j++) {
@@ -977,6 +994,22 @@ static hipError_t launch_plan(const MvArgs &a, hipStream_t s) {
         }
     }
     if (p.nw > 16u) return hipErrorNotSupported;
+    if constexpr (EPI == E_SILU && std::is_same<T, Q4K>::value) {
+        // Q4_K rows of 16 blocks whose tile pairs do not divide evenly over
+        // the CUs (7B: 688 over 256) and fit three per CU: an even range of
+        // rows per workgroup, three gate and three up tiles on sixteen waves
+        // of one block
+        const uint32_t cus = device_cus(), rpw = (a.rows[0] + cus - 1u) / cus;
+        if (a.cols == 4096u && rpw > 32u && rpw <= 48u && a.tile_end[0] % cus) {
+            MvArgs r = a;
+            const uint32_t wgs = (a.rows[0] + rpw - 1u) / rpw;
+            for (uint32_t m = 0; m < 3u; m++) {
+                r.rwg_end[m] = wgs;
+                r.rpw[m] = rpw;
+            }
+            return launch_t<T, 1, 6, 1024, NORM, EPI, true>(r, 16u, wgs, s);
+        }
+    }
     if constexpr (EPI == E_SILU)  // a gate tile and the same up tile
         return launch_ks<T, NORM, EPI, 2>(a, p, a.tile_end[0], s);
     // Unfused Q4_K launches of rows of 17-32 blocks with at least two tiles
