@@ -187,6 +187,9 @@ struct MbArgs {
     uint16_t *kc, *vc;
     uint64_t kv_seq, layer_off;
     uint32_t hd, kvd, max_ctx;
+    // ranged k_mvbr4 launches: workgroups of matrix m end at rwg_end[m]
+    // (cumulative), each taking rpw[m] rows of it (the last one of a matrix fewer)
+    uint32_t rwg_end[3], rpw[3];
 };
 
 // This lane's A row: its plane's first eight elements and first eight
@@ -638,7 +641,7 @@ struct Mvbr4Plan {
 };
 constexpr uint32_t kMvbr4Pass = 12;  // tiles per reduction pass (12 x 8 KB in the ring's 110 KB)
 
-template <uint32_t NB, uint32_t T, uint32_t R, int EPI>
+template <uint32_t NB, uint32_t T, uint32_t R, int EPI, bool RANGED = false>
 __global__ __launch_bounds__(1024) void k_mvbr4(const MbArgs a) {
     using P = Mvbr4Plan<NB, T, R>;
     constexpr uint32_t NI = P::NI, ISZ = P::ISZ;
@@ -648,20 +651,36 @@ __global__ __launch_bounds__(1024) void k_mvbr4(const MbArgs a) {
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const uint32_t n = lane & 15u, g = lane >> 4;
     const uint32_t total = a.tile_end[a.nmat - 1u], gt0 = blockIdx.x * T;
-    if (gt0 >= total) return;
+    if (!RANGED && gt0 >= total) return;
     const XbLayout L = xb_layout(cols);
     const uint32_t pl = min(n, 2u * a.batch - 1u);
     const XbView xv{reinterpret_cast<const _Float16 *>(a.xp) + 8u * pl,
                     reinterpret_cast<const _Float16 *>(a.xp + L.msum) + 8u * pl,
                     reinterpret_cast<const int *>(a.xp + L.expo)};
     const uint32_t lds0 = (uint32_t)(uintptr_t)lds, ring = lds0 + wave * R * ISZ;
-    // tile j of the workgroup: matrix, local tile and row count (tiles past
-    // the last one repeat it and are not stored)
-    auto tile = [&](uint32_t j, uint32_t &m, uint32_t &lt, uint32_t &rows) {
-        const uint32_t gt = min(gt0 + j, total - 1u);
-        m = (gt >= a.tile_end[0]) + (a.nmat > 2u && gt >= a.tile_end[1]);
-        lt = gt - (m == 0u ? 0u : m == 1u ? a.tile_end[0] : a.tile_end[1]);  // (no dynamic index
-        rows = m == 0u ? a.rows[0] : m == 1u ? a.rows[1] : a.rows[2];      // into the arguments)
+    // RANGED: the workgroup's matrix and rows [r0, r1)
+    uint32_t rm = 0, r0 = 0, r1 = 0;
+    if constexpr (RANGED) {
+        rm = (uint32_t)(blockIdx.x >= a.rwg_end[0]) + (uint32_t)(blockIdx.x >= a.rwg_end[1]);
+        const uint32_t start = rm == 0u ? 0u : rm == 1u ? a.rwg_end[0] : a.rwg_end[1];
+        const uint32_t rpw = rm == 0u ? a.rpw[0] : rm == 1u ? a.rpw[1] : a.rpw[2];
+        r0 = (blockIdx.x - start) * rpw;
+        r1 = min(r0 + rpw, rm == 0u ? a.rows[0] : rm == 1u ? a.rows[1] : a.rows[2]);
+    }
+    // tile j of the workgroup: matrix, first row and row bound (tiles past the
+    // last one repeat it and are not stored; RANGED: rows past r1 re-read row
+    // r1 - 1 and are not stored)
+    auto tile = [&](uint32_t j, uint32_t &m, uint32_t &base, uint32_t &bound) {
+        if constexpr (RANGED) {
+            m = rm;
+            base = r0 + 16u * j;
+            bound = r1;
+        } else {
+            const uint32_t gt = min(gt0 + j, total - 1u);
+            m = (gt >= a.tile_end[0]) + (a.nmat > 2u && gt >= a.tile_end[1]);
+            base = 16u * (gt - (m == 0u ? 0u : m == 1u ? a.tile_end[0] : a.tile_end[1]));  // (no dynamic
+            bound = m == 0u ? a.rows[0] : m == 1u ? a.rows[1] : a.rows[2];  // index into the arguments)
+        }
     };
     // every tile's matrix and this lane's three chunk offsets in it, computed
     // before the first DMA (argument reads inside the stream would wait for it)
@@ -669,13 +688,13 @@ __global__ __launch_bounds__(1024) void k_mvbr4(const MbArgs a) {
     uint32_t toff[T][3];
 #pragma unroll
     for (uint32_t j = 0; j < T; j++) {
-        uint32_t m, lt, rows;
-        tile(j, m, lt, rows);
+        uint32_t m, base, bound;
+        tile(j, m, base, bound);
         tw[j] = m == 0u ? a.w[0] : m == 1u ? a.w[1] : a.w[2];
 #pragma unroll
         for (uint32_t q = 0; q < 3u; q++) {
             const uint32_t c = min(64u * q + lane, 143u);  // chunk 9 n' + p of the tile
-            toff[j][q] = min(16u * lt + c / 9u, rows - 1u) * rb + 16u * (c % 9u);
+            toff[j][q] = min(base + c / 9u, bound - 1u) * rb + 16u * (c % 9u);
         }
     }
     auto issue = [&](auto ic) {
@@ -745,10 +764,10 @@ __global__ __launch_bounds__(1024) void k_mvbr4(const MbArgs a) {
             const uint32_t jj = q >> 7, l = (q >> 1) & 63u, tk = q & 1u;
             float sum = 0.f;
             for (uint32_t v = 0; v < 16u; v++) sum += red[(jj * 16u + v) * 128u + 2u * l + tk];
-            uint32_t m, lt, rows;
-            tile(j0 + jj, m, lt, rows);
-            const uint32_t row = 16u * lt + (l & 15u), t = 2u * (l >> 4) + tk;
-            const bool st = gt0 + j0 + jj < total && row < rows && t < a.batch;
+            uint32_t m, base, bound;
+            tile(j0 + jj, m, base, bound);
+            const uint32_t row = base + (l & 15u), t = 2u * (l >> 4) + tk;
+            const bool st = (RANGED || gt0 + j0 + jj < total) && row < bound && t < a.batch;
             if constexpr (EPI == E_QKV) {
                 // the RoPE partner (row ^ 1, same vector) is thread q ^ 2
                 const float other = __shfl_xor(sum, 2, 64);
@@ -779,20 +798,20 @@ __global__ __launch_bounds__(1024) void k_mvbr4(const MbArgs a) {
     });
 }
 
-template <uint32_t NB, uint32_t T, int EPI>
+template <uint32_t NB, uint32_t T, int EPI, bool RANGED = false>
 static hipError_t launch_mvbr4_t(const MbArgs &a, uint32_t wgs, hipStream_t s) {
     constexpr uint32_t R = NB * T < 3u ? NB * T : 3u;
     const size_t lds = Mvbr4Plan<NB, T, R>::lds();
     static bool granted = false;
     if (!granted) {
-        if (hipFuncSetAttribute((const void *)k_mvbr4<NB, T, R, EPI>,
+        if (hipFuncSetAttribute((const void *)k_mvbr4<NB, T, R, EPI, RANGED>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
             (void)hipGetLastError();
             return hipErrorNotSupported;
         }
         granted = true;
     }
-    k_mvbr4<NB, T, R, EPI><<<wgs, 1024, lds, s>>>(a);
+    k_mvbr4<NB, T, R, EPI, RANGED><<<wgs, 1024, lds, s>>>(a);
     return hipGetLastError();
 }
 
@@ -806,6 +825,29 @@ static hipError_t launch_mvbr4(const MbArgs &a, int epi, hipStream_t s) {
     for (uint32_t m = 0; m < a.nmat; m++)
         if (((uintptr_t)a.w[m] & 15u) || (uint64_t)a.rows[m] * nblk * 144u + 256u >= (1ull << 32))
             return hipErrorNotSupported;
+    // Q/K/V of rows of 17-32 blocks (70B: 640 tiles) where three tiles per
+    // workgroup leave CUs idle (214 workgroups): an even range of at most 48
+    // rows of one matrix per workgroup (at 70B 42 rows, 246 workgroups)
+    if (epi == E_QKV && nblk > 16u) {
+        uint32_t rows_all = 0;
+        bool even = true;
+        for (uint32_t m = 0; m < a.nmat; m++) {
+            rows_all += a.rows[m];
+            even = even && (a.rows[m] & 1u) == 0u;
+        }
+        // (ranges of 33-48 rows: the three tiles mostly hold the range's own rows)
+        for (uint32_t rpw = ((rows_all + cus - 1u) / cus + 1u) & ~1u; even && rpw > 32u && rpw <= 48u;
+             rpw += 2u) {
+            MbArgs r = a;
+            uint32_t wgs = 0;
+            for (uint32_t m = 0; m < 3u; m++) {
+                if (m < a.nmat) wgs += (a.rows[m] + rpw - 1u) / rpw;
+                r.rwg_end[m] = wgs;
+                r.rpw[m] = rpw;
+            }
+            if (wgs <= cus) return launch_mvbr4_t<2, 3, E_QKV, true>(r, wgs, s);
+        }
+    }
     const uint32_t per = (total + cus - 1u) / cus;
     const uint32_t T = per <= 1u ? 1u : per <= 2u ? 2u : per <= 3u ? 3u : per <= 6u ? 6u : 7u;
     const uint32_t wgs = (total + T - 1u) / T;
