@@ -144,6 +144,28 @@ def test_batch_7b_gate_shape(dev, host, oracle, mem, batch, rows):
         assert rel_l2(Y[b], oracle.linear(V.Q4_K, w, X[b], cols, rows)) <= LIN_TOL, b
 
 
+def test_batch_ranged_qkv_every_row(dev, host, oracle, mem):
+    """The 70B Q/K/V shape at batch 5 takes the ranged plan (an even range of
+    42 rows of one matrix per workgroup, 246 workgroups, the last range of
+    each matrix shorter): every row of every matrix against the oracle, per
+    vector, and entries past each matrix's rows untouched."""
+    shapes, cols, batch, pad = [8192, 1024, 1024], 8192, 5, 7
+    ws = [V.synth_matrix(host, V.Q4_K, r, cols, SEED, 160 + m) for m, r in enumerate(shapes)]
+    X = vectors(host, batch, cols, 170)
+    px = mem.up(X)
+    pws = [mem.up(w) for w in ws]
+    pys = [mem.up(np.full(batch * (r + pad), -3.0, np.float32)) for r in shapes]
+    dev.linear_batch_multi(V.Q4_K, pws, shapes, px, cols, pys, [r + pad for r in shapes], cols, batch)
+    for m, (w, r) in enumerate(zip(ws, shapes)):
+        Y = dev.download(pys[m], (batch, r + pad), np.float32)
+        assert np.all(Y[:, r:] == -3.0), m
+        for b in range(batch):
+            want = oracle.linear(V.Q4_K, w, X[b], cols, r, threads=16)
+            assert rel_l2(Y[b, :r], want) <= LIN_TOL, (m, b)
+            # a row of a wrong range would stand out even inside the L2 norm
+            assert np.max(np.abs(Y[b, :r] - want)) <= 1e-4 * (np.max(np.abs(want)) + 1.0), (m, b)
+
+
 @pytest.mark.parametrize("t,shapes,cols", [
     (V.Q4_K, [8192, 1024, 1024], 8192), (V.Q4_K, [4096, 1024, 1024], 4096),
     (V.Q4_K, [28672, 28672], 8192), (V.Q6_K, [4096, 1000, 13], 4096), (V.Q4_K, [37], 512)],

@@ -825,10 +825,10 @@ static hipError_t launch_mvbr4(const MbArgs &a, int epi, hipStream_t s) {
     for (uint32_t m = 0; m < a.nmat; m++)
         if (((uintptr_t)a.w[m] & 15u) || (uint64_t)a.rows[m] * nblk * 144u + 256u >= (1ull << 32))
             return hipErrorNotSupported;
-    // Q/K/V of rows of 17-32 blocks (70B: 640 tiles) where three tiles per
-    // workgroup leave CUs idle (214 workgroups): an even range of at most 48
+    // Rows of 17-32 blocks where three tiles per workgroup leave CUs idle
+    // (70B Q/K/V: 640 tiles, 214 workgroups): an even range of at most 48
     // rows of one matrix per workgroup (at 70B 42 rows, 246 workgroups)
-    if (epi == E_QKV && nblk > 16u) {
+    if (nblk > 16u) {
         uint32_t rows_all = 0;
         bool even = true;
         for (uint32_t m = 0; m < a.nmat; m++) {
@@ -845,7 +845,10 @@ static hipError_t launch_mvbr4(const MbArgs &a, int epi, hipStream_t s) {
                 r.rwg_end[m] = wgs;
                 r.rpw[m] = rpw;
             }
-            if (wgs <= cus) return launch_mvbr4_t<2, 3, E_QKV, true>(r, wgs, s);
+            if (wgs <= cus)
+                return epi == E_QKV   ? launch_mvbr4_t<2, 3, E_QKV, true>(r, wgs, s)
+                       : epi == E_ACC ? launch_mvbr4_t<2, 3, E_ACC, true>(r, wgs, s)
+                                      : launch_mvbr4_t<2, 3, E_STORE, true>(r, wgs, s);
         }
     }
     const uint32_t per = (total + cus - 1u) / cus;
