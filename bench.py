@@ -146,12 +146,7 @@ def cpu_baseline(host, weights, xs, max_seconds=20.0, beside=None):
         if t_total >= max_seconds * 0.5 or passes >= 8:
             break
     nbytes = passes * sum(algo_bytes(V.Q4_K, r, c) for _, r, c in LAYER_SET)
-    cpu = ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            cpu = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), "")
-    except OSError:
-        pass
+    cpu = host_cpu_model()
     # beside it: the oracle's row-parallel restatement on every host core
     # (bit-identical outputs to the single-threaded path, tested)
     orc_all = Oracle()
@@ -689,13 +684,25 @@ def bench_decode(dev, host, n_tokens, path="both", geo=GEO_7B, n_layers=32, ctx=
             **({"batch_decode": batched} if batched else {})}
 
 
+def host_cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            return next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), "")
+    except OSError:
+        return ""
+
+
 def decode_vs_checkers(host, toks, margins, n_oracle=4, ctx=2048):
-    """Checker leg of the config-4 decode (graph decoder, seed DECODE_SEED,
-    token 1 at position `ctx`): its tokens and top-1 minus top-2 margins
-    against the reference CPU backend's 128 (the fixture), and its first
-    `n_oracle` tokens against the oracle's forward pass, run here on the
-    host's cores over a fresh copy of the same synthetic model."""
-    from oracle_lib import Oracle
+    """Checker and CPU-baseline leg of the config-4 decode (graph decoder,
+    seed DECODE_SEED, token 1 at position `ctx`): its tokens and top-1 minus
+    top-2 margins against the reference CPU backend's 128 (the fixture), its
+    first `n_oracle` tokens against the oracle's forward pass, run here on the
+    host's cores over a fresh copy of the same synthetic model; and beside the
+    GPU rate, the same decode on the CPU: one full token of the reference's
+    own CPU backend (oracle/_ref, single-threaded as the reference is) driven
+    through its ops table by host/vbs_decode.c in the bridge's order, and the
+    oracle's forward pass on every host core (`cpu_baseline`)."""
+    from oracle_lib import REF_SO, Oracle
     out = {}
     if os.path.exists(DECODE_FIXTURE):
         fx = np.load(DECODE_FIXTURE)
@@ -708,6 +715,16 @@ def decode_vs_checkers(host, toks, margins, n_oracle=4, ctx=2048):
     model = V.SynthModel(host, n_layers=32, **GEO_7B, max_ctx=ctx + n_oracle + 1,
                          seed=DECODE_SEED)
     kc_p, vc_p = model.kv_prefill(host, ctx)
+    ref_leg = None
+    if os.path.exists(REF_SO):
+        ref = V.Backend(C.CDLL(REF_SO), "g_vbs_cpu_backend")
+        ref.init()
+        d = V.Decoder(host, ref, model)
+        d.load_kv(kc_p, vc_p, ctx)
+        t1 = time.perf_counter()
+        lg = d.step(1, ctx)
+        ref_leg = (time.perf_counter() - t1, int(np.argmax(lg)))
+        d.close()
     kvd = GEO_7B["n_kv_heads"] * GEO_7B["head_dim"]
     shape = (32, ctx + n_oracle + 1, kvd)
     kc, vc = np.zeros(shape, np.uint16), np.zeros(shape, np.uint16)
@@ -715,13 +732,35 @@ def decode_vs_checkers(host, toks, margins, n_oracle=4, ctx=2048):
     del kc_p, vc_p
     orc = Oracle()
     om = orc.model(model, kc, vc)
-    threads, tok, want = min(16, os.cpu_count() or 1), 1, []
+    threads, tok, want, t_fwd = min(16, os.cpu_count() or 1), 1, [], 0.0
     for i in range(n_oracle):
-        tok = int(np.argmax(orc.forward(om, tok, ctx + i, GEO_7B["vocab"], threads)))
+        t1 = time.perf_counter()
+        lg = orc.forward(om, tok, ctx + i, GEO_7B["vocab"], threads)
+        t_fwd += time.perf_counter() - t1
+        tok = int(np.argmax(lg))
         want.append(tok)
     out["oracle_tokens_compared"] = n_oracle
     out["oracle_agree"] = bool(np.array_equal(np.asarray(toks[:n_oracle]), want))
     out["oracle_s"] = round(time.perf_counter() - t0, 1)
+    cpu = host_cpu_model()
+    all_cores = {"tokens_per_s": round(n_oracle / t_fwd, 4), "unit": "tokens/s",
+                 "cores": threads, "kind": "port", "cpu": cpu,
+                 "sample": f"{n_oracle} greedy tokens from position {ctx} of the same model, "
+                           f"the oracle's forward pass row-parallel on {threads} threads "
+                           f"({t_fwd:.1f} s of forward passes; model build excluded)"}
+    if ref_leg is not None:
+        sec, ref_tok = ref_leg
+        out["cpu_baseline"] = {
+            "tokens_per_s": round(1.0 / sec, 5), "unit": "tokens/s", "cores": 1,
+            "kind": "reference", "cpu": cpu, "nproc": os.cpu_count(),
+            "first_token_equal": ref_tok == int(toks[0]),
+            "sample": f"1 full token (token 1 at position {ctx}, 32 layers, lm_head) of the "
+                      f"config-4 model through the reference CPU backend's ops table "
+                      f"(oracle/_ref/libvbs_ref.so), single thread, driven by "
+                      f"host/vbs_decode.c in the bridge's order: {sec:.1f} s",
+            "all_cores": all_cores}
+    else:
+        out["cpu_baseline"] = all_cores
     return out
 
 

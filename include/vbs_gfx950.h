@@ -114,9 +114,10 @@ int vbs_gfx950_attention(const float *q, const uint16_t *kc, const uint16_t *vc,
  * tight serving loops, harnesses that forbid hipMalloc). Same arguments and
  * result as vbs_gfx950_attention; the per-chunk partial results live in a
  * fixed 8 MiB device array of the library instead of the growable scratch, so
- * calls whose partials exceed it (nqh x max(ceil(1024 / nkh), ceil(seq_len /
- * 64)) x (head_dim + 2) x 4 bytes; e.g. 70B shapes up to seq_len 16128) fail
- * with a reason and launch nothing. Every call on the device shares that
+ * calls whose partials exceed it (nqh x max(ceil(640 / nkh), ceil(seq_len /
+ * 64)) x (head_dim + 2) x 4 bytes, 640 being the workgroup target of the
+ * sequence split, kMfmaTargetWgs in csrc/vbs_attn_common.h; e.g. 70B shapes
+ * up to seq_len 16128) fail with a reason and launch nothing. Every call on the device shares that
  * array: calls that overlap on the device race (the library's own calls are
  * ordered on its one stream and never overlap). */
 int vbs_gfx950_attention_noalloc(const float *q, const uint16_t *kc, const uint16_t *vc,
@@ -160,10 +161,11 @@ int vbs_gfx950_linear_batch_multi(int type, uint32_t n_mat, const void *const *w
                                   float *const *y, const uint32_t *y_stride, uint32_t cols,
                                   uint32_t batch);
 
-/* XOR checksum of a device region, as partial words: partials[i] is the XOR
- * of the 32-bit words of one span of the region (consecutive spans of up to
- * 112 KB), for i < vbs_gfx950_checksum_partials(bytes); their XOR is the
- * region's. p is 16-byte aligned and bytes a multiple of 16; partials is
+/* XOR checksum of a device region, as partial words, for
+ * i < vbs_gfx950_checksum_partials(bytes): the region is cut into consecutive
+ * spans of up to 112 KB, one per workgroup of 16 waves, and partials[16 w + v]
+ * is the XOR of the 32-bit words of wave v's share of span w (its interleaved
+ * 1 KB runs v, v + 16, v + 32, ... of the span). Their XOR is the region's. p is 16-byte aligned and bytes a multiple of 16; partials is
  * device memory.
  * Verifies uploads (the host XORs the same words) and, reading every byte
  * exactly once and nothing else, it is the read floor beside the matvec
@@ -243,6 +245,12 @@ int vbs_gfx950_bdecoder_greedy(void *handle, const uint32_t *tokens0, const uint
 /* The same with every kernel launched directly (for kernel tracers). */
 int vbs_gfx950_bdecoder_greedy_eager(void *handle, const uint32_t *tokens0, const uint32_t *pos0,
                                      uint32_t n, uint32_t *tokens, float *margins);
+/* One step of every sequence with the given tokens[b] at pos[b] (teacher
+ * forcing: the graph of vbs_gfx950_bdecoder_greedy, replayed once); the caches
+ * at pos[b] are written as by a greedy step, and logits (batch x vocab floats,
+ * host, sequence b at b * vocab) may be NULL. */
+int vbs_gfx950_bdecoder_step(void *handle, const uint32_t *tokens, const uint32_t *pos,
+                             float *logits);
 int vbs_gfx950_bdecoder_destroy(void *handle);
 
 /* ---- CPU hot-kernel table on the device (parity adapter) --------------------

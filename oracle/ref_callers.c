@@ -61,3 +61,151 @@ const void *vbs_callers_tensor_data(const vbs_gguf_model_t *m, const vbs_tensor_
 int vbs_callers_block_tier(const vbs_fabric_t *f, size_t i) {
     return i < f->n_blocks ? (int)f->blocks[i]->current_tier : -1;
 }
+
+/* ---- The specializer's emitted module (src/vbs_specializer.c) -------------
+ *
+ * vbs_engine_compile (src/vbs_engine.c:174-223) turns the model into a C
+ * module and runs it: vbs_graph_compile -> vbs_planner_build ->
+ * vbs_specializer_emit_source -> vbs_specializer_compile (the system C
+ * compiler) -> vbs_specializer_load -> verum_init(fabric, backend). The
+ * module's forward pass then calls the bridge functions above through the
+ * process's global symbol scope, so this library must be loaded with
+ * RTLD_GLOBAL (one instance per process) before a module is loaded.
+ *
+ * Two pieces of the engine that cannot be built here are restated:
+ *   - the layer-energy table vbs_engine.c:416-420 owns, which the emitter
+ *     reads (vbs_specializer.c:259-275): every layer alive, as
+ *     vbs_engine_reset_energy leaves it;
+ *   - the model profile of vbs_profiler_scan_model (src/vbs_profiler.c:
+ *     290-355): vbs_profiler.c itself also probes the CUDA and Vulkan
+ *     backends, whose sources embed prebuilt kernel images this build does
+ *     not use, so it does not link here.
+ */
+#include "vbs_graph.h"
+#include "vbs_planner.h"
+#include "vbs_specializer.h"
+#include "vbs_engine.h"
+
+float g_vbs_layer_energy[VBS_MAX_LAYERS];
+
+/* The fields vbs_profiler_scan_model fills, from the same metadata keys and
+ * name rules, with the KV capacity the engine stores after sizing its caches
+ * (src/vbs_engine.c:138-139). NULL if an essential dimension is missing. */
+vbs_model_profile_t *vbs_callers_model_profile(const vbs_gguf_model_t *m, uint32_t kv_capacity) {
+    vbs_model_profile_t *mp = calloc(1, sizeof *mp);
+    if (!mp) return NULL;
+    mp->model = m;
+    mp->n_tensor_profiles = m->n_tensors;
+    mp->tensor_profiles = calloc(m->n_tensors ? m->n_tensors : 1, sizeof *mp->tensor_profiles);
+    for (size_t i = 0; i < m->n_tensors; i++) {
+        const vbs_tensor_t *t = &m->tensors[i];
+        vbs_tensor_profile_t *tp = &mp->tensor_profiles[i];
+        int hot = strstr(t->name, "token_embd") || strstr(t->name, "output") || strstr(t->name, "norm");
+        int warm = !hot && (strstr(t->name, "attn") || strstr(t->name, ".q.") ||
+                            strstr(t->name, ".k.") || strstr(t->name, ".v."));
+        tp->tensor = t;
+        tp->bytes = t->byte_length;
+        tp->is_hot_path = hot;
+        tp->access_frequency = hot ? 100 : warm ? 50 : 10;
+        tp->estimated_compute_cost = 2.0 * (double)t->byte_length;
+        mp->total_model_bytes += t->byte_length;
+        if (hot) mp->hot_working_set_bytes += t->byte_length;
+        else if (warm) mp->warm_working_set_bytes += t->byte_length;
+        else mp->cold_working_set_bytes += t->byte_length;
+        if (hot && (strstr(t->name, "token_embd.weight") || strstr(t->name, "output.weight")))
+            mp->vocab_size = (uint32_t)t->rows;
+    }
+    vbs_gguf_get_uint32_metadata(m, "llama.block_count", &mp->n_layers);
+    vbs_gguf_get_uint32_metadata(m, "llama.attention.head_count", &mp->n_heads);
+    vbs_gguf_get_uint32_metadata(m, "llama.attention.head_count_kv", &mp->n_kv_heads);
+    vbs_gguf_get_uint32_metadata(m, "llama.embedding_length", &mp->embedding_dim);
+    vbs_gguf_get_uint32_metadata(m, "llama.context_length", &mp->context_length);
+    if (mp->n_heads && mp->embedding_dim) mp->head_dim = mp->embedding_dim / mp->n_heads;
+    mp->rope_theta = 10000.0f;
+    mp->rms_eps = 1e-5f;
+    vbs_gguf_get_float32_metadata(m, "llama.rope.freq_base", &mp->rope_theta);
+    vbs_gguf_get_float32_metadata(m, "llama.attention.layer_norm_rms_epsilon", &mp->rms_eps);
+    if (!mp->n_layers || !mp->n_heads || !mp->n_kv_heads || !mp->embedding_dim ||
+        !mp->vocab_size || !mp->head_dim || !mp->context_length) {
+        free(mp->tensor_profiles);
+        free(mp);
+        return NULL;
+    }
+    mp->kv_ctx_capacity = kv_capacity;
+    return mp;
+}
+
+typedef struct {
+    vbs_graph_t *graph;
+    vbs_execution_plan_t *plan;
+    vbs_model_profile_t *mp;
+    vbs_specialized_binary_t *bin;
+} vbs_callers_jit_t;
+
+void vbs_callers_jit_free(vbs_callers_jit_t *j) {
+    if (!j) return;
+    if (j->bin) vbs_specializer_free(j->bin);
+    if (j->plan) vbs_planner_free(j->plan);
+    if (j->graph) vbs_graph_free(j->graph);
+    if (j->mp) { free(j->mp->tensor_profiles); free(j->mp); }
+    free(j);
+}
+
+/* vbs_engine_compile's steps in its order, without the module cache lookup
+ * (every call emits and compiles afresh into `dir`). The system profile is
+ * vbs_callers_profile's; `fabric` already holds every tensor, registered in
+ * file order as vbs_engine_create does (src/vbs_engine.c:51-56), and the
+ * bridge is bound. The emitted source is kept at dir/verum_<hash>.c. */
+vbs_callers_jit_t *vbs_callers_specialize(const vbs_gguf_model_t *m, const vbs_system_profile_t *sys,
+                                          vbs_fabric_t *fabric, const vbs_backend_ops_t *backend,
+                                          uint32_t kv_capacity, const char *dir,
+                                          char *err, size_t err_cap) {
+    vbs_callers_jit_t *j = calloc(1, sizeof *j);
+    char hash[65] = {0}, src[1024], bin[1024];
+    double compile_sec = 0;
+    for (size_t i = 0; i < VBS_MAX_LAYERS; i++) g_vbs_layer_energy[i] = 1.0f;
+    if (!j) { snprintf(err, err_cap, "out of memory"); return NULL; }
+    if (!(j->mp = vbs_callers_model_profile(m, kv_capacity))) {
+        snprintf(err, err_cap, "model profile refused");
+        goto fail;
+    }
+    if (!(j->graph = vbs_graph_compile(m, err, err_cap))) goto fail;
+    if (!(j->plan = vbs_planner_build(j->graph, sys, j->mp, fabric))) {
+        snprintf(err, err_cap, "Planner failed to generate execution plan");
+        goto fail;
+    }
+    vbs_specializer_compute_hash(j->graph, sys, j->plan, hash, sizeof hash);
+    snprintf(src, sizeof src, "%s/verum_%s.c", dir, hash);
+    snprintf(bin, sizeof bin, "%s/verum_%s%s", dir, hash, VBS_DYLIB_EXT);
+    if (!vbs_specializer_emit_source(j->graph, sys, j->plan, j->mp, src)) {
+        snprintf(err, err_cap, "Failed emitting bespoke C source for specialization");
+        goto fail;
+    }
+    if (!vbs_specializer_compile(src, bin, sys, &compile_sec)) {
+        snprintf(err, err_cap, "Specializer compilation failed");
+        goto fail;
+    }
+    if (!(j->bin = vbs_specializer_load(bin, hash))) {
+        snprintf(err, err_cap, "Failed loading specialized binary module: %s", vbs_dlerror());
+        goto fail;
+    }
+    j->bin->compile_time_sec = compile_sec;
+    j->bin->n_kernels_emitted = j->plan->n_plans;
+    j->bin->init_fn(fabric, (void *)backend);
+    return j;
+fail:
+    vbs_callers_jit_free(j);
+    return NULL;
+}
+
+/* vbs_engine_forward (src/vbs_engine.c:225-229): the module's verum_forward. */
+void vbs_callers_jit_forward(vbs_callers_jit_t *j, const uint32_t *tokens, size_t n, float *logits) {
+    j->bin->forward_fn(tokens, n, logits);
+}
+
+void vbs_callers_jit_reset(vbs_callers_jit_t *j) {
+    if (j->bin->reset_cache_fn) j->bin->reset_cache_fn();
+}
+
+const char *vbs_callers_jit_path(const vbs_callers_jit_t *j) { return j->bin->binary_path; }
+size_t vbs_callers_jit_n_plans(const vbs_callers_jit_t *j) { return j->plan->n_plans; }

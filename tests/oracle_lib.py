@@ -17,6 +17,7 @@ REF_SO = os.path.join(ROOT, "oracle", "_ref", "libvbs_ref.so")
 REF_HOT_SO = os.path.join(ROOT, "oracle", "_ref", "libvbs_hotpath_ref.so")
 REF_CPU_SO = os.path.join(ROOT, "oracle", "_ref", "libvbs_cpu_ref.so")
 REF_CALLERS_SO = os.path.join(ROOT, "oracle", "_ref", "libvbs_callers_ref.so")
+REF_CALLERS_Q4K_SO = os.path.join(ROOT, "oracle", "_ref", "libvbs_callers_q4k_ref.so")
 
 _P, _U32, _I, _F = C.c_void_p, C.c_uint32, C.c_int, C.c_float
 F16FN = C.CFUNCTYPE(C.c_uint16, C.c_float)

@@ -30,14 +30,16 @@ TYPE_SUFFIX = {V.F32: "f32", V.F16: "f16", V.Q4_0: "q4_0", V.Q4_1: "q4_1", V.Q8_
 _VP, _SZ, _U32, _F32 = C.c_void_p, C.c_size_t, C.c_uint32, C.c_float
 
 
-def load_callers(tag):
+def load_callers(tag, src=REF_CALLERS_SO, global_scope=False):
     """A private copy of the callers library: the bridge keeps its runtime
     and pipeline caches in file-scope statics, so each backend under test
-    gets its own instance."""
+    gets its own instance. `global_scope` loads it RTLD_GLOBAL, which a
+    specializer module needs to find the bridge; only one such instance may
+    live in a process (a module binds to the first one loaded)."""
     d = tempfile.mkdtemp(prefix="vbs_callers_")
     path = os.path.join(d, f"libvbs_callers_{tag}.so")
-    shutil.copy(REF_CALLERS_SO, path)
-    L = C.CDLL(path)
+    shutil.copy(src, path)
+    L = C.CDLL(path, mode=(os.RTLD_GLOBAL | os.RTLD_NOW) if global_scope else C.DEFAULT_MODE)
     sig = {
         "vbs_gguf_open": (_VP, [C.c_char_p, C.c_char_p, _SZ]),
         "vbs_gguf_close": (None, [_VP]),
@@ -72,6 +74,12 @@ def load_callers(tag):
         "vbs_slice_executor_create": (_VP, [_VP, _VP, _VP, _SZ, C.c_char_p, _SZ]),
         "vbs_slice_executor_free": (None, [_VP]),
         "vbs_slice_executor_run_linear": (C.c_bool, [_VP, _VP, _VP, _VP, C.c_char_p, _SZ]),
+        "vbs_callers_specialize": (_VP, [_VP, _VP, _VP, _VP, _U32, C.c_char_p, C.c_char_p, _SZ]),
+        "vbs_callers_jit_forward": (None, [_VP, _VP, _SZ, _VP]),
+        "vbs_callers_jit_reset": (None, [_VP]),
+        "vbs_callers_jit_free": (None, [_VP]),
+        "vbs_callers_jit_path": (C.c_char_p, [_VP]),
+        "vbs_callers_jit_n_plans": (_SZ, [_VP]),
     }
     for suffix in TYPE_SUFFIX.values():
         sig[f"vbs_gpu_dispatch_vram_{suffix}"] = (None, [_VP, _VP, _VP, _SZ, _SZ])
@@ -138,9 +146,9 @@ class RefEngine:
         self.eps = m.f32("llama.attention.layer_norm_rms_epsilon")
         self.kvd = self.nkv * self.hd
         dev = self.dev = backend.device()
-        ops = C.addressof(backend.ops)
-        self.fabric = L.vbs_fabric_create(L.vbs_callers_profile(C.cast(dev, _VP), vram_bytes), ops,
-                                          16, 0, None)
+        ops = self.ops = C.addressof(backend.ops)
+        self.sys = L.vbs_callers_profile(C.cast(dev, _VP), vram_bytes)
+        self.fabric = L.vbs_fabric_create(self.sys, ops, 16, 0, None)
         for t in m.tensors:  # src/vbs_engine.c:51-56
             L.vbs_fabric_register_tensor(self.fabric, t, L.vbs_callers_tensor_data(m.ptr, t), tier,
                                          C.cast(dev, _VP))
@@ -206,6 +214,18 @@ class RefEngine:
         L.vbs_gpu_readback_logits(L.vbs_gpu_get_logits(), out.ctypes.data, self.vocab)
         return out
 
+    def specialize(self, workdir):
+        """vbs_engine_compile over this set-up: the reference's graph, planner
+        and specializer emit the model's C module into `workdir`, compile it
+        with the system compiler and bind it (verum_init). Needs the library
+        loaded with global_scope=True."""
+        err = C.create_string_buffer(1024)
+        jit = self.L.vbs_callers_specialize(self.model.ptr, self.sys, self.fabric, self.ops,
+                                            self.kv_cap, workdir.encode(), err, 1024)
+        if not jit:
+            raise RuntimeError(f"specializer: {err.value.decode()}")
+        return Module(self.L, jit, self.vocab)
+
     def close(self):
         for b in self.bufs + self.scratch:
             self.be.ops.free_buffer(b)
@@ -238,3 +258,28 @@ class SliceExecutor:
         if self.ptr:
             self.L.vbs_slice_executor_free(self.ptr)
             self.ptr = None
+
+
+class Module:
+    """A specializer-emitted module bound to a RefEngine's set-up."""
+
+    def __init__(self, L, jit, vocab):
+        self.L, self.jit, self.vocab = L, jit, vocab
+        self.path = L.vbs_callers_jit_path(jit).decode()
+        self.n_plans = int(L.vbs_callers_jit_n_plans(jit))
+
+    def forward(self, tokens):
+        """verum_forward(tokens): one token step per token at the module's
+        running position, then the logits read back."""
+        t = np.ascontiguousarray(tokens, np.uint32)
+        out = np.empty(self.vocab, np.float32)
+        self.L.vbs_callers_jit_forward(self.jit, t.ctypes.data, t.size, out.ctypes.data)
+        return out
+
+    def reset(self):
+        self.L.vbs_callers_jit_reset(self.jit)
+
+    def close(self):
+        if self.jit:
+            self.L.vbs_callers_jit_free(self.jit)
+            self.jit = None

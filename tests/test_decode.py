@@ -251,6 +251,107 @@ def test_gpu_7b_teacher_forced_logits_vs_oracle(backend, dev, host, model_7b):
           f"oracle margins min {min(margins):.4f} median {float(np.median(margins)):.4f}")
 
 
+def f16_rows_close(got, want):
+    """f16 rows equal to within one unit in the last place (the same f32
+    value rounded after a matvec that differs from the oracle's by ~1e-7)."""
+    a = got.view(np.float16).astype(np.float64)
+    b = want.view(np.float16).astype(np.float64)
+    return bool(np.all(np.abs(a - b) <= 2.0 ** -10 * np.maximum(np.abs(a), np.abs(b)) + 2.0 ** -24))
+
+
+@pytest.mark.gpu
+def test_gpu_70b_graph_decoder_teacher_forced_logits_vs_oracle(backend, dev, host):
+    """The 70B-width graph decoder (ranged fused RMSNorm + Q/K/V + RoPE + KV
+    store over 10240 rows, two-tile O, k_mvr down over 28672-wide rows, the
+    split attention over 8192 positions) against the oracle at the logit
+    level: 2 of the 80 layers, KV prefilled N(0,1) to 8192, 8 positions fed a
+    fixed pseudo-random token stream. Every step's logits within 1e-4
+    relative L2 of the oracle's with the same first-maximum argmax and
+    top-2 margin, and the K/V rows written at every position within one f16
+    ulp of the oracle's."""
+    ctx, n = 8192, 8
+    model = V.SynthModel(host, n_layers=2, **GEO_70B, max_ctx=ctx + n + 1, seed=70)
+    kc_p, vc_p = model.kv_prefill(host, ctx)
+    stream = np.random.default_rng(8192).integers(0, model.cfg["vocab"], n).tolist()
+    d = V.Decoder(host, backend, model)
+    d.load_kv(kc_p, vc_p, ctx)
+    g = V.GraphDecoder(dev, d, max_steps=4)
+    kc, vc = full_cache(model, kc_p, vc_p, ctx)
+    del kc_p, vc_p
+    oracle = Oracle()
+    om = oracle.model(model, kc, vc)
+    try:
+        for i, tok in enumerate(stream):
+            got = g.step(tok, ctx + i)
+            want = oracle.forward(om, tok, ctx + i, model.cfg["vocab"], 16)
+            err, m_want, m_got = rel_l2(got, want), top2_margin(want), top2_margin(got)
+            print(f"70B position {ctx + i}: token {tok} rel L2 {err:.2e} margin {m_want:.4f}",
+                  flush=True)
+            assert err <= 1e-4, (i, err)
+            assert int(np.argmax(got)) == int(np.argmax(want)), (i, m_want)
+            assert abs(m_got - m_want) <= 1e-3 + 1e-4 * abs(m_want), (i, m_got, m_want)
+        gk, gv = (a.reshape(2, ctx + n, -1) for a in d.read_kv(ctx + n))
+        for L in range(2):
+            for i in range(n):
+                assert f16_rows_close(gk[L, ctx + i], kc[L, ctx + i]), ("k", L, i)
+                assert f16_rows_close(gv[L, ctx + i], vc[L, ctx + i]), ("v", L, i)
+    finally:
+        g.close()
+        d.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("geo,n_layers,ctx", [(GEO_70B, 1, 8192), (GEO_7B, 2, 2048)],
+                         ids=["70b_1layer_ranged", "7b_2layers"])
+def test_gpu_batch_decoder_teacher_forced_logits_vs_oracle(host, backend, dev, geo, n_layers, ctx):
+    """The batch-8 decoder at the logit level (its fused launches: k_mvbr4's
+    Q/K/V epilogue with RoPE and the f16 K/V stores at each sequence's own
+    position -- the ranged 42-row plan at the 70B width --,
+    k_attn_merge_prep writing O's prepared input, the batched down
+    projection with the residual add): 8 sequences at 8 different positions,
+    each fed its own pseudo-random tokens for 4 steps (teacher forcing).
+    Every sequence's logits at every step within 1e-4 relative L2 of the
+    oracle's for that sequence alone, same first-maximum argmax and top-2
+    margin, and every K/V row it wrote within one f16 ulp of the oracle's."""
+    batch, n_tok = 8, 4
+    model = V.SynthModel(host, n_layers=n_layers, **geo, max_ctx=ctx + n_tok + 1, seed=88)
+    c = model.cfg
+    kvd = c["n_kv_heads"] * c["head_dim"]
+    pos0 = [ctx - 5 * b for b in range(batch)]
+    rng = np.random.default_rng(4 * ctx + n_layers)
+    streams = rng.integers(0, c["vocab"], (n_tok, batch))
+    d = V.Decoder(host, backend, model)
+    bd = V.BatchDecoder(dev, d, batch, max_steps=n_tok)
+    oracle, caches, oms = Oracle(), [], []
+    for b in range(batch):
+        n = n_layers * pos0[b] * kvd
+        kc_p = V.synth_normal_f16(host, n, 900 + b, 10)
+        vc_p = V.synth_normal_f16(host, n, 900 + b, 11)
+        bd.load_kv(b, kc_p, vc_p, pos0[b])
+        caches.append(full_cache(model, kc_p, vc_p, pos0[b]))
+        oms.append(oracle.model(model, *caches[-1]))
+    try:
+        for i in range(n_tok):
+            pos = [p + i for p in pos0]
+            got = bd.step(streams[i], pos)
+            for b in range(batch):
+                want = oracle.forward(oms[b], int(streams[i, b]), pos[b], c["vocab"], 16)
+                err, m_want = rel_l2(got[b], want), top2_margin(want)
+                m_got = top2_margin(got[b])
+                print(f"step {i} seq {b} pos {pos[b]}: rel L2 {err:.2e} margin {m_want:.4f}",
+                      flush=True)
+                assert err <= 1e-4, (i, b, err)
+                assert int(np.argmax(got[b])) == int(np.argmax(want)), (i, b, m_want)
+                assert abs(m_got - m_want) <= 1e-3 + 1e-4 * abs(m_want), (i, b, m_got, m_want)
+                for L in range(n_layers):
+                    k_row, v_row = bd.read_kv(b, L, pos[b])
+                    assert f16_rows_close(k_row, caches[b][0][L, pos[b]]), ("k", i, b, L)
+                    assert f16_rows_close(v_row, caches[b][1][L, pos[b]]), ("v", i, b, L)
+    finally:
+        bd.close()
+        d.close()
+
+
 @pytest.mark.gpu
 def test_gpu_graph_decoder_equals_dispatch_path(host, backend, dev, tiny):
     """Logits and KV stores of graph replays equal the per-dispatch driver's."""

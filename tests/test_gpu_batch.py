@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 import vbs_gfx950 as V
-from test_gpu_kernels import LIN_TOL, SEED, Mem, mem, rel_l2, synth_x  # noqa: F401 (mem: fixture)
+from test_gpu_kernels import LIN_TOL, SEED, Mem, lin_err, mem, rel_l2, synth_x  # noqa: F401 (mem: fixture)
 
 pytestmark = pytest.mark.gpu
 
@@ -46,7 +46,7 @@ def test_batch_parity(dev, host, oracle, mem, t, batch, rows, cols):
     X = vectors(host, batch, cols, 80)
     Y = run_batch(dev, mem, t, w, X, rows, cols)
     for b in range(batch):
-        assert rel_l2(Y[b], oracle.linear(t, w, X[b], cols, rows)) <= LIN_TOL, b
+        assert lin_err(Y[b], oracle.linear(t, w, X[b], cols, rows)) <= LIN_TOL, b
 
 
 @pytest.mark.parametrize("t", KQ, ids=lambda t: V.TYPE_NAMES[t])
@@ -58,7 +58,7 @@ def test_batch_strides(dev, host, oracle, mem, t):
     Y = run_batch(dev, mem, t, w, X, rows, cols, xs=cols + 40, ys=rows + 13)
     assert np.all(Y[:, rows:] == -3.0)
     for b in range(batch):
-        assert rel_l2(Y[b, :rows], oracle.linear(t, w, X[b], cols, rows)) <= LIN_TOL
+        assert lin_err(Y[b, :rows], oracle.linear(t, w, X[b], cols, rows)) <= LIN_TOL
 
 
 @pytest.mark.parametrize("t", KQ, ids=lambda t: V.TYPE_NAMES[t])
@@ -82,7 +82,7 @@ def test_batch_activation_edge_cases(dev, host, oracle, mem, t):
     for b in range(1, 8):
         want = oracle.linear(t, w, X[b], cols, rows)
         assert np.all(np.isfinite(Y[b])), b
-        assert rel_l2(Y[b], want) <= LIN_TOL, b
+        assert lin_err(Y[b], want) <= LIN_TOL, b
 
 
 @pytest.mark.parametrize("t", KQ, ids=lambda t: V.TYPE_NAMES[t])
@@ -97,7 +97,7 @@ def test_batch_non_finite_vector(dev, host, oracle, mem, t):
     Y = run_batch(dev, mem, t, w, X, rows, cols)
     assert np.all(np.isnan(Y[1])) and np.all(np.isnan(Y[2]))
     for b in (0, 3):
-        assert rel_l2(Y[b], oracle.linear(t, w, X[b], cols, rows)) <= LIN_TOL
+        assert lin_err(Y[b], oracle.linear(t, w, X[b], cols, rows)) <= LIN_TOL
 
 
 @pytest.mark.parametrize("t,rows,cols", [(V.Q4_K, 28672, 8192), (V.Q6_K, 8192, 28672),
@@ -113,7 +113,7 @@ def test_batch_70b_shapes(dev, host, oracle, mem, t, rows, cols):
     for lo in (0, rows - k):
         ws = np.ascontiguousarray(w[lo:lo + k])
         for b in range(8):
-            assert rel_l2(Y[b, lo:lo + k], oracle.linear(t, ws, X[b], cols, k)) <= LIN_TOL, (lo, b)
+            assert lin_err(Y[b, lo:lo + k], oracle.linear(t, ws, X[b], cols, k)) <= LIN_TOL, (lo, b)
 
 
 @pytest.mark.parametrize("rows,cols", [(4096, 11008), (3000, 8448), (4100, 28672), (5000, 25088)])
@@ -127,7 +127,7 @@ def test_batch_q6k_ring_shapes(dev, host, oracle, mem, rows, cols, batch):
     X = vectors(host, batch, cols, 130)
     Y = run_batch(dev, mem, V.Q6_K, w, X, rows, cols)
     for b in range(batch):
-        assert rel_l2(Y[b], oracle.linear(V.Q6_K, w, X[b], cols, rows, threads=16)) <= LIN_TOL, b
+        assert lin_err(Y[b], oracle.linear(V.Q6_K, w, X[b], cols, rows, threads=16)) <= LIN_TOL, b
 
 
 @pytest.mark.parametrize("rows", [11008, 22016])
@@ -141,7 +141,7 @@ def test_batch_7b_gate_shape(dev, host, oracle, mem, batch, rows):
     X = vectors(host, batch, cols, 130)
     Y = run_batch(dev, mem, V.Q4_K, w, X, rows, cols)
     for b in range(batch):
-        assert rel_l2(Y[b], oracle.linear(V.Q4_K, w, X[b], cols, rows)) <= LIN_TOL, b
+        assert lin_err(Y[b], oracle.linear(V.Q4_K, w, X[b], cols, rows)) <= LIN_TOL, b
 
 
 def test_batch_ranged_qkv_every_row(dev, host, oracle, mem):
@@ -161,7 +161,7 @@ def test_batch_ranged_qkv_every_row(dev, host, oracle, mem):
         assert np.all(Y[:, r:] == -3.0), m
         for b in range(batch):
             want = oracle.linear(V.Q4_K, w, X[b], cols, r, threads=16)
-            assert rel_l2(Y[b, :r], want) <= LIN_TOL, (m, b)
+            assert lin_err(Y[b, :r], want) <= LIN_TOL, (m, b)
             # a row of a wrong range would stand out even inside the L2 norm
             assert np.max(np.abs(Y[b, :r] - want)) <= 1e-4 * (np.max(np.abs(want)) + 1.0), (m, b)
 
@@ -194,7 +194,7 @@ def test_batch_multi_matrix_launch(dev, host, oracle, mem, t, shapes, cols, batc
             wsl = np.ascontiguousarray(w[lo:hi])
             for b in range(batch):
                 want = oracle.linear(t, wsl, X[b], cols, hi - lo)
-                assert rel_l2(Y[b, lo:hi], want) <= LIN_TOL, (m, lo, b)
+                assert lin_err(Y[b, lo:hi], want) <= LIN_TOL, (m, lo, b)
 
 
 def test_scratch_growth_keeps_captured_graphs(dev, host, oracle, mem):
@@ -235,7 +235,7 @@ def test_scratch_growth_keeps_captured_graphs(dev, host, oracle, mem):
             hip.launch(graph, stream)
             Y = dev.download(py, (batch, rows), np.float32)
             for b in range(batch):
-                assert rel_l2(Y[b], want[b]) <= LIN_TOL, (rep, b)
+                assert lin_err(Y[b], want[b]) <= LIN_TOL, (rep, b)
     finally:
         hip.destroy(graph)
     rc = []
@@ -245,4 +245,4 @@ def test_scratch_growth_keeps_captured_graphs(dev, host, oracle, mem):
     # the stream works on after the refused call
     dev.linear_batch(t, pw, px, cols, py, rows, cols, rows, batch)
     Y = dev.download(py, (batch, rows), np.float32)
-    assert rel_l2(Y[0], want[0]) <= LIN_TOL
+    assert lin_err(Y[0], want[0]) <= LIN_TOL

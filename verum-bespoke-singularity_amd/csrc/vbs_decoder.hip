@@ -805,7 +805,7 @@ int vbs_gfx950_bdecoder_create(const vbs_gfx950_model_t *m, uint32_t batch, uint
 }
 
 static int bdecoder_run(void *handle, const uint32_t *tokens0, const uint32_t *pos0, uint32_t n,
-                        uint32_t *tokens, float *margins, bool eager) {
+                        uint32_t *tokens, float *margins, bool eager, float *logits = nullptr) {
     if (!rt_ready()) return 0;
     BDecoder *d = (BDecoder *)handle;
     if (!d || !tokens0 || !pos0 || !tokens) return rt_fail("bdecoder_greedy: null argument");
@@ -839,6 +839,11 @@ static int bdecoder_run(void *handle, const uint32_t *tokens0, const uint32_t *p
         !rt_hip_ok(hipMemcpyAsync(margins, d->margins, (size_t)n * B * 4, hipMemcpyDeviceToHost, s),
                    "bdecoder_greedy: margins"))
         return 0;
+    if (logits &&
+        !rt_hip_ok(hipMemcpyAsync(logits, d->logits, (size_t)B * d->m.vocab * 4, hipMemcpyDeviceToHost,
+                                  s),
+                   "bdecoder_step: logits"))
+        return 0;
     return rt_hip_ok(hipStreamSynchronize(s), "bdecoder_greedy");
 }
 
@@ -850,6 +855,14 @@ int vbs_gfx950_bdecoder_greedy(void *handle, const uint32_t *tokens0, const uint
 int vbs_gfx950_bdecoder_greedy_eager(void *handle, const uint32_t *tokens0, const uint32_t *pos0,
                                      uint32_t n, uint32_t *tokens, float *margins) {
     return bdecoder_run(handle, tokens0, pos0, n, tokens, margins, true);
+}
+
+int vbs_gfx950_bdecoder_step(void *handle, const uint32_t *tokens, const uint32_t *pos,
+                             float *logits) {
+    BDecoder *d = (BDecoder *)handle;
+    if (!d) return rt_fail("bdecoder_step: null argument");
+    std::vector<uint32_t> next(d->batch);
+    return bdecoder_run(handle, tokens, pos, 1, next.data(), nullptr, false, logits);
 }
 
 int vbs_gfx950_bdecoder_destroy(void *handle) {

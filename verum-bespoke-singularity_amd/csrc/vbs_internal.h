@@ -154,7 +154,9 @@ hipError_t launch_attention_batch(const float *q, const uint16_t *kc, const uint
 hipError_t launch_silu_mul(const float *g, const float *u, float *out, uint32_t n,
                            hipStream_t s);
 // XOR of the 32-bit words of p[0, bytes) (bytes a multiple of 16, p 16-byte
-// aligned), one partial word per workgroup: checksum_partials(bytes) of them.
+// aligned) as checksum_partials(bytes) partial words: 16 per workgroup, one per
+// wave, each the XOR of that wave's interleaved 1 KB runs of the workgroup's
+// span.
 uint32_t checksum_partials(uint64_t bytes);
 hipError_t launch_checksum(const uint8_t *p, uint64_t bytes, uint32_t *partials, hipStream_t s);
 hipError_t launch_add(const float *a, const float *b, float *out, uint32_t n, hipStream_t s);

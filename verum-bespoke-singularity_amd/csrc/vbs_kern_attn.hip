@@ -9,8 +9,9 @@
 // q head of that kv head, the chunk maximum m, the sum l of exp(score - m)
 // and acc[d] = sum exp(score - m) * v[d]; the chunks are merged with
 // log-sum-exp rescaling: out = sum_c acc_c * e^(m_c-M) / sum_c l_c * e^(m_c-M).
-// The chunk length follows the sequence (attn_split) so that about 512
-// workgroups share it at any length. A second kernel merges (a hand-off
+// The chunk length follows the sequence (attn_split) so that about
+// kTargetWgs (512) workgroups of the vector-ALU kernels, or kMfmaTargetWgs
+// (vbs_attn_common.h) of the matrix-core kernel, share it at any length. A second kernel merges (a hand-off
 // inside one kernel, through device-scope stores, loads and an arrival
 // count, measured slower than the kernel boundary on this part).
 //

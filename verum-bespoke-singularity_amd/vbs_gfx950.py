@@ -159,6 +159,7 @@ _DEVICE_SIGS = {
     "bdecoder_create": (_I, [_P, _U32, _U64, _U32, C.POINTER(C.c_void_p)]),
     "bdecoder_greedy": (_I, [_P, _P, _P, _U32, _P, _P]),
     "bdecoder_greedy_eager": (_I, [_P, _P, _P, _U32, _P, _P]),
+    "bdecoder_step": (_I, [_P, _P, _P, _P]),
     "bdecoder_destroy": (_I, [_P]),
     "quantize_q8": (_I, [_P, _U32, _P, _P, _P]),
     "hot_matvec": (_I, [_I, _P, _U32, _U32, _P, _P, _P, _P]),
@@ -765,6 +766,26 @@ class BatchDecoder:
         self.dev.check(fn(self.h, t0.ctypes.data, p0.ctypes.data, n, toks.ctypes.data,
                           margins.ctypes.data), "bdecoder_greedy")
         return toks, margins
+
+    def step(self, tokens, pos) -> np.ndarray:
+        """Logits (batch, vocab) of one step of every sequence fed tokens[b]
+        at pos[b] (teacher forcing); the caches at pos[b] are written."""
+        t = np.ascontiguousarray(tokens, np.uint32)
+        p = np.ascontiguousarray(pos, np.uint32)
+        out = np.empty((self.batch, self.vocab), np.float32)
+        self.dev.check(self.dev._bdecoder_step(self.h, t.ctypes.data, p.ctypes.data,
+                                               out.ctypes.data), "bdecoder_step")
+        return out
+
+    def read_kv(self, b: int, layer: int, pos: int):
+        """Sequence b's f16 K and V rows (kv_dim each) of `layer` at `pos`."""
+        off = 2 * (b * self.seq + (layer * self.max_ctx + pos) * self.kvd)
+        out = []
+        for src in (self.kc, self.vc):
+            row = np.empty(self.kvd, np.uint16)
+            self.dev.check(self.dev._copy_d2h(row.ctypes.data, src + off, row.nbytes), "copy_d2h")
+            out.append(row)
+        return out
 
     def close(self):
         if self.h:
