@@ -252,11 +252,15 @@ def test_gpu_7b_teacher_forced_logits_vs_oracle(backend, dev, host, model_7b):
 
 
 def f16_rows_close(got, want):
-    """f16 rows equal to within one unit in the last place (the same f32
-    value rounded after a matvec that differs from the oracle's by ~1e-7)."""
+    """f16 cache rows as close as the matvec bar leaves them: each element
+    within one f16 unit in the last place plus 1e-5 of the row's rms (the
+    f32 values differ from the oracle's by ~1e-7 of the row's size, so near
+    zero the roundings may fall in different f16 steps)."""
     a = got.view(np.float16).astype(np.float64)
     b = want.view(np.float16).astype(np.float64)
-    return bool(np.all(np.abs(a - b) <= 2.0 ** -10 * np.maximum(np.abs(a), np.abs(b)) + 2.0 ** -24))
+    rms = float(np.sqrt(np.mean(b * b)))
+    tol = 2.0 ** -10 * np.maximum(np.abs(a), np.abs(b)) + 1e-5 * rms + 2.0 ** -24
+    return bool(np.all(np.abs(a - b) <= tol))
 
 
 @pytest.mark.gpu
