@@ -44,6 +44,28 @@ const vbs_system_profile_t *vbs_callers_profile(vbs_device_t *dev, uint64_t free
     return &p;
 }
 
+/* The system profile vbs_profiler_scan_system builds on a machine whose only
+ * GPU backend is HIP: its HIP branch (src/vbs_profiler.c:194-210) takes the
+ * device's max_working_set_bytes as total VRAM, 85% of it as free, and
+ * max_buffer_bytes as the largest allocation. The bandwidth it measures is
+ * left at zero (the planner then keeps device 0). */
+const vbs_system_profile_t *vbs_callers_profile_hip(vbs_device_t *dev) {
+    static vbs_system_profile_t p;
+    memset(&p, 0, sizeof p);
+    vbs_gpu_profile_t *g = &p.gpus[0];
+    p.n_gpus = 1;
+    snprintf(g->name, sizeof g->name, "%s", dev->name);
+    g->type = VBS_BACKEND_HIP;
+    g->device = dev;
+    g->total_vram_bytes = dev->max_working_set_bytes;
+    g->free_vram_bytes = dev->max_working_set_bytes * 85 / 100;
+    g->max_alloc_bytes = dev->max_buffer_bytes;
+    g->sm_count = 60;
+    g->warp_size = 64;
+    p.total_vram_bytes = g->total_vram_bytes;
+    return &p;
+}
+
 size_t vbs_callers_n_tensors(const vbs_gguf_model_t *m) { return m->n_tensors; }
 const vbs_tensor_t *vbs_callers_tensor(const vbs_gguf_model_t *m, size_t i) {
     return i < m->n_tensors ? &m->tensors[i] : NULL;

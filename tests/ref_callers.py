@@ -46,6 +46,7 @@ def load_callers(tag, src=REF_CALLERS_SO, global_scope=False):
         "vbs_gguf_get_float32_metadata": (C.c_bool, [_VP, C.c_char_p, C.POINTER(_F32)]),
         "vbs_gguf_get_uint32_metadata": (C.c_bool, [_VP, C.c_char_p, C.POINTER(_U32)]),
         "vbs_callers_profile": (_VP, [_VP, C.c_uint64]),
+        "vbs_callers_profile_hip": (_VP, [_VP]),
         "vbs_callers_n_tensors": (_SZ, [_VP]),
         "vbs_callers_tensor": (_VP, [_VP, _SZ]),
         "vbs_callers_tensor_name": (C.c_char_p, [_VP]),
@@ -131,7 +132,8 @@ class RefEngine:
     """vbs_engine_create's set-up and the specializer's emitted token step
     over `backend` (a vbs_gfx950.Backend, initialised)."""
 
-    def __init__(self, L, backend, gguf_path, tier=TIER_VRAM, vram_bytes=8 << 30):
+    def __init__(self, L, backend, gguf_path, tier=TIER_VRAM, vram_bytes=8 << 30,
+                 profile="fixed"):
         self.L, self.be = L, backend
         self.model = m = GgufModel(L, gguf_path)
         self.n_layers = m.u32("llama.block_count")
@@ -147,7 +149,10 @@ class RefEngine:
         self.kvd = self.nkv * self.hd
         dev = self.dev = backend.device()
         ops = self.ops = C.addressof(backend.ops)
-        self.sys = L.vbs_callers_profile(C.cast(dev, _VP), vram_bytes)
+        # "fixed": one GPU with vram_bytes free; "hip": the profile the
+        # reference's profiler derives from the device's own byte counts
+        self.sys = (L.vbs_callers_profile_hip(C.cast(dev, _VP)) if profile == "hip" else
+                    L.vbs_callers_profile(C.cast(dev, _VP), vram_bytes))
         self.fabric = L.vbs_fabric_create(self.sys, ops, 16, 0, None)
         for t in m.tensors:  # src/vbs_engine.c:51-56
             L.vbs_fabric_register_tensor(self.fabric, t, L.vbs_callers_tensor_data(m.ptr, t), tier,

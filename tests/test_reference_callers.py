@@ -204,3 +204,79 @@ def test_gpu_slice_executor_convention_b(host, backend, tmp_path, geometry, wind
         se.close()
     finally:
         gm.close()
+
+
+def engine_kv_capacity(free_vram, total_vram, geo, n_layers, ctx, mix=None):
+    """vbs_engine_create's KV budget (src/vbs_engine.c:94-140) for a Q4_K_M
+    llama model of this geometry: positions that fit in the free VRAM after
+    the model and the runtime buffers, capped at the context length."""
+    mix = dict(V.Q4_K_M_MIX if mix is None else mix)
+    H, F, nq, nkv, hd, vocab = (geo[k] for k in ("hidden", "ffn", "n_heads", "n_kv_heads",
+                                                 "head_dim", "vocab"))
+    qd, kvd = nq * hd, nkv * hd
+    shapes = {"q": (qd, H), "k": (kvd, H), "v": (kvd, H), "o": (H, qd),
+              "gate": (F, H), "up": (F, H), "down": (H, F)}
+    model = (n_layers * sum(r * V.row_bytes(mix[n], c) for n, (r, c) in shapes.items())
+             + n_layers * 2 * H * 4 + H * 4
+             + vocab * V.row_bytes(mix["embd"], H) + vocab * V.row_bytes(mix["head"], H))
+    scratch = 4 * (qd + kvd + kvd + qd + F + F + F + H + qd + kvd)
+    runtime = 2 * H * 4 + vocab * 4 + scratch
+    kv_pos = n_layers * nkv * hd * 2
+    base = free_vram or total_vram
+    fit = (base - model - runtime) // (2 * kv_pos) if base > model + runtime else 0
+    return min(fit, ctx), kv_pos, model
+
+
+@pytest.mark.gpu
+@have_callers
+def test_gpu_device_info_feeds_profiler_fabric_and_kv_budget(host, backend, tmp_path):
+    """The reference's selection, profiler and engine read the shim's device
+    struct: VBS_BACKEND=hip takes the table whose init succeeds and whose
+    device 0 has a name (src/vbs_backend_select.c:42-85); the profiler's HIP
+    branch turns max_working_set_bytes / max_buffer_bytes into the system
+    profile (src/vbs_profiler.c:194-210, restated in oracle/ref_callers.c:
+    vbs_profiler.c itself does not link here); the engine sizes its KV cache
+    from that profile (src/vbs_engine.c:94-140). With this device's figures
+    the 7B model gets its whole 2176-position context and the 70B model its
+    8320 (config 5 at ctx 8192 plus 128 tokens), the planner's VRAM budget
+    (src/vbs_planner.c:57) holds the whole 70B model, and the 70B caches of
+    that capacity allocate through the table. The reference fabric over the
+    same profile places the tiny model in device memory and its bridge
+    sequence equals the decode driver's."""
+    import ctypes as C
+    ops = backend.ops
+    assert ops.init() and ops.get_device_count() >= 1
+    devp = ops.get_device(0)
+    dev = devp.contents
+    assert dev.name and dev.type == 2  # VBS_BACKEND_HIP
+    L = rc().load_callers("gpu_profile")
+    prof = L.vbs_callers_profile_hip(C.cast(devp, C.c_void_p))
+    import ref_callers as rcm
+    total, free = dev.max_working_set_bytes, dev.max_working_set_bytes * 85 // 100
+    print(f"device {dev.name.decode()}: max_working_set {total / 2**30:.1f} GiB, "
+          f"max_buffer {dev.max_buffer_bytes / 2**30:.1f} GiB")
+    assert total >= 256 << 30 and dev.max_buffer_bytes >= 64 << 30
+    from test_decode import GEO_70B, GEO_7B
+    cap7, _, m7 = engine_kv_capacity(free, total, GEO_7B, 32, 2176)
+    cap70, kvpos70, m70 = engine_kv_capacity(free, total, GEO_70B, 80, 8320)
+    print(f"KV capacity: 7B {cap7} (model {m7 / 1e9:.2f} GB), 70B {cap70} "
+          f"(model {m70 / 1e9:.2f} GB)")
+    assert cap7 == 2176 and cap70 == 8320
+    assert free * 90 // 100 >= m70  # every 70B tensor planned IN_VRAM
+    kv = [backend.alloc(kvpos70 * cap70) for _ in range(2)]
+    for b in kv:
+        ops.free_buffer(b)
+    model, path = tiny_gguf(host, tmp_path, "tiny_prof.gguf")
+    eng = rcm.RefEngine(L, backend, path, profile="hip")
+    d = V.Decoder(host, backend, model)
+    try:
+        assert set(eng.tiers_after_init) == {0}  # VBS_TIER_VRAM
+        eng.zero_kv()
+        tok = 1
+        for pos in range(6):
+            got, want = eng.step(tok, pos), d.step(tok, pos)
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), pos
+            tok = int(np.argmax(want))
+    finally:
+        d.close()
+        eng.close()
