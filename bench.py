@@ -276,6 +276,14 @@ def bench_ceiling(dev, hip, stream, regions, region_bytes, reps):
     out = {}
     read_us = per_launch_us(lambda: [dev.check(dev._checksum(r, region_bytes, part), "checksum")
                                      for r in regions], len(regions), reps)
+    # the same read in two other shapes: is the floor tight?
+    variants = {}
+    for v, name in ((1, "two_8wave_workgroups_per_cu_lds_dma"),
+                    (2, "one_16wave_workgroup_per_cu_register_loads")):
+        us = per_launch_us(lambda: [dev.check(dev._checksum_variant(r, region_bytes, part, v),
+                                              "checksum") for r in regions], len(regions), reps)
+        variants[name] = {"us_per_launch": round(us, 3),
+                          "frac": round(region_bytes / us / 1e3 / PEAK_HBM_GBS, 4)}
     gib = 1 << 30
     big = dev.alloc(gib)
     try:
@@ -300,7 +308,8 @@ def bench_ceiling(dev, hip, stream, regions, region_bytes, reps):
                           "GB_per_s": gbs(region_bytes, read_us),
                           "frac": round(region_bytes / read_us / 1e3 / PEAK_HBM_GBS, 4),
                           "bytes": region_bytes,
-                          "kernel": "vbs_gfx950_checksum over the same weight copies"},
+                          "kernel": "vbs_gfx950_checksum over the same weight copies",
+                          "variants": variants},
            "stream_1GiB_GB_per_s": gbs(gib, stream_us),
            "launch_floor_us": round(one_us, 3),
            "copy_d2d_GB_per_s": {"25.4MB_read_plus_write": gbs(2 * region_bytes, cp_us),

@@ -172,6 +172,14 @@ int vbs_gfx950_linear_batch_multi(int type, uint32_t n_mat, const void *const *w
  * roofline. No counterpart in the reference. */
 uint32_t vbs_gfx950_checksum_partials(size_t bytes);
 int vbs_gfx950_checksum(const void *p, size_t bytes, uint32_t *partials);
+/* The same checksum read in another shape, to show how tight the read floor
+ * is: variant 0 is vbs_gfx950_checksum; 1 reads 56 KB spans with two 8-wave
+ * workgroups per CU (8 partials per workgroup); 2 is variant 0's shape with
+ * 16-byte vector loads into registers instead of LDS DMA. The XOR of the
+ * partials is the region's in every variant. No counterpart in the
+ * reference. */
+uint32_t vbs_gfx950_checksum_variant_partials(size_t bytes, int variant);
+int vbs_gfx950_checksum_variant(const void *p, size_t bytes, uint32_t *partials, int variant);
 
 /* The library's stream (a hipStream_t), for callers that time kernels with
  * HIP events or capture the stream into a graph.

@@ -66,19 +66,21 @@ def test_upload_is_ordered_after_earlier_kernels(dev, host):
             dev.free(p)
 
 
+@pytest.mark.parametrize("variant", [0, 1, 2], ids=["dma_1wg", "dma_2wg", "reg"])
 @pytest.mark.parametrize("nbytes", [16, 1008, 65536, 65536 + 48, 3 * 65536 - 16, 25362432])
-def test_checksum_matches_host(dev, nbytes):
-    """vbs_gfx950_checksum over regions that end inside a 1 KB run, a
-    workgroup span and exactly on one: the XOR of the partial words equals
-    the host's XOR of the same 32-bit words, and one flipped bit changes it."""
+def test_checksum_matches_host(dev, nbytes, variant):
+    """vbs_gfx950_checksum (and its read-floor variants: two workgroups per
+    CU, register loads) over regions that end inside a 1 KB run, a workgroup
+    span and exactly on one: the XOR of the partial words equals the host's
+    XOR of the same 32-bit words, and one flipped bit changes it."""
     rng = np.random.default_rng(nbytes)
     host = rng.integers(0, 2**32, nbytes // 4, dtype=np.uint32)
     p = dev.upload(host)
     try:
-        assert dev.checksum(p, nbytes) == int(np.bitwise_xor.reduce(host))
+        assert dev.checksum(p, nbytes, variant) == int(np.bitwise_xor.reduce(host))
         flipped = host.copy()
         flipped[-1] ^= 1 << 7
         dev.write(p, flipped)
-        assert dev.checksum(p, nbytes) == int(np.bitwise_xor.reduce(host)) ^ (1 << 7)
+        assert dev.checksum(p, nbytes, variant) == int(np.bitwise_xor.reduce(host)) ^ (1 << 7)
     finally:
         dev.free(p)

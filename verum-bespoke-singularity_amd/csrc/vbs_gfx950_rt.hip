@@ -517,14 +517,24 @@ int vbs_gfx950_attention_noalloc(const float *q, const uint16_t *kc, const uint1
 
 uint32_t vbs_gfx950_checksum_partials(size_t bytes) { return checksum_partials(bytes); }
 
-int vbs_gfx950_checksum(const void *p, size_t bytes, uint32_t *partials) {
+uint32_t vbs_gfx950_checksum_variant_partials(size_t bytes, int variant) {
+    return variant >= 0 && variant <= 2 ? checksum_partials(bytes, variant) : 0u;
+}
+
+int vbs_gfx950_checksum_variant(const void *p, size_t bytes, uint32_t *partials, int variant) {
     if (!ready_or_fail()) return 0;
+    if (variant < 0 || variant > 2) return fail("checksum: variant %d outside 0..2", variant);
     if (bytes == 0) return 1;
     if (!p || !partials) return fail("checksum: null pointer");
     if ((bytes & 15u) || ((uintptr_t)p & 15u))
         return fail("checksum: region must be 16-byte aligned and a multiple of 16 bytes");
-    return hip_ok(launch_checksum(static_cast<const uint8_t *>(p), bytes, partials, g_rt.stream),
+    return hip_ok(launch_checksum(static_cast<const uint8_t *>(p), bytes, partials, variant,
+                                  g_rt.stream),
                   "checksum");
+}
+
+int vbs_gfx950_checksum(const void *p, size_t bytes, uint32_t *partials) {
+    return vbs_gfx950_checksum_variant(p, bytes, partials, 0);
 }
 
 int vbs_gfx950_silu_mul(const float *g, const float *u, float *out, uint32_t n) {

@@ -156,9 +156,11 @@ hipError_t launch_silu_mul(const float *g, const float *u, float *out, uint32_t 
 // XOR of the 32-bit words of p[0, bytes) (bytes a multiple of 16, p 16-byte
 // aligned) as checksum_partials(bytes) partial words: 16 per workgroup, one per
 // wave, each the XOR of that wave's interleaved 1 KB runs of the workgroup's
-// span.
-uint32_t checksum_partials(uint64_t bytes);
-hipError_t launch_checksum(const uint8_t *p, uint64_t bytes, uint32_t *partials, hipStream_t s);
+// span. `variant` selects the shape (0 the default; 1 two 8-wave workgroups
+// per CU, 8 partials each; 2 register loads instead of LDS DMA).
+uint32_t checksum_partials(uint64_t bytes, int variant = 0);
+hipError_t launch_checksum(const uint8_t *p, uint64_t bytes, uint32_t *partials, int variant,
+                           hipStream_t s);
 hipError_t launch_add(const float *a, const float *b, float *out, uint32_t n, hipStream_t s);
 
 }  // namespace vbs

@@ -403,28 +403,20 @@ typedef _Float16 ah8 __attribute__((ext_vector_type(8)));
 typedef float af4 __attribute__((ext_vector_type(4)));
 typedef uint32_t au4 __attribute__((ext_vector_type(4)));
 
-__global__ __launch_bounds__(64) void k_attn_mfma(const float *__restrict__ q,
-                                                  const uint16_t *__restrict__ kc,
-                                                  const uint16_t *__restrict__ vc,
-                                                  float *__restrict__ part, uint32_t seq_len,
-                                                  const uint32_t *__restrict__ pos_dev,
-                                                  uint64_t layer_off, uint32_t nkh, uint32_t group,
-                                                  float scale, uint32_t stride_chunks,
-                                                  uint32_t q_bstride, uint64_t kv_bstride,
-                                                  uint64_t part_bstride) {
+// One wave's chunk: positions [s0, s0 + valid) of kv head kvh (valid >= 1,
+// nt tiles of 32) against the q heads of its group. On return every lane
+// holds, for head n & 7 of its lane n = lane & 15, the chunk maximum m and
+// l = sum e^(s - m); and a[dt][r] = the sum of e^(s - m) v[8 n + dt] of head
+// 4 (lane >> 4) + r (rows hi + lo added; lane groups 0 and 1 carry them).
+__device__ __forceinline__ void attn_mfma_wave(const float *__restrict__ q,
+                                               const uint16_t *__restrict__ kc,
+                                               const uint16_t *__restrict__ vc, uint64_t layer_off,
+                                               uint32_t s0, uint32_t valid, uint32_t nt,
+                                               uint32_t nkh, uint32_t kvh, uint32_t group,
+                                               float scale, uint32_t lane, float &m_out,
+                                               float &l_out, float (&a)[8][4]) {
     constexpr uint32_t HD = 128;
-    const uint32_t chunk = blockIdx.x, kvh = blockIdx.y, lane = threadIdx.x, bz = blockIdx.z;
     const uint32_t n = lane & 15u, g = lane >> 4;
-    // sequence bz of a batch: its q, caches, position and partials
-    q += (uint64_t)bz * q_bstride;
-    kc += bz * kv_bstride;
-    vc += bz * kv_bstride;
-    part += bz * part_bstride;
-    if (pos_dev) seq_len = pos_dev[bz] + 1u;  // graph replay: the device holds the position
-    const AttnSplit sp = attn_split(seq_len, nkh, kMfmaGran, kMfmaLmax, kMfmaTargetWgs);
-    if (chunk >= sp.n) return;  // past the sequence (the grid covers the longest split)
-    const uint32_t s0 = chunk * sp.len, valid = min(sp.len, seq_len - s0);
-    const uint32_t nt = sp.len / kMfmaGran;
     const uint64_t rstride = (uint64_t)nkh * HD;
     const uint64_t base = layer_off + (uint64_t)s0 * rstride + (uint64_t)kvh * HD;
 
@@ -555,11 +547,38 @@ __global__ __launch_bounds__(64) void k_attn_mfma(const float *__restrict__ q,
     // hi + lo of acc (lane groups g and g + 2), stored by lane groups 0 and 1
     l += lane_xor<16>(l);
     l += lane_xor<32>(l);
-    float a[8][4];
 #pragma unroll
     for (uint32_t dt = 0; dt < 8; dt++)
 #pragma unroll
         for (uint32_t r = 0; r < 4; r++) a[dt][r] = acc[dt][r] + lane_xor<32>(acc[dt][r]);
+    m_out = m;
+    l_out = l;
+}
+
+__global__ __launch_bounds__(64) void k_attn_mfma(const float *__restrict__ q,
+                                                  const uint16_t *__restrict__ kc,
+                                                  const uint16_t *__restrict__ vc,
+                                                  float *__restrict__ part, uint32_t seq_len,
+                                                  const uint32_t *__restrict__ pos_dev,
+                                                  uint64_t layer_off, uint32_t nkh, uint32_t group,
+                                                  float scale, uint32_t stride_chunks,
+                                                  uint32_t q_bstride, uint64_t kv_bstride,
+                                                  uint64_t part_bstride) {
+    constexpr uint32_t HD = 128;
+    const uint32_t chunk = blockIdx.x, kvh = blockIdx.y, lane = threadIdx.x, bz = blockIdx.z;
+    const uint32_t n = lane & 15u, g = lane >> 4;
+    // sequence bz of a batch: its q, caches, position and partials
+    q += (uint64_t)bz * q_bstride;
+    kc += bz * kv_bstride;
+    vc += bz * kv_bstride;
+    part += bz * part_bstride;
+    if (pos_dev) seq_len = pos_dev[bz] + 1u;  // graph replay: the device holds the position
+    const AttnSplit sp = attn_split(seq_len, nkh, kMfmaGran, kMfmaLmax, kMfmaTargetWgs);
+    if (chunk >= sp.n) return;  // past the sequence (the grid covers the longest split)
+    const uint32_t s0 = chunk * sp.len, valid = min(sp.len, seq_len - s0);
+    float m, l, a[8][4];
+    attn_mfma_wave(q, kc, vc, layer_off, s0, valid, sp.len / kMfmaGran, nkh, kvh, group, scale,
+                   lane, m, l, a);
     float *const pk = part + (uint64_t)kvh * group * stride_chunks * (HD + 2u);
     if (g < 2u) {
 #pragma unroll

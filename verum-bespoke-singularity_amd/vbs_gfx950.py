@@ -151,6 +151,8 @@ _DEVICE_SIGS = {
     "stream": (_P, []),
     "checksum_partials": (_U32, [_SZ]),
     "checksum": (_I, [_P, _SZ, _P]),
+    "checksum_variant_partials": (_U32, [_SZ, _I]),
+    "checksum_variant": (_I, [_P, _SZ, _P, _I]),
     "decoder_create": (_I, [_P, _U32, C.POINTER(C.c_void_p)]),
     "decoder_step": (_I, [_P, _U32, _U32, _P]),
     "decoder_greedy": (_I, [_P, _U32, _U32, _U32, _P, _P]),
@@ -253,15 +255,16 @@ class DeviceLib:
         self.check(self._hot_matvec(t, w, rows, cols, act, qd or None, qsum or None, y),
                    "hot_matvec")
 
-    def checksum(self, p, nbytes: int) -> int:
+    def checksum(self, p, nbytes: int, variant: int = 0) -> int:
         """XOR of the 32-bit words of device bytes [p, p + nbytes) (16-byte
-        aligned, a multiple of 16 bytes), from the per-workgroup partials."""
-        n = int(self._checksum_partials(nbytes))
+        aligned, a multiple of 16 bytes), from the per-wave partials of the
+        read shape `variant` (vbs_gfx950_checksum_variant)."""
+        n = int(self._checksum_variant_partials(nbytes, variant))
         if n == 0:
             return 0
         part = self.alloc(4 * n)
         try:
-            self.check(self._checksum(p, nbytes, part), "checksum")
+            self.check(self._checksum_variant(p, nbytes, part, variant), "checksum")
             return int(np.bitwise_xor.reduce(self.download(part, n, np.uint32)))
         finally:
             self.free(part)
