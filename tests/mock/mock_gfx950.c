@@ -81,3 +81,28 @@ int vbs_gfx950_add(const float *a, const float *b, float *out, uint32_t n) {
     vbs_oracle_add(a, b, out, n); return 1;
 }
 #endif
+/* The fused neighbours of a linear (vbs_gfx950_linear_fused) as the ops one
+ * by one; like the device library, only for Q4_K and Q6_K (else 2: nothing
+ * done, the shim issues the ops itself). */
+static unsigned g_fused[3]; /* launches joined with a NORMALIZE, a ROTARY, an add */
+unsigned mock_fused_count(int which) { return which >= 0 && which < 3 ? g_fused[which] : 0u; }
+
+int vbs_gfx950_linear_fused(int t, const void *w, const float *x, float *y, uint32_t cols,
+                            uint32_t rows, const float *norm_w, float eps, float *x_normed,
+                            float *acc, int rope, uint32_t pos, uint32_t hd, float theta) {
+    if (t != 12 && t != 14) return 2;
+    if ((norm_w != NULL) != (x_normed != NULL) || (acc && (norm_w || rope)) ||
+        (!acc && !norm_w && !rope))
+        return 2;
+    if (norm_w) {
+        vbs_oracle_rms_norm(x, norm_w, x_normed, cols, eps);
+        x = x_normed;
+    }
+    if (!vbs_oracle_linear_tile(t, (const uint8_t *)w, x, y, cols, rows, 0, 0, 0)) return 0;
+    if (rope) vbs_oracle_rope(y, pos, hd, rows / hd, theta);
+    if (acc) vbs_oracle_add(acc, y, acc, rows);
+    g_fused[0] += norm_w != NULL;
+    g_fused[1] += rope != 0;
+    g_fused[2] += acc != NULL;
+    return 1;
+}

@@ -164,6 +164,46 @@ def test_backend_suite_through_shim_on_host_mock(tmpdir_mod, host):
     assert len(res) >= 33
 
 
+@pytest.mark.parametrize("mix", ["q4k_m", "q8_0"])
+def test_held_ops_on_host_mock_keep_the_bridge_results(tmpdir_mod, host, mix):
+    """The shim holds back one NORMALIZE or LINEAR and joins it with the next
+    op (RMSNorm + matvec, matvec + RoPE, matvec + add) when
+    vbs_gfx950_linear_fused takes the combination. Over the host mock (whose
+    fused entry composes the oracle's ops, and declines every type but Q4_K
+    and Q6_K, so the Q8_0 model runs the ops one by one) the bridge-order
+    decode driver's logits equal the oracle's forward pass bit for bit at
+    every step, and with Q4_K the joins happened: per layer the two RMSNorms,
+    the Q and K RoPEs and the two residual adds."""
+    from test_decode import TINY, full_cache
+    so = build_mock(tmpdir_mod, f"mock_fuse_{mix}.so")
+    be, ok = fresh_shim(tmpdir_mod, so)
+    assert ok, be.last_error()
+    mock = C.CDLL(so)
+    mock.mock_fused_count.restype = C.c_uint
+    mix_d = None if mix == "q4k_m" else {r: V.Q8_0 for r in ("q", "k", "v", "o", "gate", "up",
+                                                             "down", "embd", "head")}
+    model = V.SynthModel(host, **TINY, seed=99, mix=mix_d)
+    d = V.Decoder(host, be, model)
+    orc = Oracle()
+    kc, vc = full_cache(model, None, None, 0)
+    om = orc.model(model, kc, vc)
+    before = [mock.mock_fused_count(i) for i in range(3)]
+    tok = 1
+    for pos in range(6):
+        got = d.step(tok, pos)
+        want = orc.forward(om, tok, pos, model.cfg["vocab"], 1)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), pos
+        tok = int(np.argmax(want))
+    d.close()
+    joined = [mock.mock_fused_count(i) - before[i] for i in range(3)]
+    L = TINY["n_layers"]
+    if mix == "q4k_m":
+        # norms: attn + ffn per layer, and the output norm before the lm_head
+        assert joined == [6 * (2 * L + 1), 6 * 2 * L, 6 * 2 * L], joined
+    else:
+        assert joined == [0, 0, 0], joined
+
+
 def test_shim_marshalling_rejects_malformed_arguments(tmpdir_mod):
     so = build_mock(tmpdir_mod, "mock_ok2.so")
     be, ok = fresh_shim(tmpdir_mod, so)

@@ -7,6 +7,7 @@
 // return 0; nothing aborts across the C ABI.
 #include <math.h>
 #include <stdarg.h>
+#include <vector>
 #include <stdio.h>
 #include <string.h>
 
@@ -373,6 +374,82 @@ int vbs_gfx950_linear(int type, const void *w, const float *x, float *y, uint32_
     return hip_ok(launch_linear(type, (const uint8_t *)w, x + col_off, y + row_off, cols, rows,
                                 accumulate, g_rt.stream),
                   "linear");
+}
+
+// RoPE rows of the fused linear: (cos, sin) of every pair angle for positions
+// [0, n_pos) at one (theta, head_dim), computed with the host libm as
+// vbs_gfx950_rope does, and the positions 0 .. n_pos - 1 themselves (the
+// kernels read the position through a device pointer). Rebuilt, twice as
+// long, when a call needs a later position; the previous tables are freed
+// after the stream drains (this path is never captured).
+struct RopeRows {
+    float theta = 0.f;
+    uint32_t hd = 0, n_pos = 0;
+    float2 *tab = nullptr;
+    uint32_t *pos = nullptr;
+};
+static RopeRows g_rope;
+
+static bool rope_rows(float theta, uint32_t hd, uint32_t pos) {
+    if (g_rope.tab && g_rope.theta == theta && g_rope.hd == hd && pos < g_rope.n_pos) return true;
+    uint32_t n = 4096;
+    while (n <= pos) n *= 2u;
+    if (g_rope.tab && g_rope.theta == theta && g_rope.hd == hd && n < 2u * g_rope.n_pos)
+        n = 2u * g_rope.n_pos;
+    const uint32_t pairs = hd / 2u;
+    std::vector<float2> tab((size_t)n * pairs);
+    std::vector<uint32_t> ids(n);
+    for (uint32_t p = 0; p < n; p++) {
+        ids[p] = p;
+        for (uint32_t pr = 0; pr < pairs; pr++) {
+            const float angle = (float)p * powf(theta, -(float)(2u * pr) / (float)hd);
+            tab[(size_t)p * pairs + pr] = make_float2(cosf(angle), sinf(angle));
+        }
+    }
+    float2 *t = nullptr;
+    uint32_t *ip = nullptr;
+    if (hipMalloc(&t, tab.size() * sizeof(float2)) != hipSuccess ||
+        hipMalloc(&ip, ids.size() * sizeof(uint32_t)) != hipSuccess ||
+        hipMemcpyAsync(t, tab.data(), tab.size() * sizeof(float2), hipMemcpyHostToDevice,
+                       g_rt.stream) != hipSuccess ||
+        hipMemcpyAsync(ip, ids.data(), ids.size() * sizeof(uint32_t), hipMemcpyHostToDevice,
+                       g_rt.stream) != hipSuccess ||
+        hipStreamSynchronize(g_rt.stream) != hipSuccess) {
+        if (t) (void)hipFree(t);
+        if (ip) (void)hipFree(ip);
+        return false;
+    }
+    if (g_rope.tab) (void)hipFree(g_rope.tab);
+    if (g_rope.pos) (void)hipFree(g_rope.pos);
+    g_rope = RopeRows{theta, hd, n, t, ip};
+    return true;
+}
+
+int vbs_gfx950_linear_fused(int type, const void *w, const float *x, float *y, uint32_t cols,
+                            uint32_t rows, const float *norm_w, float eps, float *x_normed,
+                            float *acc, int rope, uint32_t pos, uint32_t head_dim, float theta) {
+    if (!ready_or_fail()) return 0;
+    if (!w || !x || !y) return fail("linear_fused: null pointer");
+    if (type != kQ4_K && type != kQ6_K) return 2;
+    if (cols % 256u || rows == 0) return 2;
+    if ((norm_w != nullptr) != (x_normed != nullptr))
+        return fail("linear_fused: the RMSNorm needs both its weights and its output");
+    if (acc && (norm_w || rope)) return 2;
+    if (!acc && !norm_w && !rope) return 2;
+    const float2 *rt_rope = nullptr;
+    const uint32_t *rt_pos = nullptr;
+    if (rope) {
+        if (head_dim == 0 || (head_dim & 3u) || head_dim > 256u || rows % head_dim) return 2;
+        if (!rope_rows(theta, head_dim, pos)) return fail("linear_fused: RoPE table allocation failed");
+        rt_rope = g_rope.tab;
+        rt_pos = g_rope.pos + pos;
+    }
+    // with the add, the kernels accumulate into acc and copy the row values to y
+    const hipError_t e = launch_kq_linear_fused(type, (const uint8_t *)w, x, acc ? acc : y, cols, rows,
+                                                norm_w, eps, x_normed, acc ? y : nullptr, rt_rope,
+                                                rt_pos, rope ? head_dim : 0u, g_rt.stream);
+    if (e == hipErrorNotSupported) return 2;
+    return hip_ok(e, "linear_fused");
 }
 
 int vbs_gfx950_linear_batch(int type, const void *w, const float *x, uint32_t x_stride, float *y,

@@ -95,16 +95,31 @@ hipError_t launch_kq_linear_batch(int type, const uint8_t *w, const float *x, ui
                                   uint32_t ys, uint32_t cols, uint32_t rows, uint32_t batch,
                                   hipStream_t s);
 
+struct MvArgs;
 // Q4_K matvec with each workgroup's whole row range in flight (rows of 16
 // blocks, 4096-12288 rows, 16-byte aligned w and x); hipErrorNotSupported
-// outside that range (k_mvf then runs). Bit-identical to k_mvf.
+// outside that range (k_mvf then runs). Bit-identical to k_mvf. `extra`
+// (may be NULL) brings the backend shim's fused neighbours: norm_w / eps /
+// xn for an RMSNorm in front (not with accumulate), ycopy with accumulate.
 hipError_t launch_q4k_mvl(const uint8_t *w, const float *x, float *y, uint32_t cols, uint32_t rows,
-                          int accumulate, hipStream_t s);
+                          int accumulate, hipStream_t s, const MvArgs *extra = nullptr);
 // The ring variant (vbs_kern_mvl.hip) for Q6_K rows of 33-48 blocks over
 // 2049-4096 rows (7B down) and of 97-112 blocks over 4097-8192 rows (70B
-// down); hipErrorNotSupported elsewhere.
+// down); hipErrorNotSupported elsewhere. ycopy (accumulate only, may be
+// NULL) also receives each row value before it is added.
 hipError_t launch_q6k_mvr(const uint8_t *w, const float *x, float *y, uint32_t cols, uint32_t rows,
-                          int accumulate, hipStream_t s);
+                          int accumulate, hipStream_t s, float *ycopy = nullptr);
+// The linear op fused with its neighbour in the bridge's op sequence (the
+// backend shim's dispatch path, vbs_gfx950_linear_fused): norm_w / eps / xn
+// (RMSNorm in front, the normalised x stored to xn), ycopy (y = y + W x, W x
+// also stored to ycopy), rope / pos / hd (the result rotated at the device
+// position *pos, as the ROTARY op after it); Q4_K and Q6_K only,
+// hipErrorNotSupported (nothing launched) outside the shapes the fused
+// kernels take.
+hipError_t launch_kq_linear_fused(int type, const uint8_t *w, const float *x, float *y, uint32_t cols,
+                                  uint32_t rows, const float *norm_w, float eps, float *xn,
+                                  float *ycopy, const float2 *rope, const uint32_t *pos, uint32_t hd,
+                                  hipStream_t s);
 // Specialised Q4_K matvec; hipErrorNotSupported when the shape/alignment is
 // outside its range (the generic kernel then runs).
 hipError_t launch_q4k_fast(const uint8_t *w, const float *x, float *y, uint32_t cols,

@@ -25,7 +25,6 @@
 namespace vbs {
 
 constexpr uint32_t kCsWaves = 16, kCsRuns = 7;                  // runs per wave
-constexpr uint32_t kCsSpanMax = kCsWaves * kCsRuns * 1024u;        // 112 KB per workgroup
 constexpr uint32_t kCsWgs = 256;
 
 // 16 bytes per lane from global memory to LDS at `lds` + 16 * lane (`lds`

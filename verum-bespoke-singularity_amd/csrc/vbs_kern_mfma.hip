@@ -51,6 +51,62 @@ hipError_t launch_kq_norm_linear(int type, const uint8_t *w, const float *x, con
     return launch_type<true, E_STORE>(type, a, s);
 }
 
+hipError_t launch_kq_linear_fused(int type, const uint8_t *w, const float *x, float *y, uint32_t cols,
+                                  uint32_t rows, const float *norm_w, float eps, float *xn,
+                                  float *ycopy, const float2 *rope, const uint32_t *pos, uint32_t hd,
+                                  hipStream_t s) {
+    if (rows == 0 || !mv_fits(type, w, x, cols, rows)) return hipErrorNotSupported;
+    MvArgs ex{};
+    ex.norm_w = norm_w;
+    ex.eps = eps;
+    ex.xn = xn;
+    ex.ycopy = ycopy;
+    ex.rope = rope;
+    ex.pos = pos;
+    ex.hd = hd;
+    MvArgs a{};
+    a.w[0] = w;
+    a.y[0] = y;
+    a.rows[0] = rows;
+    a.nmat = 1;
+    a.cols = cols;
+    a.x = x;
+    a.norm_w = ex.norm_w;
+    a.eps = ex.eps;
+    a.xn = ex.xn;
+    if (ex.rope) {  // the q path of E_QKV: the row value rotated at *pos, stored as f32
+        if (ex.ycopy || (rows & 1u) || (ex.hd & 1u) || !ex.hd || rows % ex.hd) return hipErrorNotSupported;
+        a.rope = ex.rope;
+        a.pos = ex.pos;
+        a.hd = ex.hd;
+        a.role0 = 0;
+        if (type == kQ4_K) {
+            const hipError_t e = launch_q4k_mvl_qkv(a, s);
+            if (e != hipErrorNotSupported) return e;
+        }
+        set_tiles(a);
+        return a.norm_w ? launch_type<true, E_QKV>(type, a, s) : launch_type<false, E_QKV>(type, a, s);
+    }
+    if (ex.norm_w) {
+        if (ex.ycopy) return hipErrorNotSupported;
+        if (type == kQ4_K) {
+            const hipError_t e = launch_q4k_mvl(w, x, y, cols, rows, 0, s, &a);
+            if (e != hipErrorNotSupported) return e;
+        }
+        set_tiles(a);
+        return launch_type<true, E_STORE>(type, a, s);
+    }
+    if (!ex.ycopy) return hipErrorNotSupported;
+    a.ycopy = ex.ycopy;
+    {
+        const hipError_t e = type == kQ4_K ? launch_q4k_mvl(w, x, y, cols, rows, 1, s, &a)
+                                           : launch_q6k_mvr(w, x, y, cols, rows, 1, s, ex.ycopy);
+        if (e != hipErrorNotSupported) return e;
+    }
+    set_tiles(a);
+    return launch_type<false, E_ACC>(type, a, s);
+}
+
 hipError_t launch_kq_qkv(int type, const uint8_t *const wqkv[3], uint32_t n_mat, uint32_t role0,
                          const float *x, const float *norm_w, float eps, uint32_t cols,
                          const uint32_t rows[3], float *q, uint16_t *kc, uint16_t *vc,

@@ -128,6 +128,8 @@ __global__ __launch_bounds__(64 * kMvlWaves) void k_mvl(const MvArgs a, uint32_t
             const float w4[4] = {wv.x, wv.y, wv.z, wv.w};
 #pragma unroll
             for (int k = 0; k < 4; k++) v[k] = __fmul_rn(__fmul_rn(v[k], sc), w4[k]);
+            if (a.xn && blockIdx.x == 0 && own)
+                *reinterpret_cast<float4 *>(a.xn + 256u * b + 4u * lane) = make_float4(v[0], v[1], v[2], v[3]);
         }
         if (own) prep_block(v, lane, dv);
     }
@@ -198,6 +200,7 @@ __global__ __launch_bounds__(64 * kMvlWaves) void k_mvl(const MvArgs a, uint32_t
         const float s = ordered_sum(pb + t * ps, kMvlWaves);
         float *y = a.y[0] + r0 + t;
         *y = EPI == E_ACC ? __fadd_rn(*y, s) : s;
+        if (EPI == E_ACC && a.ycopy) a.ycopy[r0 + t] = s;
     }
 }
 
@@ -351,6 +354,7 @@ __global__ __launch_bounds__(1024) void k_mvr(const MvArgs a, uint32_t rpw) {
         const float s = ordered_sum(pb + t * part_stride(nblk), nblk);
         float *y = a.y[0] + r0 + t;
         *y = EPI == E_ACC ? __fadd_rn(*y, s) : s;
+        if (EPI == E_ACC && a.ycopy) a.ycopy[r0 + t] = s;
     }
 }
 
@@ -375,7 +379,7 @@ static hipError_t launch_mvr_t(const MvArgs &a, uint32_t wgs, uint32_t rpw, hipS
 // 4097-8192 rows (70B down: 8192 x 28672): two tiles, seven blocks per wave.
 // Two items in flight per wave.
 hipError_t launch_q6k_mvr(const uint8_t *w, const float *x, float *y, uint32_t cols, uint32_t rows,
-                          int accumulate, hipStream_t s) {
+                          int accumulate, hipStream_t s, float *ycopy) {
     const uint32_t nblk = cols / 256u;
     const bool narrow = nblk > 32u && nblk <= 48u, wide = nblk > 96u && nblk <= 112u;
     if (cols % 256u || !(narrow || wide) || ((uintptr_t)w & 1u) || ((uintptr_t)x & 15u))
@@ -398,6 +402,7 @@ hipError_t launch_q6k_mvr(const uint8_t *w, const float *x, float *y, uint32_t c
     a.nmat = 1;
     a.cols = cols;
     a.x = x;
+    a.ycopy = ycopy;
     const uint32_t g = (rows + rpw - 1u) / rpw;
     if (wide)
         return accumulate ? launch_mvr_t<7, 2, 2, E_ACC>(a, g, rpw, s)
@@ -407,7 +412,7 @@ hipError_t launch_q6k_mvr(const uint8_t *w, const float *x, float *y, uint32_t c
 }
 
 hipError_t launch_q4k_mvl(const uint8_t *w, const float *x, float *y, uint32_t cols, uint32_t rows,
-                          int accumulate, hipStream_t s) {
+                          int accumulate, hipStream_t s, const MvArgs *extra) {
     // rows of exactly 16 blocks (every wave busy) and 4096-12288 rows (one to
     // three tiles per workgroup): measured faster than k_mvf there, slower on
     // narrower rows, where waves sit idle
@@ -425,10 +430,19 @@ hipError_t launch_q4k_mvl(const uint8_t *w, const float *x, float *y, uint32_t c
     a.nmat = 1;
     a.cols = cols;
     a.x = x;
+    const bool norm = extra && extra->norm_w;
+    if (extra) {  // the backend shim's fused neighbours: RMSNorm in front, or the copy of t
+        if (norm && (accumulate || ((uintptr_t)extra->norm_w & 15u))) return hipErrorNotSupported;
+        a.norm_w = extra->norm_w;
+        a.eps = extra->eps;
+        a.xn = extra->xn;
+        a.ycopy = extra->ycopy;
+    }
     const uint32_t g = (rows + rpw - 1u) / rpw;  // workgroups with rows
 #define VBS_MVL(TT)                                                                              \
-    return accumulate ? launch_mvl_t<TT, false, E_ACC>(a, g, rpw, s)                             \
-                      : launch_mvl_t<TT, false, E_STORE>(a, g, rpw, s)
+    return norm         ? launch_mvl_t<TT, true, E_STORE>(a, g, rpw, s)                          \
+           : accumulate ? launch_mvl_t<TT, false, E_ACC>(a, g, rpw, s)                           \
+                        : launch_mvl_t<TT, false, E_STORE>(a, g, rpw, s)
     if (tiles == 1u) VBS_MVL(1);
     if (tiles == 2u) VBS_MVL(2);
     VBS_MVL(3);

@@ -592,6 +592,11 @@ struct MvArgs {
     // ranged launches: workgroups of matrix m end at rwg_end[m] (cumulative),
     // each taking rpw[m] rows of it (the last one of a matrix fewer)
     uint32_t rwg_end[3], rpw[3];
+    // the backend shim's fused neighbours of a linear (NULL elsewhere): NORM
+    // launches also store the normalised x here (workgroup 0), E_ACC launches
+    // also store each row value t here (the linear's own output, to which the
+    // add was applied)
+    float *xn, *ycopy;
 };
 
 // The fused attn_norm + Q/K/V + RoPE + KV store launch of k_mvl
@@ -775,6 +780,9 @@ __global__ __launch_bounds__(MAXT) void k_mvf(const MvArgs a) {
                 const float w4[4] = {wv[k].x, wv[k].y, wv[k].z, wv[k].w};
 #pragma unroll
                 for (int k = 0; k < 4; k++) v[k] = __fmul_rn(__fmul_rn(v[k], sc), w4[k]);
+                if (a.xn && blockIdx.x == 0)
+                    *reinterpret_cast<float4 *>(a.xn + 256u * blk(i) + 4u * lane) =
+                        make_float4(v[0], v[1], v[2], v[3]);
             }
             prep_block(v, lane, view(blk(i)));
         }
@@ -832,7 +840,10 @@ __global__ __launch_bounds__(MAXT) void k_mvf(const MvArgs a) {
         if (EPI == E_STORE) {
             if (st) a.y[m][row] = t;
         } else if (EPI == E_ACC) {
-            if (st) a.y[m][row] = __fadd_rn(a.y[m][row], t);
+            if (st) {
+                a.y[m][row] = __fadd_rn(a.y[m][row], t);
+                if (a.ycopy) a.ycopy[row] = t;
+            }
         } else if (EPI == E_SILU) {
             if (j == 0) {
                 prev = t;

@@ -59,9 +59,12 @@ typedef struct {
                      uint32_t, uint32_t, uint32_t, uint32_t, uint32_t, float);
     int (*silu_mul)(const float *, const float *, float *, uint32_t);
     int (*add)(const float *, const float *, float *, uint32_t);
+    int (*linear_fused)(int, const void *, const float *, float *, uint32_t, uint32_t,
+                        const float *, float, float *, float *, int, uint32_t, uint32_t, float);
 } gfx950_lib_t;
 
 static gfx950_lib_t g_lib;
+static bool flush_pending(void); /* issues the held-back op, if any (below) */
 static int g_probed, g_ready;
 static char g_err[512] = "not probed yet";
 static vbs_device_t g_device;
@@ -154,6 +157,7 @@ static bool gfx950_init(void) {
     BIND(attention, "vbs_gfx950_attention");
     BIND(silu_mul, "vbs_gfx950_silu_mul");
     BIND(add, "vbs_gfx950_add");
+    BIND(linear_fused, "vbs_gfx950_linear_fused");
 #undef BIND
 
     int ver = g_lib.abi_version();
@@ -215,6 +219,7 @@ static vbs_buffer_t *gfx950_alloc_buffer(vbs_device_t *dev, size_t bytes, bool s
 
 static void gfx950_free_buffer(vbs_buffer_t *buf) {
     if (!buf) return;
+    if (g_ready) (void)flush_pending();
     gfx950_buffer_t *b = (gfx950_buffer_t *)buf;
     if (g_ready) g_lib.free(buf->internal_handle);
     if (b->pinned) g_lib.host_free(buf->host_ptr);
@@ -224,6 +229,7 @@ static void gfx950_free_buffer(vbs_buffer_t *buf) {
 
 static bool gfx950_copy_to_device(vbs_buffer_t *dst, const void *src, size_t bytes) {
     if (!g_ready || !dst || !src) return false;
+    if (!flush_pending()) return false;
     return g_lib.copy_h2d(dst->internal_handle, src, bytes) ? true : lib_fail("copy_to_device");
 }
 
@@ -231,7 +237,88 @@ static bool gfx950_copy_to_device(vbs_buffer_t *dst, const void *src, size_t byt
  * synchronize (src/vbs_specializer_bridge.c:201-206). */
 static bool gfx950_copy_to_host(void *dst, const vbs_buffer_t *src, size_t bytes) {
     if (!g_ready || !dst || !src) return false;
+    if (!flush_pending()) return false;
     return g_lib.copy_d2h(dst, src->internal_handle, bytes) ? true : lib_fail("copy_to_host");
+}
+
+/* ---- one held-back op ----------------------------------------------------
+ * The bridge issues each token step as ~16 ops per layer (NORMALIZE, LINEAR,
+ * ROTARY, ..., src/vbs_specializer.c:270-349), and at this size each
+ * separate launch costs about as much as its work. The shim therefore holds
+ * back the last NORMALIZE or resident LINEAR and joins it with the next op
+ * when one fused kernel does both (vbs_gfx950_linear_fused):
+ *   NORMALIZE, then a LINEAR reading its output   -> RMSNorm + matvec
+ *   LINEAR, then ROTARY of its output (in place)  -> matvec + RoPE (with the
+ *                                                    RMSNorm too if it was held)
+ *   LINEAR, then ELEMENTWISE a = a + its output   -> matvec + add
+ * Each result is bit-identical to the ops run one by one, and every buffer the
+ * ops write is written (the normalised x, the linear's own output). Any other
+ * op, copy, free or synchronize first issues what is held, so the ordering the
+ * caller sees is the one it asked for; an error of a held op is reported by
+ * the call that issues it. One host thread drives the table (as the reference
+ * assumes, src/vbs_hotpath.c:3-5). */
+typedef enum { PEND_NONE = 0, PEND_NORM, PEND_LINEAR } pend_kind_t;
+
+typedef struct {
+    pend_kind_t kind;
+    int has_norm;                    /* PEND_LINEAR: a held NORMALIZE joined it */
+    const float *n_in, *n_w;         /* NORMALIZE (in, w, out, dim, eps) */
+    float *n_out;
+    uint32_t n_dim;
+    float n_eps;
+    int type;                        /* LINEAR (convention A, no offsets) */
+    const void *w;
+    const float *x;
+    float *y;
+    uint32_t cols, rows;
+} pending_t;
+
+static pending_t g_pend;
+
+static bool run_norm(const pending_t *p) {
+    return g_lib.rms_norm(p->n_in, p->n_w, p->n_out, p->n_dim, p->n_eps) ? true
+                                                                         : lib_fail("normalize");
+}
+
+static bool run_linear(const pending_t *p) {
+    if (p->has_norm && !run_norm(p)) return false;
+    return g_lib.linear(p->type, p->w, p->x, p->y, p->cols, p->rows, 0, 0, 0) ? true
+                                                                              : lib_fail("linear tile");
+}
+
+/* The held op joined with a following ROTARY (rope) or ELEMENTWISE add
+ * (acc); false with the reason on an error. Falls back to the ops one by one
+ * (the held one here, the caller's after) when no fused kernel fits: *done
+ * tells the caller whether its op was part of the launch. */
+static bool run_fused(pending_t *p, float *acc, int rope, uint32_t pos, uint32_t hd, float theta,
+                      bool *done) {
+    *done = false;
+    const int r = g_lib.linear_fused(p->type, p->w, p->has_norm ? p->n_in : p->x, p->y, p->cols,
+                                     p->rows, p->has_norm ? p->n_w : NULL, p->n_eps,
+                                     p->has_norm ? p->n_out : NULL, acc, rope, pos, hd, theta);
+    if (r == 1) {
+        *done = true;
+        return true;
+    }
+    if (r == 0) return lib_fail("linear tile (fused)");
+    return run_linear(p);
+}
+
+static bool flush_pending(void) {
+    pending_t p = g_pend;
+    g_pend.kind = PEND_NONE;
+    switch (p.kind) {
+        case PEND_NORM: return run_norm(&p);
+        case PEND_LINEAR:
+            if (p.has_norm) {
+                const int r = g_lib.linear_fused(p.type, p.w, p.n_in, p.y, p.cols, p.rows, p.n_w,
+                                                 p.n_eps, p.n_out, NULL, 0, 0, 0, 0.f);
+                if (r == 1) return true;
+                if (r == 0) return lib_fail("linear tile (fused)");
+            }
+            return run_linear(&p);
+        default: return true;
+    }
 }
 
 /* ---- pipelines ---------------------------------------------------------- */
@@ -352,11 +439,40 @@ static bool gfx950_dispatch_linear_tile(vbs_device_t *dev, void *pipeline, vbs_b
             set_err("linear tile: window smaller than the %llu-byte tile", (unsigned long long)need);
             return false;
         }
+        if (!flush_pending()) return false;
         if (!g_lib.copy_h2d(wp->internal_handle, ws->host_ptr, (size_t)need))
             return lib_fail("linear tile upload");
     }
-    if (!g_lib.linear((int)p->type, wp->internal_handle, (const float *)in->internal_handle,
-                      (float *)out->internal_handle, cols, rows, col_off, row_off,
+    const float *x = (const float *)in->internal_handle;
+    float *y = (float *)out->internal_handle;
+    if (!ws && !col_off && !row_off && !accumulate && need && wp->internal_handle && x && y &&
+        (const float *)y != x) {
+        /* convention A, the bridge's resident matvec: held back for the next op */
+        pending_t n = {0};
+        n.kind = PEND_LINEAR;
+        n.type = (int)p->type;
+        n.w = wp->internal_handle;
+        n.x = x;
+        n.y = y;
+        n.cols = cols;
+        n.rows = rows;
+        if (g_pend.kind == PEND_NORM && x == g_pend.n_out && cols == g_pend.n_dim &&
+            g_pend.n_in != (const float *)g_pend.n_out && (const float *)y != g_pend.n_in &&
+            y != g_pend.n_out) {
+            n.has_norm = 1;
+            n.n_in = g_pend.n_in;
+            n.n_w = g_pend.n_w;
+            n.n_out = g_pend.n_out;
+            n.n_dim = g_pend.n_dim;
+            n.n_eps = g_pend.n_eps;
+        } else if (!flush_pending()) {
+            return false;
+        }
+        g_pend = n;
+        return true;
+    }
+    if (!flush_pending()) return false;
+    if (!g_lib.linear((int)p->type, wp->internal_handle, x, y, cols, rows, col_off, row_off,
                       accumulate ? 1 : 0))
         return lib_fail("linear tile");
     return true;
@@ -398,6 +514,7 @@ bool vbs_hip_dispatch_linear_batch(vbs_device_t *dev, void *pipeline, vbs_buffer
                 type_name(p->type), rows, cols, batch);
         return false;
     }
+    if (!flush_pending()) return false;
     if (!g_lib.linear_batch((int)p->type, w->internal_handle, (const float *)x->internal_handle,
                             x_stride, (float *)y->internal_handle, y_stride, cols, rows, batch))
         return lib_fail("linear batch");
@@ -443,6 +560,44 @@ static bool gfx950_dispatch_primitive(vbs_device_t *dev, void *pipeline, const v
             return false;
         }
     }
+    /* the held op joined with this one, or held itself (NORMALIZE) */
+    if (pp->base.kind == VBS_OP_NORMALIZE && BUF(0) != BUF(2)) {
+        if (!flush_pending()) return false;
+        pending_t n = {0};
+        n.kind = PEND_NORM;
+        n.n_in = (const float *)BUF(0);
+        n.n_w = (const float *)BUF(1);
+        n.n_out = (float *)BUF(2);
+        n.n_dim = U32(3);
+        n.n_eps = F32(4);
+        g_pend = n;
+        return true;
+    }
+    if (g_pend.kind == PEND_LINEAR) {
+        pending_t *h = &g_pend;
+        bool joined = false, done = false;
+        if (pp->base.kind == VBS_OP_ROTARY && (float *)BUF(0) == h->y &&
+            (uint64_t)U32(2) * U32(3) == h->rows) {
+            joined = true;
+            if (!run_fused(h, NULL, 1, U32(1), U32(2), F32(4), &done)) {
+                h->kind = PEND_NONE;
+                return false;
+            }
+        } else if (pp->base.kind == VBS_OP_ELEMENTWISE && !h->has_norm && BUF(1) == h->y &&
+                   BUF(2) == BUF(0) && BUF(0) != h->y && (const float *)BUF(0) != h->x &&
+                   U32(3) == h->rows) {
+            joined = true;
+            if (!run_fused(h, (float *)BUF(0), 0, 0, 0, 0.f, &done)) {
+                h->kind = PEND_NONE;
+                return false;
+            }
+        }
+        if (joined) {
+            h->kind = PEND_NONE;
+            if (done) return true;  /* else: the held op ran alone, this one follows */
+        }
+    }
+    if (!flush_pending()) return false;
     int ok = 0;
     switch (pp->base.kind) {
         case VBS_OP_EMBEDDING:
@@ -482,7 +637,7 @@ static bool gfx950_dispatch_primitive(vbs_device_t *dev, void *pipeline, const v
 
 static void gfx950_synchronize(vbs_device_t *dev) {
     (void)dev;
-    if (g_ready && !g_lib.synchronize()) lib_fail("synchronize");
+    if (g_ready && flush_pending() && !g_lib.synchronize()) lib_fail("synchronize");
 }
 
 const vbs_backend_ops_t g_vbs_hip_backend = {

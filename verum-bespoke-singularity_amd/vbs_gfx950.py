@@ -139,6 +139,7 @@ _DEVICE_SIGS = {
     "linear": (_I, [_I, _P, _P, _P, _U32, _U32, _U32, _U32, _I]),
     "embed": (_I, [_I, _P, _U32, _P, _U32]),
     "rms_norm": (_I, [_P, _P, _P, _U32, _F]),
+    "linear_fused": (_I, [_I, _P, _P, _P, _U32, _U32, _P, _F, _P, _P, _I, _U32, _U32, _F]),
     "rope": (_I, [_P, _U32, _U32, _U32, _F]),
     "cache_store": (_I, [_P, _P, _P, _P, _U32, _U32, _U32, _U32]),
     "attention": (_I, [_P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, _U32, _F]),
