@@ -951,6 +951,7 @@ static hipError_t launch_ks(const MvArgs &a, const MvPlan &p, uint32_t wgs, hipS
     }
     if constexpr (EPI == E_QKV) {  // the Q/K/V plans of launch_plan
         if (TPW == 2u && p.ks == 1u) VBS_MV(1, 1024);
+        if (TPW == 1u && p.ks == 1u) VBS_MV(1, 1024);
         if (TPW == 1u && p.ks == 8u && p.nw <= 4u) VBS_MV(8, 256);
     }
     VBS_MV(8, 1024);
@@ -997,6 +998,9 @@ static hipError_t launch_plan(const MvArgs &a, hipStream_t s) {
         if (nblk <= 16u) {
             p.ks = 1u;
             p.nw = nblk;
+            // a few tiles (the shim's K + RoPE, 64 tiles): one per workgroup,
+            // else two per workgroup would leave most CUs idle
+            if (total < device_cus()) return launch_ks<T, NORM, EPI, 1>(a, p, total, s);
             return launch_ks<T, NORM, EPI, 2>(a, p, (total + 1u) / 2u, s);
         }
         if (nblk <= 32u) {
