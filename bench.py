@@ -37,8 +37,15 @@ decoder (vbs_gfx950_decoder_*), and through the g_vbs_hip_backend ops table
 with one dispatch per bridge call. The decode entry's `checked` block comes
 from the CPU leg, after every GPU timing: the decoded tokens against the
 reference CPU backend's 128 for the same model and start
-(tests/golden/decode_7b_greedy.npz), and the first four against the oracle's
-forward pass run on the host.
+(tests/golden/decode_7b_greedy.npz), the first four against the oracle's
+forward pass run on the host, and `checked.cpu_baseline`, the same decode on
+the host: one full token of the reference CPU backend on one thread (driven
+through its ops table in the bridge's order) and, as `all_cores`, the
+oracle's forward pass on every core.
+
+roofline.ceiling.read_floor.variants: the same 25 MB read with two
+workgroups per CU and with register loads instead of LDS DMA, timed like the
+matvec, to show how tight the read floor is.
 """
 import argparse
 import ctypes as C
