@@ -646,7 +646,8 @@ def bench_decode(dev, host, n_tokens, path="both", geo=GEO_7B, n_layers=32, ctx=
     and, for comparison, the per-dispatch ops-table path."""
     n_dispatch_tokens = min(n_dispatch_tokens, n_tokens)
     t_build = time.perf_counter()
-    model = V.SynthModel(host, n_layers=n_layers, **geo, max_ctx=ctx + n_tokens + 1, seed=seed)
+    steps = max(n_tokens, batch_tokens if batch else 0)  # the cache covers both runs
+    model = V.SynthModel(host, n_layers=n_layers, **geo, max_ctx=ctx + steps + 1, seed=seed)
     kc, vc = model.kv_prefill(host, ctx)
     be = V.gfx950_backend()
     if not be.init():
