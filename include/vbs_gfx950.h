@@ -140,24 +140,44 @@ int vbs_gfx950_add(const float *a, const float *b, float *out, uint32_t n);
 int vbs_gfx950_dequant_rows(int type, const void *w, const uint32_t *ids, uint32_t n_rows,
                             uint32_t dim, float *out);
 
-/* The linear matvec fused with its neighbour in the bridge's op sequence, for
- * the backend shim's per-dispatch path (no counterpart in the reference: the
- * shim holds back one op and joins it with the next when they fit one of these
- * kernels; results are bit-identical to the ops one by one):
- *   - norm_w and x_normed non-NULL: the NORMALIZE before it, x_normed =
- *     rms_norm(x, norm_w, eps) (stored, as that op would), then y = W x_normed;
- *   - acc non-NULL: the ELEMENTWISE add after it, y = W x, acc = acc + y;
- *   - rope non-zero: the ROTARY after it, y = W x rotated at `pos` in heads of
- *     head_dim with base theta (src/vbs_host_math.h:38-51), with or without
- *     the RMSNorm in front.
- * Q4_K and Q6_K rows of a multiple of 256; returns 1 when launched, 0 with a
- * reason on an error, and 2 (nothing launched) when no fused kernel takes
- * this combination or shape. The RoPE rows live in a device table the library
- * builds for (theta, head_dim) and regrows for later positions (it allocates;
- * not for graph capture). */
+/* The neighbours of a linear matvec that vbs_gfx950_linear_fused takes into
+ * the same launch; NULL / 0 fields are absent. */
+typedef struct vbs_gfx950_linear_join {
+    const float *norm_w;   /* NORMALIZE before: x_normed = rms_norm(x, norm_w, norm_eps) */
+    float norm_eps;
+    float *x_normed;
+    float *acc;            /* ELEMENTWISE after: acc = acc + y */
+    int rope;              /* ROTARY after: y rotated at pos in heads of head_dim, base theta */
+    uint32_t pos, head_dim;
+    float theta;
+    const float *gate;     /* ACTIVATION after: hidden = silu(gate) * y */
+    float *hidden;
+    const float *k_row;    /* CACHE after: kc[kv_off + i] = f16(k_row[i]), vc[kv_off + i] = f16(y[i]) */
+    uint16_t *kc, *vc;
+    uint64_t kv_off;       /* (layer * max_ctx + pos) * kv_dim */
+} vbs_gfx950_linear_join_t;
+
+/* The linear matvec y = W x fused with its neighbours in the bridge's op
+ * sequence, for the backend shim's per-dispatch path (no counterpart in the
+ * reference: the shim holds back one op and joins it with the next when they
+ * fit one of these kernels; results are bit-identical to the ops one by one,
+ * and y is always written):
+ *   - norm_w and x_normed: the NORMALIZE before it (src/vbs_host_math.h:28-36),
+ *     x_normed stored as that op would, then y = W x_normed; alone or with rope;
+ *   - acc: the ELEMENTWISE add after it (src/vbs_host_math.h:59-62);
+ *   - rope: the ROTARY after it (src/vbs_host_math.h:38-51);
+ *   - gate and hidden: the ACTIVATION after the up matvec
+ *     (src/vbs_host_math.h:53-57);
+ *   - k_row, kc, vc: the CACHE after the V matvec, with the reference's f16
+ *     rounding (src/vbs_host_math.h:150-159).
+ * At most one of acc / rope / gate / k_row. Q4_K and Q6_K rows of a multiple
+ * of 256; returns 1 when launched, 0 with a reason on an error, and 2
+ * (nothing launched) when no fused kernel takes this combination or shape.
+ * The RoPE rows live in a device table the library builds for (theta,
+ * head_dim) and regrows for later positions (it allocates; not for graph
+ * capture). */
 int vbs_gfx950_linear_fused(int type, const void *w, const float *x, float *y, uint32_t cols,
-                            uint32_t rows, const float *norm_w, float eps, float *x_normed,
-                            float *acc, int rope, uint32_t pos, uint32_t head_dim, float theta);
+                            uint32_t rows, const vbs_gfx950_linear_join_t *join);
 
 /* Batched decode: Y[b*y_stride + r] = sum_c deq(W[r,c]) * X[b*x_stride + c]
  * for b < batch (<= 16). Equal to `batch` calls of vbs_gfx950_linear; the

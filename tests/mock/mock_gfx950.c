@@ -82,27 +82,33 @@ int vbs_gfx950_add(const float *a, const float *b, float *out, uint32_t n) {
 }
 #endif
 /* The fused neighbours of a linear (vbs_gfx950_linear_fused) as the ops one
- * by one; like the device library, only for Q4_K and Q6_K (else 2: nothing
- * done, the shim issues the ops itself). */
-static unsigned g_fused[3]; /* launches joined with a NORMALIZE, a ROTARY, an add */
-unsigned mock_fused_count(int which) { return which >= 0 && which < 3 ? g_fused[which] : 0u; }
+ * by one; like the device library, only for Q4_K and Q6_K and for the same
+ * combinations (else 2: nothing done, the shim issues the ops itself). */
+static unsigned g_fused[5]; /* launches joined with a NORMALIZE, ROTARY, add, ACTIVATION, CACHE */
+unsigned mock_fused_count(int which) { return which >= 0 && which < 5 ? g_fused[which] : 0u; }
 
 int vbs_gfx950_linear_fused(int t, const void *w, const float *x, float *y, uint32_t cols,
-                            uint32_t rows, const float *norm_w, float eps, float *x_normed,
-                            float *acc, int rope, uint32_t pos, uint32_t hd, float theta) {
+                            uint32_t rows, const vbs_gfx950_linear_join_t *j) {
+    if (!j) return 0;
+    if ((j->norm_w != NULL) != (j->x_normed != NULL) || (j->gate != NULL) != (j->hidden != NULL) ||
+        (j->k_row != NULL) != (j->kc != NULL) || (j->k_row != NULL) != (j->vc != NULL))
+        return 0;
     if (t != 12 && t != 14) return 2;
-    if ((norm_w != NULL) != (x_normed != NULL) || (acc && (norm_w || rope)) ||
-        (!acc && !norm_w && !rope))
-        return 2;
-    if (norm_w) {
-        vbs_oracle_rms_norm(x, norm_w, x_normed, cols, eps);
-        x = x_normed;
+    const int after = (j->acc != NULL) + (j->rope != 0) + (j->gate != NULL) + (j->k_row != NULL);
+    if (after > 1 || (!after && !j->norm_w) || (j->norm_w && after && !j->rope)) return 2;
+    if (j->norm_w) {
+        vbs_oracle_rms_norm(x, j->norm_w, j->x_normed, cols, j->norm_eps);
+        x = j->x_normed;
     }
     if (!vbs_oracle_linear_tile(t, (const uint8_t *)w, x, y, cols, rows, 0, 0, 0)) return 0;
-    if (rope) vbs_oracle_rope(y, pos, hd, rows / hd, theta);
-    if (acc) vbs_oracle_add(acc, y, acc, rows);
-    g_fused[0] += norm_w != NULL;
-    g_fused[1] += rope != 0;
-    g_fused[2] += acc != NULL;
+    if (j->rope) vbs_oracle_rope(y, j->pos, j->head_dim, rows / j->head_dim, j->theta);
+    if (j->acc) vbs_oracle_add(j->acc, y, j->acc, rows);
+    if (j->gate) vbs_oracle_silu_mul(j->gate, y, j->hidden, rows);
+    if (j->k_row) vbs_oracle_cache_store(j->k_row, y, j->kc + j->kv_off, j->vc + j->kv_off, 0, 0, 1, rows);
+    g_fused[0] += j->norm_w != NULL;
+    g_fused[1] += j->rope != 0;
+    g_fused[2] += j->acc != NULL;
+    g_fused[3] += j->gate != NULL;
+    g_fused[4] += j->k_row != NULL;
     return 1;
 }

@@ -167,13 +167,14 @@ def test_backend_suite_through_shim_on_host_mock(tmpdir_mod, host):
 @pytest.mark.parametrize("mix", ["q4k_m", "q8_0"])
 def test_held_ops_on_host_mock_keep_the_bridge_results(tmpdir_mod, host, mix):
     """The shim holds back one NORMALIZE or LINEAR and joins it with the next
-    op (RMSNorm + matvec, matvec + RoPE, matvec + add) when
-    vbs_gfx950_linear_fused takes the combination. Over the host mock (whose
-    fused entry composes the oracle's ops, and declines every type but Q4_K
-    and Q6_K, so the Q8_0 model runs the ops one by one) the bridge-order
-    decode driver's logits equal the oracle's forward pass bit for bit at
-    every step, and with Q4_K the joins happened: per layer the two RMSNorms,
-    the Q and K RoPEs and the two residual adds."""
+    op (RMSNorm + matvec, matvec + RoPE, + add, + SiLU gate, + K/V store)
+    when vbs_gfx950_linear_fused takes the combination. Over the host mock
+    (whose fused entry composes the oracle's ops, and declines every type but
+    Q4_K and Q6_K, so the Q8_0 model runs the ops one by one) the
+    bridge-order decode driver's logits equal the oracle's forward pass bit
+    for bit at every step, and with K-quants the joins happened: per layer
+    the two RMSNorms, the Q and K RoPEs, the two residual adds, the SiLU gate
+    after the up matvec and the cache store after the V matvec."""
     from test_decode import TINY, full_cache
     so = build_mock(tmpdir_mod, f"mock_fuse_{mix}.so")
     be, ok = fresh_shim(tmpdir_mod, so)
@@ -187,7 +188,7 @@ def test_held_ops_on_host_mock_keep_the_bridge_results(tmpdir_mod, host, mix):
     orc = Oracle()
     kc, vc = full_cache(model, None, None, 0)
     om = orc.model(model, kc, vc)
-    before = [mock.mock_fused_count(i) for i in range(3)]
+    before = [mock.mock_fused_count(i) for i in range(5)]
     tok = 1
     for pos in range(6):
         got = d.step(tok, pos)
@@ -195,13 +196,13 @@ def test_held_ops_on_host_mock_keep_the_bridge_results(tmpdir_mod, host, mix):
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), pos
         tok = int(np.argmax(want))
     d.close()
-    joined = [mock.mock_fused_count(i) - before[i] for i in range(3)]
+    joined = [mock.mock_fused_count(i) - before[i] for i in range(5)]
     L = TINY["n_layers"]
     if mix == "q4k_m":
         # norms: attn + ffn per layer, and the output norm before the lm_head
-        assert joined == [6 * (2 * L + 1), 6 * 2 * L, 6 * 2 * L], joined
+        assert joined == [6 * (2 * L + 1), 6 * 2 * L, 6 * 2 * L, 6 * L, 6 * L], joined
     else:
-        assert joined == [0, 0, 0], joined
+        assert joined == [0] * 5, joined
 
 
 def test_shim_marshalling_rejects_malformed_arguments(tmpdir_mod):

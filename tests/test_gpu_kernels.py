@@ -167,6 +167,93 @@ def test_q4k_two_tile_plan(dev, host, oracle, mem, rows, cols, accumulate):
     assert lin_err(got, want) <= LIN_TOL
 
 
+@pytest.mark.parametrize("t,rows,cols", [(V.Q4_K, 4096, 4096), (V.Q4_K, 1024, 4096),
+                                         (V.Q4_K, 11008, 4096), (V.Q4_K, 4096, 11008),
+                                         (V.Q6_K, 4096, 4096), (V.Q6_K, 4096, 11008)],
+                         ids=["q4k_4096x4096", "q4k_1024x4096", "q4k_11008x4096",
+                              "q4k_4096x11008", "q6k_4096x4096", "q6k_4096x11008"])
+@pytest.mark.parametrize("join", ["norm", "rope", "norm_rope", "acc", "silu", "cache"])
+def test_linear_fused_equals_ops_one_by_one(dev, host, mem, t, rows, cols, join):
+    """vbs_gfx950_linear_fused with each neighbour it takes (the RMSNorm
+    before, the RoPE, residual add, SiLU gate or f16 K/V store after) writes
+    the same bits, to every buffer, as the device library's ops issued one by
+    one: the matvec, the normalised x, the rotated rows, the accumulator, the
+    hidden vector and both cache rows. The shapes cover the LDS-DMA Q4_K
+    kernel (16-block rows), the matrix-core fallback (1024 rows, 43-block
+    rows) and the Q6_K ring kernel (the add after a 43-block Q6_K row)."""
+    hd, pos, theta, eps = 128, 2175, 500000.0, 1e-5
+    layer, max_ctx = 1, 2200
+    w = V.synth_matrix(host, t, rows, cols, SEED, 131)
+    x = synth_x(host, cols, 132) * 1.7
+    nw = synth_x(host, cols, 133)
+    acc0 = synth_x(host, rows, 134)
+    gate = synth_x(host, rows, 135) * 3.0
+    krow = synth_x(host, rows, 136) * 40.0
+    pw, px, pnw, pg, pk = mem.up(w), mem.up(x), mem.up(nw), mem.up(gate), mem.up(krow)
+    norm = join in ("norm", "norm_rope")
+    cache_elems = 2 * max_ctx * rows
+
+    def buffers():
+        return dict(y=mem.zeros(rows), xn=mem.zeros(cols), acc=mem.up(acc0), hid=mem.zeros(rows),
+                    kc=mem.zeros(cache_elems, np.uint16), vc=mem.zeros(cache_elems, np.uint16))
+
+    ref, fus = buffers(), buffers()
+    # the ops one by one
+    xin = px
+    if norm:
+        dev.rms_norm(px, pnw, ref["xn"], cols, eps)
+        xin = ref["xn"]
+    dev.linear(t, pw, xin, ref["y"], cols, rows)
+    if join in ("rope", "norm_rope"):
+        dev.rope(ref["y"], pos, hd, rows // hd, theta)
+    elif join == "acc":
+        dev.add(ref["acc"], ref["y"], ref["acc"], rows)
+    elif join == "silu":
+        dev.silu_mul(pg, ref["y"], ref["hid"], rows)
+    elif join == "cache":
+        dev.cache_store(pk, ref["y"], ref["kc"], ref["vc"], pos, layer, max_ctx, rows)
+    # one launch
+    j = {}
+    if norm:
+        j.update(norm_w=pnw, norm_eps=eps, x_normed=fus["xn"])
+    if join in ("rope", "norm_rope"):
+        j.update(rope=1, pos=pos, head_dim=hd, theta=theta)
+    elif join == "acc":
+        j.update(acc=fus["acc"])
+    elif join == "silu":
+        j.update(gate=pg, hidden=fus["hid"])
+    elif join == "cache":
+        j.update(k_row=pk, kc=fus["kc"], vc=fus["vc"], kv_off=(layer * max_ctx + pos) * rows)
+    assert dev.linear_fused(t, pw, px, fus["y"], cols, rows, **j)
+    for name, n, dt in (("y", rows, np.float32), ("xn", cols, np.float32),
+                        ("acc", rows, np.float32), ("hid", rows, np.float32),
+                        ("kc", cache_elems, np.uint16), ("vc", cache_elems, np.uint16)):
+        a = dev.download(ref[name], n, dt)
+        b = dev.download(fus[name], n, dt)
+        assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), name
+
+
+def test_linear_fused_declines_and_rejects(dev, host, mem):
+    """Combinations no fused kernel takes come back as 2 (nothing launched,
+    y untouched); half-given neighbours are errors."""
+    rows, cols = 4096, 4096
+    w = V.synth_matrix(host, V.Q4_K, rows, cols, SEED, 141)
+    pw, px, py = mem.up(w), mem.up(synth_x(host, cols, 142)), mem.up(np.full(rows, 7.0, np.float32))
+    pa, pn = mem.zeros(rows), mem.up(synth_x(host, cols, 143))
+    xn = mem.zeros(cols)
+    declined = [dict(), dict(acc=pa, rope=1, pos=0, head_dim=128, theta=1e4),
+                dict(norm_w=pn, x_normed=xn, acc=pa), dict(gate=pa, hidden=pa, acc=pa),
+                dict(rope=1, pos=0, head_dim=96, theta=1e4)]
+    for j in declined:
+        assert not dev.linear_fused(V.Q4_K, pw, px, py, cols, rows, **j), j
+    qw = mem.up(V.synth_matrix(host, V.Q8_0, rows, cols, SEED, 144))
+    assert not dev.linear_fused(V.Q8_0, qw, px, py, cols, rows, acc=pa)
+    assert np.all(dev.download(py, rows, np.float32) == 7.0)
+    for j in (dict(norm_w=pn), dict(gate=pa), dict(k_row=pa, kc=pa)):
+        with pytest.raises(V.GpuError):
+            dev.linear_fused(V.Q4_K, pw, px, py, cols, rows, **j)
+
+
 @pytest.mark.parametrize("t", [V.Q4_K, V.Q6_K, V.Q8_0, V.Q4_0], ids=lambda t: V.TYPE_NAMES[t])
 def test_linear_activation_edge_cases(dev, host, oracle, mem, t):
     """x with all-zero sub-blocks, 1e4 outliers, subnormal-scale blocks and

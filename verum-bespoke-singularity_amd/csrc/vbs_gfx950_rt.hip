@@ -426,28 +426,49 @@ static bool rope_rows(float theta, uint32_t hd, uint32_t pos) {
 }
 
 int vbs_gfx950_linear_fused(int type, const void *w, const float *x, float *y, uint32_t cols,
-                            uint32_t rows, const float *norm_w, float eps, float *x_normed,
-                            float *acc, int rope, uint32_t pos, uint32_t head_dim, float theta) {
+                            uint32_t rows, const vbs_gfx950_linear_join_t *join) {
     if (!ready_or_fail()) return 0;
-    if (!w || !x || !y) return fail("linear_fused: null pointer");
+    if (!w || !x || !y || !join) return fail("linear_fused: null pointer");
+    const vbs_gfx950_linear_join_t &jn = *join;
+    if ((jn.norm_w != nullptr) != (jn.x_normed != nullptr))
+        return fail("linear_fused: the RMSNorm needs both its weights and its output");
+    if ((jn.gate != nullptr) != (jn.hidden != nullptr))
+        return fail("linear_fused: the activation needs both its gate and its output");
+    if ((jn.k_row != nullptr) != (jn.kc != nullptr) || (jn.k_row != nullptr) != (jn.vc != nullptr))
+        return fail("linear_fused: the cache store needs the k row and both caches");
     if (type != kQ4_K && type != kQ6_K) return 2;
     if (cols % 256u || rows == 0) return 2;
-    if ((norm_w != nullptr) != (x_normed != nullptr))
-        return fail("linear_fused: the RMSNorm needs both its weights and its output");
-    if (acc && (norm_w || rope)) return 2;
-    if (!acc && !norm_w && !rope) return 2;
-    const float2 *rt_rope = nullptr;
-    const uint32_t *rt_pos = nullptr;
-    if (rope) {
-        if (head_dim == 0 || (head_dim & 3u) || head_dim > 256u || rows % head_dim) return 2;
-        if (!rope_rows(theta, head_dim, pos)) return fail("linear_fused: RoPE table allocation failed");
-        rt_rope = g_rope.tab;
-        rt_pos = g_rope.pos + pos;
+    const int n_after = (jn.acc != nullptr) + (jn.rope != 0) + (jn.gate != nullptr) +
+                        (jn.k_row != nullptr);
+    if (n_after > 1 || (!n_after && !jn.norm_w)) return 2;
+    if (jn.norm_w && n_after && !jn.rope) return 2;
+    LinJoin lj;
+    lj.norm_w = jn.norm_w;
+    lj.eps = jn.norm_eps;
+    lj.xn = jn.x_normed;
+    if (jn.rope) {
+        if (jn.head_dim == 0 || (jn.head_dim & 3u) || jn.head_dim > 256u || rows % jn.head_dim)
+            return 2;
+        if (!rope_rows(jn.theta, jn.head_dim, jn.pos))
+            return fail("linear_fused: RoPE table allocation failed");
+        lj.rope = g_rope.tab;
+        lj.pos = g_rope.pos + jn.pos;
+        lj.hd = jn.head_dim;
     }
+    lj.gate_in = jn.gate;
+    lj.hid = jn.hidden;
+    lj.kin = jn.k_row;
+    lj.kc = jn.kc;
+    lj.vc = jn.vc;
+    lj.kv_off = jn.kv_off;
     // with the add, the kernels accumulate into acc and copy the row values to y
-    const hipError_t e = launch_kq_linear_fused(type, (const uint8_t *)w, x, acc ? acc : y, cols, rows,
-                                                norm_w, eps, x_normed, acc ? y : nullptr, rt_rope,
-                                                rt_pos, rope ? head_dim : 0u, g_rt.stream);
+    float *dst = y;
+    if (jn.acc) {
+        dst = jn.acc;
+        lj.ycopy = y;
+    }
+    const hipError_t e = launch_kq_linear_fused(type, (const uint8_t *)w, x, dst, cols, rows, lj,
+                                                g_rt.stream);
     if (e == hipErrorNotSupported) return 2;
     return hip_ok(e, "linear_fused");
 }

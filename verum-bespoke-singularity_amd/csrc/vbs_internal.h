@@ -109,17 +109,29 @@ hipError_t launch_q4k_mvl(const uint8_t *w, const float *x, float *y, uint32_t c
 // NULL) also receives each row value before it is added.
 hipError_t launch_q6k_mvr(const uint8_t *w, const float *x, float *y, uint32_t cols, uint32_t rows,
                           int accumulate, hipStream_t s, float *ycopy = nullptr);
-// The linear op fused with its neighbour in the bridge's op sequence (the
+// The linear op fused with its neighbours in the bridge's op sequence (the
 // backend shim's dispatch path, vbs_gfx950_linear_fused): norm_w / eps / xn
 // (RMSNorm in front, the normalised x stored to xn), ycopy (y = y + W x, W x
 // also stored to ycopy), rope / pos / hd (the result rotated at the device
-// position *pos, as the ROTARY op after it); Q4_K and Q6_K only,
-// hipErrorNotSupported (nothing launched) outside the shapes the fused
-// kernels take.
+// position *pos, as the ROTARY op after it), gate_in / hid (hid =
+// silu(gate_in) * W x, the ACTIVATION op after the up matvec), kin / kc / vc
+// / kv_off (the CACHE op after the V matvec: f16(W x) to vc and f16(kin) to
+// kc at kv_off). Q4_K and Q6_K only; hipErrorNotSupported (nothing launched)
+// outside the combinations and shapes the fused kernels take.
+struct LinJoin {
+    const float *norm_w = nullptr;
+    float eps = 0.f;
+    float *xn = nullptr, *ycopy = nullptr;
+    const float2 *rope = nullptr;
+    const uint32_t *pos = nullptr;
+    uint32_t hd = 0;
+    const float *gate_in = nullptr, *kin = nullptr;
+    float *hid = nullptr;
+    uint16_t *kc = nullptr, *vc = nullptr;
+    uint64_t kv_off = 0;
+};
 hipError_t launch_kq_linear_fused(int type, const uint8_t *w, const float *x, float *y, uint32_t cols,
-                                  uint32_t rows, const float *norm_w, float eps, float *xn,
-                                  float *ycopy, const float2 *rope, const uint32_t *pos, uint32_t hd,
-                                  hipStream_t s);
+                                  uint32_t rows, const LinJoin &j, hipStream_t s);
 // Specialised Q4_K matvec; hipErrorNotSupported when the shape/alignment is
 // outside its range (the generic kernel then runs).
 hipError_t launch_q4k_fast(const uint8_t *w, const float *x, float *y, uint32_t cols,

@@ -52,18 +52,13 @@ hipError_t launch_kq_norm_linear(int type, const uint8_t *w, const float *x, con
 }
 
 hipError_t launch_kq_linear_fused(int type, const uint8_t *w, const float *x, float *y, uint32_t cols,
-                                  uint32_t rows, const float *norm_w, float eps, float *xn,
-                                  float *ycopy, const float2 *rope, const uint32_t *pos, uint32_t hd,
-                                  hipStream_t s) {
+                                  uint32_t rows, const LinJoin &j, hipStream_t s) {
     if (rows == 0 || !mv_fits(type, w, x, cols, rows)) return hipErrorNotSupported;
-    MvArgs ex{};
-    ex.norm_w = norm_w;
-    ex.eps = eps;
-    ex.xn = xn;
-    ex.ycopy = ycopy;
-    ex.rope = rope;
-    ex.pos = pos;
-    ex.hd = hd;
+    const bool store_join = j.hid || j.kin;
+    const int n_after = (j.ycopy != nullptr) + (j.rope != nullptr) + (int)store_join;
+    if (n_after > 1 || (j.hid && j.kin) || (j.norm_w && (j.ycopy || store_join)) ||
+        (!j.norm_w && !n_after))
+        return hipErrorNotSupported;
     MvArgs a{};
     a.w[0] = w;
     a.y[0] = y;
@@ -71,14 +66,14 @@ hipError_t launch_kq_linear_fused(int type, const uint8_t *w, const float *x, fl
     a.nmat = 1;
     a.cols = cols;
     a.x = x;
-    a.norm_w = ex.norm_w;
-    a.eps = ex.eps;
-    a.xn = ex.xn;
-    if (ex.rope) {  // the q path of E_QKV: the row value rotated at *pos, stored as f32
-        if (ex.ycopy || (rows & 1u) || (ex.hd & 1u) || !ex.hd || rows % ex.hd) return hipErrorNotSupported;
-        a.rope = ex.rope;
-        a.pos = ex.pos;
-        a.hd = ex.hd;
+    a.norm_w = j.norm_w;
+    a.eps = j.eps;
+    a.xn = j.xn;
+    if (j.rope) {  // the q path of E_QKV: the row value rotated at *pos, stored as f32
+        if ((rows & 1u) || (j.hd & 1u) || !j.hd || rows % j.hd) return hipErrorNotSupported;
+        a.rope = j.rope;
+        a.pos = j.pos;
+        a.hd = j.hd;
         a.role0 = 0;
         if (type == kQ4_K) {
             const hipError_t e = launch_q4k_mvl_qkv(a, s);
@@ -87,20 +82,24 @@ hipError_t launch_kq_linear_fused(int type, const uint8_t *w, const float *x, fl
         set_tiles(a);
         return a.norm_w ? launch_type<true, E_QKV>(type, a, s) : launch_type<false, E_QKV>(type, a, s);
     }
-    if (ex.norm_w) {
-        if (ex.ycopy) return hipErrorNotSupported;
+    a.gate_in = j.gate_in;
+    a.hid = j.hid;
+    a.kin = j.kin;
+    a.kc = j.kc;
+    a.vc = j.vc;
+    a.kv_layer = j.kv_off;
+    if (j.norm_w || store_join) {  // E_STORE with the RMSNorm in front or a store join after
         if (type == kQ4_K) {
             const hipError_t e = launch_q4k_mvl(w, x, y, cols, rows, 0, s, &a);
             if (e != hipErrorNotSupported) return e;
         }
         set_tiles(a);
-        return launch_type<true, E_STORE>(type, a, s);
+        return j.norm_w ? launch_type<true, E_STORE>(type, a, s) : launch_type<false, E_STORE>(type, a, s);
     }
-    if (!ex.ycopy) return hipErrorNotSupported;
-    a.ycopy = ex.ycopy;
+    a.ycopy = j.ycopy;
     {
         const hipError_t e = type == kQ4_K ? launch_q4k_mvl(w, x, y, cols, rows, 1, s, &a)
-                                           : launch_q6k_mvr(w, x, y, cols, rows, 1, s, ex.ycopy);
+                                           : launch_q6k_mvr(w, x, y, cols, rows, 1, s, j.ycopy);
         if (e != hipErrorNotSupported) return e;
     }
     set_tiles(a);

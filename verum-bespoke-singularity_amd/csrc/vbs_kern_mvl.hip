@@ -201,6 +201,7 @@ __global__ __launch_bounds__(64 * kMvlWaves) void k_mvl(const MvArgs a, uint32_t
         float *y = a.y[0] + r0 + t;
         *y = EPI == E_ACC ? __fadd_rn(*y, s) : s;
         if (EPI == E_ACC && a.ycopy) a.ycopy[r0 + t] = s;
+        if (EPI == E_STORE) store_joins(a, r0 + t, s);
     }
 }
 
@@ -437,6 +438,13 @@ hipError_t launch_q4k_mvl(const uint8_t *w, const float *x, float *y, uint32_t c
         a.eps = extra->eps;
         a.xn = extra->xn;
         a.ycopy = extra->ycopy;
+        a.gate_in = extra->gate_in;
+        a.hid = extra->hid;
+        a.kin = extra->kin;
+        a.kc = extra->kc;
+        a.vc = extra->vc;
+        a.kv_layer = extra->kv_layer;
+        if ((a.hid || a.kin) && accumulate) return hipErrorNotSupported;
     }
     const uint32_t g = (rows + rpw - 1u) / rpw;  // workgroups with rows
 #define VBS_MVL(TT)                                                                              \

@@ -588,16 +588,33 @@ struct MvArgs {
     const uint32_t *pos;  // E_QKV: device position
     uint32_t hd, kvd, role0;
     uint16_t *kc, *vc;
-    uint64_t kv_layer;  // layer * max_ctx * kvd
+    uint64_t kv_layer;  // E_QKV: layer * max_ctx * kvd; the store joins: (layer * max_ctx + pos) * kvd
     // ranged launches: workgroups of matrix m end at rwg_end[m] (cumulative),
     // each taking rpw[m] rows of it (the last one of a matrix fewer)
     uint32_t rwg_end[3], rpw[3];
     // the backend shim's fused neighbours of a linear (NULL elsewhere): NORM
     // launches also store the normalised x here (workgroup 0), E_ACC launches
     // also store each row value t here (the linear's own output, to which the
-    // add was applied)
+    // add was applied); E_STORE launches with `hid` also store
+    // silu(gate_in[row]) * t there (the ACTIVATION op after the up matvec),
+    // and with `kin` the CACHE op after the V matvec: f16(t) to vc and
+    // f16(kin[row]) to kc at kv_layer + row
     float *xn, *ycopy;
+    const float *gate_in, *kin;
+    float *hid;
 };
+
+// The E_STORE neighbours above for row `row` with value t.
+__device__ __forceinline__ void store_joins(const MvArgs &a, uint32_t row, float t) {
+    if (a.hid) {
+        const float g = a.gate_in[row];
+        a.hid[row] = __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))), t);
+    }
+    if (a.kin) {
+        a.vc[a.kv_layer + row] = vbs_f2h(t);
+        a.kc[a.kv_layer + row] = vbs_f2h(a.kin[row]);
+    }
+}
 
 // The fused attn_norm + Q/K/V + RoPE + KV store launch of k_mvl
 // (vbs_kern_mvl.hip) for Q4_K rows of 16 blocks and 4096 or more rows in all;
@@ -838,7 +855,10 @@ __global__ __launch_bounds__(MAXT) void k_mvf(const MvArgs a) {
         const uint32_t row = RANGED ? r0 + 16u * j + n : lt[j] * 16u + n;
         const bool st = lane < 16u && own && row < (RANGED ? r1 : a.rows[m]);
         if (EPI == E_STORE) {
-            if (st) a.y[m][row] = t;
+            if (st) {
+                a.y[m][row] = t;
+                store_joins(a, row, t);
+            }
         } else if (EPI == E_ACC) {
             if (st) {
                 a.y[m][row] = __fadd_rn(a.y[m][row], t);

@@ -60,7 +60,7 @@ typedef struct {
     int (*silu_mul)(const float *, const float *, float *, uint32_t);
     int (*add)(const float *, const float *, float *, uint32_t);
     int (*linear_fused)(int, const void *, const float *, float *, uint32_t, uint32_t,
-                        const float *, float, float *, float *, int, uint32_t, uint32_t, float);
+                        const vbs_gfx950_linear_join_t *);
 } gfx950_lib_t;
 
 static gfx950_lib_t g_lib;
@@ -251,6 +251,8 @@ static bool gfx950_copy_to_host(void *dst, const vbs_buffer_t *src, size_t bytes
  *   LINEAR, then ROTARY of its output (in place)  -> matvec + RoPE (with the
  *                                                    RMSNorm too if it was held)
  *   LINEAR, then ELEMENTWISE a = a + its output   -> matvec + add
+ *   LINEAR, then CACHE with its output as V       -> matvec + f16 K/V store
+ *   LINEAR, then ACTIVATION with its output as up -> matvec + SiLU gate
  * Each result is bit-identical to the ops run one by one, and every buffer the
  * ops write is written (the normalised x, the linear's own output). Any other
  * op, copy, free or synchronize first issues what is held, so the ordering the
@@ -286,21 +288,35 @@ static bool run_linear(const pending_t *p) {
                                                                               : lib_fail("linear tile");
 }
 
-/* The held op joined with a following ROTARY (rope) or ELEMENTWISE add
- * (acc); false with the reason on an error. Falls back to the ops one by one
- * (the held one here, the caller's after) when no fused kernel fits: *done
- * tells the caller whether its op was part of the launch. */
-static bool run_fused(pending_t *p, float *acc, int rope, uint32_t pos, uint32_t hd, float theta,
-                      bool *done) {
+/* The held op joined with the op that follows it (the fields of *j past the
+ * RMSNorm, which comes from the held op); false with the reason on an error.
+ * Falls back to the ops one by one (the held one here, the caller's after)
+ * when no fused kernel fits: *done tells the caller whether its op was part
+ * of the launch. */
+static bool run_fused(const pending_t *p, vbs_gfx950_linear_join_t *j, bool *done) {
     *done = false;
+    if (p->has_norm) {
+        j->norm_w = p->n_w;
+        j->norm_eps = p->n_eps;
+        j->x_normed = p->n_out;
+    }
     const int r = g_lib.linear_fused(p->type, p->w, p->has_norm ? p->n_in : p->x, p->y, p->cols,
-                                     p->rows, p->has_norm ? p->n_w : NULL, p->n_eps,
-                                     p->has_norm ? p->n_out : NULL, acc, rope, pos, hd, theta);
+                                     p->rows, j);
     if (r == 1) {
         *done = true;
         return true;
     }
     if (r == 0) return lib_fail("linear tile (fused)");
+    if (p->has_norm && (j->rope || j->acc || j->gate || j->k_row)) {
+        /* the RMSNorm + matvec alone, then the caller's op */
+        vbs_gfx950_linear_join_t n = {0};
+        n.norm_w = p->n_w;
+        n.norm_eps = p->n_eps;
+        n.x_normed = p->n_out;
+        const int r2 = g_lib.linear_fused(p->type, p->w, p->n_in, p->y, p->cols, p->rows, &n);
+        if (r2 == 1) return true;
+        if (r2 == 0) return lib_fail("linear tile (fused)");
+    }
     return run_linear(p);
 }
 
@@ -311,10 +327,9 @@ static bool flush_pending(void) {
         case PEND_NORM: return run_norm(&p);
         case PEND_LINEAR:
             if (p.has_norm) {
-                const int r = g_lib.linear_fused(p.type, p.w, p.n_in, p.y, p.cols, p.rows, p.n_w,
-                                                 p.n_eps, p.n_out, NULL, 0, 0, 0, 0.f);
-                if (r == 1) return true;
-                if (r == 0) return lib_fail("linear tile (fused)");
+                vbs_gfx950_linear_join_t j = {0};
+                bool done;
+                return run_fused(&p, &j, &done);
             }
             return run_linear(&p);
         default: return true;
@@ -574,26 +589,50 @@ static bool gfx950_dispatch_primitive(vbs_device_t *dev, void *pipeline, const v
         return true;
     }
     if (g_pend.kind == PEND_LINEAR) {
-        pending_t *h = &g_pend;
+        const pending_t h = g_pend;
+        vbs_gfx950_linear_join_t j = {0};
         bool joined = false, done = false;
-        if (pp->base.kind == VBS_OP_ROTARY && (float *)BUF(0) == h->y &&
-            (uint64_t)U32(2) * U32(3) == h->rows) {
-            joined = true;
-            if (!run_fused(h, NULL, 1, U32(1), U32(2), F32(4), &done)) {
-                h->kind = PEND_NONE;
-                return false;
-            }
-        } else if (pp->base.kind == VBS_OP_ELEMENTWISE && !h->has_norm && BUF(1) == h->y &&
-                   BUF(2) == BUF(0) && BUF(0) != h->y && (const float *)BUF(0) != h->x &&
-                   U32(3) == h->rows) {
-            joined = true;
-            if (!run_fused(h, (float *)BUF(0), 0, 0, 0, 0.f, &done)) {
-                h->kind = PEND_NONE;
-                return false;
-            }
+        switch (pp->base.kind) {
+            case VBS_OP_ROTARY: /* (x, pos, head_dim, n_heads, theta), x the linear's output */
+                if ((float *)BUF(0) == h.y && (uint64_t)U32(2) * U32(3) == h.rows) {
+                    j.rope = 1;
+                    j.pos = U32(1);
+                    j.head_dim = U32(2);
+                    j.theta = F32(4);
+                    joined = true;
+                }
+                break;
+            case VBS_OP_ELEMENTWISE: /* (a, b, out, n): a = a + the linear's output */
+                if (!h.has_norm && BUF(1) == h.y && BUF(2) == BUF(0) && BUF(0) != h.y &&
+                    (const float *)BUF(0) != h.x && U32(3) == h.rows) {
+                    j.acc = (float *)BUF(0);
+                    joined = true;
+                }
+                break;
+            case VBS_OP_CACHE: /* (k, v, kc, vc, pos, layer, max_ctx, kv_dim), v the output */
+                if (!h.has_norm && BUF(1) == h.y && BUF(0) != h.y && U32(7) == h.rows &&
+                    U32(4) < U32(6)) {
+                    j.k_row = (const float *)BUF(0);
+                    j.kc = (uint16_t *)BUF(2);
+                    j.vc = (uint16_t *)BUF(3);
+                    j.kv_off = ((uint64_t)U32(5) * U32(6) + U32(4)) * U32(7);
+                    joined = true;
+                }
+                break;
+            case VBS_OP_ACTIVATION: /* (gate, up, out, n), up the linear's output */
+                if (!h.has_norm && BUF(1) == h.y && BUF(0) != h.y && BUF(2) != h.y &&
+                    BUF(2) != BUF(0) && (const float *)BUF(2) != h.x && U32(3) == h.rows) {
+                    j.gate = (const float *)BUF(0);
+                    j.hidden = (float *)BUF(2);
+                    joined = true;
+                }
+                break;
+            default:
+                break;
         }
         if (joined) {
-            h->kind = PEND_NONE;
+            g_pend.kind = PEND_NONE;
+            if (!run_fused(&h, &j, &done)) return false;
             if (done) return true;  /* else: the held op ran alone, this one follows */
         }
     }

@@ -121,6 +121,13 @@ class Hip:
 # --------------------------------------------------------------------------
 _P, _U32, _I, _SZ, _F, _U64 = C.c_void_p, C.c_uint32, C.c_int, C.c_size_t, C.c_float, C.c_uint64
 
+class LinearJoin(C.Structure):
+    """vbs_gfx950_linear_join_t: the neighbours vbs_gfx950_linear_fused takes."""
+    _fields_ = [("norm_w", _P), ("norm_eps", _F), ("x_normed", _P), ("acc", _P), ("rope", _I),
+                ("pos", _U32), ("head_dim", _U32), ("theta", _F), ("gate", _P), ("hidden", _P),
+                ("k_row", _P), ("kc", _P), ("vc", _P), ("kv_off", _U64)]
+
+
 _DEVICE_SIGS = {
     "abi_version": (_I, []),
     "init": (_I, []),
@@ -139,7 +146,7 @@ _DEVICE_SIGS = {
     "linear": (_I, [_I, _P, _P, _P, _U32, _U32, _U32, _U32, _I]),
     "embed": (_I, [_I, _P, _U32, _P, _U32]),
     "rms_norm": (_I, [_P, _P, _P, _U32, _F]),
-    "linear_fused": (_I, [_I, _P, _P, _P, _U32, _U32, _P, _F, _P, _P, _I, _U32, _U32, _F]),
+    "linear_fused": (_I, [_I, _P, _P, _P, _U32, _U32, C.POINTER(LinearJoin)]),
     "rope": (_I, [_P, _U32, _U32, _U32, _F]),
     "cache_store": (_I, [_P, _P, _P, _P, _U32, _U32, _U32, _U32]),
     "attention": (_I, [_P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, _U32, _F]),
@@ -245,6 +252,16 @@ class DeviceLib:
         self.check(self._linear_batch_multi(t, n, arr(C.c_void_p, ws), arr(C.c_uint32, rows), x, xs,
                                             arr(C.c_void_p, ys), arr(C.c_uint32, y_strides), cols,
                                             batch), "linear_batch_multi")
+
+    def linear_fused(self, t, w, x, y, cols, rows, **join) -> bool:
+        """y = W x with the neighbours named in `join` (the LinearJoin fields)
+        in the same launch; False when no fused kernel takes the combination
+        (nothing launched), an exception on an error."""
+        r = self._linear_fused(t, w, x, y, cols, rows, C.byref(LinearJoin(**join)))
+        if r == 2:
+            return False
+        self.check(r, "linear_fused")
+        return True
 
     def embed(self, t, w, token, out, dim):
         self.check(self._embed(t, w, token, out, dim), "embed")
