@@ -179,6 +179,36 @@ typedef struct vbs_gfx950_linear_join {
 int vbs_gfx950_linear_fused(int type, const void *w, const float *x, float *y, uint32_t cols,
                             uint32_t rows, const vbs_gfx950_linear_join_t *join);
 
+/* Grouped ops of the backend shim's per-dispatch path (no counterpart in the
+ * reference: the shim holds back the bridge's attention-input and FFN-input
+ * runs and issues each as one launch; results are bit-identical to the ops
+ * one by one, and every buffer those ops write is written):
+ *
+ * vbs_gfx950_qkv_fused -- NORMALIZE (when norm_w and x_normed are given),
+ * LINEAR q, ROTARY q, LINEAR k, ROTARY k, LINEAR v, CACHE
+ * (src/vbs_specializer.c:282-302): x_normed = rms_norm(x), q = rope(Wq xn),
+ * k = rope(Wk xn), v = Wv xn, and f16(k), f16(v) stored at
+ * ((layer * max_ctx + pos) * kv_rows + i) of kc / vc, the rotations at pos
+ * in heads of head_dim with base theta. The three matrices share the type. */
+int vbs_gfx950_qkv_fused(int type, const void *wq, const void *wk, const void *wv, const float *x,
+                         uint32_t cols, uint32_t q_rows, uint32_t kv_rows, const float *norm_w,
+                         float eps, float *x_normed, float *q, float *k, float *v, uint32_t pos,
+                         uint32_t head_dim, float theta, uint16_t *kc, uint16_t *vc,
+                         uint32_t layer, uint32_t max_ctx);
+
+/* vbs_gfx950_gate_up_fused -- NORMALIZE (optional, as above), LINEAR gate,
+ * LINEAR up, ACTIVATION (src/vbs_specializer.c:282-284, 319-329): gate = Wg xn,
+ * up = Wu xn, hidden = silu(gate) * up.
+ *
+ * Both: Q4_K and Q6_K rows of a multiple of 256, row counts of a multiple
+ * of 16; 1 when launched, 0 with a reason on an error, 2 (nothing launched)
+ * when no grouped kernel takes the shape. The RoPE rows come from the same
+ * device table as vbs_gfx950_linear_fused's (it allocates; not for graph
+ * capture). */
+int vbs_gfx950_gate_up_fused(int type, const void *wg, const void *wu, const float *x,
+                             uint32_t cols, uint32_t rows, const float *norm_w, float eps,
+                             float *x_normed, float *gate, float *up, float *hidden);
+
 /* Batched decode: Y[b*y_stride + r] = sum_c deq(W[r,c]) * X[b*x_stride + c]
  * for b < batch (<= 16). Equal to `batch` calls of vbs_gfx950_linear; the
  * weights are read once. The reference has no batched matvec

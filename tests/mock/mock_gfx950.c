@@ -84,8 +84,9 @@ int vbs_gfx950_add(const float *a, const float *b, float *out, uint32_t n) {
 /* The fused neighbours of a linear (vbs_gfx950_linear_fused) as the ops one
  * by one; like the device library, only for Q4_K and Q6_K and for the same
  * combinations (else 2: nothing done, the shim issues the ops itself). */
-static unsigned g_fused[5]; /* launches joined with a NORMALIZE, ROTARY, add, ACTIVATION, CACHE */
-unsigned mock_fused_count(int which) { return which >= 0 && which < 5 ? g_fused[which] : 0u; }
+static unsigned g_fused[7]; /* launches joined with a NORMALIZE, ROTARY, add, ACTIVATION, CACHE;
+                               grouped q/k/v and gate/up launches */
+unsigned mock_fused_count(int which) { return which >= 0 && which < 7 ? g_fused[which] : 0u; }
 
 int vbs_gfx950_linear_fused(int t, const void *w, const float *x, float *y, uint32_t cols,
                             uint32_t rows, const vbs_gfx950_linear_join_t *j) {
@@ -110,5 +111,52 @@ int vbs_gfx950_linear_fused(int t, const void *w, const float *x, float *y, uint
     g_fused[2] += j->acc != NULL;
     g_fused[3] += j->gate != NULL;
     g_fused[4] += j->k_row != NULL;
+    return 1;
+}
+
+/* The grouped q/k/v and gate/up launches as the ops one by one (built with
+ * MOCK_DECLINE_GROUPS they decline every shape, so the shim's fallbacks run). */
+int vbs_gfx950_qkv_fused(int t, const void *wq, const void *wk, const void *wv, const float *x,
+                         uint32_t cols, uint32_t q_rows, uint32_t kv_rows, const float *norm_w,
+                         float eps, float *x_normed, float *q, float *k, float *v, uint32_t pos,
+                         uint32_t hd, float theta, uint16_t *kc, uint16_t *vc, uint32_t layer,
+                         uint32_t max_ctx) {
+    if ((norm_w != NULL) != (x_normed != NULL) || pos >= max_ctx) return 0;
+#ifdef MOCK_DECLINE_GROUPS
+    return 2;
+#endif
+    if (t != 12 && t != 14) return 2;
+    if (norm_w) {
+        vbs_oracle_rms_norm(x, norm_w, x_normed, cols, eps);
+        x = x_normed;
+    }
+    if (!vbs_oracle_linear_tile(t, (const uint8_t *)wq, x, q, cols, q_rows, 0, 0, 0) ||
+        !vbs_oracle_linear_tile(t, (const uint8_t *)wk, x, k, cols, kv_rows, 0, 0, 0) ||
+        !vbs_oracle_linear_tile(t, (const uint8_t *)wv, x, v, cols, kv_rows, 0, 0, 0))
+        return 0;
+    vbs_oracle_rope(q, pos, hd, q_rows / hd, theta);
+    vbs_oracle_rope(k, pos, hd, kv_rows / hd, theta);
+    vbs_oracle_cache_store(k, v, kc, vc, pos, layer, max_ctx, kv_rows);
+    g_fused[5]++;
+    return 1;
+}
+
+int vbs_gfx950_gate_up_fused(int t, const void *wg, const void *wu, const float *x, uint32_t cols,
+                             uint32_t rows, const float *norm_w, float eps, float *x_normed,
+                             float *gate, float *up, float *hidden) {
+    if ((norm_w != NULL) != (x_normed != NULL)) return 0;
+#ifdef MOCK_DECLINE_GROUPS
+    return 2;
+#endif
+    if (t != 12 && t != 14) return 2;
+    if (norm_w) {
+        vbs_oracle_rms_norm(x, norm_w, x_normed, cols, eps);
+        x = x_normed;
+    }
+    if (!vbs_oracle_linear_tile(t, (const uint8_t *)wg, x, gate, cols, rows, 0, 0, 0) ||
+        !vbs_oracle_linear_tile(t, (const uint8_t *)wu, x, up, cols, rows, 0, 0, 0))
+        return 0;
+    vbs_oracle_silu_mul(gate, up, hidden, rows);
+    g_fused[6]++;
     return 1;
 }

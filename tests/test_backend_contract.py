@@ -164,45 +164,59 @@ def test_backend_suite_through_shim_on_host_mock(tmpdir_mod, host):
     assert len(res) >= 33
 
 
-@pytest.mark.parametrize("mix", ["q4k_m", "q8_0"])
-def test_held_ops_on_host_mock_keep_the_bridge_results(tmpdir_mod, host, mix):
-    """The shim holds back one NORMALIZE or LINEAR and joins it with the next
-    op (RMSNorm + matvec, matvec + RoPE, + add, + SiLU gate, + K/V store)
-    when vbs_gfx950_linear_fused takes the combination. Over the host mock
-    (whose fused entry composes the oracle's ops, and declines every type but
-    Q4_K and Q6_K, so the Q8_0 model runs the ops one by one) the
-    bridge-order decode driver's logits equal the oracle's forward pass bit
-    for bit at every step, and with K-quants the joins happened: per layer
-    the two RMSNorms, the Q and K RoPEs, the two residual adds, the SiLU gate
-    after the up matvec and the cache store after the V matvec."""
+HELD_CASES = {
+    # model mix, mock built to decline the grouped launches, expected joins
+    # per step and layer: [RMSNorm, RoPE, add, SiLU, cache, grouped q/k/v,
+    # grouped gate/up] as (per-layer count, once per step)
+    "q4k_m": (None, False, [(0, 1), (0, 0), (2, 0), (0, 0), (0, 0), (1, 0), (1, 0)]),
+    "q4k_m_groups_declined": (None, True, [(2, 1), (2, 0), (2, 0), (1, 0), (1, 0), (0, 0), (0, 0)]),
+    "v_up_q6k": ({"v": V.Q6_K, "up": V.Q6_K}, False,
+                 [(2, 1), (2, 0), (2, 0), (1, 0), (1, 0), (0, 0), (0, 0)]),
+    "q8_0": ({r: V.Q8_0 for r in ("q", "k", "v", "o", "gate", "up", "down", "embd", "head")},
+             False, [(0, 0)] * 7),
+}
+
+
+@pytest.mark.parametrize("case", list(HELD_CASES))
+def test_held_ops_on_host_mock_keep_the_bridge_results(tmpdir_mod, host, case):
+    """The shim holds back the bridge's NORMALIZE, q, ROTARY, k, ROTARY, v,
+    CACHE run and its NORMALIZE, gate, up, ACTIVATION run and issues each as
+    one grouped launch (vbs_gfx950_qkv_fused, vbs_gfx950_gate_up_fused), and
+    otherwise joins a held LINEAR with its neighbours (RMSNorm + matvec,
+    matvec + RoPE, + add, + SiLU gate, + K/V store) when
+    vbs_gfx950_linear_fused takes them. Over the host mock (whose fused
+    entries compose the oracle's ops and decline every type but Q4_K and
+    Q6_K, so the Q8_0 model runs the ops one by one) the bridge-order decode
+    driver's logits equal the oracle's forward pass bit for bit at every
+    step, and the launches happened as expected: grouped for the Q4_K_M mix;
+    pairwise where the mock declines the groups or the v and up matrices
+    differ in type from q and gate."""
     from test_decode import TINY, full_cache
-    so = build_mock(tmpdir_mod, f"mock_fuse_{mix}.so")
+    mix_d, decline, want = HELD_CASES[case]
+    so = build_mock(tmpdir_mod, f"mock_fuse_{case}.so",
+                    ("MOCK_DECLINE_GROUPS",) if decline else ())
     be, ok = fresh_shim(tmpdir_mod, so)
     assert ok, be.last_error()
     mock = C.CDLL(so)
     mock.mock_fused_count.restype = C.c_uint
-    mix_d = None if mix == "q4k_m" else {r: V.Q8_0 for r in ("q", "k", "v", "o", "gate", "up",
-                                                             "down", "embd", "head")}
+    if mix_d is not None:
+        mix_d = {**V.Q4_K_M_MIX, **mix_d}
     model = V.SynthModel(host, **TINY, seed=99, mix=mix_d)
     d = V.Decoder(host, be, model)
     orc = Oracle()
     kc, vc = full_cache(model, None, None, 0)
     om = orc.model(model, kc, vc)
-    before = [mock.mock_fused_count(i) for i in range(5)]
-    tok = 1
-    for pos in range(6):
+    before = [mock.mock_fused_count(i) for i in range(7)]
+    tok, steps = 1, 6
+    for pos in range(steps):
         got = d.step(tok, pos)
-        want = orc.forward(om, tok, pos, model.cfg["vocab"], 1)
-        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), pos
-        tok = int(np.argmax(want))
+        want_logits = orc.forward(om, tok, pos, model.cfg["vocab"], 1)
+        assert np.array_equal(got.view(np.uint32), want_logits.view(np.uint32)), pos
+        tok = int(np.argmax(want_logits))
     d.close()
-    joined = [mock.mock_fused_count(i) - before[i] for i in range(5)]
+    joined = [mock.mock_fused_count(i) - before[i] for i in range(7)]
     L = TINY["n_layers"]
-    if mix == "q4k_m":
-        # norms: attn + ffn per layer, and the output norm before the lm_head
-        assert joined == [6 * (2 * L + 1), 6 * 2 * L, 6 * 2 * L, 6 * L, 6 * L], joined
-    else:
-        assert joined == [0] * 5, joined
+    assert joined == [steps * (per * L + once) for per, once in want], joined
 
 
 def test_shim_marshalling_rejects_malformed_arguments(tmpdir_mod):

@@ -233,6 +233,86 @@ def test_linear_fused_equals_ops_one_by_one(dev, host, mem, t, rows, cols, join)
         assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), name
 
 
+@pytest.mark.parametrize("t,q_rows,kv_rows,cols", [
+    (V.Q4_K, 4096, 1024, 4096), (V.Q4_K, 8192, 1024, 8192), (V.Q4_K, 256, 128, 512),
+    (V.Q6_K, 4096, 1024, 4096), (V.Q4_K, 4096, 4096, 4096)],
+    ids=["q4k_7b", "q4k_70b", "q4k_small", "q6k_7b", "q4k_mha"])
+@pytest.mark.parametrize("norm", [True, False], ids=["norm", "plain"])
+def test_qkv_fused_equals_ops_one_by_one(dev, host, mem, t, q_rows, kv_rows, cols, norm):
+    """vbs_gfx950_qkv_fused (the shim's grouped NORMALIZE, q, ROTARY, k,
+    ROTARY, v, CACHE) writes the same bits to the normalised x, q, k, v and
+    both caches as the device library's ops issued one by one. The shapes
+    take the LDS-DMA kernel (16-block rows, 6144 or more rows), the
+    matrix-core kernel's ranged and tiled plans, and Q6_K."""
+    hd, pos, theta, eps, layer, max_ctx = 128, 1999, 10000.0, 1e-5, 2, 2048
+    wq = V.synth_matrix(host, t, q_rows, cols, SEED, 151)
+    wk = V.synth_matrix(host, t, kv_rows, cols, SEED, 152)
+    wv = V.synth_matrix(host, t, kv_rows, cols, SEED, 153)
+    x, nw = synth_x(host, cols, 154) * 2.0, synth_x(host, cols, 155)
+    pq, pk, pv, px, pnw = mem.up(wq), mem.up(wk), mem.up(wv), mem.up(x), mem.up(nw)
+    cache = 3 * max_ctx * kv_rows
+
+    def buffers():
+        return dict(xn=mem.zeros(cols), q=mem.zeros(q_rows), k=mem.zeros(kv_rows),
+                    v=mem.zeros(kv_rows), kc=mem.zeros(cache, np.uint16),
+                    vc=mem.zeros(cache, np.uint16))
+
+    ref, fus = buffers(), buffers()
+    xin = px
+    if norm:
+        dev.rms_norm(px, pnw, ref["xn"], cols, eps)
+        xin = ref["xn"]
+    dev.linear(t, pq, xin, ref["q"], cols, q_rows)
+    dev.rope(ref["q"], pos, hd, q_rows // hd, theta)
+    dev.linear(t, pk, xin, ref["k"], cols, kv_rows)
+    dev.rope(ref["k"], pos, hd, kv_rows // hd, theta)
+    dev.linear(t, pv, xin, ref["v"], cols, kv_rows)
+    dev.cache_store(ref["k"], ref["v"], ref["kc"], ref["vc"], pos, layer, max_ctx, kv_rows)
+    assert dev.qkv_fused(t, pq, pk, pv, px, cols, q_rows, kv_rows, pnw if norm else 0, eps,
+                         fus["xn"] if norm else 0, fus["q"], fus["k"], fus["v"], pos, hd, theta,
+                         fus["kc"], fus["vc"], layer, max_ctx)
+    for name, n, dt in (("xn", cols, np.float32), ("q", q_rows, np.float32),
+                        ("k", kv_rows, np.float32), ("v", kv_rows, np.float32),
+                        ("kc", cache, np.uint16), ("vc", cache, np.uint16)):
+        a = dev.download(ref[name], n, dt)
+        b = dev.download(fus[name], n, dt)
+        assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), name
+
+
+@pytest.mark.parametrize("t,rows,cols", [(V.Q4_K, 11008, 4096), (V.Q4_K, 28672, 8192),
+                                         (V.Q4_K, 512, 256), (V.Q6_K, 11008, 4096)],
+                         ids=["q4k_7b", "q4k_70b", "q4k_small", "q6k_7b"])
+@pytest.mark.parametrize("norm", [True, False], ids=["norm", "plain"])
+def test_gate_up_fused_equals_ops_one_by_one(dev, host, mem, t, rows, cols, norm):
+    """vbs_gfx950_gate_up_fused (the shim's grouped NORMALIZE, gate, up,
+    ACTIVATION) writes the same bits to the normalised x, gate, up and the
+    hidden vector as the ops issued one by one."""
+    eps = 1e-5
+    wg = V.synth_matrix(host, t, rows, cols, SEED, 161)
+    wu = V.synth_matrix(host, t, rows, cols, SEED, 162)
+    x, nw = synth_x(host, cols, 163) * 2.0, synth_x(host, cols, 164)
+    pg, pu, px, pnw = mem.up(wg), mem.up(wu), mem.up(x), mem.up(nw)
+
+    def buffers():
+        return dict(xn=mem.zeros(cols), gate=mem.zeros(rows), up=mem.zeros(rows),
+                    hid=mem.zeros(rows))
+
+    ref, fus = buffers(), buffers()
+    xin = px
+    if norm:
+        dev.rms_norm(px, pnw, ref["xn"], cols, eps)
+        xin = ref["xn"]
+    dev.linear(t, pg, xin, ref["gate"], cols, rows)
+    dev.linear(t, pu, xin, ref["up"], cols, rows)
+    dev.silu_mul(ref["gate"], ref["up"], ref["hid"], rows)
+    assert dev.gate_up_fused(t, pg, pu, px, cols, rows, pnw if norm else 0, eps,
+                             fus["xn"] if norm else 0, fus["gate"], fus["up"], fus["hid"])
+    for name, n in (("xn", cols), ("gate", rows), ("up", rows), ("hid", rows)):
+        a = dev.download(ref[name], n, np.float32)
+        b = dev.download(fus[name], n, np.float32)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), name
+
+
 def test_linear_fused_declines_and_rejects(dev, host, mem):
     """Combinations no fused kernel takes come back as 2 (nothing launched,
     y untouched); half-given neighbours are errors."""

@@ -473,6 +473,55 @@ int vbs_gfx950_linear_fused(int type, const void *w, const float *x, float *y, u
     return hip_ok(e, "linear_fused");
 }
 
+int vbs_gfx950_qkv_fused(int type, const void *wq, const void *wk, const void *wv, const float *x,
+                         uint32_t cols, uint32_t q_rows, uint32_t kv_rows, const float *norm_w,
+                         float eps, float *x_normed, float *q, float *k, float *v, uint32_t pos,
+                         uint32_t head_dim, float theta, uint16_t *kc, uint16_t *vc,
+                         uint32_t layer, uint32_t max_ctx) {
+    if (!ready_or_fail()) return 0;
+    if (!wq || !wk || !wv || !x || !q || !k || !v || !kc || !vc)
+        return fail("qkv_fused: null pointer");
+    if ((norm_w != nullptr) != (x_normed != nullptr))
+        return fail("qkv_fused: the RMSNorm needs both its weights and its output");
+    if (pos >= max_ctx) return fail("qkv_fused: pos %u >= max_ctx %u", pos, max_ctx);
+    if (type != kQ4_K && type != kQ6_K) return 2;
+    if (cols % 256u || q_rows == 0 || kv_rows == 0 || q_rows % 16u || kv_rows % 16u) return 2;
+    if (head_dim == 0 || (head_dim & 3u) || head_dim > 256u || q_rows % head_dim ||
+        kv_rows % head_dim)
+        return 2;
+    if (!rope_rows(theta, head_dim, pos)) return fail("qkv_fused: RoPE table allocation failed");
+    const uint8_t *w[3] = {(const uint8_t *)wq, (const uint8_t *)wk, (const uint8_t *)wv};
+    const uint32_t rows[3] = {q_rows, kv_rows, kv_rows};
+    GroupOut out;
+    out.xn = x_normed;
+    out.k = k;
+    out.v = v;
+    const hipError_t e = launch_kq_qkv(type, w, 3, 0, x, norm_w, eps, cols, rows, q, kc, vc,
+                                       (uint64_t)layer * max_ctx * kv_rows, kv_rows, g_rope.tab,
+                                       g_rope.pos + pos, head_dim, g_rt.stream, out);
+    if (e == hipErrorNotSupported) return 2;
+    return hip_ok(e, "qkv_fused");
+}
+
+int vbs_gfx950_gate_up_fused(int type, const void *wg, const void *wu, const float *x,
+                             uint32_t cols, uint32_t rows, const float *norm_w, float eps,
+                             float *x_normed, float *gate, float *up, float *hidden) {
+    if (!ready_or_fail()) return 0;
+    if (!wg || !wu || !x || !gate || !up || !hidden) return fail("gate_up_fused: null pointer");
+    if ((norm_w != nullptr) != (x_normed != nullptr))
+        return fail("gate_up_fused: the RMSNorm needs both its weights and its output");
+    if (type != kQ4_K && type != kQ6_K) return 2;
+    if (cols % 256u || rows == 0 || rows % 16u) return 2;
+    GroupOut out;
+    out.xn = x_normed;
+    out.gate = gate;
+    out.up = up;
+    const hipError_t e = launch_kq_silu(type, (const uint8_t *)wg, (const uint8_t *)wu, x, norm_w,
+                                        eps, cols, rows, hidden, g_rt.stream, out);
+    if (e == hipErrorNotSupported) return 2;
+    return hip_ok(e, "gate_up_fused");
+}
+
 int vbs_gfx950_linear_batch(int type, const void *w, const float *x, uint32_t x_stride, float *y,
                             uint32_t y_stride, uint32_t cols, uint32_t rows, uint32_t batch) {
     if (!ready_or_fail()) return 0;

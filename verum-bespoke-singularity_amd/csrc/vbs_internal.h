@@ -45,6 +45,12 @@ hipError_t launch_blk_linear(int type, const uint8_t *w, const float *x, float *
 hipError_t launch_kq_norm_linear(int type, const uint8_t *w, const float *x, const float *norm_w,
                                  float eps, float *y, uint32_t cols, uint32_t rows,
                                  hipStream_t s);
+// The f32 vectors a grouped launch also stores, for the backend shim's
+// grouped ops (each may be NULL): the normalised x, and the rows of the
+// first (q; gate) and second and third (k roped, v; up) matrices.
+struct GroupOut {
+    float *xn = nullptr, *k = nullptr, *v = nullptr, *gate = nullptr, *up = nullptr;
+};
 // Matrices q, k, v (roles role0 .. role0 + n_mat - 1, same type and cols) of
 // rms_norm(x) in one launch (norm_w may be NULL): q roped into `q`, k roped
 // and v stored as f16 at position *pos of the caches (offset kv_layer).
@@ -52,11 +58,12 @@ hipError_t launch_kq_qkv(int type, const uint8_t *const w[3], uint32_t n_mat, ui
                          const float *x, const float *norm_w, float eps, uint32_t cols,
                          const uint32_t rows[3], float *q, uint16_t *kc, uint16_t *vc,
                          uint64_t kv_layer, uint32_t kvd, const float2 *rope,
-                         const uint32_t *pos, uint32_t hd, hipStream_t s);
+                         const uint32_t *pos, uint32_t hd, hipStream_t s,
+                         const GroupOut &out = GroupOut{});
 // hid = silu(Wg * rms_norm(x)) * (Wu * rms_norm(x)) in one launch.
 hipError_t launch_kq_silu(int type, const uint8_t *wg, const uint8_t *wu, const float *x,
                           const float *norm_w, float eps, uint32_t cols, uint32_t rows,
-                          float *hid, hipStream_t s);
+                          float *hid, hipStream_t s, const GroupOut &out = GroupOut{});
 
 // Batched matrix-core matvecs in two steps: x of up to 8 vectors prepared
 // once (XP_PLAIN: x; XP_NORM: rms_norm(x) * norm_w; XP_SILU: silu(x) * x2,

@@ -110,7 +110,7 @@ hipError_t launch_kq_qkv(int type, const uint8_t *const wqkv[3], uint32_t n_mat,
                          const float *x, const float *norm_w, float eps, uint32_t cols,
                          const uint32_t rows[3], float *q, uint16_t *kc, uint16_t *vc,
                          uint64_t kv_layer, uint32_t kvd, const float2 *rope,
-                         const uint32_t *pos, uint32_t hd, hipStream_t s) {
+                         const uint32_t *pos, uint32_t hd, hipStream_t s, const GroupOut &out) {
     if (n_mat == 0 || n_mat > 3u || role0 + n_mat > 3u || (hd & 1u)) return hipErrorNotSupported;
     MvArgs a{};
     for (uint32_t m = 0; m < n_mat; m++) {
@@ -133,6 +133,9 @@ hipError_t launch_kq_qkv(int type, const uint8_t *const wqkv[3], uint32_t n_mat,
     a.kc = kc;
     a.vc = vc;
     a.kv_layer = kv_layer;
+    a.xn = out.xn;
+    a.kout = out.k;
+    a.vout = out.v;
     if (type == kQ4_K) {
         const hipError_t e = launch_q4k_mvl_qkv(a, s);
         if (e != hipErrorNotSupported) return e;
@@ -143,7 +146,7 @@ hipError_t launch_kq_qkv(int type, const uint8_t *const wqkv[3], uint32_t n_mat,
 
 hipError_t launch_kq_silu(int type, const uint8_t *wg, const uint8_t *wu, const float *x,
                           const float *norm_w, float eps, uint32_t cols, uint32_t rows,
-                          float *hid, hipStream_t s) {
+                          float *hid, hipStream_t s, const GroupOut &out) {
     if (rows == 0 || rows % 16u || !mv_fits(type, wg, x, cols, rows) || !mv_fits(type, wu, x, cols, rows))
         return hipErrorNotSupported;
     MvArgs a{};
@@ -156,6 +159,9 @@ hipError_t launch_kq_silu(int type, const uint8_t *wg, const uint8_t *wu, const 
     a.x = x;
     a.norm_w = norm_w;
     a.eps = eps;
+    a.xn = out.xn;
+    a.gout = out.gate;
+    a.uout = out.up;
     set_tiles(a);
     return norm_w ? launch_type<true, E_SILU>(type, a, s) : launch_type<false, E_SILU>(type, a, s);
 }

@@ -602,6 +602,10 @@ struct MvArgs {
     float *xn, *ycopy;
     const float *gate_in, *kin;
     float *hid;
+    // the backend shim's grouped ops also keep the f32 rows that the ops one
+    // by one write: E_QKV the rotated k rows and the v rows (kout, vout),
+    // E_SILU the gate and up rows (gout, uout); NULL elsewhere
+    float *kout, *vout, *gout, *uout;
 };
 
 // The E_STORE neighbours above for row `row` with value t.
@@ -637,10 +641,13 @@ __device__ __forceinline__ void qkv_store(const MvArgs &a, uint32_t m, uint32_t 
         v = even ? __fsub_rn(__fmul_rn(x0, cs.x), __fmul_rn(x1, cs.y))
                  : __fadd_rn(__fmul_rn(x0, cs.y), __fmul_rn(x1, cs.x));
     }
-    if (role == 0u)
+    if (role == 0u) {
         a.y[0][row] = v;
-    else
+    } else {
         (role == 1u ? a.kc : a.vc)[a.kv_layer + (uint64_t)p * a.kvd + row] = vbs_f2h(v);
+        float *const o = role == 1u ? a.kout : a.vout;
+        if (o) o[row] = v;
+    }
 }
 
 // The register set that holds a block's x operands when k_mvf reads them once
@@ -840,6 +847,8 @@ __global__ __launch_bounds__(MAXT) void k_mvf(const MvArgs a) {
             if (lane < 16u && row < r1) {
                 const float den = __fadd_rn(1.0f, expf(-gate));
                 a.y[0][row] = __fmul_rn(__fdiv_rn(gate, den), up);
+                if (a.gout) a.gout[row] = gate;
+                if (a.uout) a.uout[row] = up;
             }
         }
         return;
@@ -870,6 +879,8 @@ __global__ __launch_bounds__(MAXT) void k_mvf(const MvArgs a) {
             } else if (st) {
                 const float den = __fadd_rn(1.0f, expf(-prev));
                 a.y[0][row] = __fmul_rn(__fdiv_rn(prev, den), t);
+                if (a.gout) a.gout[row] = prev;
+                if (a.uout) a.uout[row] = t;
             }
         } else {  // E_QKV
             const float other = __shfl_xor(t, 1, 64);  // the RoPE partner row

@@ -61,6 +61,11 @@ typedef struct {
     int (*add)(const float *, const float *, float *, uint32_t);
     int (*linear_fused)(int, const void *, const float *, float *, uint32_t, uint32_t,
                         const vbs_gfx950_linear_join_t *);
+    int (*qkv_fused)(int, const void *, const void *, const void *, const float *, uint32_t,
+                     uint32_t, uint32_t, const float *, float, float *, float *, float *, float *,
+                     uint32_t, uint32_t, float, uint16_t *, uint16_t *, uint32_t, uint32_t);
+    int (*gate_up_fused)(int, const void *, const void *, const float *, uint32_t, uint32_t,
+                         const float *, float, float *, float *, float *, float *);
 } gfx950_lib_t;
 
 static gfx950_lib_t g_lib;
@@ -158,6 +163,8 @@ static bool gfx950_init(void) {
     BIND(silu_mul, "vbs_gfx950_silu_mul");
     BIND(add, "vbs_gfx950_add");
     BIND(linear_fused, "vbs_gfx950_linear_fused");
+    BIND(qkv_fused, "vbs_gfx950_qkv_fused");
+    BIND(gate_up_fused, "vbs_gfx950_gate_up_fused");
 #undef BIND
 
     int ver = g_lib.abi_version();
@@ -241,99 +248,169 @@ static bool gfx950_copy_to_host(void *dst, const vbs_buffer_t *src, size_t bytes
     return g_lib.copy_d2h(dst, src->internal_handle, bytes) ? true : lib_fail("copy_to_host");
 }
 
-/* ---- one held-back op ----------------------------------------------------
+/* ---- held-back ops --------------------------------------------------------
  * The bridge issues each token step as ~16 ops per layer (NORMALIZE, LINEAR,
  * ROTARY, ..., src/vbs_specializer.c:270-349), and at this size each
  * separate launch costs about as much as its work. The shim therefore holds
- * back the last NORMALIZE or resident LINEAR and joins it with the next op
- * when one fused kernel does both (vbs_gfx950_linear_fused):
- *   NORMALIZE, then a LINEAR reading its output   -> RMSNorm + matvec
- *   LINEAR, then ROTARY of its output (in place)  -> matvec + RoPE (with the
- *                                                    RMSNorm too if it was held)
- *   LINEAR, then ELEMENTWISE a = a + its output   -> matvec + add
- *   LINEAR, then CACHE with its output as V       -> matvec + f16 K/V store
- *   LINEAR, then ACTIVATION with its output as up -> matvec + SiLU gate
+ * back a NORMALIZE and the resident LINEARs that read its output, each with
+ * a ROTARY of its own output, and issues them with the op that ends the run:
+ *   NORMALIZE, LINEAR q, ROTARY, LINEAR k, ROTARY, LINEAR v, CACHE
+ *                                   -> one launch (vbs_gfx950_qkv_fused)
+ *   NORMALIZE, LINEAR gate, LINEAR up, ACTIVATION
+ *                                   -> one launch (vbs_gfx950_gate_up_fused)
+ * and otherwise each held LINEAR with its neighbours in one launch
+ * (vbs_gfx950_linear_fused):
+ *   the NORMALIZE before it                       -> RMSNorm + matvec
+ *   a ROTARY of its output (in place)             -> matvec + RoPE
+ *   an ELEMENTWISE a = a + its output             -> matvec + add
+ *   a CACHE with its output as V                  -> matvec + f16 K/V store
+ *   an ACTIVATION with its output as up           -> matvec + SiLU gate
  * Each result is bit-identical to the ops run one by one, and every buffer the
- * ops write is written (the normalised x, the linear's own output). Any other
- * op, copy, free or synchronize first issues what is held, so the ordering the
- * caller sees is the one it asked for; an error of a held op is reported by
- * the call that issues it. One host thread drives the table (as the reference
- * assumes, src/vbs_hotpath.c:3-5). */
-typedef enum { PEND_NONE = 0, PEND_NORM, PEND_LINEAR } pend_kind_t;
-
+ * ops write is written (the normalised x, each linear's own output). Any other
+ * op, copy, free or synchronize first issues what is held, in order, so the
+ * ordering the caller sees is the one it asked for; an error of a held op is
+ * reported by the call that issues it. An op joins the held run only if it
+ * writes no buffer that a held op reads or writes (the checks compare buffer
+ * addresses: the bridge's buffers never partly overlap). One host thread
+ * drives the table (as the reference assumes, src/vbs_hotpath.c:3-5). */
 typedef struct {
-    pend_kind_t kind;
-    int has_norm;                    /* PEND_LINEAR: a held NORMALIZE joined it */
-    const float *n_in, *n_w;         /* NORMALIZE (in, w, out, dim, eps) */
-    float *n_out;
-    uint32_t n_dim;
-    float n_eps;
     int type;                        /* LINEAR (convention A, no offsets) */
     const void *w;
     const float *x;
     float *y;
     uint32_t cols, rows;
+    int rope;                        /* a ROTARY of y held behind it */
+    uint32_t pos, hd, nh;
+    float theta;
+} held_linear_t;
+
+typedef struct {
+    int has_norm;                    /* a NORMALIZE, in front of linear 0 if any */
+    const float *n_in, *n_w;
+    float *n_out;
+    uint32_t n_dim;
+    float n_eps;
+    int n_lin;                       /* LINEARs held, in issue order, all reading lin[0].x */
+    held_linear_t lin[3];
 } pending_t;
 
 static pending_t g_pend;
+
+static void drop_pending(void) { memset(&g_pend, 0, sizeof(g_pend)); }
 
 static bool run_norm(const pending_t *p) {
     return g_lib.rms_norm(p->n_in, p->n_w, p->n_out, p->n_dim, p->n_eps) ? true
                                                                          : lib_fail("normalize");
 }
 
-static bool run_linear(const pending_t *p) {
-    if (p->has_norm && !run_norm(p)) return false;
-    return g_lib.linear(p->type, p->w, p->x, p->y, p->cols, p->rows, 0, 0, 0) ? true
-                                                                              : lib_fail("linear tile");
-}
-
-/* The held op joined with the op that follows it (the fields of *j past the
- * RMSNorm, which comes from the held op); false with the reason on an error.
- * Falls back to the ops one by one (the held one here, the caller's after)
- * when no fused kernel fits: *done tells the caller whether its op was part
- * of the launch. */
-static bool run_fused(const pending_t *p, vbs_gfx950_linear_join_t *j, bool *done) {
+/* Held linear i with what it carries (the RMSNorm in front of linear 0, its
+ * ROTARY) and the op `j` names after it (acc, gate or k_row; or none), in one
+ * launch where a fused kernel takes them, else one by one without the op `j`
+ * names: *done tells the caller whether that op was part of the launch. */
+static bool issue_linear(const pending_t *p, int i, vbs_gfx950_linear_join_t *j, bool *done) {
+    const held_linear_t *l = &p->lin[i];
+    const bool norm = i == 0 && p->has_norm;
+    const bool after = j->acc || j->gate || j->k_row;
     *done = false;
-    if (p->has_norm) {
+    if (norm) {
         j->norm_w = p->n_w;
         j->norm_eps = p->n_eps;
         j->x_normed = p->n_out;
     }
-    const int r = g_lib.linear_fused(p->type, p->w, p->has_norm ? p->n_in : p->x, p->y, p->cols,
-                                     p->rows, j);
-    if (r == 1) {
-        *done = true;
-        return true;
+    if (l->rope) {
+        j->rope = 1;
+        j->pos = l->pos;
+        j->head_dim = l->hd;
+        j->theta = l->theta;
     }
-    if (r == 0) return lib_fail("linear tile (fused)");
-    if (p->has_norm && (j->rope || j->acc || j->gate || j->k_row)) {
-        /* the RMSNorm + matvec alone, then the caller's op */
-        vbs_gfx950_linear_join_t n = {0};
-        n.norm_w = p->n_w;
-        n.norm_eps = p->n_eps;
-        n.x_normed = p->n_out;
-        const int r2 = g_lib.linear_fused(p->type, p->w, p->n_in, p->y, p->cols, p->rows, &n);
-        if (r2 == 1) return true;
-        if (r2 == 0) return lib_fail("linear tile (fused)");
+    if (norm || l->rope || after) {
+        int r = g_lib.linear_fused(l->type, l->w, norm ? p->n_in : l->x, l->y, l->cols, l->rows, j);
+        if (r == 1) {
+            *done = after;
+            return true;
+        }
+        if (r == 0) return lib_fail("linear tile (fused)");
+        if (norm && (l->rope || after)) { /* the RMSNorm + matvec alone, then the RoPE */
+            vbs_gfx950_linear_join_t n = {0};
+            n.norm_w = p->n_w;
+            n.norm_eps = p->n_eps;
+            n.x_normed = p->n_out;
+            r = g_lib.linear_fused(l->type, l->w, p->n_in, l->y, l->cols, l->rows, &n);
+            if (r == 0) return lib_fail("linear tile (fused)");
+            if (r == 1) {
+                if (l->rope && !g_lib.rope(l->y, l->pos, l->hd, l->nh, l->theta))
+                    return lib_fail("rotary");
+                return true;
+            }
+        }
     }
-    return run_linear(p);
+    if (norm && !run_norm(p)) return false;
+    if (!g_lib.linear(l->type, l->w, l->x, l->y, l->cols, l->rows, 0, 0, 0))
+        return lib_fail("linear tile");
+    if (l->rope && !g_lib.rope(l->y, l->pos, l->hd, l->nh, l->theta)) return lib_fail("rotary");
+    return true;
 }
 
 static bool flush_pending(void) {
-    pending_t p = g_pend;
-    g_pend.kind = PEND_NONE;
-    switch (p.kind) {
-        case PEND_NORM: return run_norm(&p);
-        case PEND_LINEAR:
-            if (p.has_norm) {
-                vbs_gfx950_linear_join_t j = {0};
-                bool done;
-                return run_fused(&p, &j, &done);
-            }
-            return run_linear(&p);
-        default: return true;
+    const pending_t p = g_pend;
+    drop_pending();
+    if (p.n_lin == 0) return p.has_norm ? run_norm(&p) : true;
+    for (int i = 0; i < p.n_lin; i++) {
+        vbs_gfx950_linear_join_t j = {0};
+        bool done;
+        if (!issue_linear(&p, i, &j, &done)) return false;
     }
+    return true;
+}
+
+/* The last held linear joined with the op `j` names after it, the held ops
+ * before it issued first; *done as in issue_linear. */
+static bool issue_last_with(vbs_gfx950_linear_join_t *j, bool *done) {
+    const pending_t p = g_pend;
+    drop_pending();
+    *done = false;
+    for (int i = 0; i + 1 < p.n_lin; i++) {
+        vbs_gfx950_linear_join_t none = {0};
+        bool d;
+        if (!issue_linear(&p, i, &none, &d)) return false;
+    }
+    return issue_linear(&p, p.n_lin - 1, j, done);
+}
+
+/* Whether buffer b is one that a held op reads or writes. */
+static bool touches_held(const void *b) {
+    const pending_t *h = &g_pend;
+    if (h->has_norm && (b == (const void *)h->n_in || b == (const void *)h->n_out)) return true;
+    for (int i = 0; i < h->n_lin; i++)
+        if (b == (const void *)h->lin[i].x || b == (const void *)h->lin[i].y) return true;
+    return false;
+}
+
+/* A convention-A LINEAR: joins the held run (the NORMALIZE it reads, or the
+ * q / k / v and gate / up runs above) or starts a new one. */
+static bool hold_linear(const held_linear_t *n) {
+    pending_t *h = &g_pend;
+    if (h->n_lin > 0 && h->n_lin < 3 && n->x == h->lin[0].x && n->type == h->lin[0].type &&
+        n->cols == h->lin[0].cols && !touches_held(n->y)) {
+        bool all_roped = true;
+        for (int i = 0; i < h->n_lin; i++) all_roped = all_roped && h->lin[i].rope;
+        const bool ffn = h->n_lin == 1 && !h->lin[0].rope && n->rows == h->lin[0].rows;
+        if (all_roped || ffn) {
+            h->lin[h->n_lin++] = *n;
+            return true;
+        }
+    }
+    if (h->n_lin == 0 && h->has_norm && n->x == h->n_out && n->cols == h->n_dim &&
+        h->n_in != (const float *)h->n_out && (const float *)n->y != h->n_in &&
+        n->y != h->n_out) {
+        h->lin[0] = *n;
+        h->n_lin = 1;
+        return true;
+    }
+    if (!flush_pending()) return false;
+    g_pend.lin[0] = *n;
+    g_pend.n_lin = 1;
+    return true;
 }
 
 /* ---- pipelines ---------------------------------------------------------- */
@@ -463,28 +540,14 @@ static bool gfx950_dispatch_linear_tile(vbs_device_t *dev, void *pipeline, vbs_b
     if (!ws && !col_off && !row_off && !accumulate && need && wp->internal_handle && x && y &&
         (const float *)y != x) {
         /* convention A, the bridge's resident matvec: held back for the next op */
-        pending_t n = {0};
-        n.kind = PEND_LINEAR;
+        held_linear_t n = {0};
         n.type = (int)p->type;
         n.w = wp->internal_handle;
         n.x = x;
         n.y = y;
         n.cols = cols;
         n.rows = rows;
-        if (g_pend.kind == PEND_NORM && x == g_pend.n_out && cols == g_pend.n_dim &&
-            g_pend.n_in != (const float *)g_pend.n_out && (const float *)y != g_pend.n_in &&
-            y != g_pend.n_out) {
-            n.has_norm = 1;
-            n.n_in = g_pend.n_in;
-            n.n_w = g_pend.n_w;
-            n.n_out = g_pend.n_out;
-            n.n_dim = g_pend.n_dim;
-            n.n_eps = g_pend.n_eps;
-        } else if (!flush_pending()) {
-            return false;
-        }
-        g_pend = n;
-        return true;
+        return hold_linear(&n);
     }
     if (!flush_pending()) return false;
     if (!g_lib.linear((int)p->type, wp->internal_handle, x, y, cols, rows, col_off, row_off,
@@ -575,65 +638,106 @@ static bool gfx950_dispatch_primitive(vbs_device_t *dev, void *pipeline, const v
             return false;
         }
     }
-    /* the held op joined with this one, or held itself (NORMALIZE) */
+    /* held itself (NORMALIZE, ROTARY), or issued with the held run */
     if (pp->base.kind == VBS_OP_NORMALIZE && BUF(0) != BUF(2)) {
         if (!flush_pending()) return false;
-        pending_t n = {0};
-        n.kind = PEND_NORM;
-        n.n_in = (const float *)BUF(0);
-        n.n_w = (const float *)BUF(1);
-        n.n_out = (float *)BUF(2);
-        n.n_dim = U32(3);
-        n.n_eps = F32(4);
-        g_pend = n;
+        g_pend.has_norm = 1;
+        g_pend.n_in = (const float *)BUF(0);
+        g_pend.n_w = (const float *)BUF(1);
+        g_pend.n_out = (float *)BUF(2);
+        g_pend.n_dim = U32(3);
+        g_pend.n_eps = F32(4);
         return true;
     }
-    if (g_pend.kind == PEND_LINEAR) {
-        const pending_t h = g_pend;
+    if (g_pend.n_lin > 0) {
+        const pending_t *h = &g_pend;
+        const held_linear_t *last = &h->lin[h->n_lin - 1];
         vbs_gfx950_linear_join_t j = {0};
         bool joined = false, done = false;
         switch (pp->base.kind) {
-            case VBS_OP_ROTARY: /* (x, pos, head_dim, n_heads, theta), x the linear's output */
-                if ((float *)BUF(0) == h.y && (uint64_t)U32(2) * U32(3) == h.rows) {
-                    j.rope = 1;
-                    j.pos = U32(1);
-                    j.head_dim = U32(2);
-                    j.theta = F32(4);
-                    joined = true;
+            case VBS_OP_ROTARY: /* (x, pos, head_dim, n_heads, theta), x the last output */
+                if (!last->rope && (float *)BUF(0) == last->y &&
+                    (uint64_t)U32(2) * U32(3) == last->rows) {
+                    held_linear_t *l = &g_pend.lin[h->n_lin - 1];
+                    l->rope = 1;
+                    l->pos = U32(1);
+                    l->hd = U32(2);
+                    l->nh = U32(3);
+                    l->theta = F32(4);
+                    return true;
                 }
                 break;
-            case VBS_OP_ELEMENTWISE: /* (a, b, out, n): a = a + the linear's output */
-                if (!h.has_norm && BUF(1) == h.y && BUF(2) == BUF(0) && BUF(0) != h.y &&
-                    (const float *)BUF(0) != h.x && U32(3) == h.rows) {
+            case VBS_OP_ELEMENTWISE: /* (a, b, out, n): a = a + the last output */
+                if (!last->rope && BUF(1) == last->y && BUF(2) == BUF(0) && BUF(0) != last->y &&
+                    (const float *)BUF(0) != last->x && U32(3) == last->rows) {
                     j.acc = (float *)BUF(0);
                     joined = true;
                 }
                 break;
-            case VBS_OP_CACHE: /* (k, v, kc, vc, pos, layer, max_ctx, kv_dim), v the output */
-                if (!h.has_norm && BUF(1) == h.y && BUF(0) != h.y && U32(7) == h.rows &&
-                    U32(4) < U32(6)) {
+            case VBS_OP_CACHE: { /* (k, v, kc, vc, pos, layer, max_ctx, kv_dim) */
+                const uint32_t pos = U32(4), layer = U32(5), mc = U32(6), kvd = U32(7);
+                const held_linear_t *q = &h->lin[0], *k = &h->lin[1], *v = &h->lin[2];
+                if (h->n_lin == 3 && q->rope && k->rope && !v->rope && BUF(0) == k->y &&
+                    BUF(1) == v->y && kvd == k->rows && kvd == v->rows && pos < mc &&
+                    q->pos == pos && k->pos == pos && q->hd == k->hd && q->theta == k->theta) {
+                    /* NORMALIZE, q, ROTARY, k, ROTARY, v, CACHE in one launch */
+                    const int r = g_lib.qkv_fused(
+                        q->type, q->w, k->w, v->w, h->has_norm ? h->n_in : q->x, q->cols, q->rows,
+                        kvd, h->has_norm ? h->n_w : NULL, h->n_eps, h->has_norm ? h->n_out : NULL,
+                        q->y, k->y, v->y, pos, q->hd, q->theta, (uint16_t *)BUF(2),
+                        (uint16_t *)BUF(3), layer, mc);
+                    if (r == 1) {
+                        drop_pending();
+                        return true;
+                    }
+                    if (r == 0) {
+                        drop_pending();
+                        return lib_fail("q/k/v (grouped)");
+                    }
+                }
+                if (!last->rope && BUF(1) == last->y && BUF(0) != last->y && kvd == last->rows &&
+                    pos < mc) {
                     j.k_row = (const float *)BUF(0);
                     j.kc = (uint16_t *)BUF(2);
                     j.vc = (uint16_t *)BUF(3);
-                    j.kv_off = ((uint64_t)U32(5) * U32(6) + U32(4)) * U32(7);
+                    j.kv_off = ((uint64_t)layer * mc + pos) * kvd;
                     joined = true;
                 }
                 break;
-            case VBS_OP_ACTIVATION: /* (gate, up, out, n), up the linear's output */
-                if (!h.has_norm && BUF(1) == h.y && BUF(0) != h.y && BUF(2) != h.y &&
-                    BUF(2) != BUF(0) && (const float *)BUF(2) != h.x && U32(3) == h.rows) {
+            }
+            case VBS_OP_ACTIVATION: { /* (gate, up, out, n) */
+                const held_linear_t *g = &h->lin[0], *u = &h->lin[1];
+                const void *out = BUF(2);
+                if (h->n_lin == 2 && !g->rope && !u->rope && BUF(0) == g->y && BUF(1) == u->y &&
+                    U32(3) == g->rows && U32(3) == u->rows && !touches_held(out)) {
+                    /* NORMALIZE, gate, up, ACTIVATION in one launch */
+                    const int r = g_lib.gate_up_fused(
+                        g->type, g->w, u->w, h->has_norm ? h->n_in : g->x, g->cols, g->rows,
+                        h->has_norm ? h->n_w : NULL, h->n_eps, h->has_norm ? h->n_out : NULL, g->y,
+                        u->y, (float *)out);
+                    if (r == 1) {
+                        drop_pending();
+                        return true;
+                    }
+                    if (r == 0) {
+                        drop_pending();
+                        return lib_fail("gate/up (grouped)");
+                    }
+                }
+                if (!last->rope && BUF(1) == last->y && BUF(0) != last->y && out != last->y &&
+                    out != BUF(0) && out != (const void *)last->x && U32(3) == last->rows) {
                     j.gate = (const float *)BUF(0);
-                    j.hidden = (float *)BUF(2);
+                    j.hidden = (float *)out;
                     joined = true;
                 }
                 break;
+            }
             default:
                 break;
         }
         if (joined) {
-            g_pend.kind = PEND_NONE;
-            if (!run_fused(&h, &j, &done)) return false;
-            if (done) return true;  /* else: the held op ran alone, this one follows */
+            if (!issue_last_with(&j, &done)) return false;
+            if (done) return true;  /* else: the held ops ran alone, this one follows */
         }
     }
     if (!flush_pending()) return false;

@@ -147,6 +147,9 @@ _DEVICE_SIGS = {
     "embed": (_I, [_I, _P, _U32, _P, _U32]),
     "rms_norm": (_I, [_P, _P, _P, _U32, _F]),
     "linear_fused": (_I, [_I, _P, _P, _P, _U32, _U32, C.POINTER(LinearJoin)]),
+    "qkv_fused": (_I, [_I, _P, _P, _P, _P, _U32, _U32, _U32, _P, _F, _P, _P, _P, _P, _U32, _U32,
+                       _F, _P, _P, _U32, _U32]),
+    "gate_up_fused": (_I, [_I, _P, _P, _P, _U32, _U32, _P, _F, _P, _P, _P, _P]),
     "rope": (_I, [_P, _U32, _U32, _U32, _F]),
     "cache_store": (_I, [_P, _P, _P, _P, _U32, _U32, _U32, _U32]),
     "attention": (_I, [_P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, _U32, _F]),
@@ -261,6 +264,27 @@ class DeviceLib:
         if r == 2:
             return False
         self.check(r, "linear_fused")
+        return True
+
+    def qkv_fused(self, t, wq, wk, wv, x, cols, q_rows, kv_rows, norm_w, eps, xn, q, k, v, pos,
+                  hd, theta, kc, vc, layer, max_ctx) -> bool:
+        """The grouped attention-input ops in one launch; False when no grouped
+        kernel takes the shape (nothing launched)."""
+        r = self._qkv_fused(t, wq, wk, wv, x, cols, q_rows, kv_rows, norm_w or None, eps,
+                            xn or None, q, k, v, pos, hd, theta, kc, vc, layer, max_ctx)
+        if r == 2:
+            return False
+        self.check(r, "qkv_fused")
+        return True
+
+    def gate_up_fused(self, t, wg, wu, x, cols, rows, norm_w, eps, xn, gate, up, hidden) -> bool:
+        """The grouped FFN-input ops in one launch; False when no grouped
+        kernel takes the shape (nothing launched)."""
+        r = self._gate_up_fused(t, wg, wu, x, cols, rows, norm_w or None, eps, xn or None, gate,
+                                up, hidden)
+        if r == 2:
+            return False
+        self.check(r, "gate_up_fused")
         return True
 
     def embed(self, t, w, token, out, dim):
