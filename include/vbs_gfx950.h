@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define VBS_GFX950_ABI_VERSION 2
+#define VBS_GFX950_ABI_VERSION 3
 
 /* ---- library / device ------------------------------------------------ */
 
