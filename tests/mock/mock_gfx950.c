@@ -7,6 +7,7 @@
  * product never loads it. MOCK_ABI / MOCK_DROP let a test build variants with
  * a wrong ABI version or a missing entry point.
  */
+#include <math.h>
 #include <stdlib.h>
 #include <string.h>
 #include "vbs_gfx950.h"
@@ -81,12 +82,45 @@ int vbs_gfx950_add(const float *a, const float *b, float *out, uint32_t n) {
     vbs_oracle_add(a, b, out, n); return 1;
 }
 #endif
-/* The fused neighbours of a linear (vbs_gfx950_linear_fused) as the ops one
- * by one; like the device library, only for Q4_K and Q6_K and for the same
- * combinations (else 2: nothing done, the shim issues the ops itself). */
+/* The fused neighbours of a linear (vbs_gfx950_linear_fused) and the grouped
+ * q/k/v and gate/up launches, composed of the oracle's ops; like the device
+ * library, only for Q4_K and Q6_K and for the same combinations (else 2:
+ * nothing done, the shim issues the ops itself). A GPU launch's workgroups
+ * read and write in no fixed order, so these entries take the orders that
+ * expose aliasing: the per-row inputs (acc, gate, k_row: read by the thread
+ * that writes the row) are read first, then every output is overwritten
+ * with NaN (0xFFFF in the caches), then the inputs every workgroup reads
+ * (x, the norm weights) are read and the results computed into private
+ * copies, and the outputs are written in the reverse of the ops' order.
+ * Whenever an output aliases an input or another output of the launch, the
+ * result then differs from the ops one by one, which is what the shim's
+ * aliasing checks must prevent. Built with
+ * MOCK_DECLINE_GROUPS the grouped entries decline every shape, with
+ * MOCK_DECLINE_FUSED every entry here does (the shim's fallbacks run). */
 static unsigned g_fused[7]; /* launches joined with a NORMALIZE, ROTARY, add, ACTIVATION, CACHE;
                                grouped q/k/v and gate/up launches */
 unsigned mock_fused_count(int which) { return which >= 0 && which < 7 ? g_fused[which] : 0u; }
+
+static float *fcopy(const float *src, uint32_t n) {
+    float *d = (float *)malloc(sizeof(float) * (n ? n : 1u));
+    if (d && src) memcpy(d, src, sizeof(float) * n);
+    return d;
+}
+
+static void poison(float *p, uint32_t n) {
+    for (uint32_t i = 0; i < n; i++) p[i] = NAN;
+}
+
+static void poison16(uint16_t *p, uint32_t n) {
+    for (uint32_t i = 0; i < n; i++) p[i] = 0xFFFFu;
+}
+
+/* xn = rms_norm(x) when norm_w is given (into a fresh copy; x otherwise) */
+static float *normed_copy(const float *x, const float *norm_w, uint32_t cols, float eps) {
+    float *xn = fcopy(x, cols);
+    if (xn && norm_w) vbs_oracle_rms_norm(x, norm_w, xn, cols, eps);
+    return xn;
+}
 
 int vbs_gfx950_linear_fused(int t, const void *w, const float *x, float *y, uint32_t cols,
                             uint32_t rows, const vbs_gfx950_linear_join_t *j) {
@@ -94,69 +128,117 @@ int vbs_gfx950_linear_fused(int t, const void *w, const float *x, float *y, uint
     if ((j->norm_w != NULL) != (j->x_normed != NULL) || (j->gate != NULL) != (j->hidden != NULL) ||
         (j->k_row != NULL) != (j->kc != NULL) || (j->k_row != NULL) != (j->vc != NULL))
         return 0;
+#ifdef MOCK_DECLINE_FUSED
+    return 2;
+#endif
     if (t != 12 && t != 14) return 2;
     const int after = (j->acc != NULL) + (j->rope != 0) + (j->gate != NULL) + (j->k_row != NULL);
     if (after > 1 || (!after && !j->norm_w) || (j->norm_w && after && !j->rope)) return 2;
-    if (j->norm_w) {
-        vbs_oracle_rms_norm(x, j->norm_w, j->x_normed, cols, j->norm_eps);
-        x = j->x_normed;
+    /* per-row reads, then the outputs clobbered, then the shared reads */
+    float *acc = j->acc ? fcopy(j->acc, rows) : NULL, *gate = j->gate ? fcopy(j->gate, rows) : NULL;
+    float *krow = j->k_row ? fcopy(j->k_row, rows) : NULL;
+    if (j->x_normed) poison(j->x_normed, cols);
+    poison(y, rows);
+    if (j->acc) poison(j->acc, rows);
+    if (j->hidden) poison(j->hidden, rows);
+    if (j->k_row) {
+        poison16(j->kc + j->kv_off, rows);
+        poison16(j->vc + j->kv_off, rows);
     }
-    if (!vbs_oracle_linear_tile(t, (const uint8_t *)w, x, y, cols, rows, 0, 0, 0)) return 0;
-    if (j->rope) vbs_oracle_rope(y, j->pos, j->head_dim, rows / j->head_dim, j->theta);
-    if (j->acc) vbs_oracle_add(j->acc, y, j->acc, rows);
-    if (j->gate) vbs_oracle_silu_mul(j->gate, y, j->hidden, rows);
-    if (j->k_row) vbs_oracle_cache_store(j->k_row, y, j->kc + j->kv_off, j->vc + j->kv_off, 0, 0, 1, rows);
-    g_fused[0] += j->norm_w != NULL;
-    g_fused[1] += j->rope != 0;
-    g_fused[2] += j->acc != NULL;
-    g_fused[3] += j->gate != NULL;
-    g_fused[4] += j->k_row != NULL;
-    return 1;
+    float *xn = normed_copy(x, j->norm_w, cols, j->norm_eps), *yt = fcopy(NULL, rows);
+    float *hid = j->gate ? fcopy(NULL, rows) : NULL;
+    uint16_t *kr = j->k_row ? (uint16_t *)malloc(2u * rows) : NULL;
+    uint16_t *vr = j->k_row ? (uint16_t *)malloc(2u * rows) : NULL;
+    int ok = xn && yt && vbs_oracle_linear_tile(t, (const uint8_t *)w, xn, yt, cols, rows, 0, 0, 0);
+    if (ok && j->rope) vbs_oracle_rope(yt, j->pos, j->head_dim, rows / j->head_dim, j->theta);
+    if (ok && acc) vbs_oracle_add(acc, yt, acc, rows);
+    if (ok && hid) vbs_oracle_silu_mul(gate, yt, hid, rows);
+    if (ok && kr && vr) vbs_oracle_cache_store(krow, yt, kr, vr, 0, 0, 1, rows);
+    /* writes, last op first */
+    if (ok) {
+        if (kr && vr) {
+            memcpy(j->vc + j->kv_off, vr, 2u * rows);
+            memcpy(j->kc + j->kv_off, kr, 2u * rows);
+        }
+        if (hid) memcpy(j->hidden, hid, 4u * rows);
+        if (acc) memcpy(j->acc, acc, 4u * rows);
+        memcpy(y, yt, 4u * rows);
+        if (j->norm_w) memcpy(j->x_normed, xn, 4u * cols);
+        g_fused[0] += j->norm_w != NULL;
+        g_fused[1] += j->rope != 0;
+        g_fused[2] += j->acc != NULL;
+        g_fused[3] += j->gate != NULL;
+        g_fused[4] += j->k_row != NULL;
+    }
+    free(xn); free(yt); free(acc); free(gate); free(krow); free(hid); free(kr); free(vr);
+    return ok ? 1 : 0;
 }
 
-/* The grouped q/k/v and gate/up launches as the ops one by one (built with
- * MOCK_DECLINE_GROUPS they decline every shape, so the shim's fallbacks run). */
 int vbs_gfx950_qkv_fused(int t, const void *wq, const void *wk, const void *wv, const float *x,
                          uint32_t cols, uint32_t q_rows, uint32_t kv_rows, const float *norm_w,
                          float eps, float *x_normed, float *q, float *k, float *v, uint32_t pos,
                          uint32_t hd, float theta, uint16_t *kc, uint16_t *vc, uint32_t layer,
                          uint32_t max_ctx) {
     if ((norm_w != NULL) != (x_normed != NULL) || pos >= max_ctx) return 0;
-#ifdef MOCK_DECLINE_GROUPS
+#if defined(MOCK_DECLINE_GROUPS) || defined(MOCK_DECLINE_FUSED)
     return 2;
 #endif
     if (t != 12 && t != 14) return 2;
-    if (norm_w) {
-        vbs_oracle_rms_norm(x, norm_w, x_normed, cols, eps);
-        x = x_normed;
+    const uint64_t off = ((uint64_t)layer * max_ctx + pos) * kv_rows;
+    if (x_normed) poison(x_normed, cols);
+    poison(q, q_rows);
+    poison(k, kv_rows);
+    poison(v, kv_rows);
+    poison16(kc + off, kv_rows);
+    poison16(vc + off, kv_rows);
+    float *xn = normed_copy(x, norm_w, cols, eps), *qt = fcopy(NULL, q_rows);
+    float *kt = fcopy(NULL, kv_rows), *vt = fcopy(NULL, kv_rows);
+    uint16_t *kr = (uint16_t *)malloc(2u * kv_rows), *vr = (uint16_t *)malloc(2u * kv_rows);
+    int ok = xn && qt && kt && vt && kr && vr &&
+             vbs_oracle_linear_tile(t, (const uint8_t *)wq, xn, qt, cols, q_rows, 0, 0, 0) &&
+             vbs_oracle_linear_tile(t, (const uint8_t *)wk, xn, kt, cols, kv_rows, 0, 0, 0) &&
+             vbs_oracle_linear_tile(t, (const uint8_t *)wv, xn, vt, cols, kv_rows, 0, 0, 0);
+    if (ok) {
+        vbs_oracle_rope(qt, pos, hd, q_rows / hd, theta);
+        vbs_oracle_rope(kt, pos, hd, kv_rows / hd, theta);
+        vbs_oracle_cache_store(kt, vt, kr, vr, 0, 0, 1, kv_rows);
+        memcpy(vc + off, vr, 2u * kv_rows);
+        memcpy(kc + off, kr, 2u * kv_rows);
+        memcpy(v, vt, 4u * kv_rows);
+        memcpy(k, kt, 4u * kv_rows);
+        memcpy(q, qt, 4u * q_rows);
+        if (norm_w) memcpy(x_normed, xn, 4u * cols);
+        g_fused[5]++;
     }
-    if (!vbs_oracle_linear_tile(t, (const uint8_t *)wq, x, q, cols, q_rows, 0, 0, 0) ||
-        !vbs_oracle_linear_tile(t, (const uint8_t *)wk, x, k, cols, kv_rows, 0, 0, 0) ||
-        !vbs_oracle_linear_tile(t, (const uint8_t *)wv, x, v, cols, kv_rows, 0, 0, 0))
-        return 0;
-    vbs_oracle_rope(q, pos, hd, q_rows / hd, theta);
-    vbs_oracle_rope(k, pos, hd, kv_rows / hd, theta);
-    vbs_oracle_cache_store(k, v, kc, vc, pos, layer, max_ctx, kv_rows);
-    g_fused[5]++;
-    return 1;
+    free(xn); free(qt); free(kt); free(vt); free(kr); free(vr);
+    return ok ? 1 : 0;
 }
 
 int vbs_gfx950_gate_up_fused(int t, const void *wg, const void *wu, const float *x, uint32_t cols,
                              uint32_t rows, const float *norm_w, float eps, float *x_normed,
                              float *gate, float *up, float *hidden) {
     if ((norm_w != NULL) != (x_normed != NULL)) return 0;
-#ifdef MOCK_DECLINE_GROUPS
+#if defined(MOCK_DECLINE_GROUPS) || defined(MOCK_DECLINE_FUSED)
     return 2;
 #endif
     if (t != 12 && t != 14) return 2;
-    if (norm_w) {
-        vbs_oracle_rms_norm(x, norm_w, x_normed, cols, eps);
-        x = x_normed;
+    if (x_normed) poison(x_normed, cols);
+    poison(gate, rows);
+    poison(up, rows);
+    poison(hidden, rows);
+    float *xn = normed_copy(x, norm_w, cols, eps), *gt = fcopy(NULL, rows);
+    float *ut = fcopy(NULL, rows), *ht = fcopy(NULL, rows);
+    int ok = xn && gt && ut && ht &&
+             vbs_oracle_linear_tile(t, (const uint8_t *)wg, xn, gt, cols, rows, 0, 0, 0) &&
+             vbs_oracle_linear_tile(t, (const uint8_t *)wu, xn, ut, cols, rows, 0, 0, 0);
+    if (ok) {
+        vbs_oracle_silu_mul(gt, ut, ht, rows);
+        memcpy(hidden, ht, 4u * rows);
+        memcpy(up, ut, 4u * rows);
+        memcpy(gate, gt, 4u * rows);
+        if (norm_w) memcpy(x_normed, xn, 4u * cols);
+        g_fused[6]++;
     }
-    if (!vbs_oracle_linear_tile(t, (const uint8_t *)wg, x, gate, cols, rows, 0, 0, 0) ||
-        !vbs_oracle_linear_tile(t, (const uint8_t *)wu, x, up, cols, rows, 0, 0, 0))
-        return 0;
-    vbs_oracle_silu_mul(gate, up, hidden, rows);
-    g_fused[6]++;
-    return 1;
+    free(xn); free(gt); free(ut); free(ht);
+    return ok ? 1 : 0;
 }

@@ -219,6 +219,193 @@ def test_held_ops_on_host_mock_keep_the_bridge_results(tmpdir_mod, host, case):
     assert joined == [steps * (per * L + once) for per, once in want], joined
 
 
+def test_held_ops_random_sequences_equal_ops_one_by_one(tmpdir_mod, host):
+    """Random op sequences over a small pool of buffers — bridge-like q/k/v
+    and gate/up runs with randomly chosen (often aliasing) buffers, a linear
+    with the op after it, and single NORMALIZE, LINEAR, ROTARY, CACHE,
+    ACTIVATION and ELEMENTWISE ops and read-backs — through two shims over
+    the host mock (one whose fused and grouped entries run, one built to
+    decline them all, so that the shim's fallbacks run) and, as the
+    reference, through the oracle's ops one at a time on host arrays. Every
+    buffer and both caches must agree bit for bit after every sequence: a
+    difference is the held-op logic reordering, dropping or mis-joining an
+    op (the mock's entries also expose aliasing inside one launch)."""
+    n_buf, dim, hd, mc, layers = 6, 512, 64, 16, 2
+    so_f = build_mock(tmpdir_mod, "mock_rand_fused.so")
+    so_s = build_mock(tmpdir_mod, "mock_rand_single.so", ("MOCK_DECLINE_FUSED",))
+    shims = [fresh_shim(tmpdir_mod, so) for so in (so_f, so_s)]
+    for be, ok in shims:
+        assert ok, be.last_error()
+    orc = Oracle()
+    mats = {r: V.synth_matrix(host, V.Q4_K, r, dim, 77, 200 + r) for r in (512, 256)}
+    rng = np.random.default_rng(4242)
+    A = V.Backend.buf_arg
+    norm_w = rng.standard_normal(dim).astype(np.float32)
+    states = []
+    for be, _ in shims:
+        dev = be.device()
+        st = {"be": be, "dev": dev, "keep": [],
+              "bufs": [be.upload(np.zeros(dim, np.float32)) for _ in range(n_buf)],
+              "norm_w": be.upload(norm_w),
+              "kc": be.upload(np.zeros(layers * mc * dim, np.uint16)),
+              "vc": be.upload(np.zeros(layers * mc * dim, np.uint16)),
+              "w": {r: be.upload(m) for r, m in mats.items()},
+              "lin": be.ops.compile_linear_pipeline(dev, V.Q4_K, None, 0),
+              "prim": {k: be.ops.compile_primitive_pipeline(dev, k, None, 0) for k in (
+                  V.OP_NORMALIZE, V.OP_ROTARY, V.OP_CACHE, V.OP_ACTIVATION, V.OP_ELEMENTWISE)}}
+        states.append(st)
+    ref = {"kc": np.zeros(layers * mc * dim, np.uint16),
+           "vc": np.zeros(layers * mc * dim, np.uint16)}
+
+    def run_ref(op):
+        b = ref["bufs"]
+        kind = op[0]
+        if kind == "read":
+            return b[op[1]].copy()
+        if kind == "lin":
+            _, r, i, o = op
+            b[o][:r] = orc.linear(V.Q4_K, mats[r], b[i], dim, r, threads=1)
+        elif kind == "norm":
+            _, i, o = op
+            b[o][:] = orc.rms_norm(b[i], norm_w, 1e-5)
+        elif kind == "rope":
+            _, i, pos, nh, theta = op
+            b[i][:nh * hd] = orc.rope(b[i][:nh * hd], pos, hd, nh, theta)
+        elif kind == "cache":
+            _, k, v, pos, layer, kvd = op
+            orc.cache_store(np.ascontiguousarray(b[k][:kvd]), np.ascontiguousarray(b[v][:kvd]),
+                            ref["kc"], ref["vc"], pos, layer, mc, kvd)
+        elif kind == "act":
+            _, g, u, o, n = op
+            b[o][:n] = orc.silu_mul(b[g][:n].copy(), b[u][:n].copy())
+        else:
+            _, a_, b_, o, n = op
+            b[o][:n] = orc.add(b[a_][:n].copy(), b[b_][:n].copy())
+        return True
+
+    def run(st, op):
+        be, keep, b = st["be"], st["keep"], st["bufs"]
+        U = lambda v: be.u32_arg(keep, v)
+        F = lambda v: be.f32_arg(keep, v)
+        kind = op[0]
+        if kind == "read":
+            return be.download(b[op[1]], dim, np.float32)
+        if kind == "lin":
+            _, r, i, o = op
+            return bool(be.ops.dispatch_linear_tile(st["dev"], st["lin"], st["w"][r], None, 0, b[i],
+                                                    b[o], dim, r, 0, 0, False))
+        if kind == "norm":
+            _, i, o = op
+            args = [A(b[i]), A(st["norm_w"]), A(b[o]), U(dim), F(1e-5)]
+        elif kind == "rope":
+            _, i, pos, nh, theta = op
+            args = [A(b[i]), U(pos), U(hd), U(nh), F(theta)]
+        elif kind == "cache":
+            _, k, v, pos, layer, kvd = op
+            args = [A(b[k]), A(b[v]), A(st["kc"]), A(st["vc"]), U(pos), U(layer), U(mc), U(kvd)]
+        elif kind == "act":
+            _, g, u, o, n = op
+            args = [A(b[g]), A(b[u]), A(b[o]), U(n)]
+        else:  # add
+            _, a_, b_, o, n = op
+            args = [A(b[a_]), A(b[b_]), A(b[o]), U(n)]
+        pk = {"norm": V.OP_NORMALIZE, "rope": V.OP_ROTARY, "cache": V.OP_CACHE,
+              "act": V.OP_ACTIVATION, "add": V.OP_ELEMENTWISE}[kind]
+        return be.dispatch(st["prim"][pk], args)
+
+    def pick(k=1):
+        return [int(v) for v in rng.integers(0, n_buf, k)]
+
+    def pick_run(k):  # distinct buffers (a bridge-like run) or, now and then, any
+        return [int(v) for v in rng.choice(n_buf, k, replace=False)] if rng.random() < 0.7 \
+            else pick(k)
+
+    def no_inplace_lin(ops):
+        # (a linear whose output is its input is left out: its result depends
+        # on the order in which an implementation writes rows; the bridge
+        # never issues one)
+        return [("lin", op[1], op[2], (op[3] + 1) % n_buf if op[3] == op[2] else op[3])
+                if op[0] == "lin" else op for op in ops]
+
+    def sequence():
+        # (short, with a fresh cache row per block, so that a wrong value is
+        # seldom overwritten before the buffers are compared)
+        ops = []
+        for _ in range(int(rng.integers(1, 4))):
+            pos, layer = int(rng.integers(0, mc)), int(rng.integers(0, layers))
+            c = rng.random()
+            if c < 0.3:    # a q/k/v run: norm, q, rope, k, rope, v, cache
+                x, n_, q, k, v = pick_run(5)
+                kvr = int(rng.choice([256, 512]))
+                # (now and then the k rope or the cache at another position or base)
+                pk = pos if rng.random() < 0.85 else (pos + 1) % mc
+                c3 = rng.random()
+                pc = pos if c3 < 0.8 else pk if c3 < 0.9 else (pos + 3) % mc
+                tk = 10000.0 if rng.random() < 0.85 else 500000.0
+                xv = n_ if rng.random() < 0.9 else x  # (now and then v reads another vector)
+                ops += [("norm", x, n_), ("lin", 512, n_, q), ("rope", q, pos, 512 // hd, 10000.0),
+                        ("lin", kvr, n_, k), ("rope", k, pk, kvr // hd, tk), ("lin", kvr, xv, v),
+                        ("cache", k, v, pc, layer, kvr)]
+            elif c < 0.55:  # a gate/up run
+                x, n_, g, u, h = pick_run(5)
+                r = int(rng.choice([256, 512]))
+                xu = n_ if rng.random() < 0.9 else x  # (now and then up reads another vector)
+                ops += [("norm", x, n_), ("lin", r, n_, g), ("lin", r, xu, u), ("act", g, u, h, r)]
+            elif c < 0.7:   # a linear and the op after it
+                i, o, s_, h = pick(4)
+                r = int(rng.choice([256, 512]))
+                c2 = rng.random()
+                ops += [("lin", r, i, o), ("add", s_, o, s_, r) if c2 < 0.3 else
+                        ("cache", s_, o, pos, layer, r) if c2 < 0.55 else
+                        ("act", s_, o, h, r) if c2 < 0.8 else ("rope", o, pos, r // hd, 10000.0)]
+                if c2 >= 0.8 and rng.random() < 0.5:  # a second rotation of the same rows
+                    ops.append(("rope", o, (pos + 1) % mc, r // hd, 10000.0))
+            else:           # single ops
+                c2 = rng.random()
+                i, o, a_, r = *pick(3), int(rng.choice([256, 512]))
+                ops.append(("norm", i, o) if c2 < 0.2 else ("lin", r, i, o) if c2 < 0.45 else
+                           ("rope", i, pos, r // hd, 10000.0) if c2 < 0.6 else
+                           ("cache", i, o, pos, layer, r) if c2 < 0.7 else
+                           ("act", i, o, a_, r) if c2 < 0.8 else ("add", i, o, a_, r) if c2 < 0.9
+                           else ("read", i))
+        return ops
+
+    finite = 0
+    for seq_no in range(300):
+        # fresh values each sequence (chained matvecs would grow to inf / NaN,
+        # which then hides every difference)
+        fresh = [rng.standard_normal(dim).astype(np.float32) for _ in range(n_buf)]
+        ref["bufs"] = [f.copy() for f in fresh]
+        for st in states:
+            for buf_, val in zip(st["bufs"], fresh):
+                assert st["be"].ops.copy_to_device(buf_, val.ctypes.data, val.nbytes)
+        for op in no_inplace_lin(sequence()):
+            want = run_ref(op)
+            for n_st, st in enumerate(states):
+                got = run(st, op)
+                if op[0] == "read":
+                    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), \
+                        (seq_no, n_st, op)
+                else:
+                    assert got, (seq_no, n_st, op, st["be"].last_error())
+        for i in range(n_buf):
+            for n_st, st in enumerate(states):
+                a = st["be"].download(st["bufs"][i], dim, np.float32)
+                assert np.array_equal(a.view(np.uint32), ref["bufs"][i].view(np.uint32)), \
+                    (seq_no, n_st, i)
+            finite += bool(np.all(np.isfinite(ref["bufs"][i])))
+        for c in ("kc", "vc"):
+            for n_st, st in enumerate(states):
+                a = st["be"].download(st[c], layers * mc * dim, np.uint16)
+                assert np.array_equal(a, ref[c]), (seq_no, n_st, c)
+    assert finite > 0.9 * 300 * n_buf, finite  # the comparisons were of numbers
+    # every kind of join and group happened along the way
+    mock = C.CDLL(so_f)
+    mock.mock_fused_count.restype = C.c_uint
+    counts = [mock.mock_fused_count(i) for i in range(7)]
+    assert all(c > 0 for c in counts), counts
+
+
 def test_shim_marshalling_rejects_malformed_arguments(tmpdir_mod):
     so = build_mock(tmpdir_mod, "mock_ok2.so")
     be, ok = fresh_shim(tmpdir_mod, so)

@@ -677,6 +677,7 @@ static bool gfx950_dispatch_primitive(vbs_device_t *dev, void *pipeline, const v
             case VBS_OP_CACHE: { /* (k, v, kc, vc, pos, layer, max_ctx, kv_dim) */
                 const uint32_t pos = U32(4), layer = U32(5), mc = U32(6), kvd = U32(7);
                 const held_linear_t *q = &h->lin[0], *k = &h->lin[1], *v = &h->lin[2];
+                if (touches_held(BUF(2)) || touches_held(BUF(3))) break;  /* the caches */
                 if (h->n_lin == 3 && q->rope && k->rope && !v->rope && BUF(0) == k->y &&
                     BUF(1) == v->y && kvd == k->rows && kvd == v->rows && pos < mc &&
                     q->pos == pos && k->pos == pos && q->hd == k->hd && q->theta == k->theta) {
