@@ -133,6 +133,23 @@ int vbs_gfx950_add(const float *a, const float *b, float *out, uint32_t n);
 
 /* ---- extensions (no slot in vbs_backend_ops_t) -------------------------- */
 
+/* Attention of eight kv heads at head_dim 128 (both BASELINE models) runs as
+ * one launch (chunks and merge, each kv head on one XCD) when a start-up probe
+ * finds workgroups dealt to the eight XCDs round-robin; otherwise as a chunk
+ * launch and a merge launch. The results are bit-identical either way. No
+ * counterpart in the reference: set 0 or 1 switches the one-launch form off
+ * or back on (on only if the probe passed), -1 only asks; returns 1 when it
+ * is on. Calls that overlap on one GPU race on its flag words (the library
+ * orders its own work on one stream). */
+int vbs_gfx950_attention_one_launch(int set);
+
+/* The one-launch attention's sticky error word (synchronizes the library's
+ * stream): nonzero after a launch found itself on a part with other than
+ * eight XCDs or a merge gave up waiting for its chunks (that head's output
+ * is then NaN); -1 on an error. */
+int vbs_gfx950_attention_one_launch_errors(void);
+
+
 /* Dequantise rows of a packed tensor: out[i*dim .. +dim) = deq(row ids[i])
  * (ids == NULL means rows 0..n_rows-1). `ids` is a device array. The batched
  * form of the one-token-per-dispatch EMBEDDING op, and the bit-exactness
