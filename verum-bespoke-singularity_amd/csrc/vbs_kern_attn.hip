@@ -744,10 +744,13 @@ __global__ __launch_bounds__(64) void k_xcc_probe(uint32_t *ids) {
     if (threadIdx.x == 0) ids[blockIdx.x] = x;
 }
 
-// A load that skips the CU's L1 (served by the XCD's L2).
+// A load served by the XCD's L2: the CU's L1 is dropped first (buffer_inv
+// sc0; a load's sc0 bit alone asks only for workgroup scope, which the L1
+// may serve from a line it already holds).
 __device__ __forceinline__ uint32_t load_l2(const uint32_t *p) {
     uint32_t v;
-    asm volatile("global_load_dword %0, %1, off sc0\n\ts_waitcnt vmcnt(0)" : "=v"(v) : "v"(p) : "memory");
+    asm volatile("buffer_inv sc0\n\tglobal_load_dword %0, %1, off\n\ts_waitcnt vmcnt(0)"
+                 : "=v"(v) : "v"(p) : "memory");
     return v;
 }
 
