@@ -114,10 +114,11 @@ int vbs_gfx950_attention(const float *q, const uint16_t *kc, const uint16_t *vc,
  * tight serving loops, harnesses that forbid hipMalloc). Same arguments and
  * result as vbs_gfx950_attention; the per-chunk partial results live in a
  * fixed 8 MiB device array of the library instead of the growable scratch, so
- * calls whose partials exceed it (nqh x max(ceil(640 / nkh), ceil(seq_len /
- * 64)) x (head_dim + 2) x 4 bytes, 640 being the workgroup target of the
- * sequence split, kMfmaTargetWgs in csrc/vbs_attn_common.h; e.g. 70B shapes
- * up to seq_len 16128) fail with a reason and launch nothing. Every call on the device shares that
+ * calls whose partials exceed it (nqh x R x (head_dim + 2) x 4 bytes, R =
+ * max(ceil(640 / nkh), ceil(seq_len / 64)) rounded up to a multiple of 16,
+ * 640 being the workgroup target of the sequence split, kMfmaTargetWgs in
+ * csrc/vbs_attn_common.h; e.g. 70B shapes up to seq_len 15360) fail with a
+ * reason and launch nothing. Every call on the device shares that
  * array: calls that overlap on the device race (the library's own calls are
  * ordered on its one stream and never overlap). */
 int vbs_gfx950_attention_noalloc(const float *q, const uint16_t *kc, const uint16_t *vc,

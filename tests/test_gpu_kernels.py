@@ -616,7 +616,8 @@ def test_attention_one_launch_equals_two_launches(dev, host, mem):
                 else:
                     dev.attention(pq, pkc, pvc, po, seq, layer, max_ctx, nqh, nkh, hd, scale)
                 outs.append(dev.download(po, nqh * hd, np.float32))
-            assert np.all(np.isfinite(outs[0])), (nqh, seq)
+            assert np.all(np.isfinite(outs[0])), (nqh, seq, dev.attention_one_launch_errors(),
+                                                  np.nonzero(~np.isfinite(outs[0]))[0][::128])
             for o in outs[1:]:
                 assert np.array_equal(outs[0].view(np.uint32), o.view(np.uint32)), (nqh, seq, layer)
         assert dev.attention_one_launch_errors() == 0

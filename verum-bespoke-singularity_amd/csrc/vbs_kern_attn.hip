@@ -44,10 +44,14 @@ constexpr uint32_t kTargetWgs = 512;      // workgroups the vector-ALU split aim
 
 // (attn_split, the matrix-core split's constants and fast_exp: vbs_attn_common.h)
 // Chunks per kv head of any split of a sequence of at most max_seq (every
-// len >= 64 or len >= seq * nkh / target, target <= kMfmaTargetWgs).
+// len >= 64 or len >= seq * nkh / target, target <= kMfmaTargetWgs), rounded
+// up to a multiple of 16: the partial rows' stride, so that each q head's
+// rows start on a 128-byte line of their own (16 rows of 130 floats are 65
+// lines) and no line holds two heads' rows (the one-launch attention reads a
+// head's rows while other heads' rows are still being written).
 inline uint32_t attn_max_chunks(uint32_t max_seq, uint32_t nkh) {
     const uint32_t a = (kMfmaTargetWgs + nkh - 1u) / nkh, b = (max_seq + 63u) / 64u;
-    return a > b ? a : b;
+    return ((a > b ? a : b) + 15u) & ~15u;
 }
 
 // f16 bits -> f32 with the hardware converter (exact for every finite value).
@@ -722,10 +726,12 @@ __global__ __launch_bounds__(64 * kMergeRes) void k_attn_merge_h128(
 // chunk j, does what k_attn_mfma does for it; then, once its partial stores
 // are complete (in the XCD's L2), it raises flag j of each q head of its group.
 // The last 8 x group workgroups of the grid merge: workgroup j = n_slots + hh
-// of XCD h waits until the flags of q head h * group + hh show every chunk
-// with work, drops its L1 (buffer_inv sc0), merges the partials from the same
-// L2 with merge_one_wave (bit-identical to k_attn_merge_h128) and clears the
-// flags for the next launch. Everything stays inside one XCD's L2, so no
+// of XCD h waits until the flags of q head h * group + hh, read in the L2,
+// show every chunk with work, then merges the partials with merge_one_wave
+// (bit-identical to k_attn_merge_h128) and clears the flags for the next
+// launch. Its loads of the partials miss the CU's L1: nothing in this launch
+// read those lines before (each head's rows sit on lines of their own, see
+// attn_max_chunks, and only the head's merging workgroup reads them). Everything stays inside one XCD's L2, so no
 // device-scope release or acquire is needed, and no two workgroups update one
 // word (no atomics). Every workgroup of the grid fits on the chip at once and
 // the merging ones are dealt last, so their wait cannot hold a chunk back;
@@ -744,14 +750,14 @@ __global__ __launch_bounds__(64) void k_xcc_probe(uint32_t *ids) {
     if (threadIdx.x == 0) ids[blockIdx.x] = x;
 }
 
-// A load served by the XCD's L2: the CU's L1 is dropped first (buffer_inv
-// sc0; a load's sc0 bit alone asks only for workgroup scope, which the L1
-// may serve from a line it already holds).
-__device__ __forceinline__ uint32_t load_l2(const uint32_t *p) {
-    uint32_t v;
-    asm volatile("buffer_inv sc0\n\tglobal_load_dword %0, %1, off\n\ts_waitcnt vmcnt(0)"
-                 : "=v"(v) : "v"(p) : "memory");
-    return v;
+// The word at p as the XCD's L2 holds it: an atomic add of zero (atomics are
+// performed in the L2; a plain load may be served by a line the CU's L1 took
+// at an earlier poll). The zero is hidden from the compiler so that the add
+// is not turned into a load.
+__device__ __forceinline__ uint32_t load_l2(uint32_t *p) {
+    uint32_t z = 0u;
+    asm volatile("" : "+v"(z));
+    return __hip_atomic_fetch_add(p, z, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
 __global__ __launch_bounds__(64) void k_attn_one_launch(
@@ -885,16 +891,16 @@ hipError_t launch_attention(const float *q, const uint16_t *kc, const uint16_t *
     hipError_t e;
     uint32_t gran = kChunk, lmax = kChunk, target = kTargetWgs;
     const dim3 grid(stride, nkh);
-    if (fast && hd == 128u && nkh == kAttnOneKvh && stride <= kAttnFlagStride &&
+    const uint32_t slots = mfma_grid_chunks(seq_len, nkh);
+    if (fast && hd == 128u && nkh == kAttnOneKvh && slots <= kAttnFlagStride &&
         nqh <= kAttnFlagHeads && rt_attn_one_launch()) {
-        const uint32_t slots = mfma_grid_chunks(seq_len, nkh);
         k_attn_one_launch<<<kAttnOneKvh * (slots + group), 64, 0, s>>>(
             q, kc, vc, part, out, seq_len, pos_dev, layer_off, group, scale, stride, slots,
             rt_counters());
         return hipGetLastError();
     }
     if (fast && hd == 128u) {
-        k_attn_mfma<<<dim3(mfma_grid_chunks(seq_len, nkh), nkh), 64, 0, s>>>(
+        k_attn_mfma<<<dim3(slots, nkh), 64, 0, s>>>(
             q, kc, vc, part, seq_len, pos_dev, layer_off, nkh, group, scale, stride, 0u, 0ull, 0ull);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         k_attn_merge_h128<<<nqh, 64 * kMergeRes, 0, s>>>(part, out, stride, pos_dev, seq_len, nkh,
