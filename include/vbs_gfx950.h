@@ -114,11 +114,10 @@ int vbs_gfx950_attention(const float *q, const uint16_t *kc, const uint16_t *vc,
  * tight serving loops, harnesses that forbid hipMalloc). Same arguments and
  * result as vbs_gfx950_attention; the per-chunk partial results live in a
  * fixed 8 MiB device array of the library instead of the growable scratch, so
- * calls whose partials exceed it (nqh x R x (head_dim + 2) x 4 bytes, R =
- * max(ceil(640 / nkh), ceil(seq_len / 64)) rounded up to a multiple of 16,
- * 640 being the workgroup target of the sequence split, kMfmaTargetWgs in
- * csrc/vbs_attn_common.h; e.g. 70B shapes up to seq_len 15360) fail with a
- * reason and launch nothing. Every call on the device shares that
+ * calls whose partials exceed it (nqh x max(ceil(640 / nkh), ceil(seq_len /
+ * 64)) x (head_dim + 2) x 4 bytes, 640 being the workgroup target of the
+ * sequence split, kMfmaTargetWgs in csrc/vbs_attn_common.h; e.g. 70B shapes
+ * up to seq_len 16128) fail with a reason and launch nothing. Every call on the device shares that
  * array: calls that overlap on the device race (the library's own calls are
  * ordered on its one stream and never overlap). */
 int vbs_gfx950_attention_noalloc(const float *q, const uint16_t *kc, const uint16_t *vc,
@@ -133,23 +132,6 @@ int vbs_gfx950_silu_mul(const float *gate, const float *up, float *out, uint32_t
 int vbs_gfx950_add(const float *a, const float *b, float *out, uint32_t n);
 
 /* ---- extensions (no slot in vbs_backend_ops_t) -------------------------- */
-
-/* Attention of eight kv heads at head_dim 128 (both BASELINE models) runs as
- * one launch (chunks and merge, each kv head on one XCD) when a start-up probe
- * finds workgroups dealt to the eight XCDs round-robin; otherwise as a chunk
- * launch and a merge launch. The results are bit-identical either way. No
- * counterpart in the reference: set 0 or 1 switches the one-launch form off
- * or back on (on only if the probe passed), -1 only asks; returns 1 when it
- * is on. Calls that overlap on one GPU race on its flag words (the library
- * orders its own work on one stream). */
-int vbs_gfx950_attention_one_launch(int set);
-
-/* The one-launch attention's sticky error word (synchronizes the library's
- * stream): nonzero after a launch found itself on a part with other than
- * eight XCDs or a merge gave up waiting for its chunks (that head's output
- * is then NaN); -1 on an error. */
-int vbs_gfx950_attention_one_launch_errors(void);
-
 
 /* Dequantise rows of a packed tensor: out[i*dim .. +dim) = deq(row ids[i])
  * (ids == NULL means rows 0..n_rows-1). `ids` is a device array. The batched

@@ -584,47 +584,6 @@ def test_attention(dev, host, oracle, mem, nqh, nkh, hd, seq, max_ctx, layer):
     assert np.all(np.abs(got - want) <= 1e-4 + 1e-4 * np.abs(want))
 
 
-def test_attention_one_launch_equals_two_launches(dev, host, mem):
-    """Eight kv heads at head_dim 128 run chunks and merge in one launch
-    (each kv head on one XCD, merging workgroups waiting on per-chunk flags)
-    when the start-up probe allows it. Against the two-launch form: the same
-    bits for groups 1, 2, 4 and 8 over sequences of 1 to 8193 positions
-    (one chunk to the full split), including calls in a row that shrink the
-    sequence (the flags must be clear after each launch), the no-allocation
-    entry point, and no error recorded."""
-    if not dev.attention_one_launch(-1):
-        pytest.skip("the start-up probe did not find eight XCDs dealt round-robin")
-    cases = [(8, 1, 0), (16, 7, 1), (32, 33, 0), (32, 2049, 3), (32, 2048, 3), (32, 700, 0),
-             (64, 8193, 0), (64, 8192, 1), (64, 100, 0), (32, 1, 2)]
-    hd, nkh, layers, max_ctx = 128, 8, 4, 8200
-    kvd = nkh * hd
-    kc = V.synth_normal_f16(host, layers * max_ctx * kvd, SEED, 171)
-    vc = V.synth_normal_f16(host, layers * max_ctx * kvd, SEED, 172)
-    pkc, pvc = mem.up(kc), mem.up(vc)
-    try:
-        for nqh, seq, layer in cases:
-            q = synth_x(host, nqh * hd, 173 + seq)
-            scale = np.float32(1.0 / math.sqrt(hd))
-            pq = mem.up(q)
-            outs = []
-            for one, noalloc in ((True, False), (False, False), (True, True)):
-                assert dev.attention_one_launch(int(one)) == one
-                po = mem.up(np.full(nqh * hd, 7.0, np.float32))
-                if noalloc:
-                    assert dev._attention_noalloc(pq, pkc, pvc, po, seq, layer, max_ctx, nqh, nkh,
-                                                  hd, float(scale)), dev.error()
-                else:
-                    dev.attention(pq, pkc, pvc, po, seq, layer, max_ctx, nqh, nkh, hd, scale)
-                outs.append(dev.download(po, nqh * hd, np.float32))
-            assert np.all(np.isfinite(outs[0])), (nqh, seq, dev.attention_one_launch_errors(),
-                                                  np.nonzero(~np.isfinite(outs[0]))[0][::128])
-            for o in outs[1:]:
-                assert np.array_equal(outs[0].view(np.uint32), o.view(np.uint32)), (nqh, seq, layer)
-        assert dev.attention_one_launch_errors() == 0
-    finally:
-        dev.attention_one_launch(1)
-
-
 @pytest.mark.parametrize("qscale", [1e-6, 1e4])
 def test_attention_q_magnitude(dev, host, oracle, mem, qscale):
     """q far from unit scale (the matrix-core kernel rescales each head's q

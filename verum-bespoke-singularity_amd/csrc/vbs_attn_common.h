@@ -136,13 +136,6 @@ __device__ __forceinline__ float2 merge_residue_sum(const float *ph, uint32_t nc
     return make_float2(ox, oy);
 }
 
-// The same merge by one wave: the four residue sums accumulated together in
-// chunk order (each residue's chunks still in its own order), the acc rows of
-// kOneWaveBatch chunks requested at once, the first batch with the (m, l)
-// loads. Bit-identical to the four-wave kernel's.
-constexpr uint32_t kOneWaveBatch = 40;  // (a multiple of kMergeRes)
-__device__ __forceinline__ float2 merge_one_wave(const float *ph, uint32_t nc, uint32_t lane);
-
 // The four residues in order, scaled by 1 / L.
 __device__ __forceinline__ float2 merge_finish(const float2 a[kMergeRes], float L) {
     float2 s = a[0];
@@ -153,45 +146,6 @@ __device__ __forceinline__ float2 merge_finish(const float2 a[kMergeRes], float 
     }
     const float inv = __fdiv_rn(1.0f, L);
     return make_float2(__fmul_rn(s.x, inv), __fmul_rn(s.y, inv));
-}
-
-__device__ __forceinline__ float2 merge_one_wave(const float *ph, uint32_t nc, uint32_t lane) {
-    auto load_batch = [&](uint32_t c0, float2 av[kOneWaveBatch]) {
-#pragma unroll
-        for (uint32_t k = 0; k < kOneWaveBatch; k++) {
-            const uint32_t c = c0 + k;
-            av[k] = c < nc ? *reinterpret_cast<const float2 *>(ph + (uint64_t)c * kPartRow + 2u + 2u * lane)
-                           : make_float2(0.f, 0.f);
-        }
-    };
-    float2 av[kOneWaveBatch];
-    load_batch(0u, av);
-    const MergeStats st = merge_stats(ph, nc, lane, merge_ml_load(ph, nc, lane));
-    float ox[kMergeRes] = {0.f, 0.f, 0.f, 0.f}, oy[kMergeRes] = {0.f, 0.f, 0.f, 0.f};
-    for (uint32_t c0 = 0; c0 < nc; c0 += kOneWaveBatch) {
-        if (c0) load_batch(c0, av);
-#pragma unroll
-        for (uint32_t k = 0; k < kOneWaveBatch; k++) {
-            const uint32_t c = c0 + k, r = k % kMergeRes;  // (c0 is a multiple of kMergeRes)
-            if (c < nc) {
-                float wc;
-                if (c < 128u) {  // (as merge_residue_sum: c is wave-uniform)
-                    wc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
-                                                       __builtin_bit_cast(int, c < 64u ? st.w_lane : st.w_lane64),
-                                                       (int)(c & 63u)));
-                } else {
-                    const float mc = ph[(uint64_t)c * kPartRow];
-                    wc = mc == -INFINITY ? 0.f : fast_exp(__fsub_rn(mc, st.M));
-                }
-                ox[r] = fmaf(av[k].x, wc, ox[r]);
-                oy[r] = fmaf(av[k].y, wc, oy[r]);
-            }
-        }
-    }
-    float2 a[kMergeRes];
-#pragma unroll
-    for (uint32_t r = 0; r < kMergeRes; r++) a[r] = make_float2(ox[r], oy[r]);
-    return merge_finish(a, st.L);
 }
 
 }  // namespace vbs

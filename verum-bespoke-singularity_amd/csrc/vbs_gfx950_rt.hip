@@ -43,8 +43,6 @@ struct Runtime {
     int n_retired = 0;
     void *noalloc_scratch = nullptr;  // device address of `scratch` on the library's device
     uint32_t *counters = nullptr;  // zeroed once; kernels that use one leave it at 0
-    bool attn_xcd_ok = false;      // the start-up probe found the round-robin XCD deal
-    bool attn_one_launch = false;  // attention of eight kv heads as one launch
 };
 
 Runtime g_rt;
@@ -141,8 +139,6 @@ hipStream_t rt_stream() { return g_rt.stream; }
 
 uint32_t *rt_counters() { return g_rt.counters; }
 
-bool rt_attn_one_launch() { return g_rt.attn_one_launch; }
-
 
 int rt_fail(const char *fmt, ...) {
     va_list ap;
@@ -195,15 +191,6 @@ int vbs_gfx950_init(void) {
         !hip_ok(hipMemset(g_rt.counters, 0, kCounterSlots * sizeof(uint32_t)), "hipMemset(counters)") ||
         !hip_ok(hipDeviceSynchronize(), "init"))
         return 0;
-    {  // the XCD deal the one-launch attention relies on
-        uint32_t *ids = nullptr;
-        if (!hip_ok(hipMalloc(&ids, 2048 * sizeof(uint32_t)), "hipMalloc(probe)")) return 0;
-        bool ok = false;
-        const hipError_t e = attention_xcd_probe(ids, g_rt.stream, &ok);
-        (void)hipFree(ids);
-        if (!hip_ok(e, "XCD probe")) return 0;
-        g_rt.attn_xcd_ok = g_rt.attn_one_launch = ok;
-    }
     g_rt.device = chosen;
     g_rt.ready = true;
     snprintf(g_err, sizeof(g_err), "ok");
@@ -211,23 +198,6 @@ int vbs_gfx950_init(void) {
 }
 
 int vbs_gfx950_device_count(void) { return g_rt.ready ? 1 : 0; }
-
-int vbs_gfx950_attention_one_launch(int set) {
-    if (!ready_or_fail()) return 0;
-    if (set == 0 || set == 1) g_rt.attn_one_launch = set == 1 && g_rt.attn_xcd_ok;
-    return g_rt.attn_one_launch ? 1 : 0;
-}
-
-int vbs_gfx950_attention_one_launch_errors(void) {
-    if (!ready_or_fail()) return -1;
-    uint32_t w = 0;
-    if (!hip_ok(hipMemcpyAsync(&w, g_rt.counters + kAttnErrSlot, sizeof(w), hipMemcpyDeviceToHost,
-                               g_rt.stream),
-                "attention_one_launch_errors") ||
-        !hip_ok(hipStreamSynchronize(g_rt.stream), "attention_one_launch_errors"))
-        return -1;
-    return (int)w;
-}
 
 int vbs_gfx950_device_info(int index, char *name, size_t cap, uint64_t *total, uint64_t *free_b) {
     if (!ready_or_fail()) return 0;

@@ -24,19 +24,11 @@ void *rt_scratch(size_t bytes, hipStream_t s, hipError_t *why);
 
 // The library's stream, and the last-error writer of the C ABI.
 hipStream_t rt_stream();
-// kCounterSlots flag words, zeroed at init. A kernel that raises flags in
-// them clears them before it exits, so they are zero between launches (the
-// library has one in-order stream). The one-launch attention keeps one row
-// of kAttnFlagStride chunk flags per q head (at most kAttnFlagHeads heads,
-// each row on cache lines of its own) and a sticky error word after them.
-constexpr uint32_t kAttnFlagHeads = 64, kAttnFlagStride = 128;
-constexpr uint32_t kAttnErrSlot = kAttnFlagHeads * kAttnFlagStride;
-constexpr uint32_t kCounterSlots = kAttnErrSlot + 64u;
+// kCounterSlots arrival counters, zeroed at init. A kernel that counts
+// finished workgroups in one resets it to zero before it exits, so the
+// slots are zero between launches (the library has one in-order stream).
+constexpr uint32_t kCounterSlots = 1024;
 uint32_t *rt_counters();
-// Whether attention of eight kv heads and head_dim 128 runs as one launch
-// (the start-up probe found workgroups dealt to the eight XCDs round-robin,
-// and the caller has not switched it off).
-bool rt_attn_one_launch();
 int rt_fail(const char *fmt, ...);
 int rt_hip_ok(hipError_t e, const char *what);
 bool rt_ready();
@@ -180,11 +172,6 @@ hipError_t launch_attention(const float *q, const uint16_t *kc, const uint16_t *
                             uint32_t seq_len, const uint32_t *pos_dev, float *part,
                             uint64_t layer_off, uint32_t nqh, uint32_t nkh, uint32_t hd,
                             float scale, hipStream_t s);
-// Start-up probe of the workgroup-to-XCD deal the one-launch attention relies
-// on: `ids` (2048 words of device memory) receives each workgroup's XCC_ID
-// over two launches; *ok is set when workgroup i ran on XCD (x0 + i) mod 8 in
-// both.
-hipError_t attention_xcd_probe(uint32_t *ids, hipStream_t s, bool *ok);
 // The same for `batch` sequences with their own caches and positions:
 // sequence b reads q + b q_stride, writes out + b q_stride, uses the caches at
 // + b kv_stride elements, the position pos_dev[b] and the partials at

@@ -44,14 +44,10 @@ constexpr uint32_t kTargetWgs = 512;      // workgroups the vector-ALU split aim
 
 // (attn_split, the matrix-core split's constants and fast_exp: vbs_attn_common.h)
 // Chunks per kv head of any split of a sequence of at most max_seq (every
-// len >= 64 or len >= seq * nkh / target, target <= kMfmaTargetWgs), rounded
-// up to a multiple of 16: the partial rows' stride, so that each q head's
-// rows start on a 128-byte line of their own (16 rows of 130 floats are 65
-// lines) and no line holds two heads' rows (the one-launch attention reads a
-// head's rows while other heads' rows are still being written).
+// len >= 64 or len >= seq * nkh / target, target <= kMfmaTargetWgs).
 inline uint32_t attn_max_chunks(uint32_t max_seq, uint32_t nkh) {
     const uint32_t a = (kMfmaTargetWgs + nkh - 1u) / nkh, b = (max_seq + 63u) / 64u;
-    return ((a > b ? a : b) + 15u) & ~15u;
+    return a > b ? a : b;
 }
 
 // f16 bits -> f32 with the hardware converter (exact for every finite value).
@@ -718,135 +714,6 @@ __global__ __launch_bounds__(64 * kMergeRes) void k_attn_merge_h128(
     }
 }
 
-// ---- chunks and merge in one launch (eight kv heads, head_dim 128) ---------------
-// Workgroups are dealt to the eight XCDs round-robin in flat-index order,
-// starting wherever the previous launch left off (checked at start-up by
-// attention_xcd_probe), so workgroups 8 j .. 8 j + 7 land on eight different
-// XCDs. Each takes the kv head of its own XCD (its XCC_ID register) and, as
-// chunk j, does what k_attn_mfma does for it; then, once its partial stores
-// are complete (in the XCD's L2), it raises flag j of each q head of its group.
-// The last 8 x group workgroups of the grid merge: workgroup j = n_slots + hh
-// of XCD h waits until the flags of q head h * group + hh, read in the L2,
-// show every chunk with work, then merges the partials with merge_one_wave
-// (bit-identical to k_attn_merge_h128) and clears the flags for the next
-// launch. Its loads of the partials miss the CU's L1: nothing in this launch
-// read those lines before (each head's rows sit on lines of their own, see
-// attn_max_chunks, and only the head's merging workgroup reads them). Everything stays inside one XCD's L2, so no
-// device-scope release or acquire is needed, and no two workgroups update one
-// word (no atomics). Every workgroup of the grid fits on the chip at once and
-// the merging ones are dealt last, so their wait cannot hold a chunk back;
-// the wait is bounded all the same (kAttnSpinMax polls), after which the
-// sticky error word is set and the head's output is NaN.
-constexpr uint32_t kAttnOneKvh = 8, kAttnSpinMax = 1u << 16;
-
-__device__ __forceinline__ uint32_t xcc_id() {
-    uint32_t x;
-    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
-    return x & 15u;
-}
-
-__global__ __launch_bounds__(64) void k_xcc_probe(uint32_t *ids) {
-    const uint32_t x = xcc_id();
-    if (threadIdx.x == 0) ids[blockIdx.x] = x;
-}
-
-// The word at p as the XCD's L2 holds it: an atomic add of zero (atomics are
-// performed in the L2; a plain load may be served by a line the CU's L1 took
-// at an earlier poll). The zero is hidden from the compiler so that the add
-// is not turned into a load.
-__device__ __forceinline__ uint32_t load_l2(uint32_t *p) {
-    uint32_t z = 0u;
-    asm volatile("" : "+v"(z));
-    return __hip_atomic_fetch_add(p, z, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-}
-
-__global__ __launch_bounds__(64) void k_attn_one_launch(
-    const float *__restrict__ q, const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc,
-    float *__restrict__ part, float *__restrict__ out, uint32_t seq_len,
-    const uint32_t *__restrict__ pos_dev, uint64_t layer_off, uint32_t group, float scale,
-    uint32_t stride_chunks, uint32_t n_slots, uint32_t *__restrict__ flags) {
-    constexpr uint32_t HD = 128, NKH = kAttnOneKvh;
-    const uint32_t lane = threadIdx.x, n = lane & 15u, g = lane >> 4;
-    const uint32_t kvh = xcc_id(), j = blockIdx.x / NKH;
-    if (kvh >= NKH) {  // not an eight-XCD part (the start-up probe rules this out)
-        if (lane == 0) flags[kAttnErrSlot] = 1u;
-        return;
-    }
-    if (pos_dev) seq_len = pos_dev[0] + 1u;  // graph replay: the device holds the position
-    const AttnSplit sp = attn_split(seq_len, NKH, kMfmaGran, kMfmaLmax, kMfmaTargetWgs);
-    float *const pk = part + (uint64_t)kvh * group * stride_chunks * kPartRow;
-    uint32_t *const fk = flags + kvh * group * kAttnFlagStride;
-    if (j < n_slots) {
-        // chunk j of kv head kvh, as k_attn_mfma
-        if (j >= sp.n) return;
-        const uint32_t s0 = j * sp.len, valid = min(sp.len, seq_len - s0);
-        float m, l, a[8][4];
-        attn_mfma_wave(q, kc, vc, layer_off, s0, valid, sp.len / kMfmaGran, NKH, kvh, group, scale,
-                       lane, m, l, a);
-        if (g < 2u) {
-#pragma unroll
-            for (uint32_t r = 0; r < 4; r++) {
-                const uint32_t hh = 4u * g + r;
-                if (hh < group) {
-                    float *dst = pk + ((uint64_t)hh * stride_chunks + j) * kPartRow + 2u + 8u * n;
-#pragma unroll
-                    for (uint32_t i = 0; i < 4; i++)
-                        reinterpret_cast<float2 *>(dst)[i] = make_float2(a[2 * i][r], a[2 * i + 1][r]);
-                }
-            }
-        }
-        if (g == 0 && n < group) {
-            float *dst = pk + ((uint64_t)n * stride_chunks + j) * kPartRow;
-            dst[0] = m;
-            dst[1] = l;
-        }
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the partials are in L2
-        if (lane < group) fk[lane * kAttnFlagStride + j] = 1u;
-        return;
-    }
-    // merging workgroup: q head kvh * group + hh
-    const uint32_t hh = j - n_slots;
-    if (hh >= group) return;
-    uint32_t *const fh = fk + hh * kAttnFlagStride;
-    const uint32_t nc = sp.n;
-    bool done = false;
-    for (uint32_t it = 0; it < kAttnSpinMax; it++) {
-        const uint32_t f0 = lane < nc ? load_l2(fh + lane) : 1u;
-        const uint32_t f1 = lane + 64u < nc ? load_l2(fh + lane + 64u) : 1u;
-        if (__all(f0 != 0u && f1 != 0u)) {
-            done = true;
-            break;
-        }
-        __builtin_amdgcn_s_sleep(2);
-    }
-    asm volatile("buffer_inv sc0" ::: "memory");
-    float2 o = merge_one_wave(pk + (uint64_t)hh * stride_chunks * kPartRow, nc, lane);
-    if (!done) {
-        o = make_float2(NAN, NAN);
-        if (lane == 0) flags[kAttnErrSlot] = 1u;
-    }
-    *reinterpret_cast<float2 *>(out + (uint64_t)(kvh * group + hh) * HD + 2u * lane) = o;
-    if (lane < nc) fh[lane] = 0u;
-    if (lane + 64u < nc) fh[lane + 64u] = 0u;
-}
-
-hipError_t attention_xcd_probe(uint32_t *ids, hipStream_t s, bool *ok) {
-    constexpr uint32_t kN = 2048;
-    *ok = true;
-    for (int rep = 0; rep < 2; rep++) {
-        k_xcc_probe<<<kN, 64, 0, s>>>(ids);
-        hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
-        uint32_t h[kN];
-        if ((e = hipMemcpyAsync(h, ids, sizeof(h), hipMemcpyDeviceToHost, s)) != hipSuccess ||
-            (e = hipStreamSynchronize(s)) != hipSuccess)
-            return e;
-        for (uint32_t i = 0; i < kN; i++)
-            if (h[0] >= kAttnOneKvh || h[i] != (h[0] + i) % kAttnOneKvh) *ok = false;
-    }
-    return hipSuccess;
-}
-
 size_t attention_partial_bytes(uint32_t max_seq, uint32_t nqh, uint32_t nkh, uint32_t hd) {
     return (size_t)nqh * attn_max_chunks(max_seq, nkh) * (hd + 2u) * sizeof(float);
 }
@@ -891,16 +758,8 @@ hipError_t launch_attention(const float *q, const uint16_t *kc, const uint16_t *
     hipError_t e;
     uint32_t gran = kChunk, lmax = kChunk, target = kTargetWgs;
     const dim3 grid(stride, nkh);
-    const uint32_t slots = mfma_grid_chunks(seq_len, nkh);
-    if (fast && hd == 128u && nkh == kAttnOneKvh && slots <= kAttnFlagStride &&
-        nqh <= kAttnFlagHeads && rt_attn_one_launch()) {
-        k_attn_one_launch<<<kAttnOneKvh * (slots + group), 64, 0, s>>>(
-            q, kc, vc, part, out, seq_len, pos_dev, layer_off, group, scale, stride, slots,
-            rt_counters());
-        return hipGetLastError();
-    }
     if (fast && hd == 128u) {
-        k_attn_mfma<<<dim3(slots, nkh), 64, 0, s>>>(
+        k_attn_mfma<<<dim3(mfma_grid_chunks(seq_len, nkh), nkh), 64, 0, s>>>(
             q, kc, vc, part, seq_len, pos_dev, layer_off, nkh, group, scale, stride, 0u, 0ull, 0ull);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         k_attn_merge_h128<<<nqh, 64 * kMergeRes, 0, s>>>(part, out, stride, pos_dev, seq_len, nkh,

@@ -154,8 +154,6 @@ _DEVICE_SIGS = {
     "cache_store": (_I, [_P, _P, _P, _P, _U32, _U32, _U32, _U32]),
     "attention": (_I, [_P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, _U32, _F]),
     "attention_noalloc": (_I, [_P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, _U32, _F]),
-    "attention_one_launch": (_I, [_I]),
-    "attention_one_launch_errors": (_I, []),
     "silu_mul": (_I, [_P, _P, _P, _U32]),
     "add": (_I, [_P, _P, _P, _U32]),
     "dequant_rows": (_I, [_I, _P, _P, _U32, _U32, _P]),
@@ -328,13 +326,6 @@ class DeviceLib:
     def attention(self, q, kc, vc, out, seq_len, layer, max_ctx, nqh, nkh, hd, scale):
         self.check(self._attention(q, kc, vc, out, seq_len, layer, max_ctx, nqh, nkh, hd, scale),
                    "attention")
-
-    def attention_one_launch(self, set_: int = -1) -> bool:
-        """Switch the one-launch attention off (0) or on (1), or ask (-1)."""
-        return bool(self._attention_one_launch(set_))
-
-    def attention_one_launch_errors(self) -> int:
-        return int(self._attention_one_launch_errors())
 
     def silu_mul(self, g, u, out, n):
         self.check(self._silu_mul(g, u, out, n), "silu_mul")
