@@ -20,6 +20,15 @@ namespace vbs {
 // batch 1 12.9 against 13.2-13.5 us, 7B batch 1 8.3 either way.
 constexpr uint32_t kMfmaTargetWgs = 640;
 constexpr uint32_t kMfmaGran = 32, kMfmaTiles = 8, kMfmaLmax = kMfmaGran * kMfmaTiles;
+// A batch of sequences in one chunk launch (grid z) aims for one round of the
+// 2048 resident one-wave workgroups across the batch: at most 640 per
+// sequence, 2048 / batch from three sequences on (70B, batch 8: 256 per
+// sequence, 32 chunks of 256 positions per kv head at 8192 positions).
+constexpr uint32_t kMfmaWaveSlots = 2048;
+__host__ __device__ inline uint32_t attn_batch_target(uint32_t batch) {
+    const uint32_t t = kMfmaWaveSlots / (batch ? batch : 1u);
+    return t < kMfmaTargetWgs ? t : kMfmaTargetWgs;
+}
 
 // Sequence split: chunks of `len` positions (a multiple of gran, at most lmax)
 // sized so that about `target` workgroups cover seq x nkh; n chunks per kv
@@ -35,8 +44,9 @@ __host__ __device__ inline AttnSplit attn_split(uint32_t seq, uint32_t nkh, uint
     return {len, (seq + len - 1u) / len};
 }
 // Chunks per kv head of the matrix-core kernel's split of `seq` positions.
-__host__ __device__ inline uint32_t mfma_chunks(uint32_t seq, uint32_t nkh) {
-    return attn_split(seq, nkh, kMfmaGran, kMfmaLmax, kMfmaTargetWgs).n;
+__host__ __device__ inline uint32_t mfma_chunks(uint32_t seq, uint32_t nkh,
+                                                uint32_t target = kMfmaTargetWgs) {
+    return attn_split(seq, nkh, kMfmaGran, kMfmaLmax, target).n;
 }
 
 // e^x as 2^(x log2 e) on the hardware exponential (a few ulp; the scores

@@ -80,7 +80,8 @@ hipError_t launch_mvb(int type, uint32_t nmat, const uint8_t *const w[], const u
                       float *const y[], const uint32_t ys[], int accumulate, const uint8_t *xp,
                       uint32_t cols, uint32_t batch, hipStream_t s);
 // The head_dim-128 merge of the batched attention partials (chunk stride
-// attn_max_chunks(max_seq, nkh), part_bstride floats per sequence) written as
+// attn_max_chunks(max_seq, nkh), part_bstride floats per sequence, the split
+// of attn_batch_target(batch) that launch_attention_batch used) written as
 // O's prepared x (xprep layout, nqh x 128 columns), pairs of q heads per block.
 hipError_t launch_attn_merge_prep(const float *part, uint8_t *xp, uint32_t stride_chunks,
                                   const uint32_t *pos_dev, uint32_t nqh, uint32_t nkh,

@@ -387,13 +387,13 @@ __global__ __launch_bounds__(64 * kWaves) void k_attn_chunk(
 // replay reads the position on the device, so the grid covers every
 // position up to max_seq, and workgroups beyond the current split exit at
 // once (each costs dispatch time, so the grid is no larger than this).
-inline uint32_t mfma_grid_chunks(uint32_t max_seq, uint32_t nkh) {
+inline uint32_t mfma_grid_chunks(uint32_t max_seq, uint32_t nkh, uint32_t target = kMfmaTargetWgs) {
     uint32_t best = 0;
     for (uint32_t k = 1; k <= kMfmaTiles; k++) {
-        const uint64_t hi = k < kMfmaTiles ? (uint64_t)kMfmaGran * k * kMfmaTargetWgs / nkh : max_seq;
+        const uint64_t hi = k < kMfmaTiles ? (uint64_t)kMfmaGran * k * target / nkh : max_seq;
         const uint32_t s = (uint32_t)(hi < max_seq ? hi : max_seq);
         if (s == 0) continue;
-        const uint32_t c = attn_split(s, nkh, kMfmaGran, kMfmaLmax, kMfmaTargetWgs).n;
+        const uint32_t c = attn_split(s, nkh, kMfmaGran, kMfmaLmax, target).n;
         best = c > best ? c : best;
     }
     return best;
@@ -563,7 +563,7 @@ __global__ __launch_bounds__(64) void k_attn_mfma(const float *__restrict__ q,
                                                   uint64_t layer_off, uint32_t nkh, uint32_t group,
                                                   float scale, uint32_t stride_chunks,
                                                   uint32_t q_bstride, uint64_t kv_bstride,
-                                                  uint64_t part_bstride) {
+                                                  uint64_t part_bstride, uint32_t target) {
     constexpr uint32_t HD = 128;
     const uint32_t chunk = blockIdx.x, kvh = blockIdx.y, lane = threadIdx.x, bz = blockIdx.z;
     const uint32_t n = lane & 15u, g = lane >> 4;
@@ -573,7 +573,7 @@ __global__ __launch_bounds__(64) void k_attn_mfma(const float *__restrict__ q,
     vc += bz * kv_bstride;
     part += bz * part_bstride;
     if (pos_dev) seq_len = pos_dev[bz] + 1u;  // graph replay: the device holds the position
-    const AttnSplit sp = attn_split(seq_len, nkh, kMfmaGran, kMfmaLmax, kMfmaTargetWgs);
+    const AttnSplit sp = attn_split(seq_len, nkh, kMfmaGran, kMfmaLmax, target);
     if (chunk >= sp.n) return;  // past the sequence (the grid covers the longest split)
     const uint32_t s0 = chunk * sp.len, valid = min(sp.len, seq_len - s0);
     float m, l, a[8][4];
@@ -693,13 +693,13 @@ __global__ __launch_bounds__(kMergeThreads) void k_attn_merge(const float *__res
 __global__ __launch_bounds__(64 * kMergeRes) void k_attn_merge_h128(
     const float *__restrict__ part, float *__restrict__ out, uint32_t stride_chunks,
     const uint32_t *__restrict__ pos_dev, uint32_t seq_len, uint32_t nkh, uint32_t q_bstride,
-    uint64_t part_bstride) {
+    uint64_t part_bstride, uint32_t target) {
     __shared__ float2 red[kMergeRes][64];
     const uint32_t h = blockIdx.x, bz = blockIdx.y, lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     part += bz * part_bstride;
     out += (uint64_t)bz * q_bstride;
     if (pos_dev) seq_len = pos_dev[bz] + 1u;  // seq = pos + 1
-    const uint32_t nc = mfma_chunks(seq_len, nkh);
+    const uint32_t nc = mfma_chunks(seq_len, nkh, target);
     const float *ph = part + (uint64_t)h * stride_chunks * kPartRow;
     float2 av[kMergeBatch];
     merge_residue_load(ph, nc, wave, lane, av);  // with the (m, l) loads: one round trip
@@ -760,10 +760,11 @@ hipError_t launch_attention(const float *q, const uint16_t *kc, const uint16_t *
     const dim3 grid(stride, nkh);
     if (fast && hd == 128u) {
         k_attn_mfma<<<dim3(mfma_grid_chunks(seq_len, nkh), nkh), 64, 0, s>>>(
-            q, kc, vc, part, seq_len, pos_dev, layer_off, nkh, group, scale, stride, 0u, 0ull, 0ull);
+            q, kc, vc, part, seq_len, pos_dev, layer_off, nkh, group, scale, stride, 0u, 0ull, 0ull,
+            kMfmaTargetWgs);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         k_attn_merge_h128<<<nqh, 64 * kMergeRes, 0, s>>>(part, out, stride, pos_dev, seq_len, nkh,
-                                                            0u, 0ull);
+                                                            0u, 0ull, kMfmaTargetWgs);
         return hipGetLastError();
     } else if (fast && hd == 32u) {
         gran = ChunkShape<32>::GRAN, lmax = ChunkShape<32>::LMAX;
@@ -823,14 +824,15 @@ hipError_t launch_attention_batch(const float *q, const uint16_t *kc, const uint
         }
         return hipSuccess;
     }
-    const uint32_t stride = attn_max_chunks(max_seq, nkh);
-    k_attn_mfma<<<dim3(mfma_grid_chunks(max_seq, nkh), nkh, batch), 64, 0, s>>>(
+    const uint32_t stride = attn_max_chunks(max_seq, nkh), target = attn_batch_target(batch);
+    k_attn_mfma<<<dim3(mfma_grid_chunks(max_seq, nkh, target), nkh, batch), 64, 0, s>>>(
         q, kc, vc, part, max_seq, pos_dev, layer_off, nkh, group, scale, stride, q_stride, kv_stride,
-        pstride);
+        pstride, target);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || !out) return e;  // (no out: the caller merges the partials itself)
     k_attn_merge_h128<<<dim3(nqh, batch), 64 * kMergeRes, 0, s>>>(part, out, stride, pos_dev,
-                                                                     max_seq, nkh, q_stride, pstride);
+                                                                     max_seq, nkh, q_stride, pstride,
+                                                                     target);
     return hipGetLastError();
 }
 

@@ -914,13 +914,13 @@ __global__ __launch_bounds__(512) void k_attn_merge_prep(const float *__restrict
                                                          uint8_t *__restrict__ xp, uint32_t stride_chunks,
                                                          const uint32_t *__restrict__ pos_dev,
                                                          uint32_t nkh, uint64_t part_bstride,
-                                                         uint32_t cols) {
+                                                         uint32_t cols, uint32_t target) {
     __shared__ float2 red[2][kMergeRes][64];
     __shared__ float4 outv[64];
     const uint32_t pb = blockIdx.x, bz = blockIdx.y, lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t hh = wave / kMergeRes, r = wave % kMergeRes, h = 2u * pb + hh;
     part += bz * part_bstride;
-    const uint32_t nc = mfma_chunks(pos_dev[bz] + 1u, nkh);  // seq = pos + 1
+    const uint32_t nc = mfma_chunks(pos_dev[bz] + 1u, nkh, target);  // seq = pos + 1
     const float *ph = part + (uint64_t)h * stride_chunks * kPartRow;
     float2 av[kMergeBatch];
     merge_residue_load(ph, nc, r, lane, av);
@@ -946,7 +946,8 @@ hipError_t launch_attn_merge_prep(const float *part, uint8_t *xp, uint32_t strid
                                   uint64_t part_bstride, uint32_t batch, hipStream_t s) {
     if (nqh % 2u || batch == 0 || batch > kBatchMax || !pos_dev) return hipErrorNotSupported;
     k_attn_merge_prep<<<dim3(nqh / 2u, batch), 512, 0, s>>>(part, xp, stride_chunks, pos_dev, nkh,
-                                                           part_bstride, nqh * 128u);
+                                                           part_bstride, nqh * 128u,
+                                                           attn_batch_target(batch));
     return hipGetLastError();
 }
 
