@@ -84,6 +84,12 @@ def test_shim_exports_the_reference_symbols():
     assert declared == ["vbs_hip_dispatch_linear_batch", "vbs_hip_linear_batch_version"]
     for name in declared:
         assert hasattr(lib, name), name
+    # the dispatch trace's (include/vbs_hip_trace.h)
+    hdr = open(os.path.join(ROOT, "include", "vbs_hip_trace.h")).read()
+    declared = sorted(set(re.findall(r"\b(vbs_hip_trace_\w+)\s*\(", hdr)))
+    assert declared == ["vbs_hip_trace_counters", "vbs_hip_trace_level", "vbs_hip_trace_reset"]
+    for name in declared:
+        assert hasattr(lib, name), name
 
 
 @pytest.mark.skipif(not os.path.isdir("/root/reference/include"),
@@ -217,6 +223,59 @@ def test_held_ops_on_host_mock_keep_the_bridge_results(tmpdir_mod, host, case):
     joined = [mock.mock_fused_count(i) - before[i] for i in range(7)]
     L = TINY["n_layers"]
     assert joined == [steps * (per * L + once) for per, once in want], joined
+
+
+class TraceCounter(C.Structure):
+    _fields_ = [("calls", C.c_uint64), ("launches", C.c_uint64), ("ns", C.c_uint64)]
+
+
+TRACE_KINDS = ["embedding", "normalize", "rotary", "cache", "attention", "activation",
+               "elementwise", "linear", "linear_batch", "linear_joined", "qkv_group", "ffn_group"]
+
+
+def test_dispatch_trace_counts_calls_and_launches(tmpdir_mod, host, tmp_path):
+    """VBS_TRACE=2 (include/vbs_hip_trace.h): over the host mock, two decode
+    steps of the Q4_K_M model count every table call by op kind and every
+    launch by launch kind — per layer the grouped q/k/v and gate/up
+    launches, the two matvec + add launches and the attention; per step the
+    embedding and the RMSNorm + lm_head launch — each launch timed and
+    written as one line of $VBS_TRACE_FILE. The logits are the oracle's, as
+    without the trace."""
+    from test_decode import TINY, full_cache
+    so = build_mock(tmpdir_mod, "mock_trace.so")
+    log = tmp_path / "trace.log"
+    os.environ["VBS_TRACE"], os.environ["VBS_TRACE_FILE"] = "2", str(log)
+    try:
+        be, ok = fresh_shim(tmpdir_mod, so)
+    finally:
+        del os.environ["VBS_TRACE"], os.environ["VBS_TRACE_FILE"]
+    assert ok, be.last_error()
+    assert be.lib.vbs_hip_trace_level() == 2
+    be.lib.vbs_hip_trace_reset()
+    model = V.SynthModel(host, **TINY, seed=5)
+    d = V.Decoder(host, be, model)
+    orc = Oracle()
+    kc, vc = full_cache(model, None, None, 0)  # (the oracle model writes into these)
+    om = orc.model(model, kc, vc)
+    steps, L = 2, TINY["n_layers"]
+    for pos in range(steps):
+        got = d.step(3 + pos, pos)
+        want = orc.forward(om, 3 + pos, pos, model.cfg["vocab"], 1)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), pos
+    d.close()
+    tc = (TraceCounter * len(TRACE_KINDS))()
+    be.lib.vbs_hip_trace_counters(tc)
+    got = {k: (tc[i].calls, tc[i].launches) for i, k in enumerate(TRACE_KINDS)}
+    want = {"embedding": (1, 1), "normalize": (2 * L + 1, 0), "rotary": (2 * L, 0),
+            "cache": (L, 0), "attention": (L, L), "activation": (L, 0), "elementwise": (2 * L, 0),
+            "linear": (7 * L + 1, 0), "linear_batch": (0, 0), "linear_joined": (0, 2 * L + 1),
+            "qkv_group": (0, L), "ffn_group": (0, L)}
+    assert got == {k: (steps * c, steps * n) for k, (c, n) in want.items()}, got
+    assert all(tc[i].ns > 0 for i in range(len(TRACE_KINDS)) if tc[i].launches)
+    lines = log.read_text().splitlines()
+    assert len(lines) == sum(tc[i].launches for i in range(len(TRACE_KINDS)))
+    assert all(ln.startswith("vbs_trace ") and ln.endswith(" us") for ln in lines)
+    assert any(ln.startswith("vbs_trace qkv_group Q4_K") for ln in lines), lines[:8]
 
 
 def test_held_ops_random_sequences_equal_ops_one_by_one(tmpdir_mod, host):

@@ -21,12 +21,14 @@
 #include "vbs_abi.h"
 #include "vbs_gfx950.h"
 #include "vbs_hip_batch.h"
+#include "vbs_hip_trace.h"
 
 #include <dlfcn.h>
 #include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <time.h>
 
 /* ---- the device library's entry points -------------------------------- */
 
@@ -123,9 +125,71 @@ static void *open_lib(void) {
     return h;
 }
 
+/* ---- dispatch trace (include/vbs_hip_trace.h) ---------------------------- */
+static int g_trace;
+static FILE *g_trace_out;
+static vbs_hip_trace_counter_t g_tc[VBS_HIP_TRACE_KINDS];
+static const char *const k_trace_name[VBS_HIP_TRACE_KINDS] = {
+    "embedding",  "normalize",   "rotary", "cache",        "attention",     "activation",
+    "elementwise", "linear", "linear_batch", "linear_joined", "qkv_group", "ffn_group"};
+
+static uint64_t now_ns(void) {
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return (uint64_t)ts.tv_sec * 1000000000ull + (uint64_t)ts.tv_nsec;
+}
+
+static void trace_init(void) {
+    const char *e = getenv("VBS_TRACE");
+    g_trace = e ? atoi(e) : 0;
+    g_trace = g_trace < 0 ? 0 : g_trace > 2 ? 2 : g_trace;
+    if (!g_trace) return;
+    const char *f = getenv("VBS_TRACE_FILE");
+    g_trace_out = f && *f ? fopen(f, "a") : NULL;
+    if (g_trace_out) setvbuf(g_trace_out, NULL, _IOLBF, 0);  /* whole lines, as they come */
+    else g_trace_out = stderr;
+}
+
+static void trace_call(int kind) {
+    if (g_trace) g_tc[kind].calls++;
+}
+
+static uint64_t trace_t0(void) { return g_trace > 1 ? now_ns() : 0; }
+
+/* After a device-library call that returned r (1: it launched): counts the
+ * launch, at level 2 waits for it and adds its wall time, and writes its
+ * line. Returns r (0 if the wait failed). */
+static int trace_launch(int kind, uint64_t t0, int r, const char *fmt, ...) {
+    if (!g_trace || r != 1) return r;
+    char desc[192];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(desc, sizeof(desc), fmt, ap);
+    va_end(ap);
+    g_tc[kind].launches++;
+    if (g_trace > 1) {
+        if (!g_lib.synchronize()) return 0;
+        const uint64_t dt = now_ns() - t0;
+        g_tc[kind].ns += dt;
+        fprintf(g_trace_out, "vbs_trace %s %s %.2f us\n", k_trace_name[kind], desc, (double)dt * 1e-3);
+    } else {
+        fprintf(g_trace_out, "vbs_trace %s %s\n", k_trace_name[kind], desc);
+    }
+    return r;
+}
+
+int vbs_hip_trace_level(void) { return g_trace; }
+
+void vbs_hip_trace_counters(vbs_hip_trace_counter_t out[VBS_HIP_TRACE_KINDS]) {
+    memcpy(out, g_tc, sizeof(g_tc));
+}
+
+void vbs_hip_trace_reset(void) { memset(g_tc, 0, sizeof(g_tc)); }
+
 static bool gfx950_init(void) {
     if (g_probed) return g_ready != 0;
     g_probed = 1;
+    trace_init();
     memset(&g_lib, 0, sizeof(g_lib));
     g_lib.handle = open_lib();
     if (!g_lib.handle) return false;
@@ -299,8 +363,29 @@ static pending_t g_pend;
 static void drop_pending(void) { memset(&g_pend, 0, sizeof(g_pend)); }
 
 static bool run_norm(const pending_t *p) {
-    return g_lib.rms_norm(p->n_in, p->n_w, p->n_out, p->n_dim, p->n_eps) ? true
-                                                                         : lib_fail("normalize");
+    const uint64_t t0 = trace_t0();
+    return trace_launch(VBS_HIP_TRACE_NORMALIZE, t0,
+                        g_lib.rms_norm(p->n_in, p->n_w, p->n_out, p->n_dim, p->n_eps), "%u", p->n_dim)
+               ? true
+               : lib_fail("normalize");
+}
+
+static const char *type_name(vbs_ggml_type_t t);
+
+/* A held linear's one-launch form, traced. */
+static int linear_fused_traced(const held_linear_t *l, const float *x, const vbs_gfx950_linear_join_t *j) {
+    const uint64_t t0 = trace_t0();
+    return trace_launch(VBS_HIP_TRACE_LINEAR_JOINED, t0,
+                        g_lib.linear_fused(l->type, l->w, x, l->y, l->cols, l->rows, j),
+                        "%s %ux%u%s%s%s%s%s", type_name((vbs_ggml_type_t)l->type), l->rows, l->cols,
+                        j->norm_w ? " +norm" : "", j->rope ? " +rope" : "", j->acc ? " +add" : "",
+                        j->gate ? " +silu" : "", j->k_row ? " +cache" : "");
+}
+
+static int rope_traced(const held_linear_t *l) {
+    const uint64_t t0 = trace_t0();
+    return trace_launch(VBS_HIP_TRACE_ROTARY, t0, g_lib.rope(l->y, l->pos, l->hd, l->nh, l->theta),
+                        "%ux%u pos %u", l->nh, l->hd, l->pos);
 }
 
 /* Held linear i with what it carries (the RMSNorm in front of linear 0, its
@@ -324,7 +409,7 @@ static bool issue_linear(const pending_t *p, int i, vbs_gfx950_linear_join_t *j,
         j->theta = l->theta;
     }
     if (norm || l->rope || after) {
-        int r = g_lib.linear_fused(l->type, l->w, norm ? p->n_in : l->x, l->y, l->cols, l->rows, j);
+        int r = linear_fused_traced(l, norm ? p->n_in : l->x, j);
         if (r == 1) {
             *done = after;
             return true;
@@ -335,19 +420,21 @@ static bool issue_linear(const pending_t *p, int i, vbs_gfx950_linear_join_t *j,
             n.norm_w = p->n_w;
             n.norm_eps = p->n_eps;
             n.x_normed = p->n_out;
-            r = g_lib.linear_fused(l->type, l->w, p->n_in, l->y, l->cols, l->rows, &n);
+            r = linear_fused_traced(l, p->n_in, &n);
             if (r == 0) return lib_fail("linear tile (fused)");
             if (r == 1) {
-                if (l->rope && !g_lib.rope(l->y, l->pos, l->hd, l->nh, l->theta))
-                    return lib_fail("rotary");
+                if (l->rope && !rope_traced(l)) return lib_fail("rotary");
                 return true;
             }
         }
     }
     if (norm && !run_norm(p)) return false;
-    if (!g_lib.linear(l->type, l->w, l->x, l->y, l->cols, l->rows, 0, 0, 0))
+    const uint64_t t0 = trace_t0();
+    if (!trace_launch(VBS_HIP_TRACE_LINEAR, t0,
+                      g_lib.linear(l->type, l->w, l->x, l->y, l->cols, l->rows, 0, 0, 0), "%s %ux%u",
+                      type_name((vbs_ggml_type_t)l->type), l->rows, l->cols))
         return lib_fail("linear tile");
-    if (l->rope && !g_lib.rope(l->y, l->pos, l->hd, l->nh, l->theta)) return lib_fail("rotary");
+    if (l->rope && !rope_traced(l)) return lib_fail("rotary");
     return true;
 }
 
@@ -519,6 +606,7 @@ static bool gfx950_dispatch_linear_tile(vbs_device_t *dev, void *pipeline, vbs_b
     (void)dev;
     gfx950_linear_pipe_t *p = (gfx950_linear_pipe_t *)pipeline;
     if (!g_ready || !p || !wp || !in || !out) return false;
+    trace_call(VBS_HIP_TRACE_LINEAR);
     uint64_t need = packed_row_bytes(p->type, cols) * rows;
     if (ws && ws->host_ptr) {
         size_t n = copied_bytes ? copied_bytes : (size_t)need;
@@ -550,8 +638,12 @@ static bool gfx950_dispatch_linear_tile(vbs_device_t *dev, void *pipeline, vbs_b
         return hold_linear(&n);
     }
     if (!flush_pending()) return false;
-    if (!g_lib.linear((int)p->type, wp->internal_handle, x, y, cols, rows, col_off, row_off,
-                      accumulate ? 1 : 0))
+    const uint64_t t0 = trace_t0();
+    if (!trace_launch(VBS_HIP_TRACE_LINEAR, t0,
+                      g_lib.linear((int)p->type, wp->internal_handle, x, y, cols, rows, col_off,
+                                   row_off, accumulate ? 1 : 0),
+                      "%s %ux%u at %u,%u%s%s", type_name(p->type), rows, cols, row_off, col_off,
+                      accumulate ? " +acc" : "", ws ? " staged" : ""))
         return lib_fail("linear tile");
     return true;
 }
@@ -570,6 +662,7 @@ bool vbs_hip_dispatch_linear_batch(vbs_device_t *dev, void *pipeline, vbs_buffer
         set_err("linear batch before a successful init");
         return false;
     }
+    trace_call(VBS_HIP_TRACE_LINEAR_BATCH);
     if (!p || !w || !x || !y || !w->internal_handle || !x->internal_handle || !y->internal_handle) {
         set_err("linear batch: null pipeline or buffer");
         return false;
@@ -593,8 +686,12 @@ bool vbs_hip_dispatch_linear_batch(vbs_device_t *dev, void *pipeline, vbs_buffer
         return false;
     }
     if (!flush_pending()) return false;
-    if (!g_lib.linear_batch((int)p->type, w->internal_handle, (const float *)x->internal_handle,
-                            x_stride, (float *)y->internal_handle, y_stride, cols, rows, batch))
+    const uint64_t t0 = trace_t0();
+    if (!trace_launch(VBS_HIP_TRACE_LINEAR_BATCH, t0,
+                      g_lib.linear_batch((int)p->type, w->internal_handle,
+                                         (const float *)x->internal_handle, x_stride,
+                                         (float *)y->internal_handle, y_stride, cols, rows, batch),
+                      "%s %ux%u x%u", type_name(p->type), rows, cols, batch))
         return lib_fail("linear batch");
     return true;
 }
@@ -638,6 +735,14 @@ static bool gfx950_dispatch_primitive(vbs_device_t *dev, void *pipeline, const v
             return false;
         }
     }
+    static const int trace_kind[] = {
+        [VBS_OP_EMBEDDING] = VBS_HIP_TRACE_EMBEDDING, [VBS_OP_NORMALIZE] = VBS_HIP_TRACE_NORMALIZE,
+        [VBS_OP_ROTARY] = VBS_HIP_TRACE_ROTARY,       [VBS_OP_CACHE] = VBS_HIP_TRACE_CACHE,
+        [VBS_OP_ATTENTION] = VBS_HIP_TRACE_ATTENTION, [VBS_OP_ACTIVATION] = VBS_HIP_TRACE_ACTIVATION,
+        [VBS_OP_ELEMENTWISE] = VBS_HIP_TRACE_ELEMENTWISE,
+    };
+    const int tk = trace_kind[pp->base.kind];
+    trace_call(tk);
     /* held itself (NORMALIZE, ROTARY), or issued with the held run */
     if (pp->base.kind == VBS_OP_NORMALIZE && BUF(0) != BUF(2)) {
         if (!flush_pending()) return false;
@@ -682,11 +787,16 @@ static bool gfx950_dispatch_primitive(vbs_device_t *dev, void *pipeline, const v
                     BUF(1) == v->y && kvd == k->rows && kvd == v->rows && pos < mc &&
                     q->pos == pos && k->pos == pos && q->hd == k->hd && q->theta == k->theta) {
                     /* NORMALIZE, q, ROTARY, k, ROTARY, v, CACHE in one launch */
-                    const int r = g_lib.qkv_fused(
-                        q->type, q->w, k->w, v->w, h->has_norm ? h->n_in : q->x, q->cols, q->rows,
-                        kvd, h->has_norm ? h->n_w : NULL, h->n_eps, h->has_norm ? h->n_out : NULL,
-                        q->y, k->y, v->y, pos, q->hd, q->theta, (uint16_t *)BUF(2),
-                        (uint16_t *)BUF(3), layer, mc);
+                    const uint64_t t0 = trace_t0();
+                    const int r = trace_launch(
+                        VBS_HIP_TRACE_QKV_GROUP, t0,
+                        g_lib.qkv_fused(q->type, q->w, k->w, v->w, h->has_norm ? h->n_in : q->x,
+                                        q->cols, q->rows, kvd, h->has_norm ? h->n_w : NULL,
+                                        h->n_eps, h->has_norm ? h->n_out : NULL, q->y, k->y, v->y,
+                                        pos, q->hd, q->theta, (uint16_t *)BUF(2),
+                                        (uint16_t *)BUF(3), layer, mc),
+                        "%s %u+%u+%ux%u%s pos %u", type_name((vbs_ggml_type_t)q->type), q->rows,
+                        kvd, kvd, q->cols, h->has_norm ? " +norm" : "", pos);
                     if (r == 1) {
                         drop_pending();
                         return true;
@@ -712,10 +822,15 @@ static bool gfx950_dispatch_primitive(vbs_device_t *dev, void *pipeline, const v
                 if (h->n_lin == 2 && !g->rope && !u->rope && BUF(0) == g->y && BUF(1) == u->y &&
                     U32(3) == g->rows && U32(3) == u->rows && !touches_held(out)) {
                     /* NORMALIZE, gate, up, ACTIVATION in one launch */
-                    const int r = g_lib.gate_up_fused(
-                        g->type, g->w, u->w, h->has_norm ? h->n_in : g->x, g->cols, g->rows,
-                        h->has_norm ? h->n_w : NULL, h->n_eps, h->has_norm ? h->n_out : NULL, g->y,
-                        u->y, (float *)out);
+                    const uint64_t t0 = trace_t0();
+                    const int r = trace_launch(
+                        VBS_HIP_TRACE_FFN_GROUP, t0,
+                        g_lib.gate_up_fused(g->type, g->w, u->w, h->has_norm ? h->n_in : g->x,
+                                            g->cols, g->rows, h->has_norm ? h->n_w : NULL,
+                                            h->n_eps, h->has_norm ? h->n_out : NULL, g->y, u->y,
+                                            (float *)out),
+                        "%s 2x%ux%u%s", type_name((vbs_ggml_type_t)g->type), g->rows, g->cols,
+                        h->has_norm ? " +norm" : "");
                     if (r == 1) {
                         drop_pending();
                         return true;
@@ -743,6 +858,7 @@ static bool gfx950_dispatch_primitive(vbs_device_t *dev, void *pipeline, const v
     }
     if (!flush_pending()) return false;
     int ok = 0;
+    const uint64_t t0 = trace_t0();
     switch (pp->base.kind) {
         case VBS_OP_EMBEDDING:
             ok = g_lib.embed((int)pp->type, BUF(0), U32(1), (float *)BUF(2), U32(3));
@@ -771,6 +887,20 @@ static bool gfx950_dispatch_primitive(vbs_device_t *dev, void *pipeline, const v
             break;
         default:
             break;
+    }
+    if (g_trace) {
+        char d[96];
+        switch (pp->base.kind) {
+            case VBS_OP_EMBEDDING: snprintf(d, sizeof(d), "%s token %u dim %u", type_name(pp->type), U32(1), U32(3)); break;
+            case VBS_OP_NORMALIZE: snprintf(d, sizeof(d), "%u", U32(3)); break;
+            case VBS_OP_ROTARY: snprintf(d, sizeof(d), "%ux%u pos %u", U32(3), U32(2), U32(1)); break;
+            case VBS_OP_CACHE: snprintf(d, sizeof(d), "%u pos %u layer %u", U32(7), U32(4), U32(5)); break;
+            case VBS_OP_ATTENTION:
+                snprintf(d, sizeof(d), "seq %u layer %u heads %u/%u hd %u", U32(4), U32(5), U32(7), U32(8), U32(9));
+                break;
+            default: snprintf(d, sizeof(d), "%u", U32(3)); break;
+        }
+        ok = trace_launch(tk, t0, ok, "%s", d);
     }
     return ok ? true : lib_fail("dispatch_primitive");
 }
