@@ -231,8 +231,10 @@ def engine_kv_capacity(free_vram, total_vram, geo, n_layers, ctx, mix=None):
 @have_callers
 def test_gpu_device_info_feeds_profiler_fabric_and_kv_budget(host, backend, tmp_path):
     """The reference's selection, profiler and engine read the shim's device
-    struct: VBS_BACKEND=hip takes the table whose init succeeds and whose
-    device 0 has a name (src/vbs_backend_select.c:42-85); the profiler's HIP
+    struct: VBS_BACKEND=hip takes the table when its init succeeds, and logs
+    device 0's name (src/vbs_backend_select.c:42-85; that file links the
+    Vulkan and CUDA backends, which the image cannot build, so the test
+    checks the conditions it reads: init, a device, a name); the profiler's HIP
     branch turns max_working_set_bytes / max_buffer_bytes into the system
     profile (src/vbs_profiler.c:194-210, restated in oracle/ref_callers.c:
     vbs_profiler.c itself does not link here); the engine sizes its KV cache
