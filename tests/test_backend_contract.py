@@ -516,3 +516,41 @@ def test_backend_suite_on_gfx950(backend, host):
     res = run_suite(backend, Oracle(), host)
     bad = [r[0] for r in res if not r[1]]
     assert not bad, bad
+
+
+@pytest.mark.gpu
+def test_gpu_dispatch_trace_on_device(backend, host, tmpdir_mod, tmp_path):
+    """VBS_TRACE=2 on the MI355X: a private copy of the shim over the real
+    device library counts two decode steps of the Q4_K_M model as the host
+    mock's trace does (grouped q/k/v and gate/up, two matvec + add launches
+    per layer, the embedding and the RMSNorm + lm_head per step), times every
+    launch, and leaves the logits equal to the untraced table's bit for
+    bit."""
+    from test_decode import TINY
+    log = tmp_path / "trace.log"
+    os.environ["VBS_TRACE"], os.environ["VBS_TRACE_FILE"] = "2", str(log)
+    try:
+        be, ok = fresh_shim(tmpdir_mod, V.DEVICE_LIB)
+    finally:
+        del os.environ["VBS_TRACE"], os.environ["VBS_TRACE_FILE"]
+    assert ok, be.last_error()
+    assert be.lib.vbs_hip_trace_level() == 2
+    be.lib.vbs_hip_trace_reset()
+    model = V.SynthModel(host, **TINY, seed=5)
+    outs = []
+    for b in (be, backend):
+        d = V.Decoder(host, b, model)
+        outs.append([d.step(3 + pos, pos) for pos in range(2)])
+        d.close()
+    for got, want in zip(*outs):
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    tc = (TraceCounter * len(TRACE_KINDS))()
+    be.lib.vbs_hip_trace_counters(tc)
+    L, steps = TINY["n_layers"], 2
+    launches = {k: tc[i].launches for i, k in enumerate(TRACE_KINDS)}
+    assert launches["qkv_group"] == steps * L and launches["ffn_group"] == steps * L, launches
+    assert launches["linear_joined"] == steps * (2 * L + 1) and launches["attention"] == steps * L
+    assert launches["linear"] == 0 and launches["normalize"] == 0, launches
+    assert all(tc[i].ns > 0 for i in range(len(TRACE_KINDS)) if tc[i].launches)
+    assert len(log.read_text().splitlines()) == sum(launches.values())
+
