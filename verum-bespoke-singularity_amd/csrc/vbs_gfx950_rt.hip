@@ -42,7 +42,6 @@ struct Runtime {
     void *retired[kMaxRetired] = {nullptr};  // superseded scratch buffers, kept (see rt_scratch)
     int n_retired = 0;
     void *noalloc_scratch = nullptr;  // device address of `scratch` on the library's device
-    uint32_t *counters = nullptr;  // zeroed once; kernels that use one leave it at 0
 };
 
 Runtime g_rt;
@@ -137,7 +136,6 @@ void *rt_scratch(size_t bytes, hipStream_t s, hipError_t *why) {
 
 hipStream_t rt_stream() { return g_rt.stream; }
 
-uint32_t *rt_counters() { return g_rt.counters; }
 
 
 int rt_fail(const char *fmt, ...) {
@@ -187,10 +185,7 @@ int vbs_gfx950_init(void) {
     if (!hip_ok(hipGetSymbolAddress(&g_rt.noalloc_scratch, HIP_SYMBOL(scratch)),
                 "hipGetSymbolAddress(scratch)"))
         return 0;
-    if (!hip_ok(hipMalloc(&g_rt.counters, kCounterSlots * sizeof(uint32_t)), "hipMalloc(counters)") ||
-        !hip_ok(hipMemset(g_rt.counters, 0, kCounterSlots * sizeof(uint32_t)), "hipMemset(counters)") ||
-        !hip_ok(hipDeviceSynchronize(), "init"))
-        return 0;
+    if (!hip_ok(hipDeviceSynchronize(), "init")) return 0;
     g_rt.device = chosen;
     g_rt.ready = true;
     snprintf(g_err, sizeof(g_err), "ok");

@@ -24,11 +24,6 @@ void *rt_scratch(size_t bytes, hipStream_t s, hipError_t *why);
 
 // The library's stream, and the last-error writer of the C ABI.
 hipStream_t rt_stream();
-// kCounterSlots arrival counters, zeroed at init. A kernel that counts
-// finished workgroups in one resets it to zero before it exits, so the
-// slots are zero between launches (the library has one in-order stream).
-constexpr uint32_t kCounterSlots = 1024;
-uint32_t *rt_counters();
 int rt_fail(const char *fmt, ...);
 int rt_hip_ok(hipError_t e, const char *what);
 bool rt_ready();
