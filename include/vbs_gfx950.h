@@ -302,6 +302,17 @@ int vbs_gfx950_decoder_greedy(void *handle, uint32_t token, uint32_t pos, uint32
  * kernel launches but not graph replays). */
 int vbs_gfx950_decoder_greedy_eager(void *handle, uint32_t token, uint32_t pos, uint32_t n,
                                     uint32_t *tokens, float *margins);
+/* No counterpart in the reference (a diagnostic of this decoder). Where every
+ * layer's O is Q4_K over a 4096-wide q of 128-dim heads, the decoder merges
+ * the attention partials inside the O launch: each workgroup merges one head
+ * and the workgroups on one XCD share the heads through its L2; a workgroup
+ * whose bounded wait for them runs out (one placed or started unexpectedly)
+ * merges every head itself, with identical results. Returns 1 when the
+ * decoder takes that path, with *count (may be NULL) the workgroups that
+ * merged every head themselves since it was created, 0 when it does not, -1
+ * on error. The environment variable VBS_ATTN_O_SPIN, read at create, sets
+ * the wait's bound in polls (0: no workgroup waits). */
+int vbs_gfx950_decoder_attn_o_fallbacks(void *handle, uint32_t *count);
 int vbs_gfx950_decoder_destroy(void *handle);
 
 /* ---- batched decode (extension) --------------------------------------------

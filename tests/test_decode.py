@@ -390,12 +390,18 @@ def test_gpu_graph_decoder_equals_dispatch_path(host, backend, dev, tiny):
 
 
 @pytest.mark.gpu
-def test_gpu_graph_decoder_7b_width_equals_dispatch_path(host, backend, dev):
+@pytest.mark.parametrize("spin", [None, "0"], ids=["xcd_exchange", "forced_own_merge"])
+def test_gpu_graph_decoder_7b_width_equals_dispatch_path(host, backend, dev, spin, monkeypatch):
     """At the 7B width (4096, 32 q heads of 128: k_mvl's fused attn_norm +
-    Q/K/V + RoPE + KV store launch over 6144 rows, the matrix-core attention,
-    k_mvl's O projection with the residual add) the graph decoder's logits
-    and KV rows equal the per-dispatch path's bit for bit, over 2 layers of
-    the 7B geometry and 8 teacher-forced positions from 333."""
+    Q/K/V + RoPE + KV store launch over 6144 rows, the matrix-core attention
+    chunks, then k_mvl_attn: the O projection with the attention merge in
+    front and the residual add) the graph decoder's logits and KV rows equal
+    the per-dispatch path's (a merge launch, then O) bit for bit, over 2
+    layers of the 7B geometry and 8 teacher-forced positions from 333. The
+    O launch's workgroups share the merged heads within each XCD; with
+    VBS_ATTN_O_SPIN=0 no workgroup waits for them and every one merges all
+    the heads itself instead (the bounded wait's way out), with the same
+    results."""
     model = V.SynthModel(host, n_layers=2, **GEO_7B, max_ctx=400, seed=11)
     ctx, n = 333, 8
     kc_p, vc_p = model.kv_prefill(host, ctx)
@@ -405,6 +411,8 @@ def test_gpu_graph_decoder_7b_width_equals_dispatch_path(host, backend, dev):
     want = [d.step(tok, ctx + i) for i, tok in enumerate(stream)]
     want_kc, want_vc = d.read_kv(ctx + n)
     d.load_kv(kc_p, vc_p, ctx)
+    if spin is not None:
+        monkeypatch.setenv("VBS_ATTN_O_SPIN", spin)  # (read when the decoder is created)
     g = V.GraphDecoder(dev, d, max_steps=n)
     try:
         for i, tok in enumerate(stream):
@@ -412,6 +420,12 @@ def test_gpu_graph_decoder_7b_width_equals_dispatch_path(host, backend, dev):
             assert np.array_equal(got.view(np.uint32), want[i].view(np.uint32)), i
         gk, gv = d.read_kv(ctx + n)
         assert np.array_equal(gk, want_kc) and np.array_equal(gv, want_vc)
+        fused, own = g.attn_o_fallbacks()
+        print(f"attention merged in the O launch: {fused}; workgroups that merged every head "
+              f"themselves: {own}")
+        assert fused
+        if spin == "0":  # each of the 256 workgroups, every layer and step
+            assert own == 256 * 2 * n
     finally:
         g.close()
         d.close()

@@ -9,11 +9,13 @@ for gfx950 with the ROCm LLVM tools):
 * the kernels whose loads the compiler does not track -- the LDS-DMA and
   inline-assembly loads of k_mvl, k_mvr, k_mvbr4, k_mvbr6 and k_checksum,
   each waited for by an explicit vmcnt count (csrc/vbs_lds_dma.h) -- spill
-  no register and use no scratch: the code object metadata must show
-  .vgpr_spill_count, .sgpr_spill_count and .private_segment_fixed_size of 0
-  (a spill's scratch load or store would be counted by the same vmcnt and
-  throw the hand-counted waits off, and a copy of a destination register
-  made before its wait would hold stale data);
+  no vector register and use no scratch: the code object metadata must show
+  .vgpr_spill_count and .private_segment_fixed_size of 0 (a spill's scratch
+  load or store would be counted by the same vmcnt and throw the
+  hand-counted waits off, and a copy of a destination register made before
+  its wait would hold stale data). Scalar registers spilled into lanes of a
+  vector register (v_writelane / v_readlane, no memory: the case whenever
+  .sgpr_spill_count is not 0 while the scratch size is) are allowed;
 * M0 is written only by the LDS-DMA sequence of csrc/vbs_lds_dma.h and
   csrc/vbs_kern_checksum.hip (s_mov_b32 m0, sN; s_nop 0; global_load_lds_*),
   and read by nothing else: those inline-assembly blocks set M0 without
@@ -60,8 +62,7 @@ def metadata_problems(co):
         if all(k in cur for k in ("name", "vgpr_spill_count", "sgpr_spill_count",
                                   "private_segment_fixed_size")):
             if HAND_WAITED.search(cur["name"]) and (
-                    cur["vgpr_spill_count"], cur["sgpr_spill_count"],
-                    cur["private_segment_fixed_size"]) != ("0", "0", "0"):
+                    cur["vgpr_spill_count"], cur["private_segment_fixed_size"]) != ("0", "0"):
                 bad.append(f"{cur['name']}: vgpr spills {cur['vgpr_spill_count']}, sgpr spills "
                            f"{cur['sgpr_spill_count']}, scratch {cur['private_segment_fixed_size']}")
             cur = {}

@@ -81,6 +81,22 @@ __device__ __forceinline__ MergeMl merge_ml_load(const float *ph, uint32_t nc, u
     v.l1 = lane + 64u < nc ? ph[(uint64_t)(lane + 64u) * kPartRow + 1u] : 0.f;
     return v;
 }
+// The same loads bounded by `bound` >= nc chunk rows (all inside the
+// partials) instead of by nc, so that they need not wait for the chunk count;
+// merge_ml_mask then drops the chunks from nc on.
+__device__ __forceinline__ MergeMl merge_ml_load_bounded(const float *ph, uint32_t bound, uint32_t lane) {
+    MergeMl v;
+    v.m0 = lane < bound ? ph[(uint64_t)lane * kPartRow] : -INFINITY;
+    v.l0 = lane < bound ? ph[(uint64_t)lane * kPartRow + 1u] : 0.f;
+    v.m1 = lane + 64u < bound ? ph[(uint64_t)(lane + 64u) * kPartRow] : -INFINITY;
+    v.l1 = lane + 64u < bound ? ph[(uint64_t)(lane + 64u) * kPartRow + 1u] : 0.f;
+    return v;
+}
+__device__ __forceinline__ MergeMl merge_ml_mask(MergeMl v, uint32_t nc, uint32_t lane) {
+    if (lane >= nc) v.m0 = -INFINITY, v.l0 = 0.f;
+    if (lane + 64u >= nc) v.m1 = -INFINITY, v.l1 = 0.f;
+    return v;
+}
 
 // Every lane of the wave gets M and L: lane l takes chunks l, l + 64, ... in
 // that order (chunks from 128 on are read here).
@@ -107,7 +123,8 @@ __device__ __forceinline__ MergeStats merge_stats(const float *ph, uint32_t nc, 
 }
 
 // Residue r: the acc rows of chunks c = r + 4 k, k < kMergeBatch, requested
-// at once (lane l: head dims 2l, 2l + 1) ...
+// at once (lane l: head dims 2l, 2l + 1; rows from nc on, when nc is a bound
+// on the chunk count rather than the count, are read and not used) ...
 __device__ __forceinline__ void merge_residue_load(const float *ph, uint32_t nc, uint32_t r,
                                                    uint32_t lane, float2 av[kMergeBatch]) {
 #pragma unroll
@@ -156,6 +173,51 @@ __device__ __forceinline__ float2 merge_finish(const float2 a[kMergeRes], float 
     }
     const float inv = __fdiv_rn(1.0f, L);
     return make_float2(__fmul_rn(s.x, inv), __fmul_rn(s.y, inv));
+}
+
+// The same merge by one wave: the four residue sums accumulated side by side
+// in chunk order (each residue's chunks in its own order, as the four waves
+// take them), the acc rows of B chunks requested at once (B a multiple of
+// kMergeRes), then merge_finish: bit-identical to the four-wave merge.
+template <uint32_t B>
+__device__ __forceinline__ float2 merge_one_wave(const float *ph, uint32_t nc, uint32_t lane) {
+    static_assert(B % kMergeRes == 0u, "batch");
+    auto load_batch = [&](uint32_t c0, float2 av[B]) {
+#pragma unroll
+        for (uint32_t k = 0; k < B; k++) {
+            const uint32_t c = c0 + k;
+            av[k] = c < nc ? *reinterpret_cast<const float2 *>(ph + (uint64_t)c * kPartRow + 2u + 2u * lane)
+                           : make_float2(0.f, 0.f);
+        }
+    };
+    float2 av[B];
+    load_batch(0u, av);
+    const MergeStats st = merge_stats(ph, nc, lane, merge_ml_load(ph, nc, lane));
+    float ox[kMergeRes] = {0.f, 0.f, 0.f, 0.f}, oy[kMergeRes] = {0.f, 0.f, 0.f, 0.f};
+    for (uint32_t c0 = 0; c0 < nc; c0 += B) {
+        if (c0) load_batch(c0, av);
+#pragma unroll
+        for (uint32_t k = 0; k < B; k++) {
+            const uint32_t c = c0 + k, r = k % kMergeRes;  // (c0 is a multiple of kMergeRes)
+            if (c < nc) {
+                float wc;
+                if (c < 128u) {  // (as merge_residue_sum: c is wave-uniform)
+                    wc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                                       __builtin_bit_cast(int, c < 64u ? st.w_lane : st.w_lane64),
+                                                       (int)(c & 63u)));
+                } else {
+                    const float mc = ph[(uint64_t)c * kPartRow];
+                    wc = mc == -INFINITY ? 0.f : fast_exp(__fsub_rn(mc, st.M));
+                }
+                ox[r] = fmaf(av[k].x, wc, ox[r]);
+                oy[r] = fmaf(av[k].y, wc, oy[r]);
+            }
+        }
+    }
+    float2 a[kMergeRes];
+#pragma unroll
+    for (uint32_t r = 0; r < kMergeRes; r++) a[r] = make_float2(ox[r], oy[r]);
+    return merge_finish(a, st.L);
 }
 
 }  // namespace vbs

@@ -8,7 +8,9 @@
 // matvec can carry them (same arithmetic, one kernel): attn_norm + Q/K/V +
 // RoPE + cache store; O + residual add; ffn_norm + gate/up + SiLU*up; down +
 // residual add; output_norm + lm_head: six launches per layer with attention's
-// two. Other weight types run the per-op kernels of the C ABI. The
+// two. At the 7B shape (Q4_K O over 32 heads of 128) the attention merge
+// moves into the O launch (k_mvl_attn): five. Other weight types run the
+// per-op kernels of the C ABI. The
 // position-dependent kernels read the position from device memory, so one
 // captured graph serves every token:
 //   * RoPE reads cos/sin of each pair from a [max_ctx][head_dim/2] table that
@@ -237,11 +239,37 @@ struct Decoder {
     float *margins = nullptr;
     float *part = nullptr;
     float2 *rope = nullptr;
+    // attention merged inside the O launch (attn_o_fits): the XCDs' copies of
+    // the merged vector, their flags, the count of workgroups that merged
+    // every head themselves, and the bound on each workgroup's wait
+    float *mbuf = nullptr;
+    uint32_t *mflag = nullptr, *fallbacks = nullptr;
+    uint32_t ao_spin = 0;
     uint32_t max_steps = 0;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     void *arena = nullptr;
 };
+
+// Polls of a workgroup's bounded wait for its XCD's merged heads in the O launch:
+// a poll is an L2 round trip and a short sleep, so the bound is ~1 ms, far
+// past the few microseconds the other workgroups take to publish.
+constexpr uint32_t kAttnOSpin = 2048;
+
+// The O launch takes the attention merge (launch_q4k_mvl_attn) when every
+// layer's O is Q4_K of the 7B shape: q dimension 4096 (32 heads of 128, 16
+// blocks), at most 16 rows per each of the 256 workgroups, group <= 8, the
+// weights and caches 16-byte aligned.
+static bool attn_o_fits(const vbs_gfx950_model_t &m) {
+    const uint32_t qd = m.n_heads * m.head_dim, wgs = 8u * m.n_heads;
+    if (m.head_dim != 128u || qd != 4096u || m.n_kv_heads == 0 || m.n_heads % m.n_kv_heads ||
+        m.n_heads / m.n_kv_heads > 8u || (m.hidden + wgs - 1u) / wgs > 16u ||
+        ((uintptr_t)m.kc & 15u) || ((uintptr_t)m.vc & 15u))
+        return false;
+    for (uint32_t L = 0; L < m.n_layers; L++)
+        if (m.wtype[7 * L + 3] != kQ4_K || ((uintptr_t)m.wdata[7 * L + 3] & 15u)) return false;
+    return true;
+}
 
 static hipError_t enqueue_step(const Decoder &d, hipStream_t s) {
     const vbs_gfx950_model_t &m = d.m;
@@ -284,10 +312,34 @@ static hipError_t enqueue_step(const Decoder &d, hipStream_t s) {
         } else {
             VBS_TRY(e);
         }
-        VBS_TRY(launch_attention(d.q, m.kc, m.vc, d.attn, m.max_ctx, pos_dev, d.part, layer_off,
-                                 nq, nkv, hd, scale, s));
-        // O with the residual add folded in (stream + O*attn, as the add computes it)
-        e = launch_kq_linear(t[3], w[3], d.attn, d.stream, qd, H, 1, s);
+        if (d.mbuf) {
+            // attention chunks, then O with the merge in front and the residual
+            // add folded in: two launches, the results of the three below
+            VBS_TRY(launch_attention_chunks(d.q, m.kc, m.vc, m.max_ctx, pos_dev, d.part, layer_off, nq,
+                                            nkv, hd, scale, d.mflag, attn_o_flags(qd), kAttnOFlagStride, s));
+            AttnOArgs ao{};
+            ao.w = w[3];
+            ao.y = d.stream;
+            ao.rows = H;
+            ao.cols = qd;
+            ao.rpw = (H + 8u * nq - 1u) / (8u * nq);
+            ao.part = d.part;
+            ao.stride_chunks = attention_chunk_stride(m.max_ctx, nkv);
+            ao.nkh = nkv;
+            ao.pos = pos_dev;
+            ao.attn = d.attn;
+            ao.mbuf = d.mbuf;
+            ao.mflag = d.mflag;
+            ao.spin = d.ao_spin;
+            ao.fallbacks = d.fallbacks;
+            VBS_TRY(launch_q4k_mvl_attn(ao, s));
+            e = hipSuccess;
+        } else {
+            VBS_TRY(launch_attention(d.q, m.kc, m.vc, d.attn, m.max_ctx, pos_dev, d.part, layer_off,
+                                     nq, nkv, hd, scale, s));
+            // O with the residual add folded in (stream + O*attn, as the add computes it)
+            e = launch_kq_linear(t[3], w[3], d.attn, d.stream, qd, H, 1, s);
+        }
         if (e == hipErrorNotSupported) {
             VBS_TRY(launch_linear(t[3], w[3], d.attn, d.tmp, qd, H, 0, s));
             VBS_TRY(launch_add(d.stream, d.tmp, d.stream, H, s));
@@ -382,7 +434,9 @@ int vbs_gfx950_decoder_create(const vbs_gfx950_model_t *m, uint32_t max_steps, v
     const size_t rope = (size_t)m->max_ctx * pairs * sizeof(float2);
     auto up256 = [](size_t b) { return (b + 255u) & ~(size_t)255u; };
     const size_t sz_f = up256(n_f32 * 4), sz_st = 256, sz_tok = up256(d->max_steps * 4ull);
-    const size_t total = sz_f + sz_st + 2 * sz_tok + up256(part) + up256(rope);
+    const bool ao = attn_o_fits(*m);
+    const size_t sz_ao = ao ? up256(attn_o_exchange_bytes(qd)) + 256u : 0u;
+    const size_t total = sz_f + sz_st + 2 * sz_tok + up256(part) + up256(rope) + sz_ao;
     if (hipMalloc(&d->arena, total) != hipSuccess) {
         delete d;
         return rt_fail("decoder_create: hipMalloc(%zu) failed", total);
@@ -405,7 +459,15 @@ int vbs_gfx950_decoder_create(const vbs_gfx950_model_t *m, uint32_t max_steps, v
     d->tokens = (uint32_t *)p; p += sz_tok;
     d->margins = (float *)p; p += sz_tok;
     d->part = (float *)p; p += up256(part);
-    d->rope = (float2 *)p;
+    d->rope = (float2 *)p; p += up256(rope);
+    if (ao) {
+        d->mbuf = (float *)p;
+        d->mflag = (uint32_t *)(p + (size_t)kAttnOXcds * qd * sizeof(float));
+        p += up256(attn_o_exchange_bytes(qd));
+        d->fallbacks = (uint32_t *)p;
+        const char *sp = getenv("VBS_ATTN_O_SPIN");  // (tests force the fallback with 0)
+        d->ao_spin = sp ? (uint32_t)strtoul(sp, nullptr, 10) : kAttnOSpin;
+    }
     // RoPE table with the reference's expressions (src/vbs_host_math.h:43-44)
     std::vector<float2> tab((size_t)m->max_ctx * pairs);
     for (uint32_t pos = 0; pos < m->max_ctx; pos++)
@@ -418,6 +480,7 @@ int vbs_gfx950_decoder_create(const vbs_gfx950_model_t *m, uint32_t max_steps, v
     if (!rt_hip_ok(hipMemcpyAsync(d->rope, tab.data(), rope, hipMemcpyHostToDevice, s),
                    "decoder_create: rope table") ||
         !rt_hip_ok(hipMemsetAsync(d->state, 0, sz_st, s), "decoder_create: state") ||
+        (ao && !rt_hip_ok(hipMemsetAsync(d->mbuf, 0, sz_ao, s), "decoder_create: exchange")) ||
         !rt_hip_ok(hipStreamSynchronize(s), "decoder_create")) {
         decoder_free(d);
         return 0;
@@ -513,6 +576,17 @@ int vbs_gfx950_decoder_greedy_eager(void *handle, uint32_t token, uint32_t pos, 
                    "decoder_greedy_eager: margins"))
         return 0;
     return rt_hip_ok(hipStreamSynchronize(s), "decoder_greedy_eager");
+}
+
+int vbs_gfx950_decoder_attn_o_fallbacks(void *handle, uint32_t *count) {
+    Decoder *d = (Decoder *)handle;
+    if (!d) return rt_fail("decoder: NULL handle");
+    uint32_t c = 0;
+    if (d->fallbacks && !rt_hip_ok(hipMemcpy(&c, d->fallbacks, sizeof(c), hipMemcpyDeviceToHost),
+                                   "decoder: fallbacks"))
+        return -1;
+    if (count) *count = c;
+    return d->fallbacks ? 1 : 0;
 }
 
 int vbs_gfx950_decoder_destroy(void *handle) {

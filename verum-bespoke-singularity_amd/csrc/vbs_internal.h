@@ -112,6 +112,37 @@ hipError_t launch_q4k_mvl(const uint8_t *w, const float *x, float *y, uint32_t c
 // NULL) also receives each row value before it is added.
 hipError_t launch_q6k_mvr(const uint8_t *w, const float *x, float *y, uint32_t cols, uint32_t rows,
                           int accumulate, hipStream_t s, float *ycopy = nullptr);
+// A decode step's O projection with the attention merge in front, in one
+// launch (k_mvl_attn, vbs_kern_mvl.hip): y += W attn, W Q4_K of rows of 16
+// blocks (cols = 4096 = nqh x 128), attn the head_dim-128 merge of the
+// partials launch_attention_chunks wrote (stride_chunks per q head, the
+// sequence length pos[0] + 1 read on the device), bit-identical to
+// launch_attention's merge followed by launch_q4k_mvl. 8 nqh workgroups of
+// rpw <= 16 rows. The heads travel between the workgroups of an XCD through
+// mbuf ([8][cols] floats) and mflag (attn_o_flag_words(cols) words, cleared
+// by the chunk launch before it); spin bounds each workgroup's wait for them,
+// after which it merges every head itself (fallbacks, if not NULL, counts
+// those workgroups). attn, if not NULL, also receives the merged vector.
+constexpr uint32_t kAttnOXcds = 8;
+struct AttnOArgs {
+    const uint8_t *w;
+    float *y;
+    uint32_t rows, cols, rpw;
+    const float *part;
+    uint32_t stride_chunks, nkh;
+    const uint32_t *pos;
+    float *attn, *mbuf;
+    uint32_t *mflag;
+    uint32_t spin;
+    uint32_t *fallbacks;
+};
+// One flag per (XCD, head), each on a 128-byte line of its own (polls of one
+// line by many workgroups' atomics would queue behind each other in the L2).
+constexpr uint32_t kAttnOFlagStride = 32;
+inline uint32_t attn_o_flags(uint32_t cols) { return kAttnOXcds * (cols / 128u); }
+inline uint32_t attn_o_flag_words(uint32_t cols) { return attn_o_flags(cols) * kAttnOFlagStride; }
+size_t attn_o_exchange_bytes(uint32_t cols);
+hipError_t launch_q4k_mvl_attn(const AttnOArgs &a, hipStream_t s);
 // The linear op fused with its neighbours in the bridge's op sequence (the
 // backend shim's dispatch path, vbs_gfx950_linear_fused): norm_w / eps / xn
 // (RMSNorm in front, the normalised x stored to xn), ycopy (y = y + W x, W x
@@ -168,6 +199,16 @@ hipError_t launch_attention(const float *q, const uint16_t *kc, const uint16_t *
                             uint32_t seq_len, const uint32_t *pos_dev, float *part,
                             uint64_t layer_off, uint32_t nqh, uint32_t nkh, uint32_t hd,
                             float scale, hipStream_t s);
+// Its matrix-core chunk launch alone (head_dim 128, group <= 8, 16-byte
+// aligned q and caches; hipErrorNotSupported otherwise), the partials in
+// `part` (attention_chunk_stride(seq_len, nkh) chunks per q head) for a merge
+// by the launch after it (launch_q4k_mvl_attn), the words clear[i stride]
+// for i < nclear zeroed for that launch.
+hipError_t launch_attention_chunks(const float *q, const uint16_t *kc, const uint16_t *vc,
+                                   uint32_t seq_len, const uint32_t *pos_dev, float *part,
+                                   uint64_t layer_off, uint32_t nqh, uint32_t nkh, uint32_t hd,
+                                   float scale, uint32_t *clear, uint32_t nclear, uint32_t stride,
+                                   hipStream_t s);
 // The same for `batch` sequences with their own caches and positions:
 // sequence b reads q + b q_stride, writes out + b q_stride, uses the caches at
 // + b kv_stride elements, the position pos_dev[b] and the partials at

@@ -563,10 +563,15 @@ __global__ __launch_bounds__(64) void k_attn_mfma(const float *__restrict__ q,
                                                   uint64_t layer_off, uint32_t nkh, uint32_t group,
                                                   float scale, uint32_t stride_chunks,
                                                   uint32_t q_bstride, uint64_t kv_bstride,
-                                                  uint64_t part_bstride, uint32_t target) {
+                                                  uint64_t part_bstride, uint32_t target,
+                                                  uint32_t *__restrict__ clear, uint32_t nclear,
+                                                  uint32_t clear_stride) {
     constexpr uint32_t HD = 128;
     const uint32_t chunk = blockIdx.x, kvh = blockIdx.y, lane = threadIdx.x, bz = blockIdx.z;
     const uint32_t n = lane & 15u, g = lane >> 4;
+    // the merging launch that follows (k_mvl_attn) starts from cleared flags
+    if (clear && chunk == 0u && kvh == 0u && bz == 0u)
+        for (uint32_t i = lane; i < nclear; i += 64u) clear[(uint64_t)i * clear_stride] = 0u;
     // sequence bz of a batch: its q, caches, position and partials
     q += (uint64_t)bz * q_bstride;
     kc += bz * kv_bstride;
@@ -761,7 +766,7 @@ hipError_t launch_attention(const float *q, const uint16_t *kc, const uint16_t *
     if (fast && hd == 128u) {
         k_attn_mfma<<<dim3(mfma_grid_chunks(seq_len, nkh), nkh), 64, 0, s>>>(
             q, kc, vc, part, seq_len, pos_dev, layer_off, nkh, group, scale, stride, 0u, 0ull, 0ull,
-            kMfmaTargetWgs);
+            kMfmaTargetWgs, nullptr, 0u, 0u);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         k_attn_merge_h128<<<nqh, 64 * kMergeRes, 0, s>>>(part, out, stride, pos_dev, seq_len, nkh,
                                                             0u, 0ull, kMfmaTargetWgs);
@@ -795,6 +800,24 @@ hipError_t launch_attention(const float *q, const uint16_t *kc, const uint16_t *
 
 uint32_t attention_chunk_stride(uint32_t max_seq, uint32_t nkh) { return attn_max_chunks(max_seq, nkh); }
 
+// The matrix-core chunk launch alone (head_dim 128, group <= 8), for a merge
+// done by the launch that follows it (k_mvl_attn): the partials at part with
+// attention_chunk_stride(seq_len, nkh) chunks per q head, and the words
+// clear[i stride], i < nclear, zeroed for that launch's exchange.
+hipError_t launch_attention_chunks(const float *q, const uint16_t *kc, const uint16_t *vc,
+                                   uint32_t seq_len, const uint32_t *pos_dev, float *part,
+                                   uint64_t layer_off, uint32_t nqh, uint32_t nkh, uint32_t hd,
+                                   float scale, uint32_t *clear, uint32_t nclear, uint32_t stride,
+                                   hipStream_t s) {
+    if (seq_len == 0 || nkh == 0 || nqh % nkh != 0 || hd != 128u || nqh / nkh > 8u || !part ||
+        ((uintptr_t)q & 15u) || ((uintptr_t)kc & 15u) || ((uintptr_t)vc & 15u))
+        return hipErrorNotSupported;
+    k_attn_mfma<<<dim3(mfma_grid_chunks(seq_len, nkh), nkh), 64, 0, s>>>(
+        q, kc, vc, part, seq_len, pos_dev, layer_off, nkh, nqh / nkh, scale, attn_max_chunks(seq_len, nkh),
+        0u, 0ull, 0ull, kMfmaTargetWgs, clear, nclear, stride);
+    return hipGetLastError();
+}
+
 bool attn_mfma_batch_fits(const float *q, const uint16_t *kc, const uint16_t *vc, uint32_t nqh,
                           uint32_t nkh, uint32_t hd, uint32_t q_stride, uint64_t kv_stride) {
     return nkh != 0u && nqh % nkh == 0u && hd == 128u && nqh / nkh <= 8u && ((uintptr_t)q & 15u) == 0 &&
@@ -827,7 +850,7 @@ hipError_t launch_attention_batch(const float *q, const uint16_t *kc, const uint
     const uint32_t stride = attn_max_chunks(max_seq, nkh), target = attn_batch_target(batch);
     k_attn_mfma<<<dim3(mfma_grid_chunks(max_seq, nkh, target), nkh, batch), 64, 0, s>>>(
         q, kc, vc, part, max_seq, pos_dev, layer_off, nkh, group, scale, stride, q_stride, kv_stride,
-        pstride, target);
+        pstride, target, nullptr, 0u, 0u);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || !out) return e;  // (no out: the caller merges the partials itself)
     k_attn_merge_h128<<<dim3(nqh, batch), 64 * kMergeRes, 0, s>>>(part, out, stride, pos_dev,

@@ -24,6 +24,7 @@
 // the compiler's builtin makes it insert waits for all loads before every
 // LDS access. The compiler does not see these loads, so each wait for them is
 // an explicit s_waitcnt; nothing else in these kernels uses M0.
+#include "vbs_attn_common.h"
 #include "vbs_lds_dma.h"
 #include "vbs_mfma.h"
 
@@ -455,6 +456,223 @@ hipError_t launch_q4k_mvl(const uint8_t *w, const float *x, float *y, uint32_t c
     if (tiles == 2u) VBS_MVL(2);
     VBS_MVL(3);
 #undef VBS_MVL
+}
+
+// ---- the attention merge inside the O launch -----------------------------------------
+// k_mvl_attn: y += W attn for a decode step's O projection (Q4_K rows of 16
+// blocks, one tile per workgroup), where attn -- the merge of the chunk
+// launch's partials, head_dim 128, nqh = cols / 128 heads -- is made inside
+// the launch instead of by a merge launch of its own. Workgroups are dealt to
+// the eight XCDs round-robin in flat-index order, so with 8 nqh of them each
+// XCD holds the 8 j + r for one r and every j < nqh: workgroup i merges q head
+// i / 8 (waves 0..3, as k_attn_merge_h128: bit-identical), publishes it to its
+// XCD's copy of the vector (its XCC_ID register) and raises the head's flag
+// there, a 128-byte line of its own; then its wave 0 waits for all the
+// heads' flags, read in the XCD's L2 by atomic adds of zero, copies the vector
+// into the x slots, and the launch goes on as k_mvl's E_ACC form. The merge is
+// the critical path, so its loads go out first (they cover the head's whole
+// chunk stride, so they need not wait for the position) and the weights'
+// DMAs after a barrier; waves 4..7 request blocks 0..3's weights together with
+// their own, so waves 0..3 have no DMA in flight and wait on their own loads
+// with the compiler's counts; everything else waits on explicit counts.
+// Nothing in the launch reads a head's lines before its flag is up, so no
+// CU's L1 holds a stale copy; no device-scope release or acquire is needed.
+// The wait is bounded (spin polls): past it, wave 0 merges every head itself
+// (merge_one_wave, bit-identical too), so a workgroup that ran on an
+// unexpected XCD or late costs time, never the result. The chunk launch
+// before it clears the flags.
+// Measured (7B, ctx ~2065, eager under the tracer): 9.0 us against 4.9 +
+// 4.4 us for k_mvl and the merge launch; 7B graph decode 691-695 against
+// 676-692 tok/s. Forms measured slower: one flag line per XCD polled by four
+// waves of every workgroup (the atomics on one line queue in the L2: 14.5
+// us), and the position read by a scalar load with glc (35 us).
+__device__ __forceinline__ uint32_t xcc_id() {
+    uint32_t x;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+    return x & 15u;
+}
+// The word at p as the XCD's L2 holds it: an atomic add of zero (atomics are
+// performed in the L2; a plain load may be served by a line the CU's L1 took
+// at an earlier poll). The zero is hidden from the compiler so that the add
+// is not turned into a load.
+__device__ __forceinline__ uint32_t load_l2(uint32_t *p) {
+    uint32_t z = 0u;
+    asm volatile("" : "+v"(z));
+    return __hip_atomic_fetch_add(p, z, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+// Every wave's LDS writes done, then the workgroup barrier (no wait on
+// vector memory: the DMAs in flight stay in flight).
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt and expcnt untouched
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+__global__ __launch_bounds__(64 * kMvlWaves) void k_mvl_attn(const AttnOArgs a) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    __shared__ float2 red[kMergeRes][64];
+    const uint32_t cols = a.cols, rb = kMvlWaves * 144u, nqh = cols / 128u;
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const uint32_t n = lane & 15u, g = lane >> 4;
+    const uint32_t r0 = blockIdx.x * a.rpw, r1 = min(r0 + a.rpw, a.rows);
+    const bool rows_here = r0 < r1;  // (a workgroup without rows still merges its head)
+    const uint32_t xcc = xcc_id(), hh = blockIdx.x >> 3;
+    const bool xok = xcc < kAttnOXcds;
+    // LDS: [16 waves][item of 2304 B] | 16 zero bytes | [16 waves][x / digit slot] | pb
+    const uint32_t lds0 = (uint32_t)(uintptr_t)lds;
+    uint8_t *const xq = lds + kMvlWaves * kMvlItem;
+    uint8_t *const slot0 = xq + 16u;
+    float *const pb = reinterpret_cast<float *>(xq + 16u + kMvlWaves * kMvlSlot);
+    const uint32_t ps = part_stride(kMvlWaves);
+
+    // 1. waves 0..3: the partials of q head hh requested (residue `wave`
+    // each) before any weight: the merge is the launch's critical path. The
+    // loads cover the head's stride_chunks rows, so they need not wait for
+    // the position; the rows from the chunk count on are dropped after.
+    const float *ph = a.part + (uint64_t)hh * a.stride_chunks * kPartRow;
+    float2 av[kMergeBatch];
+    MergeMl ml{};
+    if (wave < kMergeRes) {
+        merge_residue_load(ph, a.stride_chunks, wave, lane, av);
+        ml = merge_ml_load_bounded(ph, a.stride_chunks, lane);
+    }
+    if (lane < 4u) reinterpret_cast<uint32_t *>(xq)[lane] = 0u;
+    lds_barrier();
+    // 2. the items: block w's 16 x 144 bytes for wave w (waves 4..7 first
+    // request those of blocks 0..3)
+    auto issue_item = [&](uint32_t blk) {
+#pragma unroll
+        for (uint32_t q = 0; q < 3; q++) {
+            const uint32_t c = 64u * q + lane;
+            const uint32_t row = min(r0 + c / 9u, r1 - 1u);
+            const uint8_t *src = a.w + ((uint64_t)row * rb + blk * 144u + 16u * (c % 9u));
+            if (q < 2u || lane < 16u) dma16(src, lds0 + blk * kMvlItem + 1024u * q);
+        }
+    };
+    if (rows_here) {
+        if (wave >= 4u && wave < 8u) issue_item(wave - 4u);
+        if (wave >= 4u) issue_item(wave);
+    }
+
+    // the position (only waves 0..3 read it: a compiler-counted load in a
+    // wave with DMAs in flight would wait for all of them)
+    uint32_t nc = 0;
+    if (wave < kMergeRes) {
+        nc = mfma_chunks(a.pos[0] + 1u, a.nkh);  // seq = pos + 1
+        ml = merge_ml_mask(ml, nc, lane);
+    }
+
+    // 3. waves 0..3: the merge of head hh, as k_attn_merge_h128
+    MergeStats st{};
+    if (wave < kMergeRes) {
+        st = merge_stats(ph, nc, lane, ml);
+        red[wave][lane] = merge_residue_sum(ph, nc, st, wave, lane, av);
+    }
+    lds_barrier();
+
+    // 4. wave 0 publishes the head to its XCD's copy, raises its flag (a line
+    // of its own) once the stores are in the L2, then waits for the other
+    // heads' flags -- one poller per workgroup -- and copies the whole vector
+    // into the x slots
+    if (wave == 0u) {
+        float2 ar[kMergeRes];
+#pragma unroll
+        for (uint32_t r = 0; r < kMergeRes; r++) ar[r] = red[r][lane];
+        const float2 o = merge_finish(ar, st.L);
+        if (xok) *reinterpret_cast<float2 *>(a.mbuf + (uint64_t)xcc * cols + hh * 128u + 2u * lane) = o;
+        if (a.attn) *reinterpret_cast<float2 *>(a.attn + hh * 128u + 2u * lane) = o;
+        vmcnt_le<0u>();
+        asm volatile("" ::: "memory");
+        uint32_t *const fl = a.mflag + (uint64_t)xcc * nqh * kAttnOFlagStride;
+        if (xok && lane == 0u) fl[hh * kAttnOFlagStride] = 1u;
+        bool ready = false;
+        if (xok) {
+            for (uint32_t it = 0; it < a.spin; it++) {
+                const uint32_t f = lane < nqh ? load_l2(fl + lane * kAttnOFlagStride) : 1u;
+                if (__all(f != 0u)) {
+                    ready = true;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+            }
+        }
+        asm volatile("" ::: "memory");  // (the reads below stay behind the polls)
+        if (ready) {
+            const float *src = a.mbuf + (uint64_t)xcc * cols;
+            float4 v[kMvlWaves];
+#pragma unroll
+            for (uint32_t i = 0; i < kMvlWaves; i++)
+                v[i] = *reinterpret_cast<const float4 *>(src + 256u * i + 4u * lane);
+#pragma unroll
+            for (uint32_t i = 0; i < kMvlWaves; i++)
+                *reinterpret_cast<float4 *>(slot0 + i * kMvlSlot + 16u * lane) = v[i];
+        } else {  // the bounded wait ran out: every head merged here
+            if (lane == 0u && a.fallbacks) atomicAdd(a.fallbacks, 1u);
+            for (uint32_t h = 0; h < nqh; h++) {
+                const float2 oh = merge_one_wave<4u>(a.part + (uint64_t)h * a.stride_chunks * kPartRow, nc, lane);
+                *reinterpret_cast<float2 *>(slot0 + (h >> 1) * kMvlSlot + 512u * (h & 1u) + 8u * lane) = oh;
+            }
+        }
+    }
+    // waves 4..7: blocks 0..3's items have landed (their own may be in flight)
+    if (rows_here && wave >= 4u && wave < 8u) vmcnt_le<3u>();
+    lds_barrier();
+    if (!rows_here) return;
+
+    // 5. as k_mvl: the digits of x block `wave` over it, the wave's item, the
+    // row sums in block order and the residual add
+    uint8_t *const slot = slot0 + wave * kMvlSlot;
+    DigitView dv;
+    dv.zero = xq;
+    dv.base = slot;
+    dv.pstride = 256u;
+    dv.xs16 = reinterpret_cast<float *>(slot + 768u);
+    dv.xs = reinterpret_cast<float2 *>(slot + 832u);
+    {
+        const float4 xv = *reinterpret_cast<const float4 *>(slot + 16u * lane);
+        const float v[4] = {xv.x, xv.y, xv.z, xv.w};
+        prep_block(v, lane, dv);
+    }
+    const Q4K::X xo = Q4K::x_operands(dv, n, g);
+    if (wave >= 4u) {
+        vmcnt_le<0u>();
+        asm volatile("" ::: "memory");
+    }
+    {
+        const uint8_t *row = lds + wave * kMvlItem + 144u * n;
+        u32x4 r[3];
+        r[0] = lda4(row);
+        r[1] = lda4(row + 16u + 16u * g);
+        r[2] = lda4(row + 80u + 16u * g);
+        float part = Q4K::dot_x(r, xo, g);
+        part += lane_xor<16>(part);
+        part += lane_xor<32>(part);
+        if (lane < 16u && n < a.rpw) pb[n * ps + wave] = part;
+    }
+    __syncthreads();
+    const uint32_t t = threadIdx.x;
+    if (t < r1 - r0) {
+        const float s = ordered_sum(pb + t * ps, kMvlWaves);
+        float *y = a.y + r0 + t;
+        *y = __fadd_rn(*y, s);
+    }
+}
+
+size_t attn_o_exchange_bytes(uint32_t cols) {
+    return (size_t)kAttnOXcds * cols * sizeof(float) + attn_o_flag_words(cols) * sizeof(uint32_t);
+}
+
+hipError_t launch_q4k_mvl_attn(const AttnOArgs &a, hipStream_t s) {
+    const uint32_t nqh = a.cols / 128u, wgs = 8u * nqh;
+    if (a.cols != 256u * kMvlWaves || a.rows == 0 || !a.part || !a.pos || !a.mbuf || !a.mflag ||
+        ((uintptr_t)a.w & 15u) || ((uintptr_t)a.mbuf & 15u) || a.rpw == 0 || a.rpw > 16u ||
+        (uint64_t)a.rpw * wgs < a.rows)
+        return hipErrorNotSupported;
+    const size_t lds = (size_t)kMvlWaves * kMvlItem + 16u + (size_t)kMvlWaves * kMvlSlot +
+                       (size_t)a.rpw * part_stride(kMvlWaves) * sizeof(float);
+    k_mvl_attn<<<wgs, 64 * kMvlWaves, lds, s>>>(a);
+    return hipGetLastError();
 }
 
 hipError_t launch_q4k_mvl_qkv(const MvArgs &a, hipStream_t s) {

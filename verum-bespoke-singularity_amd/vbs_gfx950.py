@@ -168,6 +168,7 @@ _DEVICE_SIGS = {
     "decoder_step": (_I, [_P, _U32, _U32, _P]),
     "decoder_greedy": (_I, [_P, _U32, _U32, _U32, _P, _P]),
     "decoder_greedy_eager": (_I, [_P, _U32, _U32, _U32, _P, _P]),
+    "decoder_attn_o_fallbacks": (_I, [_P, _P]),
     "decoder_destroy": (_I, [_P]),
     "bdecoder_create": (_I, [_P, _U32, _U64, _U32, C.POINTER(C.c_void_p)]),
     "bdecoder_greedy": (_I, [_P, _P, _P, _U32, _P, _P]),
@@ -757,6 +758,15 @@ class GraphDecoder:
         self.dev.check(fn(self.h, token, pos, n, toks.ctypes.data, margins.ctypes.data),
                        "decoder_greedy")
         return toks, margins
+
+    def attn_o_fallbacks(self):
+        """(whether the O launch merges the attention, waves that merged
+        their own heads since create): vbs_gfx950_decoder_attn_o_fallbacks."""
+        c = C.c_uint32(0)
+        r = self.dev._decoder_attn_o_fallbacks(self.h, C.byref(c))
+        if r < 0:
+            raise GpuError(f"decoder_attn_o_fallbacks: {self.dev.error()}")
+        return bool(r), c.value
 
     def close(self):
         if self.h:
