@@ -30,6 +30,7 @@
 #include "vbs_dev_common.h"
 #include "vbs_gfx950.h"
 #include "vbs_internal.h"
+#include "vbs_lds_dma.h"
 
 namespace vbs {
 
@@ -259,9 +260,13 @@ constexpr uint32_t kAttnOSpin = 2048;
 // The O launch takes the attention merge (launch_q4k_mvl_attn) when every
 // layer's O is Q4_K of the 7B shape: q dimension 4096 (32 heads of 128, 16
 // blocks), at most 16 rows per each of the 256 workgroups, group <= 8, the
-// weights and caches 16-byte aligned.
+// weights and caches 16-byte aligned -- and when the device has a CU for each
+// of those workgroups (one fits a CU), so that they all run at once: a
+// workgroup's wait for the others' heads is bounded, but on fewer CUs it
+// would run out in every launch.
 static bool attn_o_fits(const vbs_gfx950_model_t &m) {
     const uint32_t qd = m.n_heads * m.head_dim, wgs = 8u * m.n_heads;
+    if (device_cus() < wgs) return false;
     if (m.head_dim != 128u || qd != 4096u || m.n_kv_heads == 0 || m.n_heads % m.n_kv_heads ||
         m.n_heads / m.n_kv_heads > 8u || (m.hidden + wgs - 1u) / wgs > 16u ||
         ((uintptr_t)m.kc & 15u) || ((uintptr_t)m.vc & 15u))
