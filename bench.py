@@ -117,8 +117,9 @@ def cpu_beside(work):
     return out
 
 
-def cpu_baseline(host, weights, xs, max_seconds=20.0, beside=None):
-    """Single-threaded reference CPU linear over the layer set (bounded)."""
+def cpu_baseline(host, weights, xs, min_seconds=10.0, beside=None):
+    """Single-threaded reference CPU linear over the layer set: whole passes
+    until at least min_seconds of CPU work (a bounded sample, ~10-12 s)."""
     from oracle_lib import REF_SO, Oracle
     kind, passes, t_total, nbytes = "port", 0, 0.0, 0
     ys = [np.zeros(r, np.float32) for _, r, _ in LAYER_SET]
@@ -150,7 +151,7 @@ def cpu_baseline(host, weights, xs, max_seconds=20.0, beside=None):
             one(i)
         passes += 1
         t_total = time.perf_counter() - t0
-        if t_total >= max_seconds * 0.5 or passes >= 8:
+        if t_total >= min_seconds:
             break
     nbytes = passes * sum(algo_bytes(V.Q4_K, r, c) for _, r, c in LAYER_SET)
     cpu = host_cpu_model()
