@@ -390,20 +390,23 @@ def test_gpu_graph_decoder_equals_dispatch_path(host, backend, dev, tiny):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("spin", [None, "0"], ids=["xcd_exchange", "forced_own_merge"])
-def test_gpu_graph_decoder_7b_width_equals_dispatch_path(host, backend, dev, spin, monkeypatch):
+@pytest.mark.parametrize("spin,ctx", [(None, 333), ("0", 333), (None, 28)],
+                         ids=["xcd_exchange", "forced_own_merge", "xcd_exchange_first_chunks"])
+def test_gpu_graph_decoder_7b_width_equals_dispatch_path(host, backend, dev, spin, ctx, monkeypatch):
     """At the 7B width (4096, 32 q heads of 128: k_mvl's fused attn_norm +
     Q/K/V + RoPE + KV store launch over 6144 rows, the matrix-core attention
     chunks, then k_mvl_attn: the O projection with the attention merge in
     front and the residual add) the graph decoder's logits and KV rows equal
     the per-dispatch path's (a merge launch, then O) bit for bit, over 2
-    layers of the 7B geometry and 8 teacher-forced positions from 333. The
+    layers of the 7B geometry and 8 teacher-forced positions from 333 (from
+    28 in the third case: the attention's chunks of 32 positions go from one
+    to two at position 32, so the merge sees its smallest counts). The
     O launch's workgroups share the merged heads within each XCD; with
     VBS_ATTN_O_SPIN=0 no workgroup waits for them and every one merges all
     the heads itself instead (the bounded wait's way out), with the same
     results."""
     model = V.SynthModel(host, n_layers=2, **GEO_7B, max_ctx=400, seed=11)
-    ctx, n = 333, 8
+    n = 8
     kc_p, vc_p = model.kv_prefill(host, ctx)
     d = V.Decoder(host, backend, model)
     d.load_kv(kc_p, vc_p, ctx)

@@ -584,6 +584,66 @@ def test_attention(dev, host, oracle, mem, nqh, nkh, hd, seq, max_ctx, layer):
     assert np.all(np.abs(got - want) <= 1e-4 + 1e-4 * np.abs(want))
 
 
+def _linear_draws(n=24, seed=SEED + 5):
+    """Seeded shapes across the launch plans: every type, rows from 1 to
+    12288, columns from one block to 16384 in the type's block size."""
+    rng = np.random.default_rng(seed)
+    block = {V.Q4_0: 32, V.Q4_1: 32, V.Q8_0: 32, V.Q4_K: 256, V.Q6_K: 256, V.F16: 32, V.F32: 32}
+    out = []
+    for i in range(n):
+        t = TYPES[i % len(TYPES)]
+        rows = int(rng.choice([1, 15, 16, 17, 100, 1000, 2049, 4096, 4097, 11008, 12288]))
+        cols = int(block[t] * rng.integers(1, 16384 // block[t] + 1))
+        out.append((t, rows, cols))
+    return out
+
+
+@pytest.mark.parametrize("t,rows,cols", _linear_draws(),
+                         ids=[f"{V.TYPE_NAMES[t]}-{r}x{c}" for t, r, c in _linear_draws()])
+def test_linear_random_shapes(dev, host, oracle, mem, t, rows, cols):
+    """Seeded random shapes against the oracle under the matvec bar, so a
+    plan chosen by shape (k_mvl, k_mvr, k_mvf and its tile counts, the
+    32-element block kernels, the VALU fallbacks) is checked away from the
+    shapes the other tests name."""
+    w = V.synth_matrix(host, t, rows, cols, SEED, 31)
+    x = synth_x(host, cols, 32)
+    pw, px, py = mem.up(w), mem.up(x), mem.zeros(rows)
+    dev.linear(t, pw, px, py, cols, rows)
+    got = dev.download(py, rows, np.float32)
+    want = oracle.linear(t, w, x, cols, rows)
+    assert lin_err(got, want) <= LIN_TOL, (V.TYPE_NAMES[t], rows, cols)
+
+
+def _attention_draws(n=12, seed=SEED + 6):
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        nkh = int(rng.choice([1, 2, 4, 8]))
+        group = int(rng.choice([1, 2, 3, 4, 8]))
+        hd = int(rng.choice([32, 64, 96, 128]))
+        seq = int(rng.integers(1, 3001))
+        max_ctx = seq + int(rng.integers(0, 100))
+        out.append((nkh * group, nkh, hd, seq, max_ctx, int(rng.integers(0, 2))))
+    return out
+
+
+@pytest.mark.parametrize("nqh,nkh,hd,seq,max_ctx,layer", _attention_draws())
+def test_attention_random_shapes(dev, host, oracle, mem, nqh, nkh, hd, seq, max_ctx, layer):
+    """Seeded random head counts, groups, head sizes (the matrix-core, VALU
+    and generic chunk kernels), sequence lengths and layers against the
+    oracle, at the attention tolerance."""
+    kvd = nkh * hd
+    kc = V.synth_normal_f16(host, (layer + 1) * max_ctx * kvd, SEED, 141)
+    vc = V.synth_normal_f16(host, (layer + 1) * max_ctx * kvd, SEED, 142)
+    q = synth_x(host, nqh * hd, 143)
+    scale = np.float32(1.0 / math.sqrt(hd))
+    pq, pkc, pvc, po = mem.up(q), mem.up(kc), mem.up(vc), mem.zeros(nqh * hd)
+    dev.attention(pq, pkc, pvc, po, seq, layer, max_ctx, nqh, nkh, hd, scale)
+    got = dev.download(po, nqh * hd, np.float32)
+    want = oracle.attention(q, kc, vc, seq, layer, max_ctx, nqh, nkh, hd, scale)
+    assert np.all(np.abs(got - want) <= 1e-4 + 1e-4 * np.abs(want))
+
+
 @pytest.mark.parametrize("qscale", [1e-6, 1e4])
 def test_attention_q_magnitude(dev, host, oracle, mem, qscale):
     """q far from unit scale (the matrix-core kernel rescales each head's q
