@@ -332,7 +332,7 @@ static hipError_t enqueue_step(const Decoder &d, hipStream_t s) {
             ao.stride_chunks = attention_chunk_stride(m.max_ctx, nkv);
             ao.nkh = nkv;
             ao.pos = pos_dev;
-            ao.attn = d.attn;
+            ao.attn = nullptr;  // (nothing in the step reads the merged vector itself)
             ao.mbuf = d.mbuf;
             ao.mflag = d.mflag;
             ao.spin = d.ao_spin;
