@@ -37,9 +37,9 @@ decoder (vbs_gfx950_decoder_*), and through the g_vbs_hip_backend ops table
 with one dispatch per bridge call. The decode entry's `checked` block comes
 from the CPU leg, after every GPU timing: the decoded tokens against the
 reference CPU backend's 128 for the same model and start
-(tests/golden/decode_7b_greedy.npz), the first four against the oracle's
-forward pass run on the host, and `checked.cpu_baseline`, the same decode on
-the host: one full token of the reference CPU backend on one thread (driven
+(tests/golden/decode_7b_greedy.npz) and the first four against the oracle's
+forward pass run on the host; beside it, the decode entry's `cpu_baseline` is
+the same decode on the host: one full token of the reference CPU backend on one thread (driven
 through its ops table in the bridge's order) and, as `all_cores`, the
 oracle's forward pass on every core.
 
@@ -913,7 +913,9 @@ def main():
     if not a.no_cpu:
         out["cpu_baseline"] = cpu_baseline(host, r["weights_host"], r["xs_host"], beside=cpu_work)
         if toks is not None and a.decode_geometry == "7b" and "tokens_per_s" in dec:
-            dec["checked"] = decode_vs_checkers(host, toks, margins)
+            checked = decode_vs_checkers(host, toks, margins)
+            dec["cpu_baseline"] = checked.pop("cpu_baseline", None)
+            dec["checked"] = checked
     print(json.dumps(out))
 
 
