@@ -390,8 +390,9 @@ def test_gpu_graph_decoder_equals_dispatch_path(host, backend, dev, tiny):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("spin,ctx", [(None, 333), ("0", 333), (None, 28)],
-                         ids=["xcd_exchange", "forced_own_merge", "xcd_exchange_first_chunks"])
+@pytest.mark.parametrize("spin,ctx", [(None, 333), ("0", 333), (None, 28), (None, 0)],
+                         ids=["xcd_exchange", "forced_own_merge", "xcd_exchange_first_chunks",
+                              "xcd_exchange_from_position_0"])
 def test_gpu_graph_decoder_7b_width_equals_dispatch_path(host, backend, dev, spin, ctx, monkeypatch):
     """At the 7B width (4096, 32 q heads of 128: k_mvl's fused attn_norm +
     Q/K/V + RoPE + KV store launch over 6144 rows, the matrix-core attention
@@ -400,20 +401,26 @@ def test_gpu_graph_decoder_7b_width_equals_dispatch_path(host, backend, dev, spi
     the per-dispatch path's (a merge launch, then O) bit for bit, over 2
     layers of the 7B geometry and 8 teacher-forced positions from 333 (from
     28 in the third case: the attention's chunks of 32 positions go from one
-    to two at position 32, so the merge sees its smallest counts). The
+    to two at position 32, so the merge sees its smallest counts; from 0 in
+    the fourth, an empty cache that each run fills itself). The
     O launch's workgroups share the merged heads within each XCD; with
     VBS_ATTN_O_SPIN=0 no workgroup waits for them and every one merges all
     the heads itself instead (the bounded wait's way out), with the same
     results."""
     model = V.SynthModel(host, n_layers=2, **GEO_7B, max_ctx=400, seed=11)
     n = 8
-    kc_p, vc_p = model.kv_prefill(host, ctx)
     d = V.Decoder(host, backend, model)
-    d.load_kv(kc_p, vc_p, ctx)
+    if ctx:
+        kc_p, vc_p = model.kv_prefill(host, ctx)
+    else:  # zeros where the steps will write, so that no row is left from the first run
+        kvd = model.cfg["n_kv_heads"] * model.cfg["head_dim"]
+        kc_p = vc_p = np.zeros(model.cfg["n_layers"] * n * kvd, np.uint16)
+    n_load = ctx or n
+    d.load_kv(kc_p, vc_p, n_load)
     stream = np.random.default_rng(333).integers(0, model.cfg["vocab"], n).tolist()
     want = [d.step(tok, ctx + i) for i, tok in enumerate(stream)]
     want_kc, want_vc = d.read_kv(ctx + n)
-    d.load_kv(kc_p, vc_p, ctx)
+    d.load_kv(kc_p, vc_p, n_load)
     if spin is not None:
         monkeypatch.setenv("VBS_ATTN_O_SPIN", spin)  # (read when the decoder is created)
     g = V.GraphDecoder(dev, d, max_steps=n)
