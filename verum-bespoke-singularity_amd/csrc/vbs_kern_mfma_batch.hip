@@ -470,12 +470,21 @@ __global__ __launch_bounds__(1024) void k_mvbr6(const MbArgs a, uint32_t rpw) {
     constexpr uint32_t NI = P::NI, ISZ = P::ISZ;
     extern __shared__ __align__(16) uint8_t lds[];
     const uint32_t cols = a.cols, nblk = cols >> 8, rb = nblk * 210u;
-    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63u;
     const uint32_t n = lane & 15u, g = lane >> 4;
     const uint32_t r0 = blockIdx.x * rpw, r1 = min(r0 + rpw, a.rows[0]);
     if (r0 >= r1) return;
     const XbLayout L = xb_layout(cols);
     const uint32_t pl = min(n, 2u * a.batch - 1u);
+    // the lane's chunk of each of an item's four DMAs: chunk c = 14 n' + k'
+    // of the tile, row n' of the tile and byte 16 k' of the row's run
+    uint32_t lrow[4], lchk[4];
+#pragma unroll
+    for (uint32_t q = 0; q < 4u; q++) {
+        const uint32_t c = min(64u * q + lane, 223u);
+        lrow[q] = c / 14u;
+        lchk[q] = 16u * (c % 14u);
+    }
     const XbView xv{reinterpret_cast<const _Float16 *>(a.xp) + 8u * pl,
                     reinterpret_cast<const _Float16 *>(a.xp + L.msum) + 8u * pl,
                     reinterpret_cast<const int *>(a.xp + L.expo)};
@@ -498,10 +507,9 @@ __global__ __launch_bounds__(1024) void k_mvbr6(const MbArgs a, uint32_t rpw) {
         const uint32_t dst = ring + (i % R) * ISZ;
 #pragma unroll
         for (uint32_t q = 0; q < 4u; q++) {
-            const uint32_t c = min(64u * q + lane, 223u);  // chunk 14 n' + k' of the tile
-            const uint32_t st = min(r0 + 16u * j + c / 14u, r1 - 1u) * rb + b * 210u;
-            const uint32_t off = ((st + wlo) & ~15u) + 16u * (c % 14u);
-            if (q < 3u || lane < 32u) dma16(w - wlo + off, dst + 1024u * q);
+            const uint32_t st = min(r0 + 16u * j + lrow[q], r1 - 1u) * rb + b * 210u;
+            const uint32_t off = ((st + wlo) & ~15u) + lchk[q];
+            if (q < 3u || lane < 32u) dma16s(w - wlo, off, dst + 1024u * q);
         }
     };
     unroll_for<0u, R>(issue);

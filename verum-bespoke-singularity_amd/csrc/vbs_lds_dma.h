@@ -25,6 +25,13 @@ __device__ __forceinline__ void dma16(const void *g, uint32_t lds) {
                  "s"(__builtin_amdgcn_readfirstlane(lds))
                  : "memory");
 }
+// The same from base + off: base wave-uniform (a scalar register pair), off a
+// 32-bit byte offset per lane, so no 64-bit address is formed per lane.
+__device__ __forceinline__ void dma16s(const void *base, uint32_t off, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base),
+                 "s"(__builtin_amdgcn_readfirstlane(lds))
+                 : "memory");
+}
 // 4 bytes per lane from g to LDS at lds + 4 lane (lds wave-uniform, in M0).
 __device__ __forceinline__ void dma4(const void *g, uint32_t lds) {
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g),
