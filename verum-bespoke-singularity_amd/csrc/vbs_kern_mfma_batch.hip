@@ -330,19 +330,29 @@ struct Q6KB {
         const uint32_t dbits = (rw[52] >> (8u * sh)) & 0xFFFFu;
         const h2 n1056 = {(_Float16)-1056.f, (_Float16)-1056.f};
         const f4 z = {0.f, 0.f, 0.f, 0.f};
-        float a0 = 0.f, a1 = 0.f;
-#pragma unroll
-        for (uint32_t G = 0; G < 16u; G++) {
+        float a0 = 0.f, a1 = 0.f, c0 = 0.f, c1 = 0.f;
+        auto bq = [&](uint32_t G) {
             const uint32_t h = G >> 3, q = (G >> 1) & 3u, u = G & 1u;
             const uint32_t l4 = (ql[4u * h + 2u * (q & 1u) + u] >> (4u * (q >> 1))) & 0x0F0F0F0Fu;
             const uint32_t h2b = (qh[2u * h + u] >> (2u * q)) & 0x03030303u;
             const uint32_t q6 = l4 | (h2b << 4);
-            const h4 B = join4(f16_bytes(q6, 0x00050004u) + n1056, f16_bytes(q6, 0x00070006u) + n1056);
-            const f4 D = __builtin_amdgcn_mfma_f32_16x16x16f16(x.g[G], B, z, 0, 0, 0);
-            const float s = (float)(int)(int8_t)(sc[G >> 2] >> (8u * (G & 3u)));
-            a0 = fmaf(s, D[0] + D[1], a0);
-            a1 = fmaf(s, D[2] + D[3], a1);
+            return join4(f16_bytes(q6, 0x00050004u) + n1056, f16_bytes(q6, 0x00070006u) + n1056);
+        };
+        auto scale = [&](uint32_t G) { return (float)(int)(int8_t)(sc[G >> 2] >> (8u * (G & 3u))); };
+        // two independent chains (groups G and G + 8): each MFMA's result is
+        // consumed after the other chain's MFMA has issued
+#pragma unroll
+        for (uint32_t G = 0; G < 8u; G++) {
+            const f4 D0 = __builtin_amdgcn_mfma_f32_16x16x16f16(x.g[G], bq(G), z, 0, 0, 0);
+            const f4 D1 = __builtin_amdgcn_mfma_f32_16x16x16f16(x.g[G + 8u], bq(G + 8u), z, 0, 0, 0);
+            const float s0 = scale(G), s1 = scale(G + 8u);
+            a0 = fmaf(s0, D0[0] + D0[1], a0);
+            a1 = fmaf(s0, D0[2] + D0[3], a1);
+            c0 = fmaf(s1, D1[0] + D1[1], c0);
+            c1 = fmaf(s1, D1[2] + D1[3], c1);
         }
+        a0 += c0;
+        a1 += c1;
         const float d = cvt_h(dbits);
         acc[0] += ldexpf(d * a0, -x.s.x);
         acc[1] += ldexpf(d * a1, -x.s.y);
