@@ -818,7 +818,11 @@ __global__ __launch_bounds__(1024) void k_mvbr4(const MbArgs a) {
 
 template <uint32_t NB, uint32_t T, int EPI, bool RANGED = false>
 static hipError_t launch_mvbr4_t(const MbArgs &a, uint32_t wgs, hipStream_t s) {
-    constexpr uint32_t R = NB * T < 3u ? NB * T : 3u;
+    // a wave's items all in flight when it has at most four (147 KB of LDS),
+    // else three slots: four slots made the longer streams slower (70B
+    // gate/up 61.6 -> 63.3-66.0 us, Q/K/V 16.8 -> 17.4-17.7 us) while the
+    // four-item O launch gained (14.6 -> 14.3 us)
+    constexpr uint32_t R = NB * T <= 4u ? NB * T : 3u;
     const size_t lds = Mvbr4Plan<NB, T, R>::lds();
     static bool granted = false;
     if (!granted) {
