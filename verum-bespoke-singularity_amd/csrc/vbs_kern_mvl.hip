@@ -85,13 +85,32 @@ __global__ __launch_bounds__(64 * kMvlWaves) void k_mvl(const MvArgs a, uint32_t
     if (w0 && lane == 0u) dma4(a.pos, (uint32_t)(uintptr_t)qpos);
     dma16(a.x + 256u * b + 4u * lane, (uint32_t)(uintptr_t)slot);
     if constexpr (NORM) dma16(a.norm_w + 256u * b + 4u * lane, (uint32_t)(uintptr_t)nslot);
+    // the lane's chunk c = 9 n' + p of each of a tile's three DMAs: row n' of
+    // the tile, piece p of its 144 bytes
+    uint32_t lrow[3], lchk[3];
+#pragma unroll
+    for (uint32_t q = 0; q < 3u; q++) {
+        lrow[q] = (64u * q + lane) / 9u;
+        lchk[q] = 16u * ((64u * q + lane) % 9u);
+    }
     auto issue_tile = [&](uint32_t j) {
+        // a tile inside one matrix (all but those across a Q/K or K/V border)
+        // takes 32-bit offsets from that matrix's base in scalar registers
+        const uint32_t t0 = r0 + 16u * j, tl = min(t0 + 15u, r1 - 1u);
+        const uint32_t m = EPI == E_QKV ? mat(t0) : 0u;
+        const bool one = EPI != E_QKV || m == mat(tl);
+        const uint32_t start = m == 0u ? 0u : m == 1u ? e0 : e1;
+        const uint8_t *const wm = m == 0u ? a.w[0] : m == 1u ? a.w[1] : a.w[2];
 #pragma unroll
         for (uint32_t q = 0; q < 3; q++) {
-            const uint32_t c = 64u * q + lane;
-            const uint32_t row = min(r0 + 16u * j + c / 9u, r1 - 1u);
-            const uint8_t *src = wrow(row) + (b * 144u + 16u * (c % 9u));
-            if (q < 2u || lane < 16u) dma16(src, stage + j * kMvlItem + 1024u * q);
+            const uint32_t row = min(t0 + lrow[q], r1 - 1u);
+            const uint32_t dst = stage + j * kMvlItem + 1024u * q;
+            if (q < 2u || lane < 16u) {
+                if (one)
+                    dma16s(wm, (row - start) * rb + b * 144u + lchk[q], dst);
+                else
+                    dma16(wrow(row) + (b * 144u + lchk[q]), dst);
+            }
         }
     };
     // With the RMSNorm, tiles from kPre on are requested after the barrier
